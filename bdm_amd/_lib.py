@@ -1,0 +1,90 @@
+"""ctypes binding of ``libbdm_hip.so`` (the C ABI declared in ``include/bdm_hip.h``).
+
+The library is built in-tree by ``bdm_amd/csrc/Makefile``.  Loading never
+falls back to anything else: a missing or unloadable library raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from functools import lru_cache
+
+LIBRARY_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'libbdm_hip.so')
+
+BDM_F32 = 0
+BDM_BF16 = 1
+BDM_ROUTE_OUT_OF_RANGE = 1
+BDM_ROUTE_DUPLICATE = 2
+
+EXPORTED_SYMBOLS = (
+    'bdm_version', 'bdm_last_error_string', 'bdm_router_select', 'bdm_dispatch_workspace_size',
+    'bdm_dispatch_build', 'bdm_forward_workspace_size', 'bdm_forward', 'bdm_decode',
+)
+
+_i32, _i64, _f32, _vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
+_size_t = ctypes.c_size_t
+
+
+class ForwardArgs(ctypes.Structure):
+    """Mirror of ``bdm_forward_args``."""
+    _fields_ = [
+        ('q', _vp), ('k', _vp), ('g', _vp), ('b', _vp), ('v', _vp), ('w', _vp),
+        ('write_weights', _vp), ('read_weights', _vp), ('read_indices', _vp),
+        ('order', _vp), ('cu_seqlens', _vp), ('initial', _vp), ('final_state', _vp), ('output', _vp),
+        ('initial_batch_stride', _i64), ('batch', _i64), ('time', _i64),
+        ('heads', _i32), ('bank_size', _i32), ('head_width', _i32), ('bank_count', _i32),
+        ('write_banks', _i32), ('read_banks', _i32),
+        ('ctrl_dtype', _i32), ('initial_dtype', _i32), ('final_dtype', _i32),
+        ('routed_decay', _i32), ('round_interval', _i32), ('scale', _f32),
+    ]
+
+
+class DecodeArgs(ctypes.Structure):
+    """Mirror of ``bdm_decode_args``."""
+    _fields_ = [
+        ('q', _vp), ('k', _vp), ('b', _vp), ('g', _vp), ('v', _vp), ('w', _vp),
+        ('write_weights', _vp), ('read_weights', _vp), ('write_indices', _vp), ('read_indices', _vp),
+        ('state', _vp), ('output', _vp), ('batch', _i64),
+        ('heads', _i32), ('bank_size', _i32), ('head_width', _i32), ('bank_count', _i32),
+        ('write_banks', _i32), ('read_banks', _i32),
+        ('ctrl_dtype', _i32), ('state_dtype', _i32), ('routed_decay', _i32), ('scale', _f32),
+    ]
+
+
+class BDMError(RuntimeError):
+    """A call into libbdm_hip returned a non-zero status."""
+
+
+@lru_cache(maxsize=None)
+def library() -> ctypes.CDLL:
+    if not os.path.exists(LIBRARY_PATH):
+        raise ImportError(f'{LIBRARY_PATH} is missing; build it with `make -C bdm_amd/csrc` '
+                          'or __graft_entry__.build()')
+    lib = ctypes.CDLL(LIBRARY_PATH)
+    lib.bdm_version.restype = _i32
+    lib.bdm_last_error_string.restype = ctypes.c_char_p
+    lib.bdm_router_select.argtypes = [_vp, _i32, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _vp]
+    lib.bdm_router_select.restype = _i32
+    lib.bdm_dispatch_workspace_size.argtypes = [_i64, _i64, _i32]
+    lib.bdm_dispatch_workspace_size.restype = _size_t
+    lib.bdm_dispatch_build.argtypes = [_vp, _vp, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp,
+                                       _vp, _size_t, _vp]
+    lib.bdm_dispatch_build.restype = _i32
+    lib.bdm_forward_workspace_size.argtypes = [ctypes.POINTER(ForwardArgs)]
+    lib.bdm_forward_workspace_size.restype = _size_t
+    lib.bdm_forward.argtypes = [ctypes.POINTER(ForwardArgs), _vp, _size_t, _vp]
+    lib.bdm_forward.restype = _i32
+    lib.bdm_decode.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
+    lib.bdm_decode.restype = _i32
+    return lib
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        message = library().bdm_last_error_string().decode(errors='replace')
+        if status in (-1,):
+            raise ValueError(f'{what}: {message}')
+        if status in (-2,):
+            raise NotImplementedError(f'{what}: {message}')
+        raise BDMError(f'{what} failed ({status}): {message}')

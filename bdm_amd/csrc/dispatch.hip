@@ -1,0 +1,201 @@
+// Causal bank dispatch: a stable counting sort of (token, bank) events into
+// per-(batch, bank) segments.
+//
+// Reference: role_bank_dispatch.py:15-38 (_keys, _bounds), :143-153
+// (metadata: torch.sort of the int64 keys ((b*J + bank)*T + t)*2 + is_read)
+// and the INVERSE/TOKENS maps of _pack (:72-73).  The keys are unique, so the
+// sorting permutation is unique; a counting sort by segment that keeps each
+// segment's events in (t, write-before-read) order produces the same one.
+//
+// Three passes over tiles of 32 tokens of one batch:
+//   1. tile_count: LDS bit-masks mask[bank] with bit 2*t_local + is_read set
+//      for every event of the tile (64-bit LDS atomic OR; order-independent,
+//      so deterministic).  popcount(mask[bank]) is the tile's bucket count.
+//   2. scan: per batch, an exclusive scan over tiles for every bank (a tile's
+//      base inside its segment), then an exclusive scan over banks (segment
+//      starts).  Batch b's segments start at b*T*(KW+KR): every token adds
+//      exactly KW+KR events to its own batch.
+//   3. scatter: rebuild the masks; an event's rank inside its tile-bucket is
+//      popcount(mask[bank] & below(bit)), i.e. the number of earlier
+//      (t, phase) slots of the tile that hit the same bank.  That is the
+//      stable order, computed without any serial step.
+#include "bdm_common.h"
+
+namespace bdm {
+namespace {
+
+constexpr int kTileTokens = 32;  // 2 bits per token in a 64-bit mask
+constexpr int kMaxBanks = 8192;  // LDS masks: 64 KiB
+
+struct DispatchGeometry {
+    int64_t batch, time, nt;
+    int kw, kr, banks;
+    int tiles;  // tiles per batch
+};
+
+__device__ __forceinline__ int load_bank(const int64_t *__restrict__ wi, const int64_t *__restrict__ ri,
+                                         const DispatchGeometry &g, int64_t token, int j, int32_t *status) {
+    const int64_t raw = j < g.kw ? wi[token * g.kw + j] : ri[token * g.kr + (j - g.kw)];
+    if (raw < 0 || raw >= g.banks) {
+        atomicOr(status, int(BDM_ROUTE_OUT_OF_RANGE));
+        return raw < 0 ? 0 : g.banks - 1;
+    }
+    return int(raw);
+}
+
+// Fill the tile's LDS masks.  Returns after a barrier.
+__device__ void build_masks(unsigned long long *masks, const int64_t *__restrict__ wi,
+                            const int64_t *__restrict__ ri, const DispatchGeometry &g, int b, int tile,
+                            int32_t *status) {
+    for (int x = threadIdx.x; x < g.banks; x += blockDim.x) masks[x] = 0ull;
+    __syncthreads();
+    const int per_token = g.kw + g.kr;
+    const int t0 = tile * kTileTokens;
+    const int ntok = min(kTileTokens, int(g.time - t0));
+    for (int i = threadIdx.x; i < ntok * per_token; i += blockDim.x) {
+        const int tl = i / per_token, j = i - tl * per_token;
+        const int64_t token = int64_t(b) * g.time + t0 + tl;
+        const int bank = load_bank(wi, ri, g, token, j, status);
+        const unsigned long long bit = 1ull << (2 * tl + (j >= g.kw));
+        const unsigned long long old = atomicOr(&masks[bank], bit);
+        if (old & bit) atomicOr(status, int(BDM_ROUTE_DUPLICATE));
+    }
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(512) void dispatch_tile_count(const int64_t *__restrict__ wi,
+                                                           const int64_t *__restrict__ ri, DispatchGeometry g,
+                                                           int32_t *__restrict__ tile_counts, int32_t *status) {
+    extern __shared__ unsigned long long masks[];
+    const int tile = blockIdx.x, b = blockIdx.y;
+    build_masks(masks, wi, ri, g, b, tile, status);
+    int32_t *out = tile_counts + (int64_t(b) * g.tiles + tile) * g.banks;
+    for (int x = threadIdx.x; x < g.banks; x += blockDim.x) out[x] = __popcll(masks[x]);
+}
+
+// One workgroup per batch.  tile_counts becomes each tile's offset inside its
+// segment; cu_seqlens receives the segment starts.
+__global__ __launch_bounds__(1024) void dispatch_scan(DispatchGeometry g, int32_t *__restrict__ tile_counts,
+                                                      int64_t *__restrict__ cu_seqlens) {
+    extern __shared__ int32_t totals[];  // [banks]
+    __shared__ int32_t wave_sums[1024 / kWave];
+    const int b = blockIdx.x;
+    int32_t *base = tile_counts + int64_t(b) * g.tiles * g.banks;
+    for (int x = threadIdx.x; x < g.banks; x += blockDim.x) {
+        int32_t running = 0;
+        for (int t = 0; t < g.tiles; ++t) {
+            const int32_t c = base[int64_t(t) * g.banks + x];
+            base[int64_t(t) * g.banks + x] = running;
+            running += c;
+        }
+        totals[x] = running;
+    }
+    __syncthreads();
+    // Exclusive scan of totals[0:banks]: each thread owns a contiguous chunk.
+    const int per = (g.banks + blockDim.x - 1) / blockDim.x;
+    const int lo = min(g.banks, int(threadIdx.x) * per), hi = min(g.banks, lo + per);
+    int32_t local = 0;
+    for (int x = lo; x < hi; ++x) local += totals[x];
+    // inclusive wave scan of `local`
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    int32_t incl = local;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const int32_t up = __shfl_up(incl, d, kWave);
+        if (lane >= d) incl += up;
+    }
+    if (lane == kWave - 1) wave_sums[wave] = incl;
+    __syncthreads();
+    int32_t wave_offset = 0;
+    for (int w = 0; w < wave; ++w) wave_offset += wave_sums[w];
+    int32_t running = wave_offset + incl - local;
+    __syncthreads();  // every thread has read its chunk of totals
+    for (int x = lo; x < hi; ++x) {
+        const int32_t c = totals[x];
+        totals[x] = running;
+        running += c;
+    }
+    __syncthreads();
+    const int64_t batch_base = int64_t(b) * g.time * (g.kw + g.kr);
+    for (int x = threadIdx.x; x < g.banks; x += blockDim.x)
+        cu_seqlens[int64_t(b) * g.banks + x] = batch_base + totals[x];
+    if (b == g.batch - 1 && threadIdx.x == 0) cu_seqlens[g.batch * g.banks] = g.nt * (g.kw + g.kr);
+}
+
+__global__ __launch_bounds__(512) void dispatch_scatter(const int64_t *__restrict__ wi,
+                                                        const int64_t *__restrict__ ri, DispatchGeometry g,
+                                                        const int32_t *__restrict__ tile_base,
+                                                        const int64_t *__restrict__ cu_seqlens,
+                                                        int64_t *__restrict__ order, int64_t *__restrict__ inverse,
+                                                        int64_t *__restrict__ tokens, int32_t *status) {
+    extern __shared__ unsigned long long masks[];
+    const int tile = blockIdx.x, b = blockIdx.y;
+    build_masks(masks, wi, ri, g, b, tile, status);
+    const int per_token = g.kw + g.kr;
+    const int t0 = tile * kTileTokens;
+    const int ntok = min(kTileTokens, int(g.time - t0));
+    const int32_t *tb = tile_base + (int64_t(b) * g.tiles + tile) * g.banks;
+    const int64_t events = g.nt * per_token;
+    for (int i = threadIdx.x; i < ntok * per_token; i += blockDim.x) {
+        const int tl = i / per_token, j = i - tl * per_token;
+        const int64_t token = int64_t(b) * g.time + t0 + tl;
+        const int64_t raw = j < g.kw ? wi[token * g.kw + j] : ri[token * g.kr + (j - g.kw)];
+        const int bank = raw < 0 ? 0 : (raw >= g.banks ? g.banks - 1 : int(raw));
+        const int bit = 2 * tl + (j >= g.kw);
+        const int rank = __popcll(masks[bank] & ((1ull << bit) - 1ull));
+        int64_t pos = cu_seqlens[int64_t(b) * g.banks + bank] + tb[bank] + rank;
+        pos = pos < 0 ? 0 : (pos >= events ? events - 1 : pos);
+        const int64_t original = j < g.kw ? token * g.kw + j : g.nt * g.kw + token * g.kr + (j - g.kw);
+        order[pos] = original;
+        inverse[original] = pos;
+        tokens[pos] = token;
+    }
+}
+
+}  // namespace
+}  // namespace bdm
+
+using bdm::kMaxBanks;
+using bdm::kTileTokens;
+
+static int64_t tiles_per_batch(int64_t time) { return (time + kTileTokens - 1) / kTileTokens; }
+
+extern "C" size_t bdm_dispatch_workspace_size(int64_t batch, int64_t time, int32_t bank_count) {
+    if (batch <= 0 || time <= 0 || bank_count <= 0) return 0;
+    return size_t(batch) * size_t(tiles_per_batch(time)) * size_t(bank_count) * sizeof(int32_t);
+}
+
+extern "C" int bdm_dispatch_build(const int64_t *write_indices, const int64_t *read_indices, int64_t batch,
+                                  int64_t time, int32_t write_banks, int32_t read_banks, int32_t bank_count,
+                                  int64_t *order, int64_t *inverse, int64_t *tokens, int64_t *cu_seqlens,
+                                  int32_t *status, void *workspace, size_t workspace_bytes, void *stream) {
+    using namespace bdm;
+    if (batch <= 0 || time <= 0 || write_banks < 0 || read_banks < 0 || write_banks + read_banks == 0 ||
+        bank_count <= 0)
+        return fail(BDM_ERR_INVALID, "dispatch: bad geometry batch=%lld time=%lld KW=%d KR=%d J=%d",
+                    (long long)batch, (long long)time, write_banks, read_banks, bank_count);
+    if (bank_count > kMaxBanks)
+        return fail(BDM_ERR_UNSUPPORTED, "dispatch: bank_count=%d above %d", bank_count, kMaxBanks);
+    const int64_t nt = batch * time;
+    const int64_t events = nt * (write_banks + read_banks);
+    if (events >= (int64_t(1) << 31) || batch > 65535)
+        return fail(BDM_ERR_UNSUPPORTED, "dispatch: %lld events exceed the int32 ranks", (long long)events);
+    if ((write_banks && !write_indices) || (read_banks && !read_indices) || !order || !inverse || !tokens ||
+        !cu_seqlens || !status)
+        return fail(BDM_ERR_INVALID, "dispatch: null pointer");
+    const size_t need = bdm_dispatch_workspace_size(batch, time, bank_count);
+    if (!workspace || workspace_bytes < need)
+        return fail(BDM_ERR_WORKSPACE, "dispatch: workspace %zu < %zu bytes", workspace_bytes, need);
+    DispatchGeometry g{batch, time, nt, write_banks, read_banks, bank_count, int(tiles_per_batch(time))};
+    hipStream_t s = as_stream(stream);
+    auto *tile_counts = static_cast<int32_t *>(workspace);
+    const size_t mask_bytes = size_t(bank_count) * sizeof(unsigned long long);
+    const dim3 tiles(unsigned(g.tiles), unsigned(batch));
+    dispatch_tile_count<<<tiles, 512, mask_bytes, s>>>(write_indices, read_indices, g, tile_counts, status);
+    if (int rc = check_launch("dispatch_tile_count")) return rc;
+    dispatch_scan<<<unsigned(batch), 1024, size_t(bank_count) * sizeof(int32_t), s>>>(g, tile_counts, cu_seqlens);
+    if (int rc = check_launch("dispatch_scan")) return rc;
+    dispatch_scatter<<<tiles, 512, mask_bytes, s>>>(write_indices, read_indices, g, tile_counts, cu_seqlens,
+                                                    order, inverse, tokens, status);
+    return check_launch("dispatch_scatter");
+}

@@ -1,0 +1,373 @@
+// Routed GDN2 bank recurrence (forward) and the r-weighted read combine.
+//
+// Reference semantics: _pack (role_bank_dispatch.py:41-73), decay_transform
+// (routed_update.py:5-13), _role_forward/_write (role_bank_kernel.py:32-73),
+// _readout (role_bank_dispatch.py:201-231); stateful variants in
+// forward_rows.py:10-194 (final state) and inference.py:70-85.
+//
+// Layout of the work (MI355X): one workgroup per (batch, bank) segment runs
+// that segment's events in packed order for every head at once.  A lane owns
+// CPL value columns of one head and keeps all S rows of those columns in
+// registers (S*CPL FP32 values), so the erase reduction over rows is in-lane
+// and a write costs three FMA-class ops per state element.  The per-event
+// metadata (token, route weight, role) is shared by all heads and staged
+// through LDS 64 events at a time; the per-token controller rows are
+// prefetched one event ahead in registers.
+//
+// Segments of one batch are mapped to one XCD where the grid allows it
+// (segment = (blockIdx % 8) * (segments / 8) + blockIdx / 8): the 16 events of
+// a token then run on the same XCD and its controller rows are fetched into
+// one L2 instead of eight.
+//
+// Read results (one S-row contraction per read event and head) go to a BF16
+// (ctrl dtype) buffer indexed by the read's original slot token*KR + j; the
+// combine kernel adds a token's KR reads in increasing bank id, rounding after
+// every add (the production readout order).
+#include "bdm_common.h"
+
+namespace bdm {
+namespace {
+
+constexpr int kStage = 64;  // events staged per LDS batch
+
+template <typename T>
+struct ForwardParams {
+    const T *q, *k, *b;
+    const float *g;
+    const T *v, *w;
+    const T *ww, *rw;
+    const int64_t *order, *cu;
+    const void *initial;
+    void *final_state;
+    T *zbuf;
+    int64_t init_bstride;
+    int64_t nt, time;
+    int heads, s_real, width, banks, kw, kr;
+    int lanes_per_head, heads_per_block;
+    int round_interval, routed_decay;
+    int init_dtype, final_dtype;
+    int xcd_remap;
+    float scale;
+};
+
+// Load `S` per-row controller values of one (token, head); rows >= s_real are 0.
+template <int S, typename E>
+__device__ __forceinline__ void load_rows(const E *p, int s_real, float (&out)[S]) {
+    if (s_real == S) {
+        load_row<S>(p, out);
+    } else {
+#pragma unroll
+        for (int r = 0; r < S; ++r) out[r] = r < s_real ? to_f32(p[r]) : 0.f;
+    }
+}
+
+template <int S, int CPL>
+__device__ __forceinline__ void load_state(const void *base, int dtype, int64_t offset, int width, int s_real,
+                                           float (&h)[S][CPL]) {
+#pragma unroll
+    for (int r = 0; r < S; ++r) {
+        if (r < s_real) {
+            if (dtype == BDM_BF16)
+                load_row<CPL>(static_cast<const bf16_t *>(base) + offset + int64_t(r) * width, h[r]);
+            else
+                load_row<CPL>(static_cast<const float *>(base) + offset + int64_t(r) * width, h[r]);
+        } else {
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) h[r][c] = 0.f;
+        }
+    }
+}
+
+template <int S, int CPL>
+__device__ __forceinline__ void store_state(void *base, int dtype, int64_t offset, int width, int s_real,
+                                            const float (&h)[S][CPL]) {
+#pragma unroll
+    for (int r = 0; r < S; ++r) {
+        if (r < s_real) {
+            if (dtype == BDM_BF16)
+                store_row<CPL>(static_cast<bf16_t *>(base) + offset + int64_t(r) * width, h[r]);
+            else
+                store_row<CPL>(static_cast<float *>(base) + offset + int64_t(r) * width, h[r]);
+        }
+    }
+}
+
+// Registers of one event's per-lane operands (one head).
+template <int S, int CPL>
+struct EventOperands {
+    float key[S];   // k for a write, q for a read
+    float gate[S];  // g
+    float erase[S]; // b
+    float value[CPL];
+    float wgate[CPL];
+};
+
+template <typename T, int S, int CPL>
+__device__ __forceinline__ void fetch_event(const ForwardParams<T> &p, int64_t token, bool is_read, int head,
+                                            int col0, EventOperands<S, CPL> &ev) {
+    const int64_t row = token * p.heads + head;
+    if (is_read) {
+        load_rows<S>(p.q + row * p.s_real, p.s_real, ev.key);
+    } else {
+        load_rows<S>(p.k + row * p.s_real, p.s_real, ev.key);
+        load_rows<S>(p.g + row * p.s_real, p.s_real, ev.gate);
+        load_rows<S>(p.b + row * p.s_real, p.s_real, ev.erase);
+        load_row<CPL>(p.v + row * p.width + col0, ev.value);
+        load_row<CPL>(p.w + row * p.width + col0, ev.wgate);
+    }
+}
+
+template <typename T, int S, int CPL>
+__global__ __launch_bounds__(256) void routed_forward_kernel(ForwardParams<T> p) {
+    __shared__ int64_t s_token[kStage];
+    __shared__ int64_t s_slot[kStage];  // read: original read slot; write: -1
+    __shared__ float s_weight[kStage];
+
+    const int nseg = gridDim.x;
+    const int seg = p.xcd_remap ? int((blockIdx.x % 8) * (nseg / 8) + blockIdx.x / 8) : int(blockIdx.x);
+    const int bank = seg % p.banks;
+    const int64_t bidx = seg / p.banks;
+    const int head = blockIdx.y * p.heads_per_block + int(threadIdx.x) / p.lanes_per_head;
+    const bool active = int(threadIdx.x) < p.heads_per_block * p.lanes_per_head && head < p.heads;
+    const int col0 = (int(threadIdx.x) % p.lanes_per_head) * CPL;
+    const int64_t start = p.cu[seg], end = p.cu[seg + 1];
+    const int64_t write_events = p.nt * p.kw;
+    const int64_t events = p.nt * (p.kw + p.kr);
+    const bool rounding = p.round_interval > 0;
+
+    float h[S][CPL];
+    const int64_t state_offset = ((int64_t(bank) * p.heads + head) * p.s_real) * p.width + col0;
+    if (active) {
+        load_state<S, CPL>(p.initial, p.init_dtype, bidx * p.init_bstride + state_offset, p.width, p.s_real, h);
+        if (rounding) {
+#pragma unroll
+            for (int r = 0; r < S; ++r)
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) h[r][c] = round_bf16(h[r][c]);
+        }
+    }
+
+    for (int64_t base = start; base < end; base += kStage) {
+        const int n = int(min(int64_t(kStage), end - base));
+        __syncthreads();
+        if (int(threadIdx.x) < n) {
+            int64_t o = p.order[base + threadIdx.x];
+            o = o < 0 ? 0 : (o >= events ? events - 1 : o);
+            const bool rd = o >= write_events;
+            const int64_t route = rd ? o - write_events : o;
+            s_token[threadIdx.x] = rd ? route / p.kr : route / p.kw;
+            s_slot[threadIdx.x] = rd ? route : -1;
+            s_weight[threadIdx.x] = rd ? to_f32(p.rw[route]) : to_f32(p.ww[route]);
+        }
+        __syncthreads();
+        if (!active) continue;
+
+        EventOperands<S, CPL> cur, nxt;
+        fetch_event<T, S, CPL>(p, s_token[0], s_slot[0] >= 0, head, col0, cur);
+        for (int i = 0; i < n; ++i) {
+            const int64_t slot = s_slot[i];
+            const float pw = s_weight[i];
+            if (i + 1 < n) fetch_event<T, S, CPL>(p, s_token[i + 1], s_slot[i + 1] >= 0, head, col0, nxt);
+            const int64_t offset = base + i - start;
+            if (rounding && offset > 0 && offset % p.round_interval == 0) {
+#pragma unroll
+                for (int r = 0; r < S; ++r)
+#pragma unroll
+                    for (int c = 0; c < CPL; ++c) h[r][c] = round_bf16(h[r][c]);
+            }
+            if (slot < 0) {
+                // write: hd = exp(eg) M ; u = bf(w p) v - (bf(b p) k)^T hd ; M = hd + k u^T
+                float decay[S], a[S];
+#pragma unroll
+                for (int r = 0; r < S; ++r) {
+                    const float eg = p.routed_decay ? cur.gate[r] * pw : cur.gate[r];
+                    decay[r] = __expf(eg);
+                    a[r] = round_to<T>(cur.erase[r] * pw) * cur.key[r];
+                }
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) {
+                    float erase = 0.f;
+#pragma unroll
+                    for (int r = 0; r < S; ++r) {
+                        h[r][c] *= decay[r];
+                        erase = fmaf(a[r], h[r][c], erase);
+                    }
+                    const float u = round_to<T>(cur.wgate[c] * pw) * cur.value[c] - erase;
+#pragma unroll
+                    for (int r = 0; r < S; ++r) h[r][c] = fmaf(cur.key[r], u, h[r][c]);
+                }
+            } else {
+                // read: z = scale * bf(q r)^T M, stored in the value dtype
+                float qr[S];
+#pragma unroll
+                for (int r = 0; r < S; ++r) qr[r] = round_to<T>(cur.key[r] * pw);
+                float z[CPL];
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) {
+                    float acc = 0.f;
+#pragma unroll
+                    for (int r = 0; r < S; ++r) acc = fmaf(qr[r], h[r][c], acc);
+                    z[c] = acc * p.scale;
+                }
+                store_row<CPL>(p.zbuf + (slot * p.heads + head) * p.width + col0, z);
+            }
+            cur = nxt;
+        }
+    }
+    if (active && p.final_state) {
+        const int64_t final_offset = bidx * (int64_t(p.banks) * p.heads * p.s_real * p.width) + state_offset;
+        store_state<S, CPL>(p.final_state, p.final_dtype, final_offset, p.width, p.s_real, h);
+    }
+}
+
+// y[token, :] = fold over the token's reads in increasing bank id of
+// bf(total + z).  One workgroup per token; a thread owns CPL columns.
+template <typename T, int CPL>
+__global__ __launch_bounds__(256) void ordered_combine_kernel(const T *__restrict__ zbuf,
+                                                              const int64_t *__restrict__ read_indices,
+                                                              T *__restrict__ y, int kr, int row_width) {
+    __shared__ int s_rank_slot[32];
+    const int64_t token = blockIdx.x;
+    if (int(threadIdx.x) < kr) {
+        const int64_t mine = read_indices[token * kr + threadIdx.x];
+        int rank = 0;
+        for (int j = 0; j < kr; ++j) {
+            const int64_t other = read_indices[token * kr + j];
+            rank += (other < mine) || (other == mine && j < int(threadIdx.x));
+        }
+        s_rank_slot[rank] = threadIdx.x;
+    }
+    __syncthreads();
+    for (int col0 = threadIdx.x * CPL; col0 < row_width; col0 += blockDim.x * CPL) {
+        float total[CPL];
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) total[c] = 0.f;
+        for (int j = 0; j < kr; ++j) {
+            float z[CPL];
+            load_row<CPL>(zbuf + (token * kr + s_rank_slot[j]) * row_width + col0, z);
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) total[c] = round_to<T>(total[c] + z[c]);
+        }
+        store_row<CPL>(y + token * row_width + col0, total);
+    }
+}
+
+// A kernel rather than hipMemsetAsync, so callers may capture it in a graph.
+template <typename T>
+__global__ __launch_bounds__(256) void zero_fill_kernel(T *__restrict__ out, int64_t count) {
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < count) out[i] = from_f32<T>(0.f);
+}
+
+template <typename T, int S, int CPL>
+int launch_forward(const bdm_forward_args &a, T *zbuf, hipStream_t stream) {
+    if (a.head_width / CPL > 256)
+        return fail(BDM_ERR_UNSUPPORTED, "forward: head_width %d needs more than 256 lanes", a.head_width);
+    ForwardParams<T> p{};
+    p.q = static_cast<const T *>(a.q);
+    p.k = static_cast<const T *>(a.k);
+    p.b = static_cast<const T *>(a.b);
+    p.g = a.g;
+    p.v = static_cast<const T *>(a.v);
+    p.w = static_cast<const T *>(a.w);
+    p.ww = static_cast<const T *>(a.write_weights);
+    p.rw = static_cast<const T *>(a.read_weights);
+    p.order = a.order;
+    p.cu = a.cu_seqlens;
+    p.initial = a.initial;
+    p.final_state = a.final_state;
+    p.zbuf = zbuf;
+    p.init_bstride = a.initial_batch_stride;
+    p.nt = a.batch * a.time;
+    p.time = a.time;
+    p.heads = a.heads;
+    p.s_real = a.bank_size;
+    p.width = a.head_width;
+    p.banks = a.bank_count;
+    p.kw = a.write_banks;
+    p.kr = a.read_banks;
+    p.lanes_per_head = a.head_width / CPL;
+    p.heads_per_block = 256 / p.lanes_per_head;
+    if (p.heads_per_block > a.heads) p.heads_per_block = a.heads;
+    p.round_interval = a.round_interval;
+    p.routed_decay = a.routed_decay;
+    p.init_dtype = a.initial_dtype;
+    p.final_dtype = a.final_dtype;
+    p.scale = a.scale;
+    const int64_t nseg = a.batch * a.bank_count;
+    p.xcd_remap = (nseg % 8 == 0) ? 1 : 0;
+    const int threads = ((p.heads_per_block * p.lanes_per_head + kWave - 1) / kWave) * kWave;
+    const dim3 grid(unsigned(nseg), unsigned((a.heads + p.heads_per_block - 1) / p.heads_per_block));
+    routed_forward_kernel<T, S, CPL><<<grid, threads, 0, stream>>>(p);
+    if (int rc = check_launch("routed_forward_kernel")) return rc;
+
+    const int row_width = a.heads * a.head_width;
+    const int64_t nt = a.batch * a.time;
+    if (a.read_banks > 0) {
+        const int cthreads = min(256, max(kWave, ((row_width / CPL + kWave - 1) / kWave) * kWave));
+        ordered_combine_kernel<T, CPL><<<unsigned(nt), cthreads, 0, stream>>>(
+            zbuf, a.read_indices, static_cast<T *>(a.output), a.read_banks, row_width);
+    } else {
+        const int64_t count = nt * row_width;
+        zero_fill_kernel<T><<<unsigned((count + 255) / 256), 256, 0, stream>>>(static_cast<T *>(a.output), count);
+    }
+    return check_launch("ordered_combine_kernel");
+}
+
+template <typename T>
+int dispatch_forward(const bdm_forward_args &a, T *zbuf, hipStream_t stream) {
+    // Vector row loads need 16-byte aligned rows: aligned bases, and a state
+    // batch stride that keeps them aligned.
+    const bool vec = a.initial_batch_stride % 8 == 0;
+    if (a.bank_size <= 8) {
+        if (vec && a.head_width % 8 == 0) return launch_forward<T, 8, 8>(a, zbuf, stream);
+        return launch_forward<T, 8, 1>(a, zbuf, stream);
+    }
+    if (a.bank_size <= 16) {
+        if (vec && a.head_width % 4 == 0) return launch_forward<T, 16, 4>(a, zbuf, stream);
+        return launch_forward<T, 16, 1>(a, zbuf, stream);
+    }
+    if (vec && a.head_width % 2 == 0) return launch_forward<T, 32, 2>(a, zbuf, stream);
+    return launch_forward<T, 32, 1>(a, zbuf, stream);
+}
+
+size_t elem_size(int dtype) { return dtype == BDM_BF16 ? 2 : 4; }
+
+}  // namespace
+}  // namespace bdm
+
+extern "C" size_t bdm_forward_workspace_size(const bdm_forward_args *a) {
+    if (!a || a->batch <= 0 || a->time <= 0 || a->heads <= 0 || a->head_width <= 0 || a->read_banks < 0) return 0;
+    const size_t bytes = size_t(a->batch) * size_t(a->time) * size_t(a->read_banks) * size_t(a->heads) *
+                         size_t(a->head_width) * bdm::elem_size(a->ctrl_dtype);
+    return (bytes + 255) / 256 * 256;
+}
+
+extern "C" int bdm_forward(const bdm_forward_args *a, void *workspace, size_t workspace_bytes, void *stream) {
+    using namespace bdm;
+    if (!a) return fail(BDM_ERR_INVALID, "forward: null args");
+    if (a->batch <= 0 || a->time <= 0 || a->heads <= 0 || a->bank_size <= 0 || a->head_width <= 0 ||
+        a->bank_count <= 0 || a->write_banks < 0 || a->read_banks < 0)
+        return fail(BDM_ERR_INVALID, "forward: bad geometry");
+    if (a->bank_size > 32) return fail(BDM_ERR_UNSUPPORTED, "forward: bank_size %d > 32", a->bank_size);
+    if (a->read_banks > 32) return fail(BDM_ERR_UNSUPPORTED, "forward: read_banks %d > 32", a->read_banks);
+    if (a->ctrl_dtype != BDM_BF16 && a->ctrl_dtype != BDM_F32)
+        return fail(BDM_ERR_INVALID, "forward: ctrl dtype %d", a->ctrl_dtype);
+    if ((a->initial_dtype != BDM_BF16 && a->initial_dtype != BDM_F32) ||
+        (a->final_state && a->final_dtype != BDM_BF16 && a->final_dtype != BDM_F32))
+        return fail(BDM_ERR_INVALID, "forward: state dtype");
+    if (a->batch * a->bank_count > int64_t(INT32_MAX) || a->batch * a->time > (int64_t(1) << 40))
+        return fail(BDM_ERR_UNSUPPORTED, "forward: grid too large");
+    if (!a->q || !a->k || !a->g || !a->b || !a->v || !a->w || !a->write_weights || !a->read_weights ||
+        !a->read_indices || !a->order || !a->cu_seqlens || !a->initial || !a->output)
+        return fail(BDM_ERR_INVALID, "forward: null pointer");
+    const void *ptrs[] = {a->q, a->k, a->g, a->b, a->v, a->w, a->initial, a->output, a->final_state, workspace};
+    for (const void *ptr : ptrs)
+        if (ptr && !aligned(ptr, 16)) return fail(BDM_ERR_INVALID, "forward: tensors must be 16-byte aligned");
+    const size_t need = bdm_forward_workspace_size(a);
+    if (need && (!workspace || workspace_bytes < need))
+        return fail(BDM_ERR_WORKSPACE, "forward: workspace %zu < %zu bytes", workspace_bytes, need);
+    hipStream_t s = as_stream(stream);
+    if (a->ctrl_dtype == BDM_BF16) return dispatch_forward<bf16_t>(*a, static_cast<bf16_t *>(workspace), s);
+    return dispatch_forward<float>(*a, static_cast<float *>(workspace), s);
+}

@@ -1,0 +1,257 @@
+"""Torch-facing wrappers of the HIP entry points.
+
+Each wrapper validates shapes and dtypes the way the reference does before a
+launch (ValueError for bad shapes/dtypes/devices), allocates outputs and the
+workspace with torch on the input's device, and enqueues the kernels on the
+current stream without synchronising.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from .config import near_square_factors
+
+Tensor = torch.Tensor
+
+
+def _dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.bfloat16:
+        return _lib.BDM_BF16
+    if dtype == torch.float32:
+        return _lib.BDM_F32
+    raise ValueError(f'unsupported dtype {dtype}; expected bfloat16 or float32')
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_gpu(*tensors: Tensor) -> torch.device:
+    device = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError('the HIP path requires tensors on a ROCm device')
+        if device is None:
+            device = t.device
+        elif t.device != device:
+            raise ValueError('all tensors must be on the same device')
+    return device
+
+
+def _aligned(t: Tensor) -> Tensor:
+    """Contiguous, 16-byte aligned view (copies only when needed)."""
+    t = t.contiguous()
+    if t.data_ptr() % 16:
+        t = t.clone()
+    return t
+
+
+def _ptr(t: Tensor | None):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+# ---------------------------------------------------------------------------
+# router
+
+def router_select(projected: Tensor, *, bank_count: int, selected_banks: int) -> tuple[Tensor, Tensor]:
+    """Product-key routing of ``projected`` [..., J1+J2] (gdn2_banks.py:74-114).
+
+    Returns ``(weights, indices)``: weights in the score dtype, int64 indices,
+    both [..., C] with C = min(B, min(B, J1, J2)^2)."""
+    if projected.ndim < 1:
+        raise ValueError('projected routes must have a factor dimension')
+    j1, j2 = near_square_factors(bank_count)
+    if projected.shape[-1] != j1 + j2:
+        raise ValueError('projected route width does not match the bank table')
+    if not 1 <= selected_banks <= bank_count:
+        raise ValueError('selected bank count is outside the bank table')
+    _require_gpu(projected)
+    scores = _aligned(projected)
+    s = min(selected_banks, j1, j2)
+    count = min(selected_banks, s * s)
+    rows = scores.numel() // scores.shape[-1]
+    weights = torch.empty((*scores.shape[:-1], count), device=scores.device, dtype=scores.dtype)
+    indices = torch.empty((*scores.shape[:-1], count), device=scores.device, dtype=torch.int64)
+    _lib.check(_lib.library().bdm_router_select(
+        _ptr(scores), _dtype_code(scores.dtype), rows, scores.shape[-1], j1, j2, selected_banks,
+        _ptr(weights), _ptr(indices), _stream(scores.device)), 'bdm_router_select')
+    return weights, indices
+
+
+# ---------------------------------------------------------------------------
+# dispatch
+
+@dataclass
+class Dispatch:
+    """Packed-event metadata (role_bank_dispatch.py:135-140)."""
+    order: Tensor
+    inverse: Tensor
+    tokens: Tensor
+    cu_seqlens: Tensor
+    status: Tensor  # int32 on device: bdm_route_flags raised while building
+
+    def check_routes(self) -> None:
+        """Synchronise and raise ValueError if the routes were malformed."""
+        flags = int(self.status.item())
+        if flags & _lib.BDM_ROUTE_OUT_OF_RANGE:
+            raise ValueError('bank indices outside [0, bank_count)')
+        if flags & _lib.BDM_ROUTE_DUPLICATE:
+            raise ValueError('a token selected the same bank twice in one role')
+
+
+def dispatch_build(write_indices: Tensor, read_indices: Tensor, bank_count: int) -> Dispatch:
+    """Stable bucketing of write/read events into (batch, bank) segments."""
+    if write_indices.ndim != 3 or read_indices.ndim != 3 or write_indices.shape[:2] != read_indices.shape[:2]:
+        raise ValueError('route indices must be [batch, time, selected] with matching batch and time')
+    if write_indices.dtype != torch.long or read_indices.dtype != torch.long:
+        raise ValueError('bank indices must be int64')
+    device = _require_gpu(write_indices, read_indices)
+    batch, time, kw = write_indices.shape
+    kr = read_indices.shape[-1]
+    wi, ri = _aligned(write_indices), _aligned(read_indices)
+    events = batch * time * (kw + kr)
+    lib = _lib.library()
+    order = torch.empty(events, device=device, dtype=torch.int64)
+    inverse = torch.empty(events, device=device, dtype=torch.int64)
+    tokens = torch.empty(events, device=device, dtype=torch.int64)
+    cu = torch.empty(batch * bank_count + 1, device=device, dtype=torch.int64)
+    status = torch.zeros(1, device=device, dtype=torch.int32)
+    ws_bytes = lib.bdm_dispatch_workspace_size(batch, time, bank_count)
+    workspace = torch.empty(max(int(ws_bytes), 1), device=device, dtype=torch.uint8)
+    _lib.check(lib.bdm_dispatch_build(
+        _ptr(wi), _ptr(ri), batch, time, kw, kr, bank_count, _ptr(order), _ptr(inverse), _ptr(tokens), _ptr(cu),
+        _ptr(status), _ptr(workspace), ws_bytes, _stream(device)), 'bdm_dispatch_build')
+    return Dispatch(order, inverse, tokens, cu, status)
+
+
+# ---------------------------------------------------------------------------
+# forward recurrence + combine
+
+def _as_heads(t: Tensor, name: str) -> Tensor:
+    if t.ndim == 3:
+        return t.unsqueeze(2)
+    if t.ndim == 4:
+        return t
+    raise ValueError(f'{name} must be [batch, time, width] or [batch, time, heads, width]')
+
+
+def routed_forward(q, k, v, g, b, w, wi, ww, ri, rw, initial: Tensor, meta: Dispatch, *, bank_count: int,
+                   scale: float, routed_decay: bool, round_interval: int = 0,
+                   final_state: Tensor | None = None) -> Tensor:
+    """Bank recurrence and ordered read combine for every head.
+
+    q,k,g,b: [B,T,S] or [B,T,H,S];  v,w: [B,T,v] or [B,T,H,v];
+    initial: [J,S,v] / [J,H,S,v] shared by the batch, or [B,J,S,v] /
+    [B,J,H,S,v] per sequence (4-D is read as per-head when q is 4-D);
+    final_state: optional [B,J,H,S,v] (or [B,J,S,v]) output, may alias initial.
+    Returns y [B, T, H*v] in the controller dtype."""
+    q4, k4, g4, b4 = (_as_heads(t, n) for t, n in ((q, 'q'), (k, 'k'), (g, 'g'), (b, 'b')))
+    v4, w4 = _as_heads(v, 'v'), _as_heads(w, 'w')
+    if not (q4.shape == k4.shape == g4.shape == b4.shape):
+        raise ValueError('q, k, g, and b must share [batch,time,heads,bank_size]')
+    if v4.shape != w4.shape or v4.shape[:3] != q4.shape[:3]:
+        raise ValueError('v and w must share [batch,time,heads,value_width] with the keys')
+    batch, time, heads, s = q4.shape
+    width = v4.shape[-1]
+    if wi.shape[:2] != (batch, time) or ri.shape[:2] != (batch, time):
+        raise ValueError('routes disagree with controller batch or time')
+    if wi.shape != ww.shape or ri.shape != rw.shape:
+        raise ValueError('route indices and weights must align')
+    dtype = q4.dtype
+    for t in (k4, b4, v4, w4, ww, rw):
+        if t.dtype != dtype:
+            raise ValueError('q, k, b, v, w and the route weights must share one dtype')
+    device = _require_gpu(q4, k4, g4, b4, v4, w4, wi, ww, ri, rw, initial, meta.order, final_state)
+    per_head_layout = q.ndim == 4
+    shared_dims = 4 if per_head_layout else 3
+    if initial.ndim == shared_dims:
+        init = initial
+        init_stride = 0
+    elif initial.ndim == shared_dims + 1:
+        if initial.shape[0] != batch:
+            raise ValueError('per-sequence initial state must lead with the batch dimension')
+        init = initial
+        init_stride = initial[0].numel()
+    else:
+        raise ValueError('initial state has the wrong rank')
+    expect = (bank_count, heads, s, width) if per_head_layout else (bank_count, s, width)
+    if tuple(init.shape[-len(expect):]) != expect:
+        raise ValueError(f'initial state must end in {expect}, got {tuple(init.shape)}')
+    init = _aligned(init)
+    if final_state is not None:
+        if final_state.numel() != batch * bank_count * heads * s * width or not final_state.is_contiguous():
+            raise ValueError('final_state must be a contiguous [batch, J, H, S, v] tensor')
+        if final_state.data_ptr() % 16:
+            raise ValueError('final_state must be 16-byte aligned')
+    qc, kc, bc, vc, wc = (_aligned(t) for t in (q4, k4, b4, v4, w4))
+    gc = _aligned(g4.float())
+    wwc, rwc, ric = _aligned(ww), _aligned(rw), _aligned(ri)
+    output = torch.empty((batch, time, heads * width), device=device, dtype=dtype)
+    args = _lib.ForwardArgs()
+    args.q, args.k, args.g, args.b, args.v, args.w = (t.data_ptr() for t in (qc, kc, gc, bc, vc, wc))
+    args.write_weights, args.read_weights, args.read_indices = wwc.data_ptr(), rwc.data_ptr(), ric.data_ptr()
+    args.order, args.cu_seqlens = meta.order.data_ptr(), meta.cu_seqlens.data_ptr()
+    args.initial = init.data_ptr()
+    args.final_state = final_state.data_ptr() if final_state is not None else None
+    args.output = output.data_ptr()
+    args.initial_batch_stride = init_stride
+    args.batch, args.time = batch, time
+    args.heads, args.bank_size, args.head_width, args.bank_count = heads, s, width, bank_count
+    args.write_banks, args.read_banks = wi.shape[-1], ri.shape[-1]
+    args.ctrl_dtype = _dtype_code(dtype)
+    args.initial_dtype = _dtype_code(init.dtype)
+    args.final_dtype = _dtype_code(final_state.dtype) if final_state is not None else 0
+    args.routed_decay = int(bool(routed_decay))
+    args.round_interval = int(round_interval)
+    args.scale = float(scale)
+    lib = _lib.library()
+    ws_bytes = lib.bdm_forward_workspace_size(ctypes.byref(args))
+    workspace = torch.empty(max(int(ws_bytes), 1), device=device, dtype=torch.uint8)
+    _lib.check(lib.bdm_forward(ctypes.byref(args), _ptr(workspace), ws_bytes, _stream(device)), 'bdm_forward')
+    return output
+
+
+# ---------------------------------------------------------------------------
+# decode
+
+def decode_step(q, k, v, g, b, w, wi, ww, ri, rw, state: Tensor, *, bank_count: int, scale: float,
+                routed_decay: bool) -> Tensor:
+    """One token per sequence against ``state`` [B,J,H,S,v] (updated in place).
+
+    q,k,g,b: [B,H,S]; v,w: [B,H,v]; wi,ww: [B,KW]; ri,rw: [B,KR].
+    Returns y [B, H*v]."""
+    if q.ndim != 3 or v.ndim != 3:
+        raise ValueError('decode controllers must be [batch, heads, width]')
+    batch, heads, s = q.shape
+    width = v.shape[-1]
+    if state.shape != (batch, bank_count, heads, s, width) or not state.is_contiguous():
+        raise ValueError('state must be a contiguous [batch, banks, heads, bank_size, head_width] tensor')
+    if state.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError('state must be FP32 or BF16')
+    device = _require_gpu(q, k, v, g, b, w, wi, ww, ri, rw, state)
+    dtype = q.dtype
+    qc, kc, bc, vc, wc = (_aligned(t) for t in (q, k, b, v, w))
+    gc = _aligned(g.float())
+    wwc, rwc, wic, ric = (_aligned(t) for t in (ww, rw, wi, ri))
+    output = torch.empty((batch, heads * width), device=device, dtype=dtype)
+    args = _lib.DecodeArgs()
+    args.q, args.k, args.b, args.g, args.v, args.w = (t.data_ptr() for t in (qc, kc, bc, gc, vc, wc))
+    args.write_weights, args.read_weights = wwc.data_ptr(), rwc.data_ptr()
+    args.write_indices, args.read_indices = wic.data_ptr(), ric.data_ptr()
+    args.state, args.output = state.data_ptr(), output.data_ptr()
+    args.batch = batch
+    args.heads, args.bank_size, args.head_width, args.bank_count = heads, s, width, bank_count
+    args.write_banks, args.read_banks = wi.shape[-1], ri.shape[-1]
+    args.ctrl_dtype = _dtype_code(dtype)
+    args.state_dtype = _dtype_code(state.dtype)
+    args.routed_decay = int(bool(routed_decay))
+    args.scale = float(scale)
+    _lib.check(_lib.library().bdm_decode(ctypes.byref(args), _stream(device)), 'bdm_decode')
+    return output

@@ -1,0 +1,164 @@
+/*
+ * bdm_hip.h — C ABI of the MI355X (gfx950) routed-memory path of the BDM layer.
+ *
+ * Every entry point takes device pointers, element counts and a HIP stream
+ * (passed as void *, a hipStream_t; NULL is the default stream), enqueues its
+ * kernels on that stream and returns without synchronising the host.  No
+ * entry point allocates device memory: scratch space is passed in as a
+ * workspace whose size the matching *_workspace_size function reports.
+ *
+ * Return value: BDM_OK (0) on success, a negative BDM_ERR_* code otherwise;
+ * bdm_last_error_string() then describes the failure (per calling thread).
+ *
+ * Layouts are token-major with token = batch_index * time + t, matching the
+ * reference tensors [batch, time, ...] in row-major order.
+ */
+#ifndef BDM_HIP_H
+#define BDM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum bdm_dtype { BDM_F32 = 0, BDM_BF16 = 1 };
+
+enum bdm_status {
+    BDM_OK = 0,
+    BDM_ERR_INVALID = -1,     /* bad pointer, shape or dtype */
+    BDM_ERR_UNSUPPORTED = -2, /* geometry outside what the kernels implement */
+    BDM_ERR_WORKSPACE = -3,   /* workspace missing or too small */
+    BDM_ERR_LAUNCH = -4       /* the HIP runtime rejected a launch */
+};
+
+/* Bits of the int32 status word that bdm_dispatch_build can raise on device. */
+enum bdm_route_flags {
+    BDM_ROUTE_OUT_OF_RANGE = 1, /* a bank index outside [0, bank_count) (clamped) */
+    BDM_ROUTE_DUPLICATE = 2     /* one token selected the same bank twice in one role */
+};
+
+int bdm_version(void);
+const char *bdm_last_error_string(void);
+
+/*
+ * Product-key router.  Replaces product_key_route
+ * (implementation/bdm/gdn2_banks.py:74-114, including the batch_factors
+ * variant at :93-102, whose selection is identical).
+ *
+ * scores   [rows, row_stride] of score_dtype; columns [0, J1) are the first
+ *          factor and [J1, J1+J2) the second, J1*J2 = bank_count.
+ * weights  [rows, C] of score_dtype: softmax (FP32) of the selected pair
+ *          sums, cast to score_dtype.  C = min(selected, s*s) with
+ *          s = min(selected, J1, J2) (gdn2_banks.py:92,107); C = selected
+ *          whenever selected <= min(J1, J2), as BDMConfig requires.
+ * indices  [rows, C] int64: row*J2 + col, in descending pair-sum order.
+ * Pair sums are rounded to score_dtype.  Equal values keep the lower index
+ * first (stable descending order), both within a factor and among pairs.
+ */
+int bdm_router_select(const void *scores, int32_t score_dtype, int64_t rows, int64_t row_stride,
+                      int32_t factor_first, int32_t factor_second, int32_t selected,
+                      void *weights, int64_t *indices, void *stream);
+
+/*
+ * Causal bank dispatch.  Replaces metadata + the INVERSE/TOKENS outputs of
+ * _pack (implementation/bdm/role_bank_dispatch.py:143-153, :15-38, :72-73).
+ *
+ * Events in original order are the writes (token*KW + j) followed by the reads
+ * (NT*KW + token*KR + j), NT = batch*time.  They are bucketed by segment
+ * (batch*bank_count + bank), stably, so a segment lists its events in
+ * (time, write-before-read) order: the permutation that sorts the reference
+ * keys ((b*J + bank)*T + t)*2 + is_read.
+ *
+ * order      [E] int64  original event index of each packed slot
+ * inverse    [E] int64  packed slot of each original event
+ * tokens     [E] int64  token of each packed slot
+ * cu_seqlens [batch*bank_count + 1] int64  segment bounds
+ * status     one int32 on device, OR-ed with bdm_route_flags; the caller zeroes it
+ * E = NT*(KW+KR).  bank_count <= 8192.
+ */
+size_t bdm_dispatch_workspace_size(int64_t batch, int64_t time, int32_t bank_count);
+int bdm_dispatch_build(const int64_t *write_indices, const int64_t *read_indices, int64_t batch,
+                       int64_t time, int32_t write_banks, int32_t read_banks, int32_t bank_count,
+                       int64_t *order, int64_t *inverse, int64_t *tokens, int64_t *cu_seqlens,
+                       int32_t *status, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * Routed GDN2 bank recurrence with the r-weighted read combine.  Replaces, for
+ * all heads at once: pack (role_bank_dispatch.py:156-185), decay_transform
+ * (routed_update.py:5-13), _role_forward (role_bank_kernel.py:46-73, and the
+ * stateful forward_rows variants, forward_rows.py:10-194), _readout
+ * (role_bank_dispatch.py:201-231) and _compact_readout (inference.py:70-85).
+ *
+ * Per segment and head, events in packed order on an S x v FP32 state M:
+ *   write (route weight p):  hd = diag(exp(eg)) M,  eg = g*p (routed_decay) or g
+ *                            u  = bf(w*p) * v - (bf(b*p) * k)^T hd
+ *                            M  = hd + k u^T
+ *   read  (route weight r):  z  = scale * bf(q*r)^T M, stored in ctrl_dtype
+ * bf() rounds to ctrl_dtype.  With round_interval > 0 the state is rounded to
+ * BF16 at the segment start and before every event whose in-segment offset is
+ * a positive multiple of round_interval (the training path's storage cadence).
+ * y[token, h*v + c] adds the token's reads in increasing bank id, rounding to
+ * ctrl_dtype after each add.
+ */
+typedef struct bdm_forward_args {
+    const void *q;             /* [NT, H, S] ctrl_dtype */
+    const void *k;             /* [NT, H, S] ctrl_dtype */
+    const float *g;            /* [NT, H, S] FP32 log decay */
+    const void *b;             /* [NT, H, S] ctrl_dtype erase gate */
+    const void *v;             /* [NT, H, v] ctrl_dtype */
+    const void *w;             /* [NT, H, v] ctrl_dtype write gate */
+    const void *write_weights; /* [NT, KW] ctrl_dtype */
+    const void *read_weights;  /* [NT, KR] ctrl_dtype */
+    const int64_t *read_indices; /* [NT, KR] */
+    const int64_t *order;      /* [E] from bdm_dispatch_build */
+    const int64_t *cu_seqlens; /* [batch*J + 1] */
+    const void *initial;       /* [J, H, S, v] (+ batch stride) of initial_dtype */
+    void *final_state;         /* NULL or [batch, J, H, S, v] of final_dtype; may alias initial */
+    void *output;              /* [NT, H*v] ctrl_dtype */
+    int64_t initial_batch_stride; /* elements between batches of `initial`; 0 = shared */
+    int64_t batch, time;
+    int32_t heads, bank_size, head_width, bank_count, write_banks, read_banks;
+    int32_t ctrl_dtype, initial_dtype, final_dtype;
+    int32_t routed_decay;
+    int32_t round_interval;
+    float scale;
+} bdm_forward_args;
+
+size_t bdm_forward_workspace_size(const bdm_forward_args *args);
+int bdm_forward(const bdm_forward_args *args, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * Single-token decode against resident bank states.  Replaces
+ * _decode_write/_decode_read/_decode_sum (implementation/bdm/inference.py:21-67,
+ * step at :161-194) and generalises them to any head count.
+ *
+ * state [batch, J, H, S, v] of state_dtype is updated in place: each of the
+ * token's KW write banks is advanced by the write rule above and stored
+ * (rounded to state_dtype); then each of the KR read banks is read from the
+ * stored state; the reads are added in increasing bank id with a rounding to
+ * ctrl_dtype after each add into output [batch, H*v].
+ * The write banks of one token must be distinct (as the router guarantees).
+ */
+typedef struct bdm_decode_args {
+    const void *q, *k, *b;     /* [batch, H, S] ctrl_dtype */
+    const float *g;            /* [batch, H, S] */
+    const void *v, *w;         /* [batch, H, v] ctrl_dtype */
+    const void *write_weights, *read_weights; /* [batch, KW], [batch, KR] */
+    const int64_t *write_indices, *read_indices;
+    void *state;
+    void *output;              /* [batch, H*v] ctrl_dtype */
+    int64_t batch;
+    int32_t heads, bank_size, head_width, bank_count, write_banks, read_banks;
+    int32_t ctrl_dtype, state_dtype, routed_decay;
+    float scale;
+} bdm_decode_args;
+
+int bdm_decode(const bdm_decode_args *args, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BDM_HIP_H */

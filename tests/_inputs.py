@@ -1,0 +1,71 @@
+"""Seeded synthetic inputs shared by the parity tests (CPU tensors)."""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from oracle import bdm_oracle as O
+
+
+def routes(batch, time, bank_count, selected, gen, dtype=torch.bfloat16, zipf: float = 0.0):
+    """Router outputs from random factor scores (optionally Zipf-biased per factor)."""
+    j1, j2 = O.near_square_factors(bank_count)
+    scores = torch.randn(batch, time, j1 + j2, generator=gen)
+    if zipf:
+        for lo, n in ((0, j1), (j1, j2)):
+            perm = torch.randperm(n, generator=gen)
+            scores[..., lo:lo + n] -= zipf * torch.log1p(perm.float())
+    scores = scores.to(dtype)
+    weights, indices = O.product_key_route(scores, bank_count=bank_count, selected_banks=selected)
+    return scores, weights, indices
+
+
+def controllers(batch, time, heads, s, v, gen, dtype=torch.bfloat16):
+    """q,k l2-normalised; v silu-like; g <= 0 log decay (FP32); b,w in (0,1)."""
+    shape = (batch, time, heads)
+    q = torch.nn.functional.normalize(torch.randn(*shape, s, generator=gen), dim=-1).to(dtype)
+    k = torch.nn.functional.normalize(torch.randn(*shape, s, generator=gen), dim=-1).to(dtype)
+    vv = torch.nn.functional.silu(torch.randn(*shape, v, generator=gen)).to(dtype)
+    g = -torch.rand(*shape, s, generator=gen) * 0.3
+    b = torch.sigmoid(torch.randn(*shape, s, generator=gen)).to(dtype)
+    w = torch.sigmoid(torch.randn(*shape, v, generator=gen)).to(dtype)
+    return q, k, vv, g, b, w
+
+
+def initial_state(bank_count, heads, s, v, gen, scale=0.1, batch=None):
+    shape = (bank_count, heads, s, v) if batch is None else (batch, bank_count, heads, s, v)
+    return torch.randn(*shape, generator=gen) * scale
+
+
+def rel_err(ours: torch.Tensor, ref: torch.Tensor) -> float:
+    """max |ours - ref| / max |ref| in FP32."""
+    ours, ref = ours.float().cpu(), ref.float().cpu()
+    return float((ours - ref).abs().max() / ref.abs().max().clamp_min(1e-30))
+
+
+def oracle_reads(q, k, v, g, b, w, wi, ww, ri, rw, state, bank_count, *, routed_decay, state_dtype,
+                 interval=None, return_final=False):
+    """Oracle of the multi-head HIP forward: per head ``bank_forward`` with the
+    production (ordered) combine, heads concatenated (heads.py:65-66)."""
+    heads = q.shape[2]
+    outs, finals = [], []
+    for h in range(heads):
+        sl = lambda x: x[:, :, h].contiguous()  # noqa: E731
+        st = state[:, h] if state.ndim == 4 else state[:, :, h]
+        res = O.bank_forward(sl(q), sl(k), sl(v), sl(g), sl(b), sl(w), wi, ww, ri, rw, st, bank_count,
+                             q.shape[-1] ** -0.5, routed_decay=routed_decay, state_dtype=state_dtype,
+                             interval=interval, combine='ordered', lockstep=True, return_final=return_final)
+        if return_final:
+            res, fin = res
+            finals.append(fin)
+        outs.append(res)
+    y = torch.cat(outs, dim=-1)
+    if return_final:
+        return y, torch.stack(finals, dim=2)
+    return y
+
+
+def scale_of(s):
+    return s ** -0.5 if s else math.nan

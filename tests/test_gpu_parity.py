@@ -1,0 +1,338 @@
+"""HIP path against the CPU oracle, through the C ABI (bdm_amd.ops wraps it).
+
+Bit-exact: router indices, dispatch permutation/inverse/tokens/bounds.
+Tolerance (BF16 state, FP32 math): max|hip - oracle| / max|oracle| <= 1e-2
+for read outputs and final bank states; router weights within one BF16 ulp.
+"""
+
+import sys
+
+import pytest
+import torch
+
+from _inputs import controllers, initial_state, oracle_reads, rel_err, routes
+from oracle import bdm_oracle as O
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-2
+
+
+def announce(*what):
+    print('CASE', *what, flush=True)
+    sys.stdout.flush()
+
+
+# ---------------------------------------------------------------------------- router
+
+@pytest.mark.parametrize('bank_count,selected', [(16, 4), (256, 8), (2048, 8), (12, 3), (6, 2), (256, 16)])
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float32])
+def test_router_bit_exact(device, bank_count, selected, dtype):
+    from bdm_amd import ops
+    gen = torch.Generator().manual_seed(bank_count * 31 + selected)
+    j1, j2 = O.near_square_factors(bank_count)
+    if selected > min(j1, j2) and selected > 8:
+        pytest.skip('geometry outside BDMConfig')
+    for kind in ('normal', 'ties'):
+        if kind == 'normal':
+            scores = torch.randn(3, 1000, j1 + j2, generator=gen).to(dtype)
+        else:  # coarse grid: many equal factor scores and pair sums
+            scores = (torch.randint(-3, 4, (3, 1000, j1 + j2), generator=gen).float() / 2).to(dtype)
+        announce('router', bank_count, selected, dtype, kind)
+        w, i = ops.router_select(scores.to(device), bank_count=bank_count, selected_banks=selected)
+        torch.cuda.synchronize()
+        wr, ir = O.product_key_route(scores, bank_count=bank_count, selected_banks=selected)
+        assert torch.equal(i.cpu(), ir), (bank_count, selected, dtype, kind)
+        # weights: one BF16 ulp (the softmax exp differs in the last FP32 bits
+        # between torch's CPU kernel and the device libm), or 1e-6 for FP32 scores
+        diff = (w.cpu().float() - wr.float()).abs()
+        ulp = wr.float().abs() * (2 ** -7 if dtype == torch.bfloat16 else 1e-6)
+        assert bool((diff <= ulp + 1e-12).all()), float(diff.max())
+
+
+def test_router_module_autograd(device):
+    from bdm_amd.routing import product_key_route
+    gen = torch.Generator().manual_seed(5)
+    scores = torch.randn(2, 64, 32, generator=gen)
+    dy = torch.randn(2, 64, 8, generator=gen)
+    cpu = scores.clone().requires_grad_(True)
+    wr, _ = O.product_key_route(cpu, bank_count=256, selected_banks=8)
+    (wr * dy).sum().backward()
+    announce('router autograd')
+    gpu = scores.to(device).requires_grad_(True)
+    w, _ = product_key_route(gpu, bank_count=256, selected_banks=8)
+    (w * dy.to(device)).sum().backward()
+    assert rel_err(gpu.grad, cpu.grad) < 1e-5
+
+
+# -------------------------------------------------------------------------- dispatch
+
+@pytest.mark.parametrize('batch,time,bank_count,kw,kr', [
+    (2, 100, 16, 4, 4), (3, 64, 256, 8, 8), (1, 7, 12, 3, 5), (4, 33, 2048, 8, 8), (2, 40, 16, 0, 4)])
+def test_dispatch_bit_exact(device, batch, time, bank_count, kw, kr):
+    from bdm_amd import ops
+    gen = torch.Generator().manual_seed(batch * 1000 + time)
+    wi = torch.stack([torch.randperm(bank_count, generator=gen)[:kw] for _ in range(batch * time)])
+    ri = torch.stack([torch.randperm(bank_count, generator=gen)[:kr] for _ in range(batch * time)])
+    wi, ri = wi.reshape(batch, time, kw), ri.reshape(batch, time, kr)
+    announce('dispatch', batch, time, bank_count, kw, kr)
+    meta = ops.dispatch_build(wi.to(device), ri.to(device), bank_count)
+    meta.check_routes()
+    ref = O.dispatch_metadata(wi, ri, bank_count)
+    assert torch.equal(meta.cu_seqlens.cpu(), ref.cu_seqlens)
+    assert torch.equal(meta.order.cpu(), ref.order)
+    assert torch.equal(meta.inverse.cpu(), ref.inverse)
+    assert torch.equal(meta.tokens.cpu(), ref.tokens)
+
+
+def test_dispatch_flags_bad_routes(device):
+    from bdm_amd import ops
+    wi = torch.tensor([[[0, 1], [2, 2]]])  # duplicate bank in one token's writes
+    ri = torch.tensor([[[0, 3], [1, 2]]])
+    announce('dispatch duplicate flag')
+    meta = ops.dispatch_build(wi.to(device), ri.to(device), 4)
+    with pytest.raises(ValueError, match='same bank twice'):
+        meta.check_routes()
+    wi = torch.tensor([[[0, 9], [2, 1]]])  # out of range
+    announce('dispatch range flag')
+    meta = ops.dispatch_build(wi.to(device), ri.to(device), 4)
+    with pytest.raises(ValueError, match='outside'):
+        meta.check_routes()
+
+
+# --------------------------------------------------------------------------- forward
+
+FORWARD_CASES = [
+    # batch, time, heads, S, v, J, K, ctrl dtype, routed, state dtype
+    (2, 64, 2, 8, 32, 16, 4, torch.bfloat16, True, torch.bfloat16),
+    (2, 80, 2, 8, 32, 16, 4, torch.bfloat16, True, torch.float32),
+    (1, 50, 1, 4, 16, 12, 3, torch.bfloat16, False, torch.bfloat16),
+    (2, 48, 3, 8, 24, 16, 4, torch.float32, True, torch.float32),
+    (2, 40, 2, 16, 64, 64, 8, torch.bfloat16, True, torch.bfloat16),
+    (1, 60, 4, 8, 128, 256, 8, torch.bfloat16, True, torch.bfloat16),
+    (1, 30, 1, 32, 8, 16, 4, torch.bfloat16, True, torch.bfloat16),
+    (3, 17, 2, 8, 12, 16, 4, torch.bfloat16, True, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize('case', FORWARD_CASES, ids=[str(i) for i in range(len(FORWARD_CASES))])
+def test_forward_matches_oracle(device, case):
+    from bdm_amd import ops
+    from bdm_amd.config import replay_interval
+    batch, time, heads, s, v, j, kk, dtype, routed, state_dtype = case
+    gen = torch.Generator().manual_seed(1000 + FORWARD_CASES.index(case))
+    _, ww, wi = routes(batch, time, j, kk, gen, dtype)
+    _, rw, ri = routes(batch, time, j, kk, gen, dtype)
+    q, k, v_, g, b, w = controllers(batch, time, heads, s, v, gen, dtype)
+    state = initial_state(j, heads, s, v, gen)
+    interval = replay_interval(s) if state_dtype == torch.bfloat16 else 0
+    ref, ref_final = oracle_reads(q, k, v_, g, b, w, wi, ww, ri, rw, state, j, routed_decay=routed,
+                                  state_dtype=state_dtype, interval=interval or 16, return_final=True)
+    dev = [t.to(device) for t in (q, k, v_, g, b, w, wi, ww, ri, rw, state)]
+    announce('forward', case)
+    meta = ops.dispatch_build(dev[6], dev[8], j)
+    final = torch.empty(batch, j, heads, s, v, device=device, dtype=torch.float32)
+    y = ops.routed_forward(*dev[:10], dev[10], meta, bank_count=j, scale=s ** -0.5, routed_decay=routed,
+                           round_interval=interval, final_state=final)
+    torch.cuda.synchronize()
+    assert y.shape == (batch, time, heads * v) and y.dtype == dtype
+    assert rel_err(y, ref) < TOL, rel_err(y, ref)
+    assert rel_err(final, ref_final) < TOL, rel_err(final, ref_final)
+
+
+def test_forward_per_head_layout_and_determinism(device):
+    from bdm_amd import bank_training
+    gen = torch.Generator().manual_seed(11)
+    batch, time, heads, s, v, j = 2, 96, 3, 8, 32, 16
+    _, ww, wi = routes(batch, time, j, 4, gen)
+    _, rw, ri = routes(batch, time, j, 4, gen)
+    q, k, v_, g, b, w = (t.to(device) for t in controllers(batch, time, heads, s, v, gen))
+    state = initial_state(j, heads, s, v, gen).to(device)
+    wi, ww, ri, rw = (t.to(device) for t in (wi, ww, ri, rw))
+    announce('per-head layout')
+    full = bank_training(q, k, v_, g, b, w, wi, ww, ri, rw, state, j, s ** -0.5, state_dtype=torch.bfloat16)
+    again = bank_training(q, k, v_, g, b, w, wi, ww, ri, rw, state, j, s ** -0.5, state_dtype=torch.bfloat16)
+    assert torch.equal(full, again)
+    for h in range(heads):
+        one = bank_training(q[:, :, h], k[:, :, h], v_[:, :, h], g[:, :, h], b[:, :, h], w[:, :, h], wi, ww,
+                            ri, rw, state[:, h].contiguous(), j, s ** -0.5, state_dtype=torch.bfloat16)
+        assert one.shape == (batch, time, v)
+        assert torch.equal(one, full[..., h * v:(h + 1) * v])
+
+
+# ---------------------------------------------------------------------------- module
+
+def _small_config(**kw):
+    from bdm_amd import BSDMConfig
+    base = dict(dim=64, bank_count=16, bank_size=8, selected_banks=4, value_width=64, num_heads=2)
+    base.update(kw)
+    return BSDMConfig(**base)
+
+
+def test_module_state_dict_interchanges_with_oracle():
+    from bdm_amd import BankedDeltaMemory
+    cfg = _small_config()
+    ours = BankedDeltaMemory(cfg, layer_id=2, seed=3)
+    oracle = O.OracleBankedDeltaMemory(cfg, layer_id=2, seed=3)
+    a, b = ours.state_dict(), oracle.state_dict()
+    assert set(a) == set(b)
+    for key in a:
+        assert torch.equal(a[key], b[key]), key
+
+
+def test_module_forward_matches_oracle(device):
+    from bdm_amd import BankedDeltaMemory
+    cfg = _small_config()
+    layer = BankedDeltaMemory(cfg, layer_id=0, seed=1).to(device=device, dtype=torch.bfloat16)
+    oracle = O.OracleBankedDeltaMemory(cfg, layer_id=0, seed=1).to(torch.bfloat16)
+    gen = torch.Generator().manual_seed(3)
+    x = torch.randn(2, 96, cfg.dim, generator=gen).to(torch.bfloat16)
+    announce('module forward')
+    with torch.no_grad():
+        xd = x.to(device)
+        q, k, v, g, b, w = layer._controllers(xd)
+        rr, wr = layer._route_projections(xd)
+        raw = layer.bank_reads(xd)
+        out = layer(xd)
+        torch.cuda.synchronize()
+        # the oracle sees the GPU's controller and score tensors
+        ww, wi = O.product_key_route(wr.cpu(), bank_count=cfg.bank_count, selected_banks=cfg.selected_banks)
+        rw, ri = O.product_key_route(rr.cpu(), bank_count=cfg.bank_count, selected_banks=cfg.selected_banks)
+        state = oracle.materialize_initial_state()
+        ref = oracle_reads(*(t.cpu() for t in (q, k, v, g, b, w)), wi, ww, ri, rw, state, cfg.bank_count,
+                           routed_decay=True, state_dtype=torch.bfloat16)
+        assert rel_err(raw, ref) < TOL
+        ref_out = oracle.project_output(x, raw.cpu())
+        assert rel_err(out, ref_out) < 2e-2
+
+
+def test_prefill_and_step_match_oracle(device):
+    from bdm_amd import BankedDeltaMemory
+    cfg = _small_config()
+    layer = BankedDeltaMemory(cfg, layer_id=0, seed=4).to(device=device, dtype=torch.bfloat16)
+    oracle = O.OracleBankedDeltaMemory(cfg, layer_id=0, seed=4).to(torch.bfloat16)
+    gen = torch.Generator().manual_seed(9)
+    x = torch.randn(2, 40, cfg.dim, generator=gen).to(torch.bfloat16)
+    nxt = torch.randn(2, 1, cfg.dim, generator=gen).to(torch.bfloat16)
+    for cache_dtype in (torch.float32, torch.bfloat16):
+        announce('prefill', cache_dtype)
+        with torch.no_grad():
+            out, state = layer.prefill(x.to(device), state_dtype=cache_dtype)
+            q, k, v, g, b, w = (t.cpu() for t in layer._controllers(x.to(device)))
+            rr, wr = (t.cpu() for t in layer._route_projections(x.to(device)))
+            ww, wi = O.product_key_route(wr, bank_count=cfg.bank_count, selected_banks=cfg.selected_banks)
+            rw, ri = O.product_key_route(rr, bank_count=cfg.bank_count, selected_banks=cfg.selected_banks)
+            init = oracle.create_state(2, torch.float32)
+            raw_ref, final_ref = oracle_reads(q, k, v, g, b, w, wi, ww, ri, rw, init.float(), cfg.bank_count,
+                                              routed_decay=True, state_dtype=torch.float32, return_final=True)
+            assert state.dtype == cache_dtype
+            assert rel_err(state, final_ref) < TOL
+            announce('step', cache_dtype)
+            cpu_state = state.cpu().clone()
+            out1, state = layer.step(nxt.to(device), state)
+            # oracle step on the same controllers/routes as the GPU step
+            q1, k1, v1, g1, b1, w1 = (t.cpu() for t in layer._controllers(nxt.to(device)))
+            rr1, wr1 = (t.cpu() for t in layer._route_projections(nxt.to(device)))
+            ww1, wi1 = O.product_key_route(wr1, bank_count=cfg.bank_count, selected_banks=cfg.selected_banks)
+            rw1, ri1 = O.product_key_route(rr1, bank_count=cfg.bank_count, selected_banks=cfg.selected_banks)
+            oracle_state = cpu_state
+            heads = []
+            for h in range(cfg.num_heads):
+                st = oracle_state[:, :, h].float()
+                for jj in range(cfg.selected_banks):
+                    rows = torch.arange(2)
+                    bank = wi1[:, 0, jj]
+                    p = ww1[:, 0, jj]
+                    eg = g1[:, 0, h].float() * p.float()[:, None]
+                    eb = (b1[:, 0, h] * p[:, None]).to(torch.bfloat16)
+                    ew = (w1[:, 0, h] * p[:, None]).to(torch.bfloat16)
+                    new = O.write_update(st[rows, bank], k1[:, 0, h], eg, eb, ew, v1[:, 0, h])
+                    st[rows, bank] = new.to(cache_dtype).float()
+                oracle_state[:, :, h] = st.to(cache_dtype)
+                vals = []
+                for jj in range(cfg.selected_banks):
+                    eq = (q1[:, 0, h] * rw1[:, 0, jj][:, None]).to(torch.bfloat16)
+                    vals.append(O.read_value(st[torch.arange(2), ri1[:, 0, jj]], eq,
+                                             cfg.bank_size ** -0.5).to(torch.bfloat16))
+                order = torch.argsort(ri1[:, 0], dim=-1, stable=True)
+                total = torch.zeros(2, vals[0].shape[-1])
+                stacked = torch.stack(vals, 1)
+                for jj in range(cfg.selected_banks):
+                    total = (total + stacked[torch.arange(2), order[:, jj]].float()).to(torch.bfloat16).float()
+                heads.append(total)
+            raw1 = torch.cat(heads, -1)
+            assert rel_err(state, oracle_state) < TOL
+            ref_out1 = oracle.project_output(nxt, raw1.to(torch.bfloat16).unsqueeze(1))
+            assert rel_err(out1, ref_out1) < 2e-2
+
+
+def test_decode_kernel_matches_oracle(device):
+    from bdm_amd import ops
+    gen = torch.Generator().manual_seed(21)
+    batch, heads, s, v, j, kk = 6, 3, 8, 128, 64, 8
+    _, ww, wi = routes(batch, 1, j, kk, gen)
+    _, rw, ri = routes(batch, 1, j, kk, gen)
+    ri[0, 0, :3] = wi[0, 0, :3]  # reads of banks written by the same token
+    q, k, v_, g, b, w = controllers(batch, 1, heads, s, v, gen)
+    for state_dtype in (torch.bfloat16, torch.float32):
+        state = (torch.randn(batch, j, heads, s, v, generator=gen) * 0.02).to(state_dtype)
+        expect = state.clone()
+        rows = torch.arange(batch)
+        ys = []
+        for h in range(heads):
+            st = expect[:, :, h]
+            for jj in range(kk):
+                bank, p = wi[:, 0, jj], ww[:, 0, jj]
+                new = O.write_update(st[rows, bank].float(), k[:, 0, h], g[:, 0, h] * p.float()[:, None],
+                                     (b[:, 0, h] * p[:, None]).to(b.dtype), (w[:, 0, h] * p[:, None]).to(w.dtype),
+                                     v_[:, 0, h])
+                st[rows, bank] = new.to(state_dtype)
+            vals = torch.stack([O.read_value(st[rows, ri[:, 0, jj]].float(),
+                                             (q[:, 0, h] * rw[:, 0, jj][:, None]).to(q.dtype), s ** -0.5)
+                                .to(torch.bfloat16) for jj in range(kk)], 1)
+            order = torch.argsort(ri[:, 0], dim=-1, stable=True)
+            total = torch.zeros(batch, v)
+            for jj in range(kk):
+                total = (total + vals[rows, order[:, jj]].float()).to(torch.bfloat16).float()
+            ys.append(total)
+        announce('decode', state_dtype)
+        dstate = state.to(device)
+        y = ops.decode_step(*(t[:, 0].to(device) for t in (q, k, v_, g, b, w, wi, ww, ri, rw)), dstate,
+                            bank_count=j, scale=s ** -0.5, routed_decay=True)
+        torch.cuda.synchronize()
+        assert rel_err(dstate, expect) < TOL
+        assert rel_err(y, torch.cat(ys, -1)) < TOL
+        touched = torch.zeros(batch, j, dtype=torch.bool)
+        touched[rows[:, None], wi[:, 0]] = True
+        assert torch.equal(dstate.cpu()[~touched], state[~touched])  # untouched banks are bit-identical
+
+
+# ---------------------------------------------------------------- full benchmark size
+
+def test_full_size_prefill_c2(device):
+    """C2 geometry (B8 T4096 H8 S8 v128 J256 K8): dispatch bit-exact against the
+    CPU oracle over all 524,288 events; read outputs and final states of
+    sequence 0 against the oracle recurrence (sequences are independent)."""
+    from bdm_amd import ops
+    gen = torch.Generator().manual_seed(2026)
+    batch, time, heads, s, v, j, kk = 8, 4096, 8, 8, 128, 256, 8
+    _, ww, wi = routes(batch, time, j, kk, gen)
+    _, rw, ri = routes(batch, time, j, kk, gen)
+    q, k, v_, g, b, w = controllers(batch, time, heads, s, v, gen)
+    state = initial_state(j, heads, s, v, gen, scale=0.05)
+    dev = [t.to(device) for t in (q, k, v_, g, b, w, wi, ww, ri, rw, state)]
+    announce('full size C2 dispatch')
+    meta = ops.dispatch_build(dev[6], dev[8], j)
+    ref = O.dispatch_metadata(wi, ri, j)
+    assert torch.equal(meta.order.cpu(), ref.order)
+    assert torch.equal(meta.cu_seqlens.cpu(), ref.cu_seqlens)
+    assert torch.equal(meta.inverse.cpu(), ref.inverse)
+    announce('full size C2 forward')
+    final = torch.empty(batch, j, heads, s, v, device=device, dtype=torch.bfloat16)
+    y = ops.routed_forward(*dev[:10], dev[10], meta, bank_count=j, scale=s ** -0.5, routed_decay=True,
+                           round_interval=16, final_state=final)
+    torch.cuda.synchronize()
+    one = lambda t: t[:1]  # noqa: E731
+    ref_y, ref_final = oracle_reads(*(one(t) for t in (q, k, v_, g, b, w, wi, ww, ri, rw)), state, j,
+                                    routed_decay=True, state_dtype=torch.bfloat16, return_final=True)
+    assert rel_err(y[:1], ref_y) < TOL, rel_err(y[:1], ref_y)
+    assert rel_err(final[:1], ref_final) < TOL, rel_err(final[:1], ref_final)
