@@ -1,0 +1,344 @@
+"""Benchmark of the BDM routed-memory hot path on one MI355X.
+
+``python bench.py [--gpus 1] [--steps K] [--warmup W]`` prints ONE JSON line.
+
+Workload ("C2"): BSDM layer geometry d_model=1024, H=8,
+J=256 banks (16x16 product key), S=8 rows per bank, B=8 read and 8 write
+banks, v=128 per head, batch 8, T=4096 -> 32,768 tokens.  Weights are the
+seeded random init of ``BankedDeltaMemory``, x ~ N(0,1) (synthetic data).
+Controllers and router scores are computed once before the timed region; a
+timed step is one prefill pass of the hot path over the batch:
+
+    router (write and read roles) -> dispatch -> recurrence + ordered read
+    combine, final bank state written (BF16 cache), FP32 recurrence math
+
+``value`` is tokens/s of that step with every input already in HBM.  Extra
+fields report the full-layer prefill (controller GEMMs and output interface
+included), the C3 decode step (batch 64 against a resident BF16 state of
+[64, 256, 8, 8, 128]) and an HBM copy probe.
+
+roofline: the dominant launch is ``bdm_forward`` (recurrence + ordered
+combine).  Its algorithmic bytes per token are the bytes it must move once:
+q,k,b (3*H*S*2), g (H*S*4), v,w (2*V*2), route weights ww,rw ((KW+KR)*2),
+read indices (KR*8), packed order ((KW+KR)*8), y (V*2) and the final state
+(J*H*S*v*2 per sequence, spread over its T tokens), plus the shared initial
+state once per launch.  ``achieved`` divides them by the launch's average
+duration, measured with events on the stream the kernels run on.
+
+cpu_baseline: the CPU oracle's port of the reference ``backend='reference'``
+path (per-event loop, oracle/bdm_oracle.py) on a bounded sample of the same
+workload: one sequence of the C2 geometry, the first ``--cpu-tokens`` tokens,
+routes and controllers from the same layer.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, 'profiles', 'forward_c2_traffic.json')
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.split('\n')[0])
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=20)
+    ap.add_argument('--warmup', type=int, default=3)
+    ap.add_argument('--batch', type=int, default=8)
+    ap.add_argument('--time', type=int, default=4096)
+    ap.add_argument('--decode-steps', type=int, default=256)
+    ap.add_argument('--cpu-tokens', type=int, default=512,
+                    help='tokens of sequence 0 the CPU oracle runs (0 skips the CPU baseline)')
+    ap.add_argument('--no-extras', action='store_true', help='skip the full-layer and decode measurements')
+    return ap.parse_args()
+
+
+def c2_config():
+    from bdm_amd import BSDMConfig
+    return BSDMConfig(dim=1024, bank_count=256, bank_size=8, selected_banks=8, value_width=1024, num_heads=8)
+
+
+def make_inputs(layer, batch, time_, device, seed=0):
+    import torch
+    gen = torch.Generator().manual_seed(seed)
+    x = torch.randn(batch, time_, layer.hidden_size, generator=gen).to(torch.bfloat16).to(device)
+    with torch.no_grad():
+        q, k, v, g, b, w = layer._controllers(x)
+        read_scores, write_scores = layer._route_projections(x)
+        initial = layer._state_heads(layer.materialize_initial_state()).contiguous()
+    return x, (q, k, v, g, b, w), (read_scores, write_scores), initial
+
+
+def forward_algorithmic_bytes(cfg, batch, time_, initial_bytes):
+    """Bytes one bdm_forward launch must move once (module docstring)."""
+    h, s, j, kk = cfg.num_heads, cfg.bank_size, cfg.bank_count, cfg.selected_banks
+    v_total = cfg.value_width
+    per_token = (3 * h * s * 2 + h * s * 4 + 2 * v_total * 2 + 2 * kk * 2 + kk * 8 + 2 * kk * 8 + v_total * 2)
+    final = batch * j * h * s * (v_total // h) * 2
+    return per_token * batch * time_ + final + initial_bytes
+
+
+def hot_path_algorithmic_bytes(cfg, batch, time_):
+    """Hot path from router scores and controllers to y, final state written:
+    2*(J1+J2)*2 + 3*H*S*2 + H*S*4 + 2*V*2 + V*2 per token + J*H*S*v*2 per
+    sequence (7,936 B/token at C2)."""
+    from bdm_amd.config import near_square_factors
+    j1, j2 = near_square_factors(cfg.bank_count)
+    h, s, v_total = cfg.num_heads, cfg.bank_size, cfg.value_width
+    per_token = 2 * (j1 + j2) * 2 + 3 * h * s * 2 + h * s * 4 + 2 * v_total * 2 + v_total * 2
+    return per_token * batch * time_ + batch * cfg.bank_count * h * s * (v_total // h) * 2
+
+
+def timed(fn, steps, warmup):
+    """Run fn warmup times, then time exactly `steps` calls between two
+    device synchronisations.  Returns (seconds per step, last result)."""
+    import torch
+    out = None
+    for _ in range(warmup):
+        out = fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out = fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps, out
+
+
+def copy_probe(device):
+    """Achieved HBM bandwidth of a plain streaming kernel (read + write bytes):
+    torch.neg over 512 MiB of BF16 into another 512 MiB.  It is also the
+    known-size kernel that calibrates the FETCH_SIZE/WRITE_SIZE counters."""
+    import torch
+    n = 1 << 28  # 256 Mi bf16 = 512 MiB each way
+    src = torch.empty(n, device=device, dtype=torch.bfloat16).normal_()
+    dst = torch.empty_like(src)
+    sec, _ = timed(lambda: torch.neg(src, out=dst), 10, 2)
+    del src, dst
+    return 2 * n * 2 / sec / 1e9
+
+
+def decode_bench(layer, device, steps, seed=1):
+    """C3: batch 64, one token per sequence, resident BF16 state ~ N(0, 0.02)."""
+    import torch
+    from bdm_amd import ops
+    cfg = layer.config
+    batch = 64
+    gen = torch.Generator().manual_seed(seed)
+    state = (torch.randn(batch, cfg.bank_count, cfg.num_heads, cfg.bank_size, cfg.head_value_width,
+                         generator=gen) * 0.02).to(torch.bfloat16).to(device)
+    xs = torch.randn(steps, batch, 1, cfg.dim, generator=gen).to(torch.bfloat16).to(device)
+    # kernel-only: controllers and routes of every step precomputed
+    pre = []
+    with torch.no_grad():
+        for i in range(steps):
+            q, k, v, g, b, w = layer._controllers(xs[i])
+            rr, wr = layer._route_projections(xs[i])
+            ww, wi = layer._route(wr, cfg.selected_banks)
+            rw, ri = layer._route(rr, cfg.selected_banks)
+            pre.append(tuple(t[:, 0].contiguous() for t in (q, k, v, g, b, w, wi, ww, ri, rw)))
+    torch.cuda.synchronize()
+    scale = cfg.bank_size ** -0.5
+    launch = lambda i: ops.decode_step(*pre[i], state, bank_count=cfg.bank_count, scale=scale,  # noqa: E731
+                                       routed_decay=True)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.no_grad():
+        for i in range(min(8, steps)):  # warmup
+            launch(i)
+        torch.cuda.synchronize()
+        # kernel-only: the decode launches of every step captured in one HIP
+        # graph and replayed, so host launch overhead is not in the figure
+        side = torch.cuda.Stream(device)
+        side.wait_stream(torch.cuda.current_stream(device))
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(graph, stream=side):
+                for i in range(steps):
+                    launch(i)
+        torch.cuda.current_stream(device).wait_stream(side)
+        graph.replay()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream(device)
+        start.record(stream)
+        graph.replay()
+        stop.record(stream)
+        torch.cuda.synchronize()
+        kernel_us = start.elapsed_time(stop) * 1e3 / steps
+        # eager launches of the decode entry point (host overhead included)
+        eager_sec, _ = timed(lambda: [launch(i) for i in range(steps)], 1, 0)
+        # full step: controllers, routes, decode kernel and output interface
+        sec, _ = timed(lambda: [layer.step(xs[i], state) for i in range(steps)], 1, 1)
+    state_bytes = batch * (2 * cfg.selected_banks + cfg.selected_banks) * cfg.num_heads * cfg.bank_size * \
+        cfg.head_value_width * 2
+    return {'batch': batch, 'steps': steps, 'kernel_us_per_step': round(kernel_us, 3),
+            'eager_launch_us_per_step': round(eager_sec * 1e6 / steps, 2),
+            'full_step_us_eager': round(sec * 1e6 / steps, 2), 'state_bytes_per_step': state_bytes,
+            'state_GBps': round(state_bytes / (kernel_us * 1e-6) / 1e9, 1),
+            'state_frac_of_hbm_peak': round(state_bytes / (kernel_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
+
+
+def cpu_baseline(layer_gpu, cfg, tokens):
+    """The oracle's per-event loop (port of reference_packed_gdn2 + index_add_
+    readout) on the first `tokens` tokens of one C2 sequence, on the host."""
+    import torch
+    from oracle import bdm_oracle as O
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    gen = torch.Generator().manual_seed(7)
+    x = torch.randn(1, tokens, cfg.dim, generator=gen).to(torch.bfloat16)
+    with torch.no_grad():
+        xd = x.to(next(layer_gpu.parameters()).device)
+        q, k, v, g, b, w = (t.cpu() for t in layer_gpu._controllers(xd))
+        rr, wr = (t.cpu() for t in layer_gpu._route_projections(xd))
+        initial = layer_gpu._state_heads(layer_gpu.materialize_initial_state()).cpu()
+
+    def run():
+        with torch.no_grad():
+            ww, wi = O.product_key_route(wr, bank_count=cfg.bank_count, selected_banks=cfg.selected_banks)
+            rw, ri = O.product_key_route(rr, bank_count=cfg.bank_count, selected_banks=cfg.selected_banks)
+            outs = []
+            for h in range(cfg.num_heads):
+                sl = lambda t: t[:, :, h].contiguous()  # noqa: E731
+                outs.append(O.bank_forward(sl(q), sl(k), sl(v), sl(g), sl(b), sl(w), wi, ww, ri, rw,
+                                           initial[:, h], cfg.bank_count, cfg.bank_size ** -0.5,
+                                           routed_decay=True, state_dtype=torch.float32,
+                                           combine='index_add', lockstep=False))
+            return torch.cat(outs, -1)
+
+    run()  # warmup
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    model = ''
+    try:
+        with open('/proc/cpuinfo') as f:
+            for line in f:
+                if line.startswith('model name'):
+                    model = line.split(':', 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {'value': round(tokens / med, 2), 'unit': 'tokens/s', 'cores': threads, 'kind': 'port',
+            'sample': (f'batch 1 x T={tokens} of the C2 geometry (H8 S8 v128 J256 KW=KR=8), FP32 state, '
+                       f'per-event loop of oracle/bdm_oracle.py packed_recurrence, median of 3 '
+                       f'({med:.2f} s each); host CPU: {model}')}
+
+
+def load_traffic():
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
+
+
+def progress(*what):
+    print('bench:', *what, file=sys.stderr, flush=True)
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
+        print('bench.py measures one GPU only: this build has no multi-GPU path '
+              '(every GPU box here has one GPU); run with --gpus 1', file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from bdm_amd import BankedDeltaMemory, ops
+
+    if not torch.cuda.is_available():
+        print('bench.py needs a ROCm GPU', file=sys.stderr)
+        sys.exit(2)
+    device = torch.device('cuda', 0)
+    cfg = c2_config()
+    batch, time_ = args.batch, args.time
+    layer = BankedDeltaMemory(cfg, layer_id=0, seed=0).to(device=device, dtype=torch.bfloat16)
+    x, (q, k, v, g, b, w), (read_scores, write_scores), initial = make_inputs(layer, batch, time_, device)
+    final = torch.empty(batch, cfg.bank_count, cfg.num_heads, cfg.bank_size, cfg.head_value_width,
+                        device=device, dtype=torch.bfloat16)
+    j, kk, scale = cfg.bank_count, cfg.selected_banks, cfg.bank_size ** -0.5
+    stream = torch.cuda.current_stream(device)
+    ev_start = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ev_stop = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    record = {'on': False, 'i': 0}
+
+    def step():
+        ww, wi = ops.router_select(write_scores, bank_count=j, selected_banks=kk)
+        rw, ri = ops.router_select(read_scores, bank_count=j, selected_banks=kk)
+        meta = ops.dispatch_build(wi, ri, j)
+        if record['on']:
+            ev_start[record['i']].record(stream)
+        y = ops.routed_forward(q, k, v, g, b, w, wi, ww, ri, rw, initial, meta, bank_count=j, scale=scale,
+                               routed_decay=True, round_interval=0, final_state=final)
+        if record['on']:
+            ev_stop[record['i']].record(stream)
+            record['i'] += 1
+        return y
+
+    progress('hot path', batch, time_)
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        record['on'] = True
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t0
+        record['on'] = False
+    sec = elapsed / args.steps
+    tokens = batch * time_
+    fwd_ms = statistics.mean(a.elapsed_time(bb) for a, bb in zip(ev_start, ev_stop))
+    fwd_bytes = forward_algorithmic_bytes(cfg, batch, time_, initial.numel() * initial.element_size())
+    achieved = fwd_bytes / (fwd_ms * 1e-3) / 1e9
+    hot_bytes = hot_path_algorithmic_bytes(cfg, batch, time_)
+    traffic = load_traffic()
+
+    result = {
+        'metric': 'BDM-layer prefill tokens/sec (routed-memory hot path, N=2048,S=8,B=8)',
+        'value': round(tokens / sec, 1), 'unit': 'tokens/s', 'n_gpus': 1, 'steps': args.steps,
+        'warmup': args.warmup, 'ms_per_step': round(sec * 1e3, 4), 'higher_is_better': True,
+        'scaling': 'weak', 'vs_baseline': None, 'dtype': 'bf16 storage, fp32 recurrence',
+        'data': 'synthetic: x ~ N(0,1), seeded random-init BSDM layer weights',
+        'config': {'workload': 'C2 prefill hot path: router x2 + dispatch + recurrence + ordered combine '
+                               '+ final BF16 state', 'batch': batch, 'seq_len': time_, 'd_model': cfg.dim,
+                   'heads': cfg.num_heads, 'bank_count': j, 'bank_size': cfg.bank_size,
+                   'selected_banks': kk, 'head_value_width': cfg.head_value_width},
+        'roofline': {'bound': 'hbm', 'kernel': 'bdm_forward (routed_forward_kernel + ordered_combine_kernel)',
+                     'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBPS, 'unit': 'GB/s',
+                     'frac': round(achieved / HBM_PEAK_GBPS, 4),
+                     'traffic': traffic.get('bytes_per_launch') if traffic else None,
+                     'launch_ms': round(fwd_ms, 4), 'algorithmic_bytes': fwd_bytes},
+        'hot_path_roofline_frac': round(hot_bytes / sec / 1e9 / HBM_PEAK_GBPS, 4),
+    }
+    if not args.no_extras:
+        progress('full layer prefill')
+        with torch.no_grad():
+            layer_sec, _ = timed(lambda: layer.prefill(x), max(3, args.steps // 4), 1)
+        result['full_layer_prefill_tokens_per_s'] = round(tokens / layer_sec, 1)
+        progress('decode C3')
+        result['decode_c3'] = decode_bench(layer, device, args.decode_steps)
+    progress('copy probe')
+    result['hbm_copy_GBps'] = round(copy_probe(device), 1)
+    if args.cpu_tokens > 0:
+        progress('cpu baseline', args.cpu_tokens, 'tokens')
+        result['cpu_baseline'] = cpu_baseline(layer, cfg, args.cpu_tokens)
+    else:
+        result['cpu_baseline'] = None
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == '__main__':
+    main()
