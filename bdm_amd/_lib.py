@@ -19,7 +19,8 @@ BDM_ROUTE_DUPLICATE = 2
 
 EXPORTED_SYMBOLS = (
     'bdm_version', 'bdm_last_error_string', 'bdm_router_select', 'bdm_dispatch_workspace_size',
-    'bdm_dispatch_build', 'bdm_forward_workspace_size', 'bdm_forward', 'bdm_decode',
+    'bdm_dispatch_build', 'bdm_forward_workspace_size', 'bdm_forward', 'bdm_snapshot_rows',
+    'bdm_backward_workspace_size', 'bdm_backward', 'bdm_decode',
 )
 
 _i32, _i64, _f32, _vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
@@ -37,6 +38,23 @@ class ForwardArgs(ctypes.Structure):
         ('write_banks', _i32), ('read_banks', _i32),
         ('ctrl_dtype', _i32), ('initial_dtype', _i32), ('final_dtype', _i32),
         ('routed_decay', _i32), ('round_interval', _i32), ('scale', _f32),
+        ('snapshots', _vp), ('snapshot_interval', _i32), ('snapshot_dtype', _i32),
+    ]
+
+
+class BackwardArgs(ctypes.Structure):
+    """Mirror of ``bdm_backward_args``."""
+    _fields_ = [
+        ('q', _vp), ('k', _vp), ('g', _vp), ('b', _vp), ('v', _vp), ('w', _vp),
+        ('write_weights', _vp), ('read_weights', _vp), ('order', _vp), ('cu_seqlens', _vp),
+        ('initial', _vp), ('snapshots', _vp), ('grad_output', _vp),
+        ('grad_q', _vp), ('grad_k', _vp), ('grad_g', _vp), ('grad_b', _vp), ('grad_v', _vp), ('grad_w', _vp),
+        ('grad_write_weights', _vp), ('grad_read_weights', _vp), ('grad_initial', _vp),
+        ('initial_batch_stride', _i64), ('batch', _i64), ('time', _i64),
+        ('heads', _i32), ('bank_size', _i32), ('head_width', _i32), ('bank_count', _i32),
+        ('write_banks', _i32), ('read_banks', _i32),
+        ('ctrl_dtype', _i32), ('initial_dtype', _i32), ('snapshot_dtype', _i32), ('routed_decay', _i32),
+        ('round_interval', _i32), ('snapshot_interval', _i32), ('scale', _f32),
     ]
 
 
@@ -75,6 +93,12 @@ def library() -> ctypes.CDLL:
     lib.bdm_forward_workspace_size.restype = _size_t
     lib.bdm_forward.argtypes = [ctypes.POINTER(ForwardArgs), _vp, _size_t, _vp]
     lib.bdm_forward.restype = _i32
+    lib.bdm_snapshot_rows.argtypes = [_i64, _i32]
+    lib.bdm_snapshot_rows.restype = _i64
+    lib.bdm_backward_workspace_size.argtypes = [ctypes.POINTER(BackwardArgs)]
+    lib.bdm_backward_workspace_size.restype = _size_t
+    lib.bdm_backward.argtypes = [ctypes.POINTER(BackwardArgs), _vp, _size_t, _vp]
+    lib.bdm_backward.restype = _i32
     lib.bdm_decode.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
     lib.bdm_decode.restype = _i32
     return lib

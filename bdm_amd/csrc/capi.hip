@@ -34,6 +34,11 @@ int check_launch(const char *what) {
 
 }  // namespace bdm
 
-extern "C" int bdm_version(void) { return 1; }
+extern "C" int bdm_version(void) { return 2; }
 
 extern "C" const char *bdm_last_error_string(void) { return bdm::g_last_error.c_str(); }
+
+extern "C" int64_t bdm_snapshot_rows(int64_t events, int32_t interval) {
+    if (events <= 0 || interval <= 0) return 0;
+    return events / interval;
+}

@@ -24,6 +24,7 @@
 // combine kernel adds a token's KR reads in increasing bank id, rounding after
 // every add (the production readout order).
 #include "bdm_common.h"
+#include "recurrence_ops.h"
 
 namespace bdm {
 namespace {
@@ -39,13 +40,15 @@ struct ForwardParams {
     const int64_t *order, *cu;
     const void *initial;
     void *final_state;
+    void *snap;
     T *zbuf;
     int64_t init_bstride;
     int64_t nt, time;
     int heads, s_real, width, banks, kw, kr;
     int lanes_per_head, heads_per_block;
     int round_interval, routed_decay;
-    int init_dtype, final_dtype;
+    int snap_interval;  // events between snapshots (0: none); equals round_interval when rounding
+    int init_dtype, final_dtype, snap_dtype;
     int xcd_remap;
     float scale;
 };
@@ -169,33 +172,32 @@ __global__ __launch_bounds__(256) void routed_forward_kernel(ForwardParams<T> p)
             const float pw = s_weight[i];
             if (i + 1 < n) fetch_event<T, S, CPL>(p, s_token[i + 1], s_slot[i + 1] >= 0, head, col0, nxt);
             const int64_t offset = base + i - start;
-            if (rounding && offset > 0 && offset % p.round_interval == 0) {
+            if (p.snap_interval > 0 && offset > 0 && offset % p.snap_interval == 0) {
+                if (rounding) {
 #pragma unroll
-                for (int r = 0; r < S; ++r)
+                    for (int r = 0; r < S; ++r)
 #pragma unroll
-                    for (int c = 0; c < CPL; ++c) h[r][c] = round_bf16(h[r][c]);
+                        for (int c = 0; c < CPL; ++c) h[r][c] = round_bf16(h[r][c]);
+                }
+                // Snapshot of the state before event base+i, the start of a
+                // replay chunk (role_bank_kernel.py:59-66).  Boundaries of one
+                // segment are snap_interval apart and segments are disjoint,
+                // so slot = position / interval - 1 is unique per boundary.
+                if (p.snap) {
+                    const int64_t slot = (base + i) / p.snap_interval - 1;
+                    store_state<S, CPL>(p.snap, p.snap_dtype,
+                                        ((slot * p.heads + head) * p.s_real) * p.width + col0, p.width,
+                                        p.s_real, h);
+                }
             }
             if (slot < 0) {
                 // write: hd = exp(eg) M ; u = bf(w p) v - (bf(b p) k)^T hd ; M = hd + k u^T
-                float decay[S], a[S];
+                WriteRows<S> rows;
+                prepare_write_rows<T, S>(cur.key, cur.gate, cur.erase, pw, p.routed_decay, rows);
+                float ew[CPL];
 #pragma unroll
-                for (int r = 0; r < S; ++r) {
-                    const float eg = p.routed_decay ? cur.gate[r] * pw : cur.gate[r];
-                    decay[r] = __expf(eg);
-                    a[r] = round_to<T>(cur.erase[r] * pw) * cur.key[r];
-                }
-#pragma unroll
-                for (int c = 0; c < CPL; ++c) {
-                    float erase = 0.f;
-#pragma unroll
-                    for (int r = 0; r < S; ++r) {
-                        h[r][c] *= decay[r];
-                        erase = fmaf(a[r], h[r][c], erase);
-                    }
-                    const float u = round_to<T>(cur.wgate[c] * pw) * cur.value[c] - erase;
-#pragma unroll
-                    for (int r = 0; r < S; ++r) h[r][c] = fmaf(cur.key[r], u, h[r][c]);
-                }
+                for (int c = 0; c < CPL; ++c) ew[c] = round_to<T>(cur.wgate[c] * pw);
+                apply_write<S, CPL>(h, rows, ew, cur.value);
             } else {
                 // read: z = scale * bf(q r)^T M, stored in the value dtype
                 float qr[S];
@@ -291,6 +293,9 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, hipStream_t stream) {
     if (p.heads_per_block > a.heads) p.heads_per_block = a.heads;
     p.round_interval = a.round_interval;
     p.routed_decay = a.routed_decay;
+    p.snap = a.snapshots;
+    p.snap_interval = a.round_interval > 0 ? a.round_interval : (a.snapshots ? a.snapshot_interval : 0);
+    p.snap_dtype = a.snapshot_dtype;
     p.init_dtype = a.initial_dtype;
     p.final_dtype = a.final_dtype;
     p.scale = a.scale;
@@ -361,7 +366,17 @@ extern "C" int bdm_forward(const bdm_forward_args *a, void *workspace, size_t wo
     if (!a->q || !a->k || !a->g || !a->b || !a->v || !a->w || !a->write_weights || !a->read_weights ||
         !a->read_indices || !a->order || !a->cu_seqlens || !a->initial || !a->output)
         return fail(BDM_ERR_INVALID, "forward: null pointer");
-    const void *ptrs[] = {a->q, a->k, a->g, a->b, a->v, a->w, a->initial, a->output, a->final_state, workspace};
+    if (a->snapshots) {
+        if (a->snapshot_interval <= 0 || (a->round_interval > 0 && a->round_interval != a->snapshot_interval))
+            return fail(BDM_ERR_INVALID, "forward: snapshot interval %d must be positive and equal the rounding "
+                        "interval %d", a->snapshot_interval, a->round_interval);
+        if (a->snapshot_dtype != BDM_BF16 && a->snapshot_dtype != BDM_F32)
+            return fail(BDM_ERR_INVALID, "forward: snapshot dtype");
+        if (a->round_interval == 0 && a->snapshot_dtype != BDM_F32)
+            return fail(BDM_ERR_INVALID, "forward: an unrounded state needs FP32 snapshots");
+    }
+    const void *ptrs[] = {a->q, a->k, a->g, a->b, a->v, a->w, a->initial, a->output, a->final_state, a->snapshots,
+                          workspace};
     for (const void *ptr : ptrs)
         if (ptr && !aligned(ptr, 16)) return fail(BDM_ERR_INVALID, "forward: tensors must be 16-byte aligned");
     const size_t need = bdm_forward_workspace_size(a);

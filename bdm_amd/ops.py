@@ -142,16 +142,36 @@ def _as_heads(t: Tensor, name: str) -> Tensor:
     raise ValueError(f'{name} must be [batch, time, width] or [batch, time, heads, width]')
 
 
-def routed_forward(q, k, v, g, b, w, wi, ww, ri, rw, initial: Tensor, meta: Dispatch, *, bank_count: int,
-                   scale: float, routed_decay: bool, round_interval: int = 0,
-                   final_state: Tensor | None = None) -> Tensor:
-    """Bank recurrence and ordered read combine for every head.
+@dataclass
+class RoutedInputs:
+    """Validated, contiguous, 16-byte aligned operands of the routed recurrence
+    with their geometry (shared by the forward and the backward)."""
+    q: Tensor
+    k: Tensor
+    g: Tensor
+    b: Tensor
+    v: Tensor
+    w: Tensor
+    ww: Tensor
+    rw: Tensor
+    ri: Tensor
+    initial: Tensor
+    initial_stride: int
+    batch: int
+    time: int
+    heads: int
+    bank_size: int
+    width: int
+    write_banks: int
+    read_banks: int
+    per_head_layout: bool
+    dtype: torch.dtype
+    device: torch.device
 
-    q,k,g,b: [B,T,S] or [B,T,H,S];  v,w: [B,T,v] or [B,T,H,v];
-    initial: [J,S,v] / [J,H,S,v] shared by the batch, or [B,J,S,v] /
-    [B,J,H,S,v] per sequence (4-D is read as per-head when q is 4-D);
-    final_state: optional [B,J,H,S,v] (or [B,J,S,v]) output, may alias initial.
-    Returns y [B, T, H*v] in the controller dtype."""
+
+def prepare_routed(q, k, v, g, b, w, wi, ww, ri, rw, initial: Tensor, *, bank_count: int) -> RoutedInputs:
+    """Shape/dtype validation of the routed operator's operands
+    (role_bank_dispatch.py:156-166 and routed_update.py:18-22 assert the same)."""
     q4, k4, g4, b4 = (_as_heads(t, n) for t, n in ((q, 'q'), (k, 'k'), (g, 'g'), (b, 'b')))
     v4, w4 = _as_heads(v, 'v'), _as_heads(w, 'w')
     if not (q4.shape == k4.shape == g4.shape == b4.shape):
@@ -168,54 +188,135 @@ def routed_forward(q, k, v, g, b, w, wi, ww, ri, rw, initial: Tensor, meta: Disp
     for t in (k4, b4, v4, w4, ww, rw):
         if t.dtype != dtype:
             raise ValueError('q, k, b, v, w and the route weights must share one dtype')
-    device = _require_gpu(q4, k4, g4, b4, v4, w4, wi, ww, ri, rw, initial, meta.order, final_state)
+    device = _require_gpu(q4, k4, g4, b4, v4, w4, wi, ww, ri, rw, initial)
     per_head_layout = q.ndim == 4
     shared_dims = 4 if per_head_layout else 3
     if initial.ndim == shared_dims:
-        init = initial
         init_stride = 0
     elif initial.ndim == shared_dims + 1:
         if initial.shape[0] != batch:
             raise ValueError('per-sequence initial state must lead with the batch dimension')
-        init = initial
         init_stride = initial[0].numel()
     else:
         raise ValueError('initial state has the wrong rank')
     expect = (bank_count, heads, s, width) if per_head_layout else (bank_count, s, width)
-    if tuple(init.shape[-len(expect):]) != expect:
-        raise ValueError(f'initial state must end in {expect}, got {tuple(init.shape)}')
-    init = _aligned(init)
+    if tuple(initial.shape[-len(expect):]) != expect:
+        raise ValueError(f'initial state must end in {expect}, got {tuple(initial.shape)}')
+    if initial.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError('initial state must be FP32 or BF16')
+    return RoutedInputs(
+        q=_aligned(q4), k=_aligned(k4), g=_aligned(g4.float()), b=_aligned(b4), v=_aligned(v4), w=_aligned(w4),
+        ww=_aligned(ww), rw=_aligned(rw), ri=_aligned(ri), initial=_aligned(initial), initial_stride=init_stride,
+        batch=batch, time=time, heads=heads, bank_size=s, width=width, write_banks=wi.shape[-1],
+        read_banks=ri.shape[-1], per_head_layout=per_head_layout, dtype=dtype, device=device)
+
+
+def snapshot_buffer(x: RoutedInputs, interval: int, dtype: torch.dtype) -> Tensor:
+    """Snapshot storage for a forward with backward: [E // interval, H, S, v]."""
+    events = x.batch * x.time * (x.write_banks + x.read_banks)
+    rows = int(_lib.library().bdm_snapshot_rows(events, interval))
+    return torch.empty((max(rows, 1), x.heads, x.bank_size, x.width), device=x.device, dtype=dtype)
+
+
+def routed_forward(q, k, v, g, b, w, wi, ww, ri, rw, initial: Tensor, meta: Dispatch, *, bank_count: int,
+                   scale: float, routed_decay: bool, round_interval: int = 0,
+                   final_state: Tensor | None = None, snapshots: Tensor | None = None,
+                   snapshot_interval: int = 0, prepared: RoutedInputs | None = None) -> Tensor:
+    """Bank recurrence and ordered read combine for every head.
+
+    q,k,g,b: [B,T,S] or [B,T,H,S];  v,w: [B,T,v] or [B,T,H,v];
+    initial: [J,S,v] / [J,H,S,v] shared by the batch, or [B,J,S,v] /
+    [B,J,H,S,v] per sequence (4-D is read as per-head when q is 4-D);
+    final_state: optional [B,J,H,S,v] (or [B,J,S,v]) output, may alias initial;
+    snapshots: optional buffer from ``snapshot_buffer`` for the backward.
+    Returns y [B, T, H*v] in the controller dtype."""
+    x = prepared or prepare_routed(q, k, v, g, b, w, wi, ww, ri, rw, initial, bank_count=bank_count)
+    _require_gpu(meta.order, final_state, snapshots)
     if final_state is not None:
-        if final_state.numel() != batch * bank_count * heads * s * width or not final_state.is_contiguous():
+        if final_state.numel() != x.batch * bank_count * x.heads * x.bank_size * x.width \
+                or not final_state.is_contiguous():
             raise ValueError('final_state must be a contiguous [batch, J, H, S, v] tensor')
         if final_state.data_ptr() % 16:
             raise ValueError('final_state must be 16-byte aligned')
-    qc, kc, bc, vc, wc = (_aligned(t) for t in (q4, k4, b4, v4, w4))
-    gc = _aligned(g4.float())
-    wwc, rwc, ric = _aligned(ww), _aligned(rw), _aligned(ri)
-    output = torch.empty((batch, time, heads * width), device=device, dtype=dtype)
+    output = torch.empty((x.batch, x.time, x.heads * x.width), device=x.device, dtype=x.dtype)
     args = _lib.ForwardArgs()
-    args.q, args.k, args.g, args.b, args.v, args.w = (t.data_ptr() for t in (qc, kc, gc, bc, vc, wc))
-    args.write_weights, args.read_weights, args.read_indices = wwc.data_ptr(), rwc.data_ptr(), ric.data_ptr()
+    args.q, args.k, args.g, args.b, args.v, args.w = (t.data_ptr() for t in (x.q, x.k, x.g, x.b, x.v, x.w))
+    args.write_weights, args.read_weights, args.read_indices = x.ww.data_ptr(), x.rw.data_ptr(), x.ri.data_ptr()
     args.order, args.cu_seqlens = meta.order.data_ptr(), meta.cu_seqlens.data_ptr()
-    args.initial = init.data_ptr()
+    args.initial = x.initial.data_ptr()
     args.final_state = final_state.data_ptr() if final_state is not None else None
     args.output = output.data_ptr()
-    args.initial_batch_stride = init_stride
-    args.batch, args.time = batch, time
-    args.heads, args.bank_size, args.head_width, args.bank_count = heads, s, width, bank_count
-    args.write_banks, args.read_banks = wi.shape[-1], ri.shape[-1]
-    args.ctrl_dtype = _dtype_code(dtype)
-    args.initial_dtype = _dtype_code(init.dtype)
+    args.initial_batch_stride = x.initial_stride
+    args.batch, args.time = x.batch, x.time
+    args.heads, args.bank_size, args.head_width, args.bank_count = x.heads, x.bank_size, x.width, bank_count
+    args.write_banks, args.read_banks = x.write_banks, x.read_banks
+    args.ctrl_dtype = _dtype_code(x.dtype)
+    args.initial_dtype = _dtype_code(x.initial.dtype)
     args.final_dtype = _dtype_code(final_state.dtype) if final_state is not None else 0
     args.routed_decay = int(bool(routed_decay))
     args.round_interval = int(round_interval)
     args.scale = float(scale)
+    if snapshots is not None:
+        args.snapshots = snapshots.data_ptr()
+        args.snapshot_interval = int(snapshot_interval)
+        args.snapshot_dtype = _dtype_code(snapshots.dtype)
     lib = _lib.library()
     ws_bytes = lib.bdm_forward_workspace_size(ctypes.byref(args))
-    workspace = torch.empty(max(int(ws_bytes), 1), device=device, dtype=torch.uint8)
-    _lib.check(lib.bdm_forward(ctypes.byref(args), _ptr(workspace), ws_bytes, _stream(device)), 'bdm_forward')
+    workspace = torch.empty(max(int(ws_bytes), 1), device=x.device, dtype=torch.uint8)
+    _lib.check(lib.bdm_forward(ctypes.byref(args), _ptr(workspace), ws_bytes, _stream(x.device)), 'bdm_forward')
     return output
+
+
+@dataclass
+class RoutedGrads:
+    q: Tensor
+    k: Tensor
+    v: Tensor
+    g: Tensor
+    b: Tensor
+    w: Tensor
+    ww: Tensor
+    rw: Tensor
+    initial: Tensor  # FP32 [B, J, H, S, v] adjoint of each sequence's initial state
+
+
+def routed_backward(x: RoutedInputs, meta: Dispatch, grad_output: Tensor, snapshots: Tensor, *, bank_count: int,
+                    scale: float, routed_decay: bool, round_interval: int, snapshot_interval: int) -> RoutedGrads:
+    """Gradients of ``routed_forward`` (RoutedUpdate.backward, routed_update.py:31-49)."""
+    if grad_output.shape != (x.batch, x.time, x.heads * x.width):
+        grad_output = grad_output.reshape(x.batch, x.time, x.heads * x.width)
+    dy = _aligned(grad_output.to(x.dtype))
+    ctrl = (x.batch, x.time, x.heads, x.bank_size)
+    vals = (x.batch, x.time, x.heads, x.width)
+    empty = lambda shape, dtype=x.dtype: torch.empty(shape, device=x.device, dtype=dtype)  # noqa: E731
+    out = RoutedGrads(q=empty(ctrl), k=empty(ctrl), v=empty(vals), g=empty(ctrl, torch.float32), b=empty(ctrl),
+                      w=empty(vals), ww=empty(x.ww.shape), rw=empty(x.rw.shape),
+                      initial=empty((x.batch, bank_count, x.heads, x.bank_size, x.width), torch.float32))
+    args = _lib.BackwardArgs()
+    args.q, args.k, args.g, args.b, args.v, args.w = (t.data_ptr() for t in (x.q, x.k, x.g, x.b, x.v, x.w))
+    args.write_weights, args.read_weights = x.ww.data_ptr(), x.rw.data_ptr()
+    args.order, args.cu_seqlens = meta.order.data_ptr(), meta.cu_seqlens.data_ptr()
+    args.initial, args.snapshots, args.grad_output = x.initial.data_ptr(), snapshots.data_ptr(), dy.data_ptr()
+    args.grad_q, args.grad_k, args.grad_g = out.q.data_ptr(), out.k.data_ptr(), out.g.data_ptr()
+    args.grad_b, args.grad_v, args.grad_w = out.b.data_ptr(), out.v.data_ptr(), out.w.data_ptr()
+    args.grad_write_weights, args.grad_read_weights = out.ww.data_ptr(), out.rw.data_ptr()
+    args.grad_initial = out.initial.data_ptr()
+    args.initial_batch_stride = x.initial_stride
+    args.batch, args.time = x.batch, x.time
+    args.heads, args.bank_size, args.head_width, args.bank_count = x.heads, x.bank_size, x.width, bank_count
+    args.write_banks, args.read_banks = x.write_banks, x.read_banks
+    args.ctrl_dtype = _dtype_code(x.dtype)
+    args.initial_dtype = _dtype_code(x.initial.dtype)
+    args.snapshot_dtype = _dtype_code(snapshots.dtype)
+    args.routed_decay = int(bool(routed_decay))
+    args.round_interval = int(round_interval)
+    args.snapshot_interval = int(snapshot_interval)
+    args.scale = float(scale)
+    lib = _lib.library()
+    ws_bytes = lib.bdm_backward_workspace_size(ctypes.byref(args))
+    workspace = torch.empty(max(int(ws_bytes), 1), device=x.device, dtype=torch.uint8)
+    _lib.check(lib.bdm_backward(ctypes.byref(args), _ptr(workspace), ws_bytes, _stream(x.device)), 'bdm_backward')
+    return out
 
 
 # ---------------------------------------------------------------------------

@@ -28,24 +28,56 @@ def _round_interval(bank_size: int, state_dtype: torch.dtype) -> int:
 class RoutedUpdate(torch.autograd.Function):
     """Autograd type of the routed path (routed_update.py:16-53).
 
-    Forward: one shared dispatch, then the fused recurrence + ordered combine.
+    Forward: one shared dispatch for every head, then the fused recurrence +
+    ordered combine; when a gradient is needed the forward also stores the
+    state at every replay boundary (BF16 when the training state is BF16,
+    role_bank_kernel.py:59-66).  Backward: exact chunk replay and reverse
+    adjoint, then the token-level VJP; returns gradients for
+    (q, k, v, g, b, w, ww, rw, state) and None for wi, ri and the options
+    (routed_update.py:49).
     """
 
     @staticmethod
     def forward(ctx, q, k, v, g, b, w, wi, ww, ri, rw, state, bank_count, scale, compact_replay, state_dtype,
                 routed_decay):
-        meta = ops.dispatch_build(wi, ri, bank_count)
         interval = _round_interval(q.shape[-1], state_dtype)
+        meta = ops.dispatch_build(wi, ri, bank_count)
+        x = ops.prepare_routed(q, k, v, g, b, w, wi, ww, ri, rw, state, bank_count=bank_count)
+        wants_grad = any(ctx.needs_input_grad[i] for i in (0, 1, 2, 3, 4, 5, 7, 9, 10))
+        snapshots, snap_interval = None, 0
+        if wants_grad:
+            snap_interval = interval or replay_interval(q.shape[-1])
+            snapshots = ops.snapshot_buffer(x, snap_interval, torch.bfloat16 if interval else torch.float32)
         raw = ops.routed_forward(q, k, v, g, b, w, wi, ww, ri, rw, state, meta, bank_count=bank_count,
-                                 scale=scale, routed_decay=routed_decay, round_interval=interval)
-        ctx.mark_non_differentiable(wi, ri)
+                                 scale=scale, routed_decay=routed_decay, round_interval=interval,
+                                 snapshots=snapshots, snapshot_interval=snap_interval, prepared=x)
+        if wants_grad:
+            ctx.save_for_backward(q, k, v, g, b, w, wi, ww, ri, rw, state, meta.order, meta.cu_seqlens, snapshots)
+            ctx.options = (bank_count, scale, routed_decay, interval, snap_interval)
         if q.ndim == 3:
             raw = raw.view(q.shape[0], q.shape[1], v.shape[-1])
         return raw
 
     @staticmethod
     def backward(ctx, grad_output):
-        raise NotImplementedError('the HIP backward of the routed bank path is not built yet')
+        q, k, v, g, b, w, wi, ww, ri, rw, state, order, cu, snapshots = ctx.saved_tensors
+        bank_count, scale, routed_decay, interval, snap_interval = ctx.options
+        meta = ops.Dispatch(order, None, None, cu, None)
+        x = ops.prepare_routed(q, k, v, g, b, w, wi, ww, ri, rw, state, bank_count=bank_count)
+        grads = ops.routed_backward(x, meta, grad_output.contiguous(), snapshots, bank_count=bank_count,
+                                    scale=scale, routed_decay=routed_decay, round_interval=interval,
+                                    snapshot_interval=snap_interval)
+        shape = lambda t, like: t.reshape(like.shape).to(like.dtype)  # noqa: E731
+        dq, dk, dv, dg, db, dw = (shape(t, like) for t, like in ((grads.q, q), (grads.k, k), (grads.v, v),
+                                                                  (grads.g, g), (grads.b, b), (grads.w, w)))
+        # role_bank_kernel.py:256 / routed_update.py:48: round to the state dtype,
+        # then sum the per-sequence adjoints over the batch
+        ds = grads.initial.to(state.dtype)
+        if x.initial_stride == 0:
+            ds = ds.sum(0)
+        ds = ds.reshape(state.shape)
+        return (dq, dk, dv, dg, db, dw, None, grads.ww.to(ww.dtype), None, grads.rw.to(rw.dtype), ds,
+                None, None, None, None, None)
 
 
 def bank_training(q, k, v, g, b, w, wi, ww, ri, rw, state, bank_count, scale, *, compact_replay=None,

@@ -101,6 +101,13 @@ int bdm_dispatch_build(const int64_t *write_indices, const int64_t *read_indices
  * a positive multiple of round_interval (the training path's storage cadence).
  * y[token, h*v + c] adds the token's reads in increasing bank id, rounding to
  * ctrl_dtype after each add.
+ *
+ * Snapshots for the backward (role_bank_kernel.py:57-66): when `snapshots` is
+ * not NULL the state before every event whose in-segment offset is a positive
+ * multiple of snapshot_interval (after the rounding above, which must then use
+ * the same interval) is stored at row (packed position / interval - 1) of
+ * snapshots [bdm_snapshot_rows(E, interval), H, S, v] in snapshot_dtype.
+ * Rows that no boundary maps to are left untouched.
  */
 typedef struct bdm_forward_args {
     const void *q;             /* [NT, H, S] ctrl_dtype */
@@ -124,10 +131,63 @@ typedef struct bdm_forward_args {
     int32_t routed_decay;
     int32_t round_interval;
     float scale;
+    void *snapshots;           /* NULL or [rows, H, S, v] of snapshot_dtype (see above) */
+    int32_t snapshot_interval;
+    int32_t snapshot_dtype;    /* BDM_BF16 only with round_interval == snapshot_interval */
 } bdm_forward_args;
+
+/* Rows of the snapshot buffer for E packed events: E / interval. */
+int64_t bdm_snapshot_rows(int64_t events, int32_t interval);
 
 size_t bdm_forward_workspace_size(const bdm_forward_args *args);
 int bdm_forward(const bdm_forward_args *args, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * Backward of bdm_forward.  Replaces RoutedUpdate.backward / RoleBankTraining
+ * .backward (implementation/bdm/routed_update.py:31-49,
+ * role_bank_kernel.py:231-256): the chunk replay and reverse adjoint of
+ * _role_backward (role_bank_kernel.py:76-150) and the token-level VJP _vjp
+ * (role_bank_dispatch.py:76-132), with its BF16 rounding points, plus the
+ * routed-decay term of d(ww) (routed_update.py:43-47).
+ *
+ * Inputs are those of the forward (same layouts), its snapshots (taken with
+ * snapshot_interval = C: 16 for S <= 8, 8 for S <= 16, 4 for S <= 32 — the
+ * reference replay chunk, role_bank_kernel.py:153-154) and grad_output
+ * [NT, H*v] in ctrl_dtype.  Outputs, token-major like the inputs:
+ *   grad_q, grad_k, grad_b [NT, H, S] ctrl_dtype;  grad_g [NT, H, S] FP32;
+ *   grad_v, grad_w [NT, H, v] ctrl_dtype;
+ *   grad_write_weights [NT, KW], grad_read_weights [NT, KR] ctrl_dtype, the
+ *     heads' contributions summed;
+ *   grad_initial [batch, J, H, S, v] FP32: the adjoint of each sequence's
+ *     initial bank state (sum over the batch for a shared initial state).
+ * Every output element is written.  Route order within a token (j = 0..K-1)
+ * is the order the reference folds the token's events in.
+ */
+typedef struct bdm_backward_args {
+    const void *q, *k;         /* [NT, H, S] ctrl_dtype */
+    const float *g;            /* [NT, H, S] */
+    const void *b;             /* [NT, H, S] ctrl_dtype */
+    const void *v, *w;         /* [NT, H, v] ctrl_dtype */
+    const void *write_weights, *read_weights; /* [NT, KW], [NT, KR] ctrl_dtype */
+    const int64_t *order, *cu_seqlens;        /* from bdm_dispatch_build */
+    const void *initial;       /* as in bdm_forward_args */
+    const void *snapshots;     /* written by bdm_forward */
+    const void *grad_output;   /* [NT, H*v] ctrl_dtype */
+    void *grad_q, *grad_k;
+    float *grad_g;
+    void *grad_b, *grad_v, *grad_w;
+    void *grad_write_weights, *grad_read_weights;
+    float *grad_initial;
+    int64_t initial_batch_stride, batch, time;
+    int32_t heads, bank_size, head_width, bank_count, write_banks, read_banks;
+    int32_t ctrl_dtype, initial_dtype, snapshot_dtype, routed_decay, round_interval, snapshot_interval;
+    float scale;
+} bdm_backward_args;
+
+/* Scratch of bdm_backward: per-event du (FP32, NT*KW*H*v) and per-event
+ * S-wide partial gradients; the workspace must be 256-byte aligned. */
+size_t bdm_backward_workspace_size(const bdm_backward_args *args);
+int bdm_backward(const bdm_backward_args *args, void *workspace, size_t workspace_bytes, void *stream);
 
 /*
  * Single-token decode against resident bank states.  Replaces

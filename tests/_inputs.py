@@ -41,7 +41,7 @@ def initial_state(bank_count, heads, s, v, gen, scale=0.1, batch=None):
 
 def rel_err(ours: torch.Tensor, ref: torch.Tensor) -> float:
     """max |ours - ref| / max |ref| in FP32."""
-    ours, ref = ours.float().cpu(), ref.float().cpu()
+    ours, ref = ours.detach().float().cpu(), ref.detach().float().cpu()
     return float((ours - ref).abs().max() / ref.abs().max().clamp_min(1e-30))
 
 

@@ -79,3 +79,54 @@ def test_python_errors_mirror_the_reference():
         layer(torch.zeros(1, 0, 32))
     with pytest.raises(ValueError):
         layer(torch.zeros(1, 3, 32))  # CPU tensors: the HIP path never falls back
+
+
+def test_backward_rejects_bad_arguments(lib):
+    from bdm_amd import _lib
+    assert lib.bdm_backward(None, None, 0, None) == -1
+    args = _lib.BackwardArgs()
+    args.batch, args.time, args.heads, args.bank_size, args.head_width = 1, 4, 1, 8, 16
+    args.bank_count, args.write_banks, args.read_banks = 4, 1, 1
+    args.ctrl_dtype = args.initial_dtype = args.snapshot_dtype = _lib.BDM_BF16
+    args.round_interval, args.snapshot_interval = 16, 16
+    assert lib.bdm_backward(ctypes.byref(args), None, 0, None) == -1  # null operands
+    assert b'null pointer' in lib.bdm_last_error_string()
+    args.round_interval, args.snapshot_interval = 16, 8
+    assert lib.bdm_backward(ctypes.byref(args), None, 0, None) == -1
+    args.round_interval, args.snapshot_interval = 0, 16
+    assert lib.bdm_backward(ctypes.byref(args), None, 0, None) == -1  # BF16 snapshots of an unrounded state
+    # du (NT*KW*H*v FP32) + dk/db/dg (3*NT*KW*H*S) + dq (NT*KR*H*S), each 256-byte aligned
+    args.snapshot_dtype = _lib.BDM_F32
+    size = lib.bdm_backward_workspace_size(ctypes.byref(args))
+    up = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    assert size == up(4 * 16 * 4) + up(3 * 4 * 8 * 4) + up(4 * 8 * 4)
+    assert lib.bdm_snapshot_rows(1000, 16) == 62 and lib.bdm_snapshot_rows(0, 16) == 0
+
+
+def test_struct_layouts_match_the_header(tmp_path):
+    """sizeof/offsetof of every argument struct, compiled from the header with
+    gcc, equal the ctypes mirrors the Python layer passes."""
+    import shutil
+    import subprocess
+    from bdm_amd import _lib
+    gcc = shutil.which('gcc')
+    if gcc is None:
+        pytest.skip('no host C compiler')
+    mirrors = {'bdm_forward_args': _lib.ForwardArgs, 'bdm_backward_args': _lib.BackwardArgs,
+               'bdm_decode_args': _lib.DecodeArgs}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', 'int main(void) {']
+    for struct, mirror in mirrors.items():
+        lines.append(f'printf("{struct} size %zu\\n", sizeof({struct}));')
+        for field, _ in mirror._fields_:
+            lines.append(f'printf("{struct} {field} %zu\\n", offsetof({struct}, {field}));')
+    lines.append('return 0; }')
+    src = tmp_path / 'layout.c'
+    src.write_text('\n'.join(lines))
+    exe = tmp_path / 'layout'
+    subprocess.run([gcc, str(src), '-o', str(exe)], check=True)
+    out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split('\n')
+    got = {tuple(line.split()[:2]): int(line.split()[2]) for line in out if line}
+    for struct, mirror in mirrors.items():
+        assert got[(struct, 'size')] == ctypes.sizeof(mirror), struct
+        for field, _ in mirror._fields_:
+            assert got[(struct, field)] == getattr(mirror, field).offset, (struct, field)
