@@ -23,6 +23,8 @@
 // (ctrl dtype) buffer indexed by the read's original slot token*KR + j; the
 // combine kernel adds a token's KR reads in increasing bank id, rounding after
 // every add (the production readout order).
+#include <type_traits>
+
 #include "bdm_common.h"
 #include "recurrence_ops.h"
 
@@ -222,6 +224,316 @@ __global__ __launch_bounds__(256) void routed_forward_kernel(ForwardParams<T> p)
     }
 }
 
+// ----------------------------------------------------------------------------
+// Lazy-decay segment kernel for S <= 8 (the production geometry).
+//
+// The state of one (segment, head) is kept as M = diag(s) * Mh with a per-row
+// scale s.  A write's decay then only updates s (s' = s * exp(eg)), and with
+// a = bf(b*p) * k, x = bf(w*p) * v:
+//   erase = sum_r (a_r s'_r) Mh_r,   u = x - erase,   Mh_r += (k_r / s'_r) u
+// which is M' = hd + k u^T divided row-wise by s', at two FMAs per state
+// element instead of three.  Stages of kLazyStage events start at segment
+// offsets that are multiples of 16, the rounding/snapshot interval, and s is
+// folded back into Mh (Mh *= s, s = 1) at every stage start and at the
+// segment end, so every rounding point and snapshot sees the true state, as
+// the reference rounds it.  A stage in which some row's s would fall below
+// kScaleFloor runs in eager form instead (Mh = M: hd = exp(eg) * M applied
+// explicitly: M' = diag(d) M + k u^T, erase = sum_r (a_r d_r) M_r), so
+// k / s' stays finite.  A read uses
+// gamma_r = scale * bf(q*r)_r * s_r.
+//
+// The row quantities of every (event, head, row) are computed once per stage
+// for the workgroup: all threads compute exp(eg), k, a (or scale*bf(q*r)) in
+// parallel, then one lane per (head, row) scans the stage carrying s and
+// turns them into alpha = a s', beta = k / s' (or, eager, a and k with the
+// decay kept) or gamma.  The lanes that own value columns read them from LDS
+// by broadcast; the event loop never rescales the state conditionally.
+// CPL consecutive columns of T kept as raw 32-bit words (BF16 pairs unpacked
+// on use), so a prefetched row costs CPL/2 (BF16) or CPL (FP32) registers.
+template <typename T, int CPL>
+struct RawCols;
+
+template <int CPL>
+struct RawCols<bf16_t, CPL> {
+    static_assert(CPL % 2 == 0, "BF16 pairs");
+    uint32_t u[CPL / 2];
+    __device__ __forceinline__ void load(const bf16_t *p) {
+        if constexpr (CPL % 8 == 0) {
+#pragma unroll
+            for (int i = 0; i < CPL / 8; ++i) {
+                const uint4 q = reinterpret_cast<const uint4 *>(p)[i];
+                u[4 * i] = q.x;
+                u[4 * i + 1] = q.y;
+                u[4 * i + 2] = q.z;
+                u[4 * i + 3] = q.w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < CPL / 4; ++i) {
+                const uint2 q = reinterpret_cast<const uint2 *>(p)[i];
+                u[2 * i] = q.x;
+                u[2 * i + 1] = q.y;
+            }
+        }
+    }
+    __device__ __forceinline__ float get(int c) const {
+        const uint32_t word = u[c / 2];
+        return __uint_as_float((c & 1) ? (word & 0xffff0000u) : (word << 16));
+    }
+};
+
+template <int CPL>
+struct RawCols<float, CPL> {
+    float f[CPL];
+    __device__ __forceinline__ void load(const float *p) { load_row<CPL>(p, f); }
+    __device__ __forceinline__ float get(int c) const { return f[c]; }
+};
+
+__device__ __forceinline__ int64_t uniform_i64(int64_t x) {
+    const int lo = __builtin_amdgcn_readfirstlane(int(uint32_t(uint64_t(x))));
+    const int hi = __builtin_amdgcn_readfirstlane(int(uint32_t(uint64_t(x) >> 32)));
+    return int64_t((uint64_t(uint32_t(hi)) << 32) | uint64_t(uint32_t(lo)));
+}
+
+constexpr int kLazyStage = 16;
+constexpr int kLazyHeads = 8;  // heads per workgroup
+constexpr float kScaleFloor = 0x1p-32f;
+
+template <typename T, int CPL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void lazy_forward_kernel(
+    ForwardParams<T> p) {
+    constexpr int S = 8;
+    __shared__ int64_t s_token[kLazyStage];
+    __shared__ int64_t s_slot[kLazyStage];  // read: original read slot; write: -1
+    __shared__ float s_weight[kLazyStage];
+    __shared__ float s_rows[kLazyStage][kLazyHeads][3][S];
+    __shared__ float s_fold[kLazyHeads][S];
+    __shared__ int s_eager;
+    __shared__ int s_wpos[kLazyStage + 1];  // event index of each write of the stage, then n
+    __shared__ int s_nw;
+
+    const int nseg = gridDim.x;
+    const int seg = p.xcd_remap ? int((blockIdx.x % 8) * (nseg / 8) + blockIdx.x / 8) : int(blockIdx.x);
+    const int bank = seg % p.banks;
+    const int64_t bidx = seg / p.banks;
+    const int head0 = blockIdx.y * p.heads_per_block;
+    const int nheads = min(p.heads_per_block, p.heads - head0);
+    const int tid = threadIdx.x;
+    // Lanes past the block's heads (when nheads * lanes_per_head is not a
+    // multiple of the wave) shadow lanes of the last head: they compute the
+    // identical values and store them to the same addresses, so every lane
+    // runs the same control flow and no store needs a lane condition.
+    const int lh = min(tid / p.lanes_per_head, nheads - 1);  // head within the block
+    const int head = head0 + lh;
+    const int col0 = (tid % p.lanes_per_head) * CPL;
+    const bool scanner = tid < nheads * S;  // all in the first wave
+    const int scan_head = tid / S, scan_row = tid % S;
+    const int64_t start = p.cu[seg], end = p.cu[seg + 1];
+    const int64_t write_events = p.nt * p.kw;
+    const int64_t events = p.nt * (p.kw + p.kr);
+    const bool rounding = p.round_interval > 0;
+    float sc = 1.f;  // the scanner's s of (scan_head, scan_row)
+
+    float h[S][CPL];
+    const int64_t state_offset = ((int64_t(bank) * p.heads + head) * p.s_real) * p.width + col0;
+    load_state<S, CPL>(p.initial, p.init_dtype, bidx * p.init_bstride + state_offset, p.width, p.s_real, h);
+    if (rounding) {
+#pragma unroll
+        for (int r = 0; r < S; ++r)
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) h[r][c] = round_bf16(h[r][c]);
+    }
+
+    for (int64_t base = start; base < end; base += kLazyStage) {
+        const int n = int(min(int64_t(kLazyStage), end - base));
+        __syncthreads();  // the previous stage's readers are done
+        if (tid < n) {
+            int64_t o = p.order[base + tid];
+            o = o < 0 ? 0 : (o >= events ? events - 1 : o);
+            const bool rd = o >= write_events;
+            const int64_t route = rd ? o - write_events : o;
+            s_token[tid] = rd ? route / p.kr : route / p.kw;
+            s_slot[tid] = rd ? route : -1;
+            s_weight[tid] = rd ? to_f32(p.rw[route]) : to_f32(p.ww[route]);
+        }
+        if (tid == 0) s_eager = 0;
+        __syncthreads();
+        if (tid == 0) {
+            int nw = 0;
+            for (int i = 0; i < n; ++i)
+                if (s_slot[i] < 0) s_wpos[nw++] = i;
+            s_wpos[nw] = n;
+            s_nw = nw;
+        }
+        // (1) per (event, head, row): exp(eg), k, a for a write; scale*bf(q*r) for a read
+        for (int e = tid; e < n * nheads * S; e += blockDim.x) {
+            const int i = e / (nheads * S), hl = (e / S) % nheads, r = e % S;
+            const int64_t at = (s_token[i] * p.heads + head0 + hl) * p.s_real + r;
+            const bool live = r < p.s_real;
+            const float pw = s_weight[i];
+            if (s_slot[i] >= 0) {
+                const float q = live ? to_f32(p.q[at]) : 0.f;
+                s_rows[i][hl][0][r] = p.scale * round_to<T>(q * pw);
+            } else {
+                const float k = live ? to_f32(p.k[at]) : 0.f;
+                const float g = live ? p.g[at] : 0.f;
+                const float b = live ? to_f32(p.b[at]) : 0.f;
+                s_rows[i][hl][0][r] = __expf(p.routed_decay ? g * pw : g);
+                s_rows[i][hl][1][r] = k;
+                s_rows[i][hl][2][r] = round_to<T>(b * pw) * k;
+            }
+        }
+        __syncthreads();
+        // (2) one lane per (head, row): fold s at the stage start, then scan
+        if (scanner) {
+            s_fold[scan_head][scan_row] = sc;
+            float run = 1.f;
+            bool low = false;
+#pragma unroll 1
+            for (int i = 0; i < n; ++i) {
+                if (s_slot[i] < 0) {
+                    run *= s_rows[i][scan_head][0][scan_row];
+                    low |= !(run >= kScaleFloor);  // NaN also takes the eager form
+                }
+            }
+            if (low) s_eager = 1;  // benign race: every writer stores 1
+        }
+        __syncthreads();
+        // LDS values every lane reads alike are made wave-uniform explicitly, so
+        // the branches on them are scalar and the state is never copied
+        const bool eager = __builtin_amdgcn_readfirstlane(s_eager) != 0;
+        if (scanner) {
+            sc = 1.f;
+#pragma unroll 1
+            for (int i = 0; i < n; ++i) {
+                float *row = &s_rows[i][scan_head][0][scan_row];
+                if (s_slot[i] >= 0) {
+                    row[0] *= sc;  // gamma
+                } else if (!eager) {
+                    const float d = row[0], k = row[S], a = row[2 * S];
+                    sc *= d;
+                    row[0] = a * sc;  // alpha
+                    row[S] = k / sc;  // beta
+                } else {
+                    // eager: alpha = a * decay, beta = k, and the decay itself
+                    const float d = row[0], a = row[2 * S];
+                    row[0] = a * d;
+                    row[2 * S] = d;
+                }
+            }
+        }
+        __syncthreads();
+
+        // (3) the value columns.  Fold s into Mh: the true state at the stage
+        // start, which is a rounding/snapshot point when the offset is > 0.
+#pragma unroll
+        for (int r = 0; r < S; ++r) {
+            const float f = s_fold[lh][r];
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) h[r][c] *= f;
+        }
+        if (base > start) {
+            if (rounding) {
+#pragma unroll
+                for (int r = 0; r < S; ++r)
+#pragma unroll
+                    for (int c = 0; c < CPL; ++c) h[r][c] = round_bf16(h[r][c]);
+            }
+            // snapshot of the state before event `base` (see routed_forward_kernel)
+            if (p.snap) {
+                const int64_t slot = base / p.snap_interval - 1;
+                store_state<S, CPL>(p.snap, p.snap_dtype, ((slot * p.heads + head) * p.s_real) * p.width + col0,
+                                    p.width, p.s_real, h);
+            }
+        }
+        // Events in packed order, as runs: the reads before each write, then
+        // the write, so the state is updated exactly once per iteration and
+        // never merged from branches.  The next write's v and w are
+        // prefetched as raw rows.
+        auto read_event = [&](int i) {
+            const int64_t slot = uniform_i64(s_slot[i]);
+            const float *row = &s_rows[i][lh][0][0];
+            float gamma[S];
+#pragma unroll
+            for (int r = 0; r < S; ++r) gamma[r] = row[r];
+            float z[CPL];
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+                float acc = 0.f;
+#pragma unroll
+                for (int r = 0; r < S; ++r) acc = fmaf(gamma[r], h[r][c], acc);
+                z[c] = acc;
+            }
+            store_row<CPL>(p.zbuf + (slot * p.heads + head) * p.width + col0, z);
+        };
+        auto fetch = [&](int i, RawCols<T, CPL> &vv, RawCols<T, CPL> &ww) {
+            const int64_t row = uniform_i64(s_token[i]) * p.heads + head;
+            vv.load(p.v + row * p.width + col0);
+            ww.load(p.w + row * p.width + col0);
+        };
+        const int nw = __builtin_amdgcn_readfirstlane(s_nw);
+        // One loop nest per write form, so the state is carried through a
+        // single update form and only merged once per stage.
+        auto run = [&](auto eager_form) {
+            constexpr bool kEager = decltype(eager_form)::value;
+            RawCols<T, CPL> vn, wn;
+            if (nw > 0) fetch(__builtin_amdgcn_readfirstlane(s_wpos[0]), vn, wn);
+            int i = 0;
+#pragma unroll 1
+            for (int wk = 0; wk < nw; ++wk) {
+                const int wi_ = __builtin_amdgcn_readfirstlane(s_wpos[wk]);
+                const RawCols<T, CPL> vc = vn, wc = wn;
+                if (wk + 1 < nw) fetch(__builtin_amdgcn_readfirstlane(s_wpos[wk + 1]), vn, wn);
+#pragma unroll 1
+                for (; i < wi_; ++i) read_event(i);
+                i = wi_ + 1;
+                const float *row = &s_rows[wi_][lh][0][0];
+                const float pw = s_weight[wi_];
+                float alpha[S], beta[S], decay[S];
+#pragma unroll
+                for (int r = 0; r < S; ++r) {
+                    alpha[r] = row[r];
+                    beta[r] = row[S + r];
+                    if constexpr (kEager) decay[r] = row[2 * S + r];
+                }
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) {
+                    float erase = 0.f;
+#pragma unroll
+                    for (int r = 0; r < S; ++r) erase = fmaf(alpha[r], h[r][c], erase);
+                    const float u = round_to<T>(wc.get(c) * pw) * vc.get(c) - erase;
+#pragma unroll
+                    for (int r = 0; r < S; ++r) {
+                        if constexpr (kEager)
+                            h[r][c] = fmaf(decay[r], h[r][c], beta[r] * u);  // M' = d M + k u
+                        else
+                            h[r][c] = fmaf(beta[r], u, h[r][c]);  // Mh' = Mh + (k / s') u
+                    }
+                }
+            }
+#pragma unroll 1
+            for (; i < n; ++i) read_event(i);
+        };
+        if (eager)
+            run(std::true_type{});
+        else
+            run(std::false_type{});
+    }
+    __syncthreads();
+    if (scanner) s_fold[scan_head][scan_row] = sc;
+    __syncthreads();
+    if (p.final_state) {
+#pragma unroll
+        for (int r = 0; r < S; ++r) {
+            const float f = s_fold[lh][r];
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) h[r][c] *= f;
+        }
+        const int64_t final_offset = bidx * (int64_t(p.banks) * p.heads * p.s_real * p.width) + state_offset;
+        store_state<S, CPL>(p.final_state, p.final_dtype, final_offset, p.width, p.s_real, h);
+    }
+}
+
 // y[token, :] = fold over the token's reads in increasing bank id of
 // bf(total + z).  One workgroup per token; a thread owns CPL columns.
 template <typename T, int CPL>
@@ -261,7 +573,7 @@ __global__ __launch_bounds__(256) void zero_fill_kernel(T *__restrict__ out, int
     if (i < count) out[i] = from_f32<T>(0.f);
 }
 
-template <typename T, int S, int CPL>
+template <typename T, int S, int CPL, bool kLazy = false>
 int launch_forward(const bdm_forward_args &a, T *zbuf, hipStream_t stream) {
     if (a.head_width / CPL > 256)
         return fail(BDM_ERR_UNSUPPORTED, "forward: head_width %d needs more than 256 lanes", a.head_width);
@@ -290,6 +602,7 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, hipStream_t stream) {
     p.kr = a.read_banks;
     p.lanes_per_head = a.head_width / CPL;
     p.heads_per_block = 256 / p.lanes_per_head;
+    if (kLazy && p.heads_per_block > kLazyHeads) p.heads_per_block = kLazyHeads;
     if (p.heads_per_block > a.heads) p.heads_per_block = a.heads;
     p.round_interval = a.round_interval;
     p.routed_decay = a.routed_decay;
@@ -303,8 +616,13 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, hipStream_t stream) {
     p.xcd_remap = (nseg % 8 == 0) ? 1 : 0;
     const int threads = ((p.heads_per_block * p.lanes_per_head + kWave - 1) / kWave) * kWave;
     const dim3 grid(unsigned(nseg), unsigned((a.heads + p.heads_per_block - 1) / p.heads_per_block));
-    routed_forward_kernel<T, S, CPL><<<grid, threads, 0, stream>>>(p);
-    if (int rc = check_launch("routed_forward_kernel")) return rc;
+    if constexpr (kLazy) {
+        lazy_forward_kernel<T, CPL><<<grid, threads, 0, stream>>>(p);
+        if (int rc = check_launch("lazy_forward_kernel")) return rc;
+    } else {
+        routed_forward_kernel<T, S, CPL><<<grid, threads, 0, stream>>>(p);
+        if (int rc = check_launch("routed_forward_kernel")) return rc;
+    }
 
     const int row_width = a.heads * a.head_width;
     const int64_t nt = a.batch * a.time;
@@ -325,6 +643,9 @@ int dispatch_forward(const bdm_forward_args &a, T *zbuf, hipStream_t stream) {
     // batch stride that keeps them aligned.
     const bool vec = a.initial_batch_stride % 8 == 0;
     if (a.bank_size <= 8) {
+        const int fold = a.round_interval > 0 ? a.round_interval : (a.snapshots ? a.snapshot_interval : kLazyStage);
+        if (vec && a.head_width % 4 == 0 && a.head_width / 4 <= 64 && fold == kLazyStage)
+            return launch_forward<T, 8, 4, true>(a, zbuf, stream);
         if (vec && a.head_width % 8 == 0) return launch_forward<T, 8, 8>(a, zbuf, stream);
         return launch_forward<T, 8, 1>(a, zbuf, stream);
     }

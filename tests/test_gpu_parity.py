@@ -139,6 +139,43 @@ def test_forward_matches_oracle(device, case):
     assert rel_err(final, ref_final) < TOL, rel_err(final, ref_final)
 
 
+@pytest.mark.parametrize('decay', ['strong', 'mixed', 'none'])
+@pytest.mark.parametrize('state_dtype', [torch.bfloat16, torch.float32])
+def test_forward_decay_extremes_match_oracle(device, decay, state_dtype):
+    """The forward keeps the decay of a stage lazily in a per-row scale and
+    switches a stage to explicit decay when that scale would underflow:
+    'strong' (g down to -40: every stage explicit), 'mixed' (a few tokens with
+    g down to -60 among mild ones) and 'none' (g = 0, the scale stays 1) all
+    match the oracle, with final states."""
+    from bdm_amd import ops
+    gen = torch.Generator().manual_seed({'strong': 1, 'mixed': 2, 'none': 3}[decay])
+    batch, time, heads, s, v, j, kk = 2, 96, 2, 8, 128, 8, 4
+    _, ww, wi = routes(batch, time, j, kk, gen)
+    _, rw, ri = routes(batch, time, j, kk, gen)
+    q, k, v_, g, b, w = controllers(batch, time, heads, s, v, gen)
+    if decay == 'strong':
+        g = -torch.rand(g.shape, generator=gen) * 40
+    elif decay == 'mixed':
+        spikes = torch.rand(batch, time, 1, 1, generator=gen) < 0.05
+        g = torch.where(spikes, -torch.rand(g.shape, generator=gen) * 60, g)
+    else:
+        g = torch.zeros_like(g)
+    state = initial_state(j, heads, s, v, gen)
+    interval = 16 if state_dtype == torch.bfloat16 else 0
+    ref, ref_final = oracle_reads(q, k, v_, g, b, w, wi, ww, ri, rw, state, j, routed_decay=True,
+                                  state_dtype=state_dtype, interval=16, return_final=True)
+    dev = [t.to(device) for t in (q, k, v_, g, b, w, wi, ww, ri, rw, state)]
+    announce('forward decay', decay, state_dtype)
+    meta = ops.dispatch_build(dev[6], dev[8], j)
+    final = torch.empty(batch, j, heads, s, v, device=device, dtype=torch.float32)
+    y = ops.routed_forward(*dev[:10], dev[10], meta, bank_count=j, scale=s ** -0.5, routed_decay=True,
+                           round_interval=interval, final_state=final)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y).all() and torch.isfinite(final).all()
+    assert rel_err(y, ref) < TOL, rel_err(y, ref)
+    assert rel_err(final, ref_final) < TOL, rel_err(final, ref_final)
+
+
 def test_forward_per_head_layout_and_determinism(device):
     from bdm_amd import bank_training
     gen = torch.Generator().manual_seed(11)
