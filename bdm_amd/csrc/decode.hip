@@ -6,13 +6,15 @@
 // any head count and bank size <= 32.
 //
 // One workgroup per (sequence, head).  Lane group j (head_width / CPL lanes)
-// owns write slot j and read slot j.  Everything a step touches in HBM is
-// requested up front: the write banks' states and the states of read banks
-// that are not also written this step.  Writes are applied and stored (rounded
+// owns write slot j and read slot j.  A step makes two dependent trips to HBM:
+// first the bank indices and controller rows (all independent of a bank id),
+// then every bank state the step touches — the write banks and the read banks
+// that are not also written — requested at once.  Writes are applied and stored (rounded
 // to the state dtype), and also kept in LDS, so a read of a bank written by the
 // same token sees the stored value without another trip to HBM.  The reads are
 // then combined in increasing bank id with a rounding after every add.
 #include "bdm_common.h"
+#include "recurrence_ops.h"
 
 namespace bdm {
 namespace {
@@ -40,55 +42,89 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeParams<T> p) {
     // smem layout: written states [kw][S][width], read values [kr][width]
     float *written = smem;
     float *reads = smem + p.kw * S * p.width;
-    __shared__ int64_t s_wbank[kMaxSlots], s_rbank[kMaxSlots];
     __shared__ int s_rank_slot[kMaxSlots];
 
     const int64_t seq = blockIdx.x / p.heads;
     const int head = blockIdx.x % p.heads;
     const int slot = threadIdx.x / p.lanes_per_slot;
     const int col0 = (threadIdx.x % p.lanes_per_slot) * CPL;
-    if (int(threadIdx.x) < p.kw) {
-        int64_t bank = p.wi[seq * p.kw + threadIdx.x];
-        s_wbank[threadIdx.x] = bank < 0 ? 0 : (bank >= p.banks ? p.banks - 1 : bank);
-    }
-    if (int(threadIdx.x) < p.kr) {
-        int64_t bank = p.ri[seq * p.kr + threadIdx.x];
-        s_rbank[threadIdx.x] = bank < 0 ? 0 : (bank >= p.banks ? p.banks - 1 : bank);
-    }
-    __syncthreads();
-    if (int(threadIdx.x) < p.kr) {
-        const int64_t mine = s_rbank[threadIdx.x];
-        int rank = 0;
-        for (int j = 0; j < p.kr; ++j) {
-            const int64_t other = s_rbank[j];
-            rank += (other < mine) || (other == mine && j < int(threadIdx.x));
-        }
-        s_rank_slot[rank] = threadIdx.x;
-    }
-
-    const int64_t bank_stride = int64_t(p.heads) * p.s_real * p.width;  // elements per bank
-    const int64_t seq_base = seq * p.banks * bank_stride + int64_t(head) * p.s_real * p.width + col0;
     const int64_t row = seq * p.heads + head;
-
-    // ---- issue every HBM read of the step
-    float hw[S][CPL], hr[S][CPL];
     const bool has_write = slot < p.kw;
     const bool has_read = slot < p.kr;
+
+    // ---- round trip 1: everything that does not depend on a bank index.  The
+    // per-token values are loaded once for the workgroup, one element per lane
+    // of the first wave(s), and shared through LDS (a conditional scalar load
+    // per value would serialise them).
+    __shared__ int64_t s_wbank[kMaxSlots], s_rbank[kMaxSlots];
+    __shared__ float s_pw[kMaxSlots], s_pr[kMaxSlots];
+    __shared__ float s_ctrl[4][32];  // k, g, b, q rows (S <= 32)
+    {
+        const int nk = p.kw + p.kr;
+        for (int t = threadIdx.x; t < nk + 4 * S; t += blockDim.x) {
+            if (t < p.kw) {
+                const int64_t bank = p.wi[seq * p.kw + t];
+                s_wbank[t] = bank < 0 ? 0 : (bank >= p.banks ? p.banks - 1 : bank);
+                s_pw[t] = to_f32(p.ww[seq * p.kw + t]);
+            } else if (t < nk) {
+                const int j = t - p.kw;
+                const int64_t bank = p.ri[seq * p.kr + j];
+                s_rbank[j] = bank < 0 ? 0 : (bank >= p.banks ? p.banks - 1 : bank);
+                s_pr[j] = to_f32(p.rw[seq * p.kr + j]);
+            } else {
+                const int e = t - nk, which = e / S, r = e % S;
+                float x = 0.f;
+                if (r < p.s_real) {
+                    const int64_t at = row * p.s_real + r;
+                    x = which == 0 ? to_f32(p.k[at])
+                                   : which == 1 ? p.g[at] : which == 2 ? to_f32(p.b[at]) : to_f32(p.q[at]);
+                }
+                s_ctrl[which][r] = x;
+            }
+        }
+    }
+    float vv[CPL], wv[CPL];
+    load_row<CPL>(p.v + row * p.width + col0, vv);
+    load_row<CPL>(p.w + row * p.width + col0, wv);
+    __syncthreads();
+    float kk[S], gg[S], bb[S], qq[S];
+#pragma unroll
+    for (int r = 0; r < S; ++r) {
+        kk[r] = s_ctrl[0][r];
+        gg[r] = s_ctrl[1][r];
+        bb[r] = s_ctrl[2][r];
+        qq[r] = s_ctrl[3][r];
+    }
+    const float pw = has_write ? s_pw[slot] : 0.f;
+    const float pr = has_read ? s_pr[slot] : 0.f;
+    // this lane group's write bank and read bank; a read of a bank written by
+    // the same token is served from the stored post-write value in LDS
+    const int64_t my_w = has_write ? s_wbank[slot] : 0;
+    const int64_t my_r = has_read ? s_rbank[slot] : 0;
     int read_from_write = -1;
     if (has_read) {
         for (int j = 0; j < p.kw; ++j)
-            if (s_wbank[j] == s_rbank[slot]) read_from_write = j;
+            if (s_wbank[j] == my_r) read_from_write = j;
     }
-#pragma unroll
-    for (int r = 0; r < S; ++r) {
-#pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-            hw[r][c] = 0.f;
-            hr[r][c] = 0.f;
-        }
+    // thread t < KR ranks read slot t by (bank id, slot)
+    if (int(threadIdx.x) < p.kr) {
+        const int t = threadIdx.x;
+        const int64_t mine = s_rbank[t];
+        int rank = 0;
+        for (int j = 0; j < p.kr; ++j) rank += (s_rbank[j] < mine) || (s_rbank[j] == mine && j < t);
+        s_rank_slot[rank] = t;
     }
+
+    // ---- round trip 2: the bank states this step touches
+    const int64_t bank_stride = int64_t(p.heads) * p.s_real * p.width;  // elements per bank
+    const int64_t seq_base = seq * p.banks * bank_stride + int64_t(head) * p.s_real * p.width + col0;
+    float hw[S][CPL], hr[S][CPL];
+#pragma unroll
+    for (int r = 0; r < S; ++r)
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) hw[r][c] = hr[r][c] = 0.f;
     if (has_write) {
-        const int64_t base = seq_base + s_wbank[slot] * bank_stride;
+        const int64_t base = seq_base + my_w * bank_stride;
 #pragma unroll
         for (int r = 0; r < S; ++r) {
             if (r >= p.s_real) continue;
@@ -99,7 +135,7 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeParams<T> p) {
         }
     }
     if (has_read && read_from_write < 0) {
-        const int64_t base = seq_base + s_rbank[slot] * bank_stride;
+        const int64_t base = seq_base + my_r * bank_stride;
 #pragma unroll
         for (int r = 0; r < S; ++r) {
             if (r >= p.s_real) continue;
@@ -109,41 +145,16 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeParams<T> p) {
                 load_row<CPL>(static_cast<const float *>(p.state) + base + int64_t(r) * p.width, hr[r]);
         }
     }
-    float kk[S], gg[S], bb[S], qq[S];
-#pragma unroll
-    for (int r = 0; r < S; ++r) {
-        const bool live = r < p.s_real;
-        kk[r] = live ? to_f32(p.k[row * p.s_real + r]) : 0.f;
-        gg[r] = live ? p.g[row * p.s_real + r] : 0.f;
-        bb[r] = live ? to_f32(p.b[row * p.s_real + r]) : 0.f;
-        qq[r] = live ? to_f32(p.q[row * p.s_real + r]) : 0.f;
-    }
-    float vv[CPL], wv[CPL];
-    load_row<CPL>(p.v + row * p.width + col0, vv);
-    load_row<CPL>(p.w + row * p.width + col0, wv);
 
-    // ---- writes (inference.py:21-34 with role_bank_kernel.py:40-43)
+    // ---- writes (inference.py:21-34 with the write rule of role_bank_kernel.py:40-43)
     if (has_write) {
-        const float pw = to_f32(p.ww[seq * p.kw + slot]);
-        float decay[S], a[S];
+        WriteRows<S> rows;
+        prepare_write_rows<T, S>(kk, gg, bb, pw, p.routed_decay, rows);
+        float ew[CPL];
 #pragma unroll
-        for (int r = 0; r < S; ++r) {
-            decay[r] = __expf(p.routed_decay ? gg[r] * pw : gg[r]);
-            a[r] = round_to<T>(bb[r] * pw) * kk[r];
-        }
-#pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-            float erase = 0.f;
-#pragma unroll
-            for (int r = 0; r < S; ++r) {
-                hw[r][c] *= decay[r];
-                erase = fmaf(a[r], hw[r][c], erase);
-            }
-            const float u = round_to<T>(wv[c] * pw) * vv[c] - erase;
-#pragma unroll
-            for (int r = 0; r < S; ++r) hw[r][c] = fmaf(kk[r], u, hw[r][c]);
-        }
-        const int64_t base = seq_base + s_wbank[slot] * bank_stride;
+        for (int c = 0; c < CPL; ++c) ew[c] = round_to<T>(wv[c] * pw);
+        apply_write<S, CPL>(hw, rows, ew, vv);
+        const int64_t base = seq_base + my_w * bank_stride;
 #pragma unroll
         for (int r = 0; r < S; ++r) {
             if (r >= p.s_real) continue;
@@ -169,7 +180,6 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeParams<T> p) {
                 for (int c = 0; c < CPL; ++c)
                     hr[r][c] = r < p.s_real ? written[(read_from_write * S + r) * p.width + col0 + c] : 0.f;
         }
-        const float pr = to_f32(p.rw[seq * p.kr + slot]);
         float qr[S];
 #pragma unroll
         for (int r = 0; r < S; ++r) qr[r] = round_to<T>(qq[r] * pr);

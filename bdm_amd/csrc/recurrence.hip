@@ -299,6 +299,11 @@ constexpr int kLazyStage = 16;
 constexpr int kLazyHeads = 8;  // heads per workgroup
 constexpr float kScaleFloor = 0x1p-32f;
 
+// Writes whose v, w rows are in flight.  Measured on C2: deeper prefetch (2,
+// 3) or 8 columns per lane at 2 waves/SIMD were slower than this 1-deep
+// prefetch with 4 columns per lane at 4 waves/SIMD (128 VGPRs).
+constexpr int kPrefetch = 1;
+
 template <typename T, int CPL>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void lazy_forward_kernel(
     ForwardParams<T> p) {
@@ -476,14 +481,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         // single update form and only merged once per stage.
         auto run = [&](auto eager_form) {
             constexpr bool kEager = decltype(eager_form)::value;
-            RawCols<T, CPL> vn, wn;
-            if (nw > 0) fetch(__builtin_amdgcn_readfirstlane(s_wpos[0]), vn, wn);
+            // v and w of the next kPrefetch writes are in flight while a write
+            // and its preceding reads run
+            RawCols<T, CPL> vq[kPrefetch], wq[kPrefetch];
+#pragma unroll
+            for (int d = 0; d < kPrefetch; ++d)
+                if (d < nw) fetch(__builtin_amdgcn_readfirstlane(s_wpos[d]), vq[d], wq[d]);
             int i = 0;
 #pragma unroll 1
             for (int wk = 0; wk < nw; ++wk) {
                 const int wi_ = __builtin_amdgcn_readfirstlane(s_wpos[wk]);
-                const RawCols<T, CPL> vc = vn, wc = wn;
-                if (wk + 1 < nw) fetch(__builtin_amdgcn_readfirstlane(s_wpos[wk + 1]), vn, wn);
+                const RawCols<T, CPL> vc = vq[0], wc = wq[0];
+#pragma unroll
+                for (int d = 0; d + 1 < kPrefetch; ++d) {
+                    vq[d] = vq[d + 1];
+                    wq[d] = wq[d + 1];
+                }
+                if (wk + kPrefetch < nw)
+                    fetch(__builtin_amdgcn_readfirstlane(s_wpos[wk + kPrefetch]), vq[kPrefetch - 1], wq[kPrefetch - 1]);
 #pragma unroll 1
                 for (; i < wi_; ++i) read_event(i);
                 i = wi_ + 1;
@@ -644,8 +659,9 @@ int dispatch_forward(const bdm_forward_args &a, T *zbuf, hipStream_t stream) {
     const bool vec = a.initial_batch_stride % 8 == 0;
     if (a.bank_size <= 8) {
         const int fold = a.round_interval > 0 ? a.round_interval : (a.snapshots ? a.snapshot_interval : kLazyStage);
-        if (vec && a.head_width % 4 == 0 && a.head_width / 4 <= 64 && fold == kLazyStage)
-            return launch_forward<T, 8, 4, true>(a, zbuf, stream);
+        constexpr int lc = 4;  // value columns per lane of the lazy kernel
+        if (vec && a.head_width % lc == 0 && a.head_width / lc <= 64 && fold == kLazyStage)
+            return launch_forward<T, 8, lc, true>(a, zbuf, stream);
         if (vec && a.head_width % 8 == 0) return launch_forward<T, 8, 8>(a, zbuf, stream);
         return launch_forward<T, 8, 1>(a, zbuf, stream);
     }

@@ -177,9 +177,21 @@ def decode_bench(layer, device, steps, seed=1):
         eager_sec, _ = timed(lambda: [launch(i) for i in range(steps)], 1, 0)
         # full step: controllers, routes, decode kernel and output interface
         sec, _ = timed(lambda: [layer.step(xs[i], state) for i in range(steps)], 1, 1)
-    state_bytes = batch * (2 * cfg.selected_banks + cfg.selected_banks) * cfg.num_heads * cfg.bank_size * \
-        cfg.head_value_width * 2
+    bank_bytes = cfg.num_heads * cfg.bank_size * cfg.head_value_width * 2
+    # BASELINE's figure: every step reads and writes KW banks and reads KR banks
+    state_bytes = batch * (2 * cfg.selected_banks + cfg.selected_banks) * bank_bytes
+    # what the kernel must move: reads of banks written by the same token come
+    # from the written values (at random init the read and write routes of a
+    # token coincide, the router residuals being zero)
+    touched = 0
+    for i in range(steps):
+        wi, ri = pre[i][6].cpu(), pre[i][8].cpu()
+        extra = sum(len(set(ri[b].tolist()) - set(wi[b].tolist())) for b in range(batch))
+        touched += (2 * wi.numel() + extra) * bank_bytes
+    touched /= steps
     return {'batch': batch, 'steps': steps, 'kernel_us_per_step': round(kernel_us, 3),
+            'touched_state_bytes_per_step': round(touched),
+            'touched_state_GBps': round(touched / (kernel_us * 1e-6) / 1e9, 1),
             'eager_launch_us_per_step': round(eager_sec * 1e6 / steps, 2),
             'full_step_us_eager': round(sec * 1e6 / steps, 2), 'state_bytes_per_step': state_bytes,
             'state_GBps': round(state_bytes / (kernel_us * 1e-6) / 1e9, 1),
