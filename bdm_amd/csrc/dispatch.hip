@@ -11,9 +11,9 @@
 //   1. tile_count: LDS bit-masks mask[bank] with bit 2*t_local + is_read set
 //      for every event of the tile (64-bit LDS atomic OR; order-independent,
 //      so deterministic).  popcount(mask[bank]) is the tile's bucket count.
-//   2. scan: per batch, an exclusive scan over tiles for every bank (a tile's
-//      base inside its segment), then an exclusive scan over banks (segment
-//      starts).  Batch b's segments start at b*T*(KW+KR): every token adds
+//   2. scan: an exclusive scan over tiles for every (batch, bank) — a tile's
+//      base inside its segment — in parallel over banks and tile ranges, then
+//      per batch an exclusive scan over banks (segment starts).  Batch b's segments start at b*T*(KW+KR): every token adds
 //      exactly KW+KR events to its own batch.
 //   3. scatter: rebuild the masks; an event's rank inside its tile-bucket is
 //      popcount(mask[bank] & below(bit)), i.e. the number of earlier
@@ -73,30 +73,53 @@ __global__ __launch_bounds__(512) void dispatch_tile_count(const int64_t *__rest
     for (int x = threadIdx.x; x < g.banks; x += blockDim.x) out[x] = __popcll(masks[x]);
 }
 
-// One workgroup per batch.  tile_counts becomes each tile's offset inside its
-// segment; cu_seqlens receives the segment starts.
-__global__ __launch_bounds__(1024) void dispatch_scan(DispatchGeometry g, int32_t *__restrict__ tile_counts,
-                                                      int64_t *__restrict__ cu_seqlens) {
-    extern __shared__ int32_t totals[];  // [banks]
-    __shared__ int32_t wave_sums[1024 / kWave];
+// Per (batch, 64-bank chunk): tile_counts[b][t][bank] becomes each tile's
+// offset inside its segment, and totals[b][bank] the segment length.  The
+// tiles are split over the four waves of the workgroup; a wave first sums its
+// range (loads in flight together), the waves' sums are scanned through LDS,
+// then each wave rewrites its range as running offsets.
+__global__ __launch_bounds__(256) void dispatch_tile_scan(DispatchGeometry g, int32_t *__restrict__ tile_counts,
+                                                          int32_t *__restrict__ totals) {
+    __shared__ int32_t part[4][kWave];
     const int b = blockIdx.x;
-    int32_t *base = tile_counts + int64_t(b) * g.tiles * g.banks;
-    for (int x = threadIdx.x; x < g.banks; x += blockDim.x) {
-        int32_t running = 0;
-        for (int t = 0; t < g.tiles; ++t) {
-            const int32_t c = base[int64_t(t) * g.banks + x];
-            base[int64_t(t) * g.banks + x] = running;
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+    const int bank = blockIdx.y * kWave + lane;
+    const bool live = bank < g.banks;
+    const int per = (g.tiles + 3) / 4;
+    const int t0 = min(g.tiles, wave * per), t1 = min(g.tiles, t0 + per);
+    int32_t *base = tile_counts + int64_t(b) * g.tiles * g.banks + bank;
+    int32_t sum = 0;
+    if (live) {
+#pragma unroll 8
+        for (int t = t0; t < t1; ++t) sum += base[int64_t(t) * g.banks];
+    }
+    part[wave][lane] = sum;
+    __syncthreads();
+    int32_t running = 0;
+    for (int w = 0; w < wave; ++w) running += part[w][lane];
+    if (live) {
+        for (int t = t0; t < t1; ++t) {
+            const int32_t c = base[int64_t(t) * g.banks];
+            base[int64_t(t) * g.banks] = running;
             running += c;
         }
-        totals[x] = running;
+        if (wave == 3) totals[int64_t(b) * g.banks + bank] = running;
     }
-    __syncthreads();
-    // Exclusive scan of totals[0:banks]: each thread owns a contiguous chunk.
+}
+
+// One workgroup per batch: exclusive scan of the segment lengths over banks
+// gives the segment starts.  Batch b's segments start at b*T*(KW+KR): every
+// token adds exactly KW+KR events to its own batch.
+__global__ __launch_bounds__(1024) void dispatch_bank_scan(DispatchGeometry g, const int32_t *__restrict__ totals,
+                                                           int64_t *__restrict__ cu_seqlens) {
+    __shared__ int32_t wave_sums[1024 / kWave];
+    const int b = blockIdx.x;
+    const int32_t *tot = totals + int64_t(b) * g.banks;
+    // each thread owns a contiguous chunk of banks
     const int per = (g.banks + blockDim.x - 1) / blockDim.x;
     const int lo = min(g.banks, int(threadIdx.x) * per), hi = min(g.banks, lo + per);
     int32_t local = 0;
-    for (int x = lo; x < hi; ++x) local += totals[x];
-    // inclusive wave scan of `local`
+    for (int x = lo; x < hi; ++x) local += tot[x];
     const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
     int32_t incl = local;
 #pragma unroll
@@ -106,19 +129,13 @@ __global__ __launch_bounds__(1024) void dispatch_scan(DispatchGeometry g, int32_
     }
     if (lane == kWave - 1) wave_sums[wave] = incl;
     __syncthreads();
-    int32_t wave_offset = 0;
-    for (int w = 0; w < wave; ++w) wave_offset += wave_sums[w];
-    int32_t running = wave_offset + incl - local;
-    __syncthreads();  // every thread has read its chunk of totals
-    for (int x = lo; x < hi; ++x) {
-        const int32_t c = totals[x];
-        totals[x] = running;
-        running += c;
-    }
-    __syncthreads();
+    int32_t running = incl - local;
+    for (int w = 0; w < wave; ++w) running += wave_sums[w];
     const int64_t batch_base = int64_t(b) * g.time * (g.kw + g.kr);
-    for (int x = threadIdx.x; x < g.banks; x += blockDim.x)
-        cu_seqlens[int64_t(b) * g.banks + x] = batch_base + totals[x];
+    for (int x = lo; x < hi; ++x) {
+        cu_seqlens[int64_t(b) * g.banks + x] = batch_base + running;
+        running += tot[x];
+    }
     if (b == g.batch - 1 && threadIdx.x == 0) cu_seqlens[g.batch * g.banks] = g.nt * (g.kw + g.kr);
 }
 
@@ -162,7 +179,8 @@ static int64_t tiles_per_batch(int64_t time) { return (time + kTileTokens - 1) /
 
 extern "C" size_t bdm_dispatch_workspace_size(int64_t batch, int64_t time, int32_t bank_count) {
     if (batch <= 0 || time <= 0 || bank_count <= 0) return 0;
-    return size_t(batch) * size_t(tiles_per_batch(time)) * size_t(bank_count) * sizeof(int32_t);
+    // per-tile bucket counts, then per-segment totals
+    return size_t(batch) * (size_t(tiles_per_batch(time)) + 1) * size_t(bank_count) * sizeof(int32_t);
 }
 
 extern "C" int bdm_dispatch_build(const int64_t *write_indices, const int64_t *read_indices, int64_t batch,
@@ -193,8 +211,12 @@ extern "C" int bdm_dispatch_build(const int64_t *write_indices, const int64_t *r
     const dim3 tiles(unsigned(g.tiles), unsigned(batch));
     dispatch_tile_count<<<tiles, 512, mask_bytes, s>>>(write_indices, read_indices, g, tile_counts, status);
     if (int rc = check_launch("dispatch_tile_count")) return rc;
-    dispatch_scan<<<unsigned(batch), 1024, size_t(bank_count) * sizeof(int32_t), s>>>(g, tile_counts, cu_seqlens);
-    if (int rc = check_launch("dispatch_scan")) return rc;
+    int32_t *totals = tile_counts + int64_t(batch) * g.tiles * bank_count;
+    dispatch_tile_scan<<<dim3(unsigned(batch), unsigned((bank_count + kWave - 1) / kWave)), 256, 0, s>>>(
+        g, tile_counts, totals);
+    if (int rc = check_launch("dispatch_tile_scan")) return rc;
+    dispatch_bank_scan<<<unsigned(batch), 1024, 0, s>>>(g, totals, cu_seqlens);
+    if (int rc = check_launch("dispatch_bank_scan")) return rc;
     dispatch_scatter<<<tiles, 512, mask_bytes, s>>>(write_indices, read_indices, g, tile_counts, cu_seqlens,
                                                     order, inverse, tokens, status);
     return check_launch("dispatch_scatter");

@@ -555,13 +555,16 @@ template <typename T, int CPL>
 __global__ __launch_bounds__(256) void ordered_combine_kernel(const T *__restrict__ zbuf,
                                                               const int64_t *__restrict__ read_indices,
                                                               T *__restrict__ y, int kr, int row_width) {
+    __shared__ int64_t s_idx[32];
     __shared__ int s_rank_slot[32];
     const int64_t token = blockIdx.x;
+    if (int(threadIdx.x) < kr) s_idx[threadIdx.x] = read_indices[token * kr + threadIdx.x];
+    __syncthreads();
     if (int(threadIdx.x) < kr) {
-        const int64_t mine = read_indices[token * kr + threadIdx.x];
+        const int64_t mine = s_idx[threadIdx.x];
         int rank = 0;
         for (int j = 0; j < kr; ++j) {
-            const int64_t other = read_indices[token * kr + j];
+            const int64_t other = s_idx[j];
             rank += (other < mine) || (other == mine && j < int(threadIdx.x));
         }
         s_rank_slot[rank] = threadIdx.x;
@@ -642,9 +645,17 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, hipStream_t stream) {
     const int row_width = a.heads * a.head_width;
     const int64_t nt = a.batch * a.time;
     if (a.read_banks > 0) {
-        const int cthreads = min(256, max(kWave, ((row_width / CPL + kWave - 1) / kWave) * kWave));
-        ordered_combine_kernel<T, CPL><<<unsigned(nt), cthreads, 0, stream>>>(
-            zbuf, a.read_indices, static_cast<T *>(a.output), a.read_banks, row_width);
+        // 16-byte rows where the layout allows (8 BF16 or 4 FP32 columns)
+        constexpr int CC = sizeof(T) == 2 ? 8 : 4;
+        if (row_width % CC == 0 && a.head_width % CC == 0) {
+            const int cthreads = min(256, max(kWave, ((row_width / CC + kWave - 1) / kWave) * kWave));
+            ordered_combine_kernel<T, CC><<<unsigned(nt), cthreads, 0, stream>>>(
+                zbuf, a.read_indices, static_cast<T *>(a.output), a.read_banks, row_width);
+        } else {
+            const int cthreads = min(256, max(kWave, ((row_width + kWave - 1) / kWave) * kWave));
+            ordered_combine_kernel<T, 1><<<unsigned(nt), cthreads, 0, stream>>>(
+                zbuf, a.read_indices, static_cast<T *>(a.output), a.read_banks, row_width);
+        }
     } else {
         const int64_t count = nt * row_width;
         zero_fill_kernel<T><<<unsigned((count + 255) / 256), 256, 0, stream>>>(static_cast<T *>(a.output), count);

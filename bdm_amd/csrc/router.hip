@@ -33,8 +33,11 @@ __device__ __forceinline__ void insert_sorted(float (&val)[N], int (&idx)[N], fl
     }
 }
 
+// Elements per 16-byte load of a score row.
+template <typename T> constexpr int kVec = 16 / int(sizeof(T));
+
 template <typename T, int SMAX>
-__global__ __launch_bounds__(256) void router_kernel(const T *__restrict__ scores, int64_t rows,
+__global__ __launch_bounds__(64) void router_kernel(const T *__restrict__ scores, int64_t rows,
                                                      int64_t stride, int j1, int j2, int selected,
                                                      T *__restrict__ weights,
                                                      int64_t *__restrict__ indices) {
@@ -51,8 +54,24 @@ __global__ __launch_bounds__(256) void router_kernel(const T *__restrict__ score
         fv[p] = sv[p] = -INFINITY;
         fi[p] = si[p] = INT32_MAX;
     }
-    for (int i = 0; i < j1; ++i) insert_sorted(fv, fi, to_f32(z[i]), i);
-    for (int i = 0; i < j2; ++i) insert_sorted(sv, si, to_f32(z[j1 + i]), i);
+    if ((stride * int64_t(sizeof(T))) % 16 == 0 && (j1 + j2) % kVec<T> == 0) {
+        // whole 16-byte chunks of the row
+        for (int i0 = 0; i0 < j1 + j2; i0 += kVec<T>) {
+            float chunk[kVec<T>];
+            load_row<kVec<T>>(z + i0, chunk);
+#pragma unroll
+            for (int e = 0; e < kVec<T>; ++e) {
+                const int i = i0 + e;
+                if (i < j1)
+                    insert_sorted(fv, fi, chunk[e], i);
+                else
+                    insert_sorted(sv, si, chunk[e], i - j1);
+            }
+        }
+    } else {
+        for (int i = 0; i < j1; ++i) insert_sorted(fv, fi, to_f32(z[i]), i);
+        for (int i = 0; i < j2; ++i) insert_sorted(sv, si, to_f32(z[j1 + i]), i);
+    }
 
     float pv[SMAX];
     int pi[SMAX];
@@ -104,7 +123,9 @@ __global__ __launch_bounds__(256) void router_kernel(const T *__restrict__ score
 template <typename T>
 int launch_router(const void *scores, int64_t rows, int64_t stride, int j1, int j2, int selected,
                   void *weights, int64_t *indices, hipStream_t stream) {
-    const dim3 block(256), grid(unsigned((rows + 255) / 256));
+    // 64 rows per workgroup: one row per lane, and enough workgroups to cover
+    // every CU at the benchmark sizes (32K rows -> 512 workgroups)
+    const dim3 block(64), grid(unsigned((rows + 63) / 64));
     if (selected <= 8) {
         router_kernel<T, 8><<<grid, block, 0, stream>>>(static_cast<const T *>(scores), rows, stride, j1,
                                                         j2, selected, static_cast<T *>(weights), indices);
@@ -130,7 +151,8 @@ extern "C" int bdm_router_select(const void *scores, int32_t score_dtype, int64_
     if (selected > 16) return fail(BDM_ERR_UNSUPPORTED, "router: selected=%d > 16 is not implemented", selected);
     if (rows == 0) return BDM_OK;
     if (!scores || !weights || !indices) return fail(BDM_ERR_INVALID, "router: null pointer");
-    if (rows > int64_t(INT32_MAX) * 128) return fail(BDM_ERR_UNSUPPORTED, "router: too many rows");
+    if (!aligned(scores, 16)) return fail(BDM_ERR_INVALID, "router: scores must be 16-byte aligned");
+    if (rows > int64_t(INT32_MAX) * 64) return fail(BDM_ERR_UNSUPPORTED, "router: too many rows");
     switch (score_dtype) {
         case BDM_BF16:
             return launch_router<bf16_t>(scores, rows, row_stride, factor_first, factor_second, selected, weights,

@@ -36,8 +36,8 @@ def test_library_exports_every_declared_symbol(lib):
 
 
 def test_workspace_sizes(lib):
-    # tiles of 32 tokens x banks x int32 per batch
-    assert lib.bdm_dispatch_workspace_size(8, 4096, 256) == 8 * 128 * 256 * 4
+    # (tiles of 32 tokens + one row of segment totals) x banks x int32 per batch
+    assert lib.bdm_dispatch_workspace_size(8, 4096, 256) == 8 * (128 + 1) * 256 * 4
     assert lib.bdm_dispatch_workspace_size(0, 4096, 256) == 0
     from bdm_amd import _lib
     args = _lib.ForwardArgs()
