@@ -36,6 +36,20 @@ template <typename T> __device__ __forceinline__ float round_to(float x) { retur
 
 __device__ __forceinline__ float round_bf16(float x) { return float((__bf16)x); }
 
+// Round two values to T with one conversion instruction (v_cvt_pk_bf16_f32
+// rounds both halves to nearest even) and widen them back.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+template <typename T> __device__ __forceinline__ void round_pair(float &a, float &b);
+template <> __device__ __forceinline__ void round_pair<float>(float &, float &) {}
+template <> __device__ __forceinline__ void round_pair<bf16_t>(float &a, float &b) {
+    const f32x2_t f = {a, b};
+    const bf16x2_t h = __builtin_convertvector(f, bf16x2_t);
+    const uint32_t bits = __builtin_bit_cast(uint32_t, h);
+    a = __uint_as_float(bits << 16);
+    b = __uint_as_float(bits & 0xffff0000u);
+}
+
 // Load `N` consecutive elements of T starting at p (16-byte aligned when the
 // caller's layout guarantees it) and widen them to FP32.
 template <int N>

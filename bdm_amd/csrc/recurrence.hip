@@ -370,9 +370,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
             s_wpos[nw] = n;
             s_nw = nw;
         }
-        // (1) per (event, head, row): exp(eg), k, a for a write; scale*bf(q*r) for a read
-        for (int e = tid; e < n * nheads * S; e += blockDim.x) {
-            const int i = e / (nheads * S), hl = (e / S) % nheads, r = e % S;
+        // (1) per (event, head, row): exp(eg), k, a for a write; scale*bf(q*r) for
+        // a read.  Thread t owns (head, row) = ((t % 64) / S, t % S) and visits
+        // every (blockDim / 64)-th event.
+        for (int i = tid / (kLazyHeads * S); i < n; i += blockDim.x / (kLazyHeads * S)) {
+            const int hl = (tid % (kLazyHeads * S)) / S, r = tid % S;
+            if (hl >= nheads) continue;
             const int64_t at = (s_token[i] * p.heads + head0 + hl) * p.s_real + r;
             const bool live = r < p.s_real;
             const float pw = s_weight[i];
@@ -511,12 +514,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
                     beta[r] = row[S + r];
                     if constexpr (kEager) decay[r] = row[2 * S + r];
                 }
+                // x = bf(w p) * v, rounded two columns per conversion
+                float x[CPL];
+#pragma unroll
+                for (int c = 0; c < CPL; c += 2) {
+                    float e0 = wc.get(c) * pw, e1 = wc.get(c + 1) * pw;
+                    round_pair<T>(e0, e1);
+                    x[c] = e0 * vc.get(c);
+                    x[c + 1] = e1 * vc.get(c + 1);
+                }
 #pragma unroll
                 for (int c = 0; c < CPL; ++c) {
                     float erase = 0.f;
 #pragma unroll
                     for (int r = 0; r < S; ++r) erase = fmaf(alpha[r], h[r][c], erase);
-                    const float u = round_to<T>(wc.get(c) * pw) * vc.get(c) - erase;
+                    const float u = x[c] - erase;
 #pragma unroll
                     for (int r = 0; r < S; ++r) {
                         if constexpr (kEager)
