@@ -198,6 +198,66 @@ def decode_bench(layer, device, steps, seed=1):
             'state_frac_of_hbm_peak': round(state_bytes / (kernel_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
 
 
+def c4_forward(device, steps=3):
+    """C4: batch 4, T8192, J2048 (32x64), Zipf s=1.1 bias on the factor scores,
+    hot-path prefill forward (router x2, dispatch, recurrence + combine, final
+    state).  Reports tokens/s and the segment-length skew."""
+    import torch
+    from bdm_amd import BSDMConfig, BankedDeltaMemory, ops
+    from bdm_amd.config import near_square_factors
+    cfg = BSDMConfig(dim=1024, bank_count=2048, bank_size=8, selected_banks=8, value_width=1024, num_heads=8)
+    layer = BankedDeltaMemory(cfg, layer_id=0, seed=0).to(device=device, dtype=torch.bfloat16)
+    x, (q, k, v, g, b, w), (rr, wr), initial = make_inputs(layer, 4, 8192, device, seed=4)
+    j1, j2 = near_square_factors(cfg.bank_count)
+    gen = torch.Generator().manual_seed(11)
+    bias = torch.cat([-1.1 * torch.log1p(torch.randperm(j1, generator=gen).float()),
+                      -1.1 * torch.log1p(torch.randperm(j2, generator=gen).float())]).to(device)
+    rr = (rr.float() + bias).to(rr.dtype)
+    wr = (wr.float() + bias).to(wr.dtype)
+    final = torch.empty(4, cfg.bank_count, cfg.num_heads, cfg.bank_size, cfg.head_value_width, device=device,
+                        dtype=torch.bfloat16)
+
+    def step():
+        ww, wi = ops.router_select(wr, bank_count=cfg.bank_count, selected_banks=8)
+        rw, ri = ops.router_select(rr, bank_count=cfg.bank_count, selected_banks=8)
+        meta = ops.dispatch_build(wi, ri, cfg.bank_count)
+        ops.routed_forward(q, k, v, g, b, w, wi, ww, ri, rw, initial, meta, bank_count=cfg.bank_count,
+                           scale=cfg.bank_size ** -0.5, routed_decay=True, round_interval=0, final_state=final)
+        return meta
+
+    with torch.no_grad():
+        sec, meta = timed(step, steps, 1)
+    lengths = (meta.cu_seqlens[1:] - meta.cu_seqlens[:-1]).float()
+    return {'tokens_per_s': round(4 * 8192 / sec, 1), 'ms_per_step': round(sec * 1e3, 3),
+            'max_segment_events': int(lengths.max()), 'mean_segment_events': round(float(lengths.mean()), 1)}
+
+
+def c5_training(device, steps=3):
+    """C5: batch 4, T2048, H8, BF16 training state: routed operator forward +
+    backward (bank_training with all controller, route and state gradients)."""
+    import torch
+    from bdm_amd import BankedDeltaMemory, bank_training
+    cfg = c2_config()
+    layer = BankedDeltaMemory(cfg, layer_id=0, seed=0).to(device=device, dtype=torch.bfloat16)
+    x, ctrl, (rr, wr), initial = make_inputs(layer, 4, 2048, device, seed=5)
+    gen = torch.Generator().manual_seed(12)
+    dy = torch.randn(4, 2048, cfg.value_width, generator=gen).to(torch.bfloat16).to(device)
+    with torch.no_grad():
+        ww, wi = layer._route(wr, cfg.selected_banks)
+        rw, ri = layer._route(rr, cfg.selected_banks)
+    leaves = [t.detach().clone().requires_grad_(True) for t in (*ctrl, ww, rw, initial)]
+
+    def step():
+        for t in leaves:
+            t.grad = None
+        y = bank_training(*leaves[:6], wi, leaves[6], ri, leaves[7], leaves[8], cfg.bank_count,
+                          cfg.bank_size ** -0.5, state_dtype=torch.bfloat16)
+        y.backward(dy)
+
+    sec, _ = timed(step, steps, 1)
+    return {'tokens_per_s': round(4 * 2048 / sec, 1), 'ms_per_step': round(sec * 1e3, 3)}
+
+
 def cpu_baseline(layer_gpu, cfg, tokens):
     """The oracle's per-event loop (port of reference_packed_gdn2 + index_add_
     readout) on the first `tokens` tokens of one C2 sequence, on the host."""
@@ -342,6 +402,10 @@ def main():
         result['full_layer_prefill_tokens_per_s'] = round(tokens / layer_sec, 1)
         progress('decode C3')
         result['decode_c3'] = decode_bench(layer, device, args.decode_steps)
+        progress('skewed forward C4')
+        result['forward_c4'] = c4_forward(device)
+        progress('training C5')
+        result['training_c5'] = c5_training(device)
     progress('copy probe')
     result['hbm_copy_GBps'] = round(copy_probe(device), 1)
     if args.cpu_tokens > 0:
