@@ -225,29 +225,42 @@ __global__ __launch_bounds__(256) void routed_forward_kernel(ForwardParams<T> p)
 }
 
 // ----------------------------------------------------------------------------
-// Lazy-decay segment kernel for S <= 8 (the production geometry).
+// Lazy-decay segment kernel for S = 8 (the production geometry).
 //
 // The state of one (segment, head) is kept as M = diag(s) * Mh with a per-row
 // scale s.  A write's decay then only updates s (s' = s * exp(eg)), and with
 // a = bf(b*p) * k, x = bf(w*p) * v:
-//   erase = sum_r (a_r s'_r) Mh_r,   u = x - erase,   Mh_r += (k_r / s'_r) u
+//   u = x - sum_r (a_r s'_r) Mh_r,   Mh_r += (k_r / s'_r) u
 // which is M' = hd + k u^T divided row-wise by s', at two FMAs per state
 // element instead of three.  Stages of kLazyStage events start at segment
 // offsets that are multiples of 16, the rounding/snapshot interval, and s is
 // folded back into Mh (Mh *= s, s = 1) at every stage start and at the
 // segment end, so every rounding point and snapshot sees the true state, as
 // the reference rounds it.  A stage in which some row's s would fall below
-// kScaleFloor runs in eager form instead (Mh = M: hd = exp(eg) * M applied
-// explicitly: M' = diag(d) M + k u^T, erase = sum_r (a_r d_r) M_r), so
-// k / s' stays finite.  A read uses
+// kScaleFloor runs in eager form instead (Mh = M: hd = diag(d) M, then
+// u = x - sum_r a_r hd_r, M' = hd + k u^T), so k / s' stays finite.  A read uses
 // gamma_r = scale * bf(q*r)_r * s_r.
 //
-// The row quantities of every (event, head, row) are computed once per stage
-// for the workgroup: all threads compute exp(eg), k, a (or scale*bf(q*r)) in
-// parallel, then one lane per (head, row) scans the stage carrying s and
-// turns them into alpha = a s', beta = k / s' (or, eager, a and k with the
-// decay kept) or gamma.  The lanes that own value columns read them from LDS
-// by broadcast; the event loop never rescales the state conditionally.
+// Work of a stage is split in two so its latency is off the critical path:
+//  * prep: one lane per (event, head, half of the rows) loads the event's
+//    q/k/g/b rows and route weight, computes exp(eg), k, a (or scale*bf(q*r)),
+//    and the running scale s of its 4 rows as an inclusive prefix product
+//    over the stage's 16 events with DPP row shifts (a 16-lane DPP row holds
+//    the 16 events of one (head, half)); it writes -alpha = -a s', beta =
+//    k / s' (or the eager operands) and gamma to LDS.
+//  * value columns: a lane owns CPL columns of one head with all 8 rows in
+//    registers and runs the stage's events in order, reading the row
+//    operands from LDS by broadcast.
+// The prep of stage s+1 overlaps the value loop of stage s: its row loads are
+// issued before the value loop and consumed after it, and the packed order of
+// stage s+2 is loaded one stage earlier still (event metadata ring of 3).
+// v and w of the next write are prefetched one write ahead, across stages.
+//
+// x = bf(w*p) * v: for BF16 controllers the products w*p and bf(w*p)*v are
+// formed with v_dot2c_f32_bf16 against an operand whose other half is zero,
+// which yields the exact FP32 product of the two BF16 values (what the
+// reference computes), then v_cvt_pk_bf16_f32 rounds w*p to nearest even.
+
 // CPL consecutive columns of T kept as raw 32-bit words (BF16 pairs unpacked
 // on use), so a prefetched row costs CPL/2 (BF16) or CPL (FP32) registers.
 template <typename T, int CPL>
@@ -255,30 +268,15 @@ struct RawCols;
 
 template <int CPL>
 struct RawCols<bf16_t, CPL> {
-    static_assert(CPL % 2 == 0, "BF16 pairs");
+    static_assert(CPL % 4 == 0, "BF16 column groups of 4");
     uint32_t u[CPL / 2];
     __device__ __forceinline__ void load(const bf16_t *p) {
-        if constexpr (CPL % 8 == 0) {
 #pragma unroll
-            for (int i = 0; i < CPL / 8; ++i) {
-                const uint4 q = reinterpret_cast<const uint4 *>(p)[i];
-                u[4 * i] = q.x;
-                u[4 * i + 1] = q.y;
-                u[4 * i + 2] = q.z;
-                u[4 * i + 3] = q.w;
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < CPL / 4; ++i) {
-                const uint2 q = reinterpret_cast<const uint2 *>(p)[i];
-                u[2 * i] = q.x;
-                u[2 * i + 1] = q.y;
-            }
+        for (int i = 0; i < CPL / 4; ++i) {
+            const uint2 q = reinterpret_cast<const uint2 *>(p)[i];
+            u[2 * i] = q.x;
+            u[2 * i + 1] = q.y;
         }
-    }
-    __device__ __forceinline__ float get(int c) const {
-        const uint32_t word = u[c / 2];
-        return __uint_as_float((c & 1) ? (word & 0xffff0000u) : (word << 16));
     }
 };
 
@@ -286,36 +284,107 @@ template <int CPL>
 struct RawCols<float, CPL> {
     float f[CPL];
     __device__ __forceinline__ void load(const float *p) { load_row<CPL>(p, f); }
-    __device__ __forceinline__ float get(int c) const { return f[c]; }
 };
 
-__device__ __forceinline__ int64_t uniform_i64(int64_t x) {
-    const int lo = __builtin_amdgcn_readfirstlane(int(uint32_t(uint64_t(x))));
-    const int hi = __builtin_amdgcn_readfirstlane(int(uint32_t(uint64_t(x) >> 32)));
-    return int64_t((uint64_t(uint32_t(hi)) << 32) | uint64_t(uint32_t(lo)));
+typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
+
+// Exact FP32 product of the BF16 halves selected by `mask` (0x0000ffff: the
+// low halves, 0xffff0000: the high halves) of two packed pairs.
+__device__ __forceinline__ float dot_half(uint32_t a, uint32_t b_masked) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v_t, a), __builtin_bit_cast(bf16x2v_t, b_masked),
+                                           0.f, false);
+}
+
+// x[c] = bf(w[c] * pw) * v[c] for CPL columns.
+template <int CPL>
+__device__ __forceinline__ void gated_values(const RawCols<bf16_t, CPL> &w, const RawCols<bf16_t, CPL> &v, float pw,
+                                             float (&x)[CPL]) {
+    const uint32_t pbits = __float_as_uint(pw) >> 16;  // pw is a BF16 value
+    const uint32_t p_lo = pbits, p_hi = pbits << 16;
+#pragma unroll
+    for (int i = 0; i < CPL / 2; ++i) {
+        const float e0 = dot_half(w.u[i], p_lo);  // w[2i] * pw
+        const float e1 = dot_half(w.u[i], p_hi);  // w[2i+1] * pw
+        const f32x2_t f = {e0, e1};
+        const uint32_t ew = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
+        x[2 * i] = dot_half(ew, v.u[i] & 0x0000ffffu);
+        x[2 * i + 1] = dot_half(ew, v.u[i] & 0xffff0000u);
+    }
+}
+
+template <int CPL>
+__device__ __forceinline__ void gated_values(const RawCols<float, CPL> &w, const RawCols<float, CPL> &v, float pw,
+                                             float (&x)[CPL]) {
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) x[c] = (w.f[c] * pw) * v.f[c];
+}
+
+// Inclusive prefix product over the 16 lanes of a DPP row (lane order).
+__device__ __forceinline__ float row_prefix_product(float x) {
+    const int one = __float_as_int(1.f);
+    x *= __int_as_float(__builtin_amdgcn_update_dpp(one, __float_as_int(x), 0x111, 0xf, 0xf, false));  // row_shr:1
+    x *= __int_as_float(__builtin_amdgcn_update_dpp(one, __float_as_int(x), 0x112, 0xf, 0xf, false));  // row_shr:2
+    x *= __int_as_float(__builtin_amdgcn_update_dpp(one, __float_as_int(x), 0x114, 0xf, 0xf, false));  // row_shr:4
+    x *= __int_as_float(__builtin_amdgcn_update_dpp(one, __float_as_int(x), 0x118, 0xf, 0xf, false));  // row_shr:8
+    return x;
 }
 
 constexpr int kLazyStage = 16;
 constexpr int kLazyHeads = 8;  // heads per workgroup
 constexpr float kScaleFloor = 0x1p-32f;
 
-// Writes whose v, w rows are in flight.  Measured on C2: deeper prefetch (2,
-// 3) or 8 columns per lane at 2 waves/SIMD were slower than this 1-deep
-// prefetch with 4 columns per lane at 4 waves/SIMD (128 VGPRs).
-constexpr int kPrefetch = 1;
+// Raw row data one prep lane loads for its (event, head, 4 rows).
+template <typename T>
+struct PrepLoads;
+template <>
+struct PrepLoads<bf16_t> {
+    uint2 key, erase;  // k (or q for a read), b: 4 BF16 each
+    float4 gate;       // g
+    uint32_t weight;   // route weight, BF16 in the low half
+    __device__ __forceinline__ float key_at(int r) const {
+        const uint32_t w = r < 2 ? key.x : key.y;
+        return __uint_as_float((r & 1) ? (w & 0xffff0000u) : (w << 16));
+    }
+    __device__ __forceinline__ float erase_at(int r) const {
+        const uint32_t w = r < 2 ? erase.x : erase.y;
+        return __uint_as_float((r & 1) ? (w & 0xffff0000u) : (w << 16));
+    }
+    __device__ __forceinline__ float weight_f() const { return __uint_as_float(weight << 16); }
+};
+template <>
+struct PrepLoads<float> {
+    float4 key, erase, gate;
+    float weight_raw;
+    __device__ __forceinline__ float key_at(int r) const { return (&key.x)[r]; }
+    __device__ __forceinline__ float erase_at(int r) const { return (&erase.x)[r]; }
+    __device__ __forceinline__ float weight_f() const { return weight_raw; }
+};
+
+template <typename T>
+__device__ __forceinline__ void load_vec4(const T *p, uint2 &out) {
+    out = *reinterpret_cast<const uint2 *>(p);
+}
+__device__ __forceinline__ void load_vec4(const float *p, float4 &out) { out = *reinterpret_cast<const float4 *>(p); }
 
 template <typename T, int CPL>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void lazy_forward_kernel(
     ForwardParams<T> p) {
     constexpr int S = 8;
-    __shared__ int64_t s_token[kLazyStage];
-    __shared__ int64_t s_slot[kLazyStage];  // read: original read slot; write: -1
-    __shared__ float s_weight[kLazyStage];
-    __shared__ float s_rows[kLazyStage][kLazyHeads][3][S];
-    __shared__ float s_fold[kLazyHeads][S];
-    __shared__ int s_eager;
-    __shared__ int s_wpos[kLazyStage + 1];  // event index of each write of the stage, then n
-    __shared__ int s_nw;
+    constexpr int NE = kLazyStage;
+    // event metadata ring: stage s lives in slot s % 3
+    __shared__ int s_tok[3][NE];
+    __shared__ int s_route[3][NE];
+    __shared__ int s_wpos[3][NE + 1];  // stage positions of the writes, then n
+    __shared__ int s_nw[3];
+    __shared__ int s_n[3];
+    __shared__ unsigned s_rmask[3];    // bit e: event e of the stage is a read
+    // row operands of stage s in buffer s & 1: lazy [0] = -alpha, [1] = beta;
+    // eager [0] = -a, [1] = k, [2] = d; a read [0] = gamma
+    __shared__ float s_rows[2][NE][kLazyHeads][3][S];
+    __shared__ float s_fold[2][kLazyHeads][S];  // s at the end of the stage (1 for eager)
+    __shared__ float s_pw[2][NE];               // route weight of each event of the stage
+    __shared__ int s_eager[2];
+    __shared__ int s_flag[2];
 
     const int nseg = gridDim.x;
     const int seg = p.xcd_remap ? int((blockIdx.x % 8) * (nseg / 8) + blockIdx.x / 8) : int(blockIdx.x);
@@ -324,123 +393,182 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     const int head0 = blockIdx.y * p.heads_per_block;
     const int nheads = min(p.heads_per_block, p.heads - head0);
     const int tid = threadIdx.x;
-    // Lanes past the block's heads (when nheads * lanes_per_head is not a
-    // multiple of the wave) shadow lanes of the last head: they compute the
-    // identical values and store them to the same addresses, so every lane
-    // runs the same control flow and no store needs a lane condition.
-    const int lh = min(tid / p.lanes_per_head, nheads - 1);  // head within the block
+    // value-column role.  Lanes past the block's heads shadow lanes of the
+    // last head: identical values to identical addresses.
+    const int lh = min(tid / p.lanes_per_head, nheads - 1);
     const int head = head0 + lh;
     const int col0 = (tid % p.lanes_per_head) * CPL;
-    const bool scanner = tid < nheads * S;  // all in the first wave
-    const int scan_head = tid / S, scan_row = tid % S;
+    const int64_t hw = int64_t(p.heads) * p.width;         // elements of one token row of v, w, z
+    const int64_t lane_col = int64_t(head) * p.width + col0;  // this lane's offset in such a row
+    // prep role: (event pe, head ph, rows 4*half .. 4*half+3)
+    const int pe = tid & (NE - 1);
+    const int ph = (tid >> 4) >> 1;
+    const int half = (tid >> 4) & 1;
+    const bool prep_head = ph < nheads;
+
     const int64_t start = p.cu[seg], end = p.cu[seg + 1];
     const int64_t write_events = p.nt * p.kw;
     const int64_t events = p.nt * (p.kw + p.kr);
     const bool rounding = p.round_interval > 0;
-    float sc = 1.f;  // the scanner's s of (scan_head, scan_row)
+    const int nstages = int((end - start + NE - 1) / NE);
 
+    // ---- metadata of a stage from its packed order entries (lanes 0..15)
+    auto load_order = [&](int stage) -> int64_t {
+        const int64_t pos = start + int64_t(stage) * NE + tid;
+        if (tid < NE && stage < nstages && pos < end) return p.order[pos];
+        return -1;
+    };
+    auto decode_order = [&](int stage, int64_t o) {
+        // lanes 0..15 of wave 0; the other lanes of the wave take part in the ballot
+        const int slot = stage % 3;
+        const bool live = o >= 0;
+        o = o < 0 ? 0 : (o >= events ? events - 1 : o);
+        const bool rd = o >= write_events;
+        const int64_t route = rd ? o - write_events : o;
+        const uint64_t live_mask = __ballot(live && tid < NE);
+        const uint64_t read_mask = __ballot(live && rd && tid < NE);
+        const uint64_t write_mask = live_mask & ~read_mask;
+        if (tid < NE) {
+            s_tok[slot][tid] = int(rd ? route / p.kr : route / p.kw);
+            s_route[slot][tid] = int(route);
+            if (live && !rd) s_wpos[slot][__popcll(write_mask & ((uint64_t(1) << tid) - 1))] = tid;
+        }
+        if (tid == 0) {
+            const int n = __popcll(live_mask), nw = __popcll(write_mask);
+            s_n[slot] = n;
+            s_nw[slot] = nw;
+            s_wpos[slot][nw] = n;
+            s_rmask[slot] = unsigned(read_mask);
+        }
+    };
+
+    // ---- prep loads of a stage (issued before, consumed after a value loop)
+    PrepLoads<T> pl{};
+    auto issue_prep = [&](int stage) {
+        const int slot = stage % 3;
+        if (stage >= nstages || !prep_head || pe >= s_n[slot]) return;
+        const bool rd = (s_rmask[slot] >> pe) & 1u;
+        const int64_t row = (int64_t(s_tok[slot][pe]) * p.heads + head0 + ph) * S + 4 * half;
+        const int route = s_route[slot][pe];
+        if (rd) {
+            load_vec4(p.q + row, pl.key);
+            if constexpr (std::is_same<T, bf16_t>::value)
+                pl.weight = p.rw[route].bits;
+            else
+                pl.weight_raw = p.rw[route];
+        } else {
+            load_vec4(p.k + row, pl.key);
+            load_vec4(p.b + row, pl.erase);
+            pl.gate = *reinterpret_cast<const float4 *>(p.g + row);
+            if constexpr (std::is_same<T, bf16_t>::value)
+                pl.weight = p.ww[route].bits;
+            else
+                pl.weight_raw = p.ww[route];
+        }
+    };
+    // compute the row operands of `stage` into buffer stage & 1 (two barriers)
+    auto finish_prep = [&](int stage) {
+        const int slot = stage % 3, buf = stage & 1;
+        const int n = s_n[slot];
+        const bool live = prep_head && pe < n && stage < nstages;
+        const bool rd = live && ((s_rmask[slot] >> pe) & 1u);
+        const float pw = live ? pl.weight_f() : 0.f;
+        float d[4], kk[4], a[4], sc[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            if (live && !rd) {
+                const float g = (&pl.gate.x)[r];
+                d[r] = __expf(p.routed_decay ? g * pw : g);
+                kk[r] = pl.key_at(r);
+                a[r] = round_to<T>(pl.erase_at(r) * pw) * kk[r];
+            } else {
+                d[r] = 1.f;
+                kk[r] = live ? p.scale * round_to<T>(pl.key_at(r) * pw) : 0.f;  // gamma for a read
+                a[r] = 0.f;
+            }
+            sc[r] = row_prefix_product(d[r]);
+        }
+        bool low = false;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) low |= !(sc[r] >= kScaleFloor);  // NaN also takes the eager form
+        if (__ballot(low) != 0 && (tid & 63) == 0) atomicOr(&s_flag[buf], 1);
+        __syncthreads();
+        const bool eager = s_flag[buf] != 0;
+        if (live) {
+            float(*row)[S] = s_rows[buf][pe][ph];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int rr = 4 * half + r;
+                if (rd) {
+                    row[0][rr] = eager ? kk[r] : kk[r] * sc[r];
+                } else if (!eager) {
+                    row[0][rr] = -(a[r] * sc[r]);
+                    row[1][rr] = kk[r] / sc[r];
+                } else {
+                    row[0][rr] = -a[r];
+                    row[1][rr] = kk[r];
+                    row[2][rr] = d[r];
+                }
+            }
+            if (tid < NE) s_pw[buf][pe] = pw;
+            if (pe == n - 1) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) s_fold[buf][ph][4 * half + r] = eager ? 1.f : sc[r];
+            }
+        }
+        if (tid == 0) s_eager[buf] = eager ? 1 : 0;
+        __syncthreads();
+        if (tid == 0) s_flag[buf] = 0;  // next read after two more barriers
+    };
+
+    // ---- prologue: metadata of stages 0 and 1, operands of stage 0
     float h[S][CPL];
-    const int64_t state_offset = ((int64_t(bank) * p.heads + head) * p.s_real) * p.width + col0;
-    load_state<S, CPL>(p.initial, p.init_dtype, bidx * p.init_bstride + state_offset, p.width, p.s_real, h);
+    const int64_t state_offset = ((int64_t(bank) * p.heads + head) * S) * p.width + col0;
+    load_state<S, CPL>(p.initial, p.init_dtype, bidx * p.init_bstride + state_offset, p.width, S, h);
     if (rounding) {
 #pragma unroll
         for (int r = 0; r < S; ++r)
 #pragma unroll
             for (int c = 0; c < CPL; ++c) h[r][c] = round_bf16(h[r][c]);
     }
+    if (tid < 2) s_flag[tid] = 0;
+    if (tid < kLazyHeads * S) s_fold[1][tid / S][tid % S] = 1.f;  // "stage -1"
+    {
+        const int64_t o0 = load_order(0), o1 = load_order(1);
+        if (tid < 64) {
+            decode_order(0, o0);
+            decode_order(1, o1);
+        }
+    }
+    __syncthreads();
+    issue_prep(0);
+    finish_prep(0);
 
-    for (int64_t base = start; base < end; base += kLazyStage) {
-        const int n = int(min(int64_t(kLazyStage), end - base));
-        __syncthreads();  // the previous stage's readers are done
-        if (tid < n) {
-            int64_t o = p.order[base + tid];
-            o = o < 0 ? 0 : (o >= events ? events - 1 : o);
-            const bool rd = o >= write_events;
-            const int64_t route = rd ? o - write_events : o;
-            s_token[tid] = rd ? route / p.kr : route / p.kw;
-            s_slot[tid] = rd ? route : -1;
-            s_weight[tid] = rd ? to_f32(p.rw[route]) : to_f32(p.ww[route]);
-        }
-        if (tid == 0) s_eager = 0;
-        __syncthreads();
-        if (tid == 0) {
-            int nw = 0;
-            for (int i = 0; i < n; ++i)
-                if (s_slot[i] < 0) s_wpos[nw++] = i;
-            s_wpos[nw] = n;
-            s_nw = nw;
-        }
-        // (1) per (event, head, row): exp(eg), k, a for a write; scale*bf(q*r) for
-        // a read.  Thread t owns (head, row) = ((t % 64) / S, t % S) and visits
-        // every (blockDim / 64)-th event.
-        for (int i = tid / (kLazyHeads * S); i < n; i += blockDim.x / (kLazyHeads * S)) {
-            const int hl = (tid % (kLazyHeads * S)) / S, r = tid % S;
-            if (hl >= nheads) continue;
-            const int64_t at = (s_token[i] * p.heads + head0 + hl) * p.s_real + r;
-            const bool live = r < p.s_real;
-            const float pw = s_weight[i];
-            if (s_slot[i] >= 0) {
-                const float q = live ? to_f32(p.q[at]) : 0.f;
-                s_rows[i][hl][0][r] = p.scale * round_to<T>(q * pw);
-            } else {
-                const float k = live ? to_f32(p.k[at]) : 0.f;
-                const float g = live ? p.g[at] : 0.f;
-                const float b = live ? to_f32(p.b[at]) : 0.f;
-                s_rows[i][hl][0][r] = __expf(p.routed_decay ? g * pw : g);
-                s_rows[i][hl][1][r] = k;
-                s_rows[i][hl][2][r] = round_to<T>(b * pw) * k;
-            }
-        }
-        __syncthreads();
-        // (2) one lane per (head, row): fold s at the stage start, then scan
-        if (scanner) {
-            s_fold[scan_head][scan_row] = sc;
-            float run = 1.f;
-            bool low = false;
-#pragma unroll 1
-            for (int i = 0; i < n; ++i) {
-                if (s_slot[i] < 0) {
-                    run *= s_rows[i][scan_head][0][scan_row];
-                    low |= !(run >= kScaleFloor);  // NaN also takes the eager form
-                }
-            }
-            if (low) s_eager = 1;  // benign race: every writer stores 1
-        }
-        __syncthreads();
-        // LDS values every lane reads alike are made wave-uniform explicitly, so
-        // the branches on them are scalar and the state is never copied
-        const bool eager = __builtin_amdgcn_readfirstlane(s_eager) != 0;
-        if (scanner) {
-            sc = 1.f;
-#pragma unroll 1
-            for (int i = 0; i < n; ++i) {
-                float *row = &s_rows[i][scan_head][0][scan_row];
-                if (s_slot[i] >= 0) {
-                    row[0] *= sc;  // gamma
-                } else if (!eager) {
-                    const float d = row[0], k = row[S], a = row[2 * S];
-                    sc *= d;
-                    row[0] = a * sc;  // alpha
-                    row[S] = k / sc;  // beta
-                } else {
-                    // eager: alpha = a * decay, beta = k, and the decay itself
-                    const float d = row[0], a = row[2 * S];
-                    row[0] = a * d;
-                    row[2 * S] = d;
-                }
-            }
-        }
-        __syncthreads();
+    // v, w of the next write in stream order (across stages)
+    RawCols<T, CPL> nv, nw_;
+    auto fetch = [&](int slot, int e, RawCols<T, CPL> &vv, RawCols<T, CPL> &ww) {
+        const int64_t off = int64_t(s_tok[slot][e]) * hw + lane_col;
+        vv.load(p.v + off);
+        ww.load(p.w + off);
+    };
+    bool prefetched = false;  // nv, nw_ hold the current stage's first write
 
-        // (3) the value columns.  Fold s into Mh: the true state at the stage
-        // start, which is a rounding/snapshot point when the offset is > 0.
+    for (int st = 0; st < nstages; ++st) {
+        const int slot = st % 3, buf = st & 1;
+        const int64_t base = start + int64_t(st) * NE;
+        // next stages' loads, in flight during this stage's value loop
+        const int64_t o2 = load_order(st + 2);
+        issue_prep(st + 1);
+
+        // Fold s into Mh: the true state at the stage start, which is a
+        // rounding/snapshot point when the offset is > 0.
 #pragma unroll
         for (int r = 0; r < S; ++r) {
-            const float f = s_fold[lh][r];
+            const float f = s_fold[buf ^ 1][lh][r];
 #pragma unroll
             for (int c = 0; c < CPL; ++c) h[r][c] *= f;
         }
-        if (base > start) {
+        if (st > 0) {
             if (rounding) {
 #pragma unroll
                 for (int r = 0; r < S; ++r)
@@ -449,18 +577,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
             }
             // snapshot of the state before event `base` (see routed_forward_kernel)
             if (p.snap) {
-                const int64_t slot = base / p.snap_interval - 1;
-                store_state<S, CPL>(p.snap, p.snap_dtype, ((slot * p.heads + head) * p.s_real) * p.width + col0,
-                                    p.width, p.s_real, h);
+                const int64_t sslot = base / p.snap_interval - 1;
+                store_state<S, CPL>(p.snap, p.snap_dtype, ((sslot * p.heads + head) * S) * p.width + col0, p.width,
+                                    S, h);
             }
         }
-        // Events in packed order, as runs: the reads before each write, then
-        // the write, so the state is updated exactly once per iteration and
-        // never merged from branches.  The next write's v and w are
-        // prefetched as raw rows.
+
+        const int n = __builtin_amdgcn_readfirstlane(s_n[slot]);
+        const int nw = __builtin_amdgcn_readfirstlane(s_nw[slot]);
+        const bool eager = __builtin_amdgcn_readfirstlane(s_eager[buf]) != 0;
+        const int next_slot = (st + 1) % 3;
+        const bool next_has_write = st + 1 < nstages && s_nw[next_slot] > 0;
+
         auto read_event = [&](int i) {
-            const int64_t slot = uniform_i64(s_slot[i]);
-            const float *row = &s_rows[i][lh][0][0];
+            const int64_t zrow = int64_t(__builtin_amdgcn_readfirstlane(s_route[slot][i]));
+            const float *row = &s_rows[buf][i][lh][0][0];
             float gamma[S];
 #pragma unroll
             for (int r = 0; r < S; ++r) gamma[r] = row[r];
@@ -472,92 +603,80 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
                 for (int r = 0; r < S; ++r) acc = fmaf(gamma[r], h[r][c], acc);
                 z[c] = acc;
             }
-            store_row<CPL>(p.zbuf + (slot * p.heads + head) * p.width + col0, z);
+            store_row<CPL>(p.zbuf + zrow * hw + lane_col, z);
         };
-        auto fetch = [&](int i, RawCols<T, CPL> &vv, RawCols<T, CPL> &ww) {
-            const int64_t row = uniform_i64(s_token[i]) * p.heads + head;
-            vv.load(p.v + row * p.width + col0);
-            ww.load(p.w + row * p.width + col0);
-        };
-        const int nw = __builtin_amdgcn_readfirstlane(s_nw);
-        // One loop nest per write form, so the state is carried through a
-        // single update form and only merged once per stage.
-        auto run = [&](auto eager_form) {
-            constexpr bool kEager = decltype(eager_form)::value;
-            // v and w of the next kPrefetch writes are in flight while a write
-            // and its preceding reads run
-            RawCols<T, CPL> vq[kPrefetch], wq[kPrefetch];
-#pragma unroll
-            for (int d = 0; d < kPrefetch; ++d)
-                if (d < nw) fetch(__builtin_amdgcn_readfirstlane(s_wpos[d]), vq[d], wq[d]);
+        // Events in packed order, as runs: the reads before each write, then
+        // the write, so the state is updated exactly once per iteration and
+        // never merged from branches.
+        {
+            if (nw > 0 && !prefetched) fetch(slot, __builtin_amdgcn_readfirstlane(s_wpos[slot][0]), nv, nw_);
+            prefetched = false;
             int i = 0;
 #pragma unroll 1
             for (int wk = 0; wk < nw; ++wk) {
-                const int wi_ = __builtin_amdgcn_readfirstlane(s_wpos[wk]);
-                const RawCols<T, CPL> vc = vq[0], wc = wq[0];
-#pragma unroll
-                for (int d = 0; d + 1 < kPrefetch; ++d) {
-                    vq[d] = vq[d + 1];
-                    wq[d] = wq[d + 1];
+                const int wi_ = __builtin_amdgcn_readfirstlane(s_wpos[slot][wk]);
+                const RawCols<T, CPL> vc = nv, wc = nw_;
+                if (wk + 1 < nw) {
+                    fetch(slot, __builtin_amdgcn_readfirstlane(s_wpos[slot][wk + 1]), nv, nw_);
+                } else if (next_has_write) {
+                    fetch(next_slot, __builtin_amdgcn_readfirstlane(s_wpos[next_slot][0]), nv, nw_);
+                    prefetched = true;
                 }
-                if (wk + kPrefetch < nw)
-                    fetch(__builtin_amdgcn_readfirstlane(s_wpos[wk + kPrefetch]), vq[kPrefetch - 1], wq[kPrefetch - 1]);
 #pragma unroll 1
                 for (; i < wi_; ++i) read_event(i);
                 i = wi_ + 1;
-                const float *row = &s_rows[wi_][lh][0][0];
-                const float pw = s_weight[wi_];
-                float alpha[S], beta[S], decay[S];
-#pragma unroll
-                for (int r = 0; r < S; ++r) {
-                    alpha[r] = row[r];
-                    beta[r] = row[S + r];
-                    if constexpr (kEager) decay[r] = row[2 * S + r];
-                }
-                // x = bf(w p) * v, rounded two columns per conversion
-                float x[CPL];
-#pragma unroll
-                for (int c = 0; c < CPL; c += 2) {
-                    float e0 = wc.get(c) * pw, e1 = wc.get(c + 1) * pw;
-                    round_pair<T>(e0, e1);
-                    x[c] = e0 * vc.get(c);
-                    x[c + 1] = e1 * vc.get(c + 1);
-                }
-#pragma unroll
-                for (int c = 0; c < CPL; ++c) {
-                    float erase = 0.f;
-#pragma unroll
-                    for (int r = 0; r < S; ++r) erase = fmaf(alpha[r], h[r][c], erase);
-                    const float u = x[c] - erase;
+                const float *row = &s_rows[buf][wi_][lh][0][0];
+                const float pw = s_pw[buf][wi_];
+                if (eager) {
+                    // hd = diag(d) M first; the update below then uses a and k
+                    // (a wave-uniform branch: the stage's form is uniform)
 #pragma unroll
                     for (int r = 0; r < S; ++r) {
-                        if constexpr (kEager)
-                            h[r][c] = fmaf(decay[r], h[r][c], beta[r] * u);  // M' = d M + k u
-                        else
-                            h[r][c] = fmaf(beta[r], u, h[r][c]);  // Mh' = Mh + (k / s') u
+                        const float d = row[2 * S + r];
+#pragma unroll
+                        for (int c = 0; c < CPL; ++c) h[r][c] *= d;
                     }
+                }
+                float nalpha[S], beta[S];
+#pragma unroll
+                for (int r = 0; r < S; ++r) {
+                    nalpha[r] = row[r];
+                    beta[r] = row[S + r];
+                }
+                float x[CPL];
+                gated_values<CPL>(wc, vc, pw, x);
+                // lazy: u = x - sum (a s') Mh, Mh += (k / s') u;  eager: u = x - sum a hd, M = hd + k u
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) {
+                    float u = x[c];
+#pragma unroll
+                    for (int r = 0; r < S; ++r) u = fmaf(nalpha[r], h[r][c], u);
+#pragma unroll
+                    for (int r = 0; r < S; ++r) h[r][c] = fmaf(beta[r], u, h[r][c]);
                 }
             }
 #pragma unroll 1
             for (; i < n; ++i) read_event(i);
-        };
-        if (eager)
-            run(std::true_type{});
-        else
-            run(std::false_type{});
+        }
+
+        // metadata of stage st+2 and operands of stage st+1
+        if (tid < 64) decode_order(st + 2, o2);
+        if (st + 1 < nstages) finish_prep(st + 1);
+        else __syncthreads();
     }
     __syncthreads();
-    if (scanner) s_fold[scan_head][scan_row] = sc;
-    __syncthreads();
     if (p.final_state) {
+        const int lbuf = (nstages - 1) & 1;
+        if (nstages > 0) {
 #pragma unroll
-        for (int r = 0; r < S; ++r) {
-            const float f = s_fold[lh][r];
+            for (int r = 0; r < S; ++r) {
+                const float f = s_fold[lbuf][lh][r];
 #pragma unroll
-            for (int c = 0; c < CPL; ++c) h[r][c] *= f;
+                for (int c = 0; c < CPL; ++c) h[r][c] *= f;
+            }
         }
-        const int64_t final_offset = bidx * (int64_t(p.banks) * p.heads * p.s_real * p.width) + state_offset;
-        store_state<S, CPL>(p.final_state, p.final_dtype, final_offset, p.width, p.s_real, h);
+        const int64_t final_offset = bidx * (int64_t(p.banks) * p.heads * S * p.width) + state_offset;
+        store_state<S, CPL>(p.final_state, p.final_dtype, final_offset, p.width, S, h);
     }
 }
 
@@ -647,7 +766,8 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, hipStream_t stream) {
     const int threads = ((p.heads_per_block * p.lanes_per_head + kWave - 1) / kWave) * kWave;
     const dim3 grid(unsigned(nseg), unsigned((a.heads + p.heads_per_block - 1) / p.heads_per_block));
     if constexpr (kLazy) {
-        lazy_forward_kernel<T, CPL><<<grid, threads, 0, stream>>>(p);
+        // 256 threads always: the prep role needs one lane per (event, head, half)
+        lazy_forward_kernel<T, CPL><<<grid, 256, 0, stream>>>(p);
         if (int rc = check_launch("lazy_forward_kernel")) return rc;
     } else {
         routed_forward_kernel<T, S, CPL><<<grid, threads, 0, stream>>>(p);
@@ -683,7 +803,11 @@ int dispatch_forward(const bdm_forward_args &a, T *zbuf, hipStream_t stream) {
     if (a.bank_size <= 8) {
         const int fold = a.round_interval > 0 ? a.round_interval : (a.snapshots ? a.snapshot_interval : kLazyStage);
         constexpr int lc = 4;  // value columns per lane of the lazy kernel
-        if (vec && a.head_width % lc == 0 && a.head_width / lc <= 64 && fold == kLazyStage)
+        // the lazy kernel keeps token and route indices in 32 bits
+        const int64_t nt = a.batch * a.time;
+        const bool small_index = nt * (a.write_banks > a.read_banks ? a.write_banks : a.read_banks) < INT32_MAX;
+        if (vec && a.bank_size == 8 && a.head_width % lc == 0 && a.head_width / lc <= 64 && fold == kLazyStage &&
+            small_index)
             return launch_forward<T, 8, lc, true>(a, zbuf, stream);
         if (vec && a.head_width % 8 == 0) return launch_forward<T, 8, 8>(a, zbuf, stream);
         return launch_forward<T, 8, 1>(a, zbuf, stream);

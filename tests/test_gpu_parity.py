@@ -139,6 +139,40 @@ def test_forward_matches_oracle(device, case):
     assert rel_err(final, ref_final) < TOL, rel_err(final, ref_final)
 
 
+@pytest.mark.parametrize('state_dtype', [torch.bfloat16, torch.float32])
+def test_forward_long_read_runs_match_oracle(device, state_dtype):
+    """Segments whose events are runs of more than one 16-event stage of reads
+    only, between runs of writes (the write of a later stage must not use the
+    value/gate rows of an earlier one)."""
+    from bdm_amd import ops
+    gen = torch.Generator().manual_seed(77)
+    batch, time, heads, s, v, j = 2, 160, 2, 8, 128, 4
+    t = torch.arange(time)
+    # one write and one read bank per token: bank 0 is read by every token and
+    # written only in tokens [40, 56) and [120, 128); the other banks share the rest
+    wi = torch.where(((t >= 40) & (t < 56)) | ((t >= 120) & (t < 128)), 0, 1 + t % 3)
+    wi = wi.expand(batch, time)[..., None].contiguous()
+    ri = torch.zeros(batch, time, 1, dtype=torch.long)
+    ri[1] = (t % j)[:, None]
+    ww = torch.rand(batch, time, 1, generator=gen).to(torch.bfloat16)
+    rw = torch.rand(batch, time, 1, generator=gen).to(torch.bfloat16)
+    q, k, v_, g, b, w = controllers(batch, time, heads, s, v, gen)
+    state = initial_state(j, heads, s, v, gen)
+    interval = 16 if state_dtype == torch.bfloat16 else 0
+    ref, ref_final = oracle_reads(q, k, v_, g, b, w, wi, ww, ri, rw, state, j, routed_decay=True,
+                                  state_dtype=state_dtype, interval=16, return_final=True)
+    dev = [x.to(device) for x in (q, k, v_, g, b, w, wi, ww, ri, rw, state)]
+    announce('forward long read runs', state_dtype)
+    meta = ops.dispatch_build(dev[6], dev[8], j)
+    final = torch.empty(batch, j, heads, s, v, device=device, dtype=torch.float32)
+    y = ops.routed_forward(*dev[:10], dev[10], meta, bank_count=j, scale=s ** -0.5, routed_decay=True,
+                           round_interval=interval, final_state=final)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y).all() and torch.isfinite(final).all()
+    assert rel_err(y, ref) < TOL, rel_err(y, ref)
+    assert rel_err(final, ref_final) < TOL, rel_err(final, ref_final)
+
+
 @pytest.mark.parametrize('decay', ['strong', 'mixed', 'none'])
 @pytest.mark.parametrize('state_dtype', [torch.bfloat16, torch.float32])
 def test_forward_decay_extremes_match_oracle(device, decay, state_dtype):
