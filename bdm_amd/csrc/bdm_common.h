@@ -98,6 +98,13 @@ __device__ __forceinline__ void load_row(const float *p, float (&out)[N]) {
     }
 }
 
+// Two FP32 values rounded to BF16 (nearest even) and packed, low half first,
+// with one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    const f32x2_t f = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
+}
+
 template <int N>
 __device__ __forceinline__ void store_row(bf16_t *p, const float (&in)[N]) {
     if constexpr (N % 8 == 0) {
@@ -105,20 +112,14 @@ __device__ __forceinline__ void store_row(bf16_t *p, const float (&in)[N]) {
         for (int i = 0; i < N / 8; ++i) {
             uint32_t w[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                uint32_t lo = from_f32<bf16_t>(in[8 * i + 2 * j]).bits;
-                uint32_t hi = from_f32<bf16_t>(in[8 * i + 2 * j + 1]).bits;
-                w[j] = lo | (hi << 16);
-            }
+            for (int j = 0; j < 4; ++j) w[j] = pack_bf16x2(in[8 * i + 2 * j], in[8 * i + 2 * j + 1]);
             reinterpret_cast<uint4 *>(p)[i] = make_uint4(w[0], w[1], w[2], w[3]);
         }
     } else if constexpr (N % 4 == 0) {
 #pragma unroll
-        for (int i = 0; i < N / 4; ++i) {
-            uint32_t w0 = from_f32<bf16_t>(in[4 * i]).bits | (uint32_t(from_f32<bf16_t>(in[4 * i + 1]).bits) << 16);
-            uint32_t w1 = from_f32<bf16_t>(in[4 * i + 2]).bits | (uint32_t(from_f32<bf16_t>(in[4 * i + 3]).bits) << 16);
-            reinterpret_cast<uint2 *>(p)[i] = make_uint2(w0, w1);
-        }
+        for (int i = 0; i < N / 4; ++i)
+            reinterpret_cast<uint2 *>(p)[i] =
+                make_uint2(pack_bf16x2(in[4 * i], in[4 * i + 1]), pack_bf16x2(in[4 * i + 2], in[4 * i + 3]));
     } else {
 #pragma unroll
         for (int i = 0; i < N; ++i) p[i] = from_f32<bf16_t>(in[i]);

@@ -136,8 +136,9 @@ __global__ __launch_bounds__(256) void routed_forward_kernel(ForwardParams<T> p)
     const bool active = int(threadIdx.x) < p.heads_per_block * p.lanes_per_head && head < p.heads;
     const int col0 = (int(threadIdx.x) % p.lanes_per_head) * CPL;
     const int64_t start = p.cu[seg], end = p.cu[seg + 1];
-    const int64_t write_events = p.nt * p.kw;
-    const int64_t events = p.nt * (p.kw + p.kr);
+    // event and route indices fit in 32 bits (checked by the launcher)
+    const int write_events = int(p.nt * p.kw);
+    const int events = int(p.nt * (p.kw + p.kr));
     const bool rounding = p.round_interval > 0;
 
     float h[S][CPL];
@@ -256,10 +257,10 @@ __global__ __launch_bounds__(256) void routed_forward_kernel(ForwardParams<T> p)
 // stage s+2 is loaded one stage earlier still (event metadata ring of 3).
 // v and w of the next write are prefetched one write ahead, across stages.
 //
-// x = bf(w*p) * v: for BF16 controllers the products w*p and bf(w*p)*v are
-// formed with v_dot2c_f32_bf16 against an operand whose other half is zero,
-// which yields the exact FP32 product of the two BF16 values (what the
-// reference computes), then v_cvt_pk_bf16_f32 rounds w*p to nearest even.
+// x = bf(w*p) * v: w*p is an exact FP32 product of two BF16 values, rounded
+// to nearest even by v_cvt_pk_bf16_f32; the product bf(w*p) * v is added to
+// the erase sum by v_dot2c_f32_bf16 against an operand whose other half is
+// zero, which adds the exact FP32 product of the two BF16 values.
 
 // CPL consecutive columns of T kept as raw 32-bit words (BF16 pairs unpacked
 // on use), so a prefetched row costs CPL/2 (BF16) or CPL (FP32) registers.
@@ -288,36 +289,46 @@ struct RawCols<float, CPL> {
 
 typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
 
-// Exact FP32 product of the BF16 halves selected by `mask` (0x0000ffff: the
-// low halves, 0xffff0000: the high halves) of two packed pairs.
-__device__ __forceinline__ float dot_half(uint32_t a, uint32_t b_masked) {
+// acc + (the exact FP32 product of the BF16 halves of a and b_masked that
+// b_masked keeps; its other half is zero): v_dot2c_f32_bf16.
+__device__ __forceinline__ float dot_half_acc(float acc, uint32_t a, uint32_t b_masked) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v_t, a), __builtin_bit_cast(bf16x2v_t, b_masked),
-                                           0.f, false);
+                                           acc, false);
 }
 
-// x[c] = bf(w[c] * pw) * v[c] for CPL columns.
+// The gated value of a write, x[c] = bf(w[c] * pw) * v[c], kept in a form
+// whose product is added to an accumulator as the last step of the erase sum.
+template <typename T, int CPL>
+struct GatedValues;
+
 template <int CPL>
-__device__ __forceinline__ void gated_values(const RawCols<bf16_t, CPL> &w, const RawCols<bf16_t, CPL> &v, float pw,
-                                             float (&x)[CPL]) {
-    const uint32_t pbits = __float_as_uint(pw) >> 16;  // pw is a BF16 value
-    const uint32_t p_lo = pbits, p_hi = pbits << 16;
+struct GatedValues<bf16_t, CPL> {
+    uint32_t ew[CPL / 2];  // bf(w * pw), packed pairs
+    uint32_t v[CPL / 2];
+    __device__ __forceinline__ void make(const RawCols<bf16_t, CPL> &w, const RawCols<bf16_t, CPL> &vv, float pw) {
 #pragma unroll
-    for (int i = 0; i < CPL / 2; ++i) {
-        const float e0 = dot_half(w.u[i], p_lo);  // w[2i] * pw
-        const float e1 = dot_half(w.u[i], p_hi);  // w[2i+1] * pw
-        const f32x2_t f = {e0, e1};
-        const uint32_t ew = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
-        x[2 * i] = dot_half(ew, v.u[i] & 0x0000ffffu);
-        x[2 * i + 1] = dot_half(ew, v.u[i] & 0xffff0000u);
+        for (int i = 0; i < CPL / 2; ++i) {
+            const float e0 = __uint_as_float(w.u[i] << 16) * pw;        // exact: BF16 * BF16
+            const float e1 = __uint_as_float(w.u[i] & 0xffff0000u) * pw;
+            ew[i] = pack_bf16x2(e0, e1);
+            v[i] = vv.u[i];
+        }
     }
-}
+    // acc + x[c]
+    __device__ __forceinline__ float add_to(float acc, int c) const {
+        return dot_half_acc(acc, ew[c / 2], (c & 1) ? (v[c / 2] & 0xffff0000u) : (v[c / 2] & 0x0000ffffu));
+    }
+};
 
 template <int CPL>
-__device__ __forceinline__ void gated_values(const RawCols<float, CPL> &w, const RawCols<float, CPL> &v, float pw,
-                                             float (&x)[CPL]) {
+struct GatedValues<float, CPL> {
+    float x[CPL];
+    __device__ __forceinline__ void make(const RawCols<float, CPL> &w, const RawCols<float, CPL> &vv, float pw) {
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) x[c] = (w.f[c] * pw) * v.f[c];
-}
+        for (int c = 0; c < CPL; ++c) x[c] = (w.f[c] * pw) * vv.f[c];
+    }
+    __device__ __forceinline__ float add_to(float acc, int c) const { return acc + x[c]; }
+};
 
 // Inclusive prefix product over the 16 lanes of a DPP row (lane order).
 __device__ __forceinline__ float row_prefix_product(float x) {
@@ -378,13 +389,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     __shared__ int s_nw[3];
     __shared__ int s_n[3];
     __shared__ unsigned s_rmask[3];    // bit e: event e of the stage is a read
-    // row operands of stage s in buffer s & 1: lazy [0] = -alpha, [1] = beta;
-    // eager [0] = -a, [1] = k, [2] = d; a read [0] = gamma
-    __shared__ float s_rows[2][NE][kLazyHeads][3][S];
-    __shared__ float s_fold[2][kLazyHeads][S];  // s at the end of the stage (1 for eager)
-    __shared__ float s_pw[2][NE];               // route weight of each event of the stage
-    __shared__ int s_eager[2];
-    __shared__ int s_flag[2];
+    // Row operands of the current stage (written by the prep of a stage after
+    // every wave has left the previous stage's value loop): lazy [0] = -alpha,
+    // [1] = beta; eager [0] = -a, [1] = k, [2] = d; a read [0] = gamma.
+    __shared__ float s_rows[NE][kLazyHeads][3][S];
+    __shared__ float s_fold[kLazyHeads][S];  // s at the end of the stage (1 for eager)
+    __shared__ float s_pw[NE];               // route weight of each event of the stage
+    __shared__ int s_eager;
+    __shared__ int s_flag[2];  // by stage parity: reset two barriers before its next use
 
     const int nseg = gridDim.x;
     const int seg = p.xcd_remap ? int((blockIdx.x % 8) * (nseg / 8) + blockIdx.x / 8) : int(blockIdx.x);
@@ -398,8 +410,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     const int lh = min(tid / p.lanes_per_head, nheads - 1);
     const int head = head0 + lh;
     const int col0 = (tid % p.lanes_per_head) * CPL;
-    const int64_t hw = int64_t(p.heads) * p.width;         // elements of one token row of v, w, z
-    const int64_t lane_col = int64_t(head) * p.width + col0;  // this lane's offset in such a row
+    const int64_t hw = int64_t(p.heads) * p.width;  // elements of one token row of v, w, z
+    // this lane's byte offset in such a row (rows are addressed from a
+    // wave-uniform base plus this 32-bit offset)
+    const uint32_t lane_bytes = uint32_t((head * p.width + col0) * int(sizeof(T)));
     // prep role: (event pe, head ph, rows 4*half .. 4*half+3)
     const int pe = tid & (NE - 1);
     const int ph = (tid >> 4) >> 1;
@@ -413,24 +427,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     const int nstages = int((end - start + NE - 1) / NE);
 
     // ---- metadata of a stage from its packed order entries (lanes 0..15)
-    auto load_order = [&](int stage) -> int64_t {
+    auto load_order = [&](int stage) -> int {
         const int64_t pos = start + int64_t(stage) * NE + tid;
-        if (tid < NE && stage < nstages && pos < end) return p.order[pos];
+        if (tid < NE && stage < nstages && pos < end) return int(p.order[pos]);
         return -1;
     };
-    auto decode_order = [&](int stage, int64_t o) {
+    auto decode_order = [&](int stage, int o) {
         // lanes 0..15 of wave 0; the other lanes of the wave take part in the ballot
         const int slot = stage % 3;
         const bool live = o >= 0;
         o = o < 0 ? 0 : (o >= events ? events - 1 : o);
         const bool rd = o >= write_events;
-        const int64_t route = rd ? o - write_events : o;
+        const int route = rd ? o - write_events : o;
         const uint64_t live_mask = __ballot(live && tid < NE);
         const uint64_t read_mask = __ballot(live && rd && tid < NE);
         const uint64_t write_mask = live_mask & ~read_mask;
         if (tid < NE) {
-            s_tok[slot][tid] = int(rd ? route / p.kr : route / p.kw);
-            s_route[slot][tid] = int(route);
+            s_tok[slot][tid] = int(uint32_t(route) / uint32_t(rd ? p.kr : p.kw));
+            s_route[slot][tid] = route;
             if (live && !rd) s_wpos[slot][__popcll(write_mask & ((uint64_t(1) << tid) - 1))] = tid;
         }
         if (tid == 0) {
@@ -468,7 +482,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     };
     // compute the row operands of `stage` into buffer stage & 1 (two barriers)
     auto finish_prep = [&](int stage) {
-        const int slot = stage % 3, buf = stage & 1;
+        const int slot = stage % 3;
         const int n = s_n[slot];
         const bool live = prep_head && pe < n && stage < nstages;
         const bool rd = live && ((s_rmask[slot] >> pe) & 1u);
@@ -491,11 +505,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         bool low = false;
 #pragma unroll
         for (int r = 0; r < 4; ++r) low |= !(sc[r] >= kScaleFloor);  // NaN also takes the eager form
-        if (__ballot(low) != 0 && (tid & 63) == 0) atomicOr(&s_flag[buf], 1);
-        __syncthreads();
-        const bool eager = s_flag[buf] != 0;
+        if (__ballot(low) != 0 && (tid & 63) == 0) atomicOr(&s_flag[stage & 1], 1);
+        __syncthreads();  // also: every wave has left the previous value loop
+        const bool eager = s_flag[stage & 1] != 0;
         if (live) {
-            float(*row)[S] = s_rows[buf][pe][ph];
+            float(*row)[S] = s_rows[pe][ph];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int rr = 4 * half + r;
@@ -503,22 +517,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
                     row[0][rr] = eager ? kk[r] : kk[r] * sc[r];
                 } else if (!eager) {
                     row[0][rr] = -(a[r] * sc[r]);
-                    row[1][rr] = kk[r] / sc[r];
+                    row[1][rr] = kk[r] * __builtin_amdgcn_rcpf(sc[r]);  // k / s' (v_rcp_f32)
                 } else {
                     row[0][rr] = -a[r];
                     row[1][rr] = kk[r];
                     row[2][rr] = d[r];
                 }
             }
-            if (tid < NE) s_pw[buf][pe] = pw;
+            if (tid < NE) s_pw[pe] = pw;
             if (pe == n - 1) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) s_fold[buf][ph][4 * half + r] = eager ? 1.f : sc[r];
+                for (int r = 0; r < 4; ++r) s_fold[ph][4 * half + r] = eager ? 1.f : sc[r];
             }
         }
-        if (tid == 0) s_eager[buf] = eager ? 1 : 0;
+        if (tid == 0) s_eager = eager ? 1 : 0;
         __syncthreads();
-        if (tid == 0) s_flag[buf] = 0;  // next read after two more barriers
+        if (tid == 0) s_flag[stage & 1] = 0;
     };
 
     // ---- prologue: metadata of stages 0 and 1, operands of stage 0
@@ -532,9 +546,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
             for (int c = 0; c < CPL; ++c) h[r][c] = round_bf16(h[r][c]);
     }
     if (tid < 2) s_flag[tid] = 0;
-    if (tid < kLazyHeads * S) s_fold[1][tid / S][tid % S] = 1.f;  // "stage -1"
     {
-        const int64_t o0 = load_order(0), o1 = load_order(1);
+        const int o0 = load_order(0), o1 = load_order(1);
         if (tid < 64) {
             decode_order(0, o0);
             decode_order(1, o1);
@@ -547,27 +560,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     // v, w of the next write in stream order (across stages)
     RawCols<T, CPL> nv, nw_;
     auto fetch = [&](int slot, int e, RawCols<T, CPL> &vv, RawCols<T, CPL> &ww) {
-        const int64_t off = int64_t(s_tok[slot][e]) * hw + lane_col;
-        vv.load(p.v + off);
-        ww.load(p.w + off);
+        const int64_t row = int64_t(__builtin_amdgcn_readfirstlane(s_tok[slot][e])) * hw;
+        vv.load(reinterpret_cast<const T *>(reinterpret_cast<const char *>(p.v + row) + lane_bytes));
+        ww.load(reinterpret_cast<const T *>(reinterpret_cast<const char *>(p.w + row) + lane_bytes));
     };
     bool prefetched = false;  // nv, nw_ hold the current stage's first write
 
     for (int st = 0; st < nstages; ++st) {
-        const int slot = st % 3, buf = st & 1;
-        const int64_t base = start + int64_t(st) * NE;
+        const int slot = st % 3;
         // next stages' loads, in flight during this stage's value loop
-        const int64_t o2 = load_order(st + 2);
+        const int o2 = load_order(st + 2);
         issue_prep(st + 1);
 
-        // Fold s into Mh: the true state at the stage start, which is a
-        // rounding/snapshot point when the offset is > 0.
-#pragma unroll
-        for (int r = 0; r < S; ++r) {
-            const float f = s_fold[buf ^ 1][lh][r];
-#pragma unroll
-            for (int c = 0; c < CPL; ++c) h[r][c] *= f;
-        }
+        // The state at the stage start (folded at the end of the previous
+        // stage) is a rounding/snapshot point when the offset is > 0.
         if (st > 0) {
             if (rounding) {
 #pragma unroll
@@ -577,7 +583,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
             }
             // snapshot of the state before event `base` (see routed_forward_kernel)
             if (p.snap) {
-                const int64_t sslot = base / p.snap_interval - 1;
+                // stage starts are the multiples of snap_interval = kLazyStage
+                const int64_t sslot = (start / NE) + st - 1;
                 store_state<S, CPL>(p.snap, p.snap_dtype, ((sslot * p.heads + head) * S) * p.width + col0, p.width,
                                     S, h);
             }
@@ -585,13 +592,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 
         const int n = __builtin_amdgcn_readfirstlane(s_n[slot]);
         const int nw = __builtin_amdgcn_readfirstlane(s_nw[slot]);
-        const bool eager = __builtin_amdgcn_readfirstlane(s_eager[buf]) != 0;
+        const bool eager = __builtin_amdgcn_readfirstlane(s_eager) != 0;
         const int next_slot = (st + 1) % 3;
         const bool next_has_write = st + 1 < nstages && s_nw[next_slot] > 0;
 
         auto read_event = [&](int i) {
-            const int64_t zrow = int64_t(__builtin_amdgcn_readfirstlane(s_route[slot][i]));
-            const float *row = &s_rows[buf][i][lh][0][0];
+            const int64_t zrow = int64_t(__builtin_amdgcn_readfirstlane(s_route[slot][i])) * hw;
+            const float *row = &s_rows[i][lh][0][0];
             float gamma[S];
 #pragma unroll
             for (int r = 0; r < S; ++r) gamma[r] = row[r];
@@ -603,7 +610,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
                 for (int r = 0; r < S; ++r) acc = fmaf(gamma[r], h[r][c], acc);
                 z[c] = acc;
             }
-            store_row<CPL>(p.zbuf + zrow * hw + lane_col, z);
+            store_row<CPL>(reinterpret_cast<T *>(reinterpret_cast<char *>(p.zbuf + zrow) + lane_bytes), z);
         };
         // Events in packed order, as runs: the reads before each write, then
         // the write, so the state is updated exactly once per iteration and
@@ -625,8 +632,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 #pragma unroll 1
                 for (; i < wi_; ++i) read_event(i);
                 i = wi_ + 1;
-                const float *row = &s_rows[buf][wi_][lh][0][0];
-                const float pw = s_pw[buf][wi_];
+                const float *row = &s_rows[wi_][lh][0][0];
+                const float pw = s_pw[wi_];
                 if (eager) {
                     // hd = diag(d) M first; the update below then uses a and k
                     // (a wave-uniform branch: the stage's form is uniform)
@@ -643,14 +650,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
                     nalpha[r] = row[r];
                     beta[r] = row[S + r];
                 }
-                float x[CPL];
-                gated_values<CPL>(wc, vc, pw, x);
+                GatedValues<T, CPL> x;
+                x.make(wc, vc, pw);
                 // lazy: u = x - sum (a s') Mh, Mh += (k / s') u;  eager: u = x - sum a hd, M = hd + k u
 #pragma unroll
                 for (int c = 0; c < CPL; ++c) {
-                    float u = x[c];
+                    float u = nalpha[0] * h[0][c];
 #pragma unroll
-                    for (int r = 0; r < S; ++r) u = fmaf(nalpha[r], h[r][c], u);
+                    for (int r = 1; r < S; ++r) u = fmaf(nalpha[r], h[r][c], u);
+                    u = x.add_to(u, c);
 #pragma unroll
                     for (int r = 0; r < S; ++r) h[r][c] = fmaf(beta[r], u, h[r][c]);
                 }
@@ -659,22 +667,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
             for (; i < n; ++i) read_event(i);
         }
 
+        // fold s into Mh: the true state at the stage end
+#pragma unroll
+        for (int r = 0; r < S; ++r) {
+            const float f = s_fold[lh][r];
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) h[r][c] *= f;
+        }
         // metadata of stage st+2 and operands of stage st+1
         if (tid < 64) decode_order(st + 2, o2);
         if (st + 1 < nstages) finish_prep(st + 1);
-        else __syncthreads();
     }
-    __syncthreads();
     if (p.final_state) {
-        const int lbuf = (nstages - 1) & 1;
-        if (nstages > 0) {
-#pragma unroll
-            for (int r = 0; r < S; ++r) {
-                const float f = s_fold[lbuf][lh][r];
-#pragma unroll
-                for (int c = 0; c < CPL; ++c) h[r][c] *= f;
-            }
-        }
         const int64_t final_offset = bidx * (int64_t(p.banks) * p.heads * S * p.width) + state_offset;
         store_state<S, CPL>(p.final_state, p.final_dtype, final_offset, p.width, S, h);
     }
