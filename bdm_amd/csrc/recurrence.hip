@@ -20,8 +20,9 @@
 // one L2 instead of eight.
 //
 // Read results (one S-row contraction per read event and head) go to a BF16
-// (ctrl dtype) buffer indexed by the read's original slot token*KR + j; the
-// combine kernel adds a token's KR reads in increasing bank id, rounding after
+// (ctrl dtype) buffer at row token*KR + rank, where rank orders the token's
+// reads by bank id (read_slot_kernel); the combine kernel then streams each
+// token's KR consecutive rows and adds them in that order, rounding after
 // every add (the production readout order).
 #include <type_traits>
 
@@ -44,6 +45,7 @@ struct ForwardParams {
     void *final_state;
     void *snap;
     T *zbuf;
+    const int *zslot;  // read route -> its row of zbuf (token*KR + rank of the bank)
     int64_t init_bstride;
     int64_t nt, time;
     int heads, s_real, width, banks, kw, kr;
@@ -162,7 +164,7 @@ __global__ __launch_bounds__(256) void routed_forward_kernel(ForwardParams<T> p)
             const bool rd = o >= write_events;
             const int64_t route = rd ? o - write_events : o;
             s_token[threadIdx.x] = rd ? route / p.kr : route / p.kw;
-            s_slot[threadIdx.x] = rd ? route : -1;
+            s_slot[threadIdx.x] = rd ? p.zslot[route] : -1;
             s_weight[threadIdx.x] = rd ? to_f32(p.rw[route]) : to_f32(p.ww[route]);
         }
         __syncthreads();
@@ -341,7 +343,6 @@ __device__ __forceinline__ float row_prefix_product(float x) {
 }
 
 constexpr int kLazyStage = 16;
-constexpr int kLazyHeads = 8;  // heads per workgroup
 constexpr float kScaleFloor = 0x1p-32f;
 
 // Raw row data one prep lane loads for its (event, head, 4 rows).
@@ -352,6 +353,7 @@ struct PrepLoads<bf16_t> {
     uint2 key, erase;  // k (or q for a read), b: 4 BF16 each
     float4 gate;       // g
     uint32_t weight;   // route weight, BF16 in the low half
+    int zrow;          // a read's row of the read buffer
     __device__ __forceinline__ float key_at(int r) const {
         const uint32_t w = r < 2 ? key.x : key.y;
         return __uint_as_float((r & 1) ? (w & 0xffff0000u) : (w << 16));
@@ -366,6 +368,7 @@ template <>
 struct PrepLoads<float> {
     float4 key, erase, gate;
     float weight_raw;
+    int zrow;
     __device__ __forceinline__ float key_at(int r) const { return (&key.x)[r]; }
     __device__ __forceinline__ float erase_at(int r) const { return (&erase.x)[r]; }
     __device__ __forceinline__ float weight_f() const { return weight_raw; }
@@ -377,7 +380,10 @@ __device__ __forceinline__ void load_vec4(const T *p, uint2 &out) {
 }
 __device__ __forceinline__ void load_vec4(const float *p, float4 &out) { out = *reinterpret_cast<const float4 *>(p); }
 
-template <typename T, int CPL>
+// HB heads per workgroup of 32 * HB threads (HB = 2: one wave, so its
+// barriers never wait for other waves; HB = 8 for narrow heads, where the
+// value columns of 8 heads fit in 256 lanes).
+template <typename T, int CPL, int HB>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void lazy_forward_kernel(
     ForwardParams<T> p) {
     constexpr int S = 8;
@@ -392,8 +398,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     // Row operands of the current stage (written by the prep of a stage after
     // every wave has left the previous stage's value loop): lazy [0] = -alpha,
     // [1] = beta; eager [0] = -a, [1] = k, [2] = d; a read [0] = gamma.
-    __shared__ float s_rows[NE][kLazyHeads][3][S];
-    __shared__ float s_fold[kLazyHeads][S];  // s at the end of the stage (1 for eager)
+    __shared__ float s_rows[NE][HB][3][S];
+    __shared__ float s_fold[HB][S];  // s at the end of the stage (1 for eager)
     __shared__ float s_pw[NE];               // route weight of each event of the stage
     __shared__ int s_eager;
     __shared__ int s_flag[2];  // by stage parity: reset two barriers before its next use
@@ -414,7 +420,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     // this lane's byte offset in such a row (rows are addressed from a
     // wave-uniform base plus this 32-bit offset)
     const uint32_t lane_bytes = uint32_t((head * p.width + col0) * int(sizeof(T)));
-    // prep role: (event pe, head ph, rows 4*half .. 4*half+3)
+    // prep role: (event pe, head ph, rows 4*half .. 4*half+3); 32 lanes per head
     const int pe = tid & (NE - 1);
     const int ph = (tid >> 4) >> 1;
     const int half = (tid >> 4) & 1;
@@ -465,6 +471,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         const int64_t row = (int64_t(s_tok[slot][pe]) * p.heads + head0 + ph) * S + 4 * half;
         const int route = s_route[slot][pe];
         if (rd) {
+            if (tid < NE) pl.zrow = p.zslot[route];
             load_vec4(p.q + row, pl.key);
             if constexpr (std::is_same<T, bf16_t>::value)
                 pl.weight = p.rw[route].bits;
@@ -524,7 +531,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
                     row[2][rr] = d[r];
                 }
             }
-            if (tid < NE) s_pw[pe] = pw;
+            if (tid < NE) {
+                s_pw[pe] = pw;
+                if (rd) s_route[slot][pe] = pl.zrow;  // from here on: the read's row of zbuf
+            }
             if (pe == n - 1) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) s_fold[ph][4 * half + r] = eager ? 1.f : sc[r];
@@ -684,39 +694,49 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     }
 }
 
+// zslot[token*KR + j] = token*KR + (rank of read j among the token's reads
+// in increasing bank id, ties by j): the row of the read buffer that read
+// goes to, so the combine folds a token's rows in their stored order.
+__global__ __launch_bounds__(256) void read_slot_kernel(const int64_t *__restrict__ read_indices, int64_t routes,
+                                                        int kr, int *__restrict__ zslot) {
+    // one thread per read route; the token's KR indices are independent loads
+    const int64_t route = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (route >= routes) return;
+    const int64_t first = route - route % kr;
+    const int j = int(route - first);
+    const int64_t mine = read_indices[route];
+    int rank = 0;
+#pragma unroll 8
+    for (int jj = 0; jj < kr; ++jj) {
+        const int64_t other = read_indices[first + jj];
+        rank += (other < mine) || (other == mine && jj < j);
+    }
+    zslot[route] = int(first + rank);
+}
+
 // y[token, :] = fold over the token's reads in increasing bank id of
-// bf(total + z).  One workgroup per token; a thread owns CPL columns.
+// bf(total + z) (role_bank_dispatch.py:209-215): the token's KR rows of the
+// read buffer are already in that order.  One thread per (token, CPL columns).
 template <typename T, int CPL>
-__global__ __launch_bounds__(256) void ordered_combine_kernel(const T *__restrict__ zbuf,
-                                                              const int64_t *__restrict__ read_indices,
-                                                              T *__restrict__ y, int kr, int row_width) {
-    __shared__ int64_t s_idx[32];
-    __shared__ int s_rank_slot[32];
-    const int64_t token = blockIdx.x;
-    if (int(threadIdx.x) < kr) s_idx[threadIdx.x] = read_indices[token * kr + threadIdx.x];
-    __syncthreads();
-    if (int(threadIdx.x) < kr) {
-        const int64_t mine = s_idx[threadIdx.x];
-        int rank = 0;
-        for (int j = 0; j < kr; ++j) {
-            const int64_t other = s_idx[j];
-            rank += (other < mine) || (other == mine && j < int(threadIdx.x));
-        }
-        s_rank_slot[rank] = threadIdx.x;
-    }
-    __syncthreads();
-    for (int col0 = threadIdx.x * CPL; col0 < row_width; col0 += blockDim.x * CPL) {
-        float total[CPL];
+__global__ __launch_bounds__(256) void ordered_combine_kernel(const T *__restrict__ zbuf, T *__restrict__ y,
+                                                              int64_t nt, int kr, int row_width) {
+    const int chunks = row_width / CPL;
+    const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t token = idx / chunks;
+    if (token >= nt) return;
+    const int col0 = int(idx - token * chunks) * CPL;
+    const T *z = zbuf + token * kr * row_width + col0;
+    float total[CPL];
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) total[c] = 0.f;
-        for (int j = 0; j < kr; ++j) {
-            float z[CPL];
-            load_row<CPL>(zbuf + (token * kr + s_rank_slot[j]) * row_width + col0, z);
+    for (int c = 0; c < CPL; ++c) total[c] = 0.f;
+#pragma unroll 8
+    for (int j = 0; j < kr; ++j) {
+        float v[CPL];
+        load_row<CPL>(z + int64_t(j) * row_width, v);
 #pragma unroll
-            for (int c = 0; c < CPL; ++c) total[c] = round_to<T>(total[c] + z[c]);
-        }
-        store_row<CPL>(y + token * row_width + col0, total);
+        for (int c = 0; c < CPL; ++c) total[c] = round_to<T>(total[c] + v[c]);
     }
+    store_row<CPL>(y + token * row_width + col0, total);
 }
 
 // A kernel rather than hipMemsetAsync, so callers may capture it in a graph.
@@ -727,7 +747,7 @@ __global__ __launch_bounds__(256) void zero_fill_kernel(T *__restrict__ out, int
 }
 
 template <typename T, int S, int CPL, bool kLazy = false>
-int launch_forward(const bdm_forward_args &a, T *zbuf, hipStream_t stream) {
+int launch_forward(const bdm_forward_args &a, T *zbuf, int *zslot, hipStream_t stream) {
     if (a.head_width / CPL > 256)
         return fail(BDM_ERR_UNSUPPORTED, "forward: head_width %d needs more than 256 lanes", a.head_width);
     ForwardParams<T> p{};
@@ -744,6 +764,7 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, hipStream_t stream) {
     p.initial = a.initial;
     p.final_state = a.final_state;
     p.zbuf = zbuf;
+    p.zslot = zslot;
     p.init_bstride = a.initial_batch_stride;
     p.nt = a.batch * a.time;
     p.time = a.time;
@@ -755,7 +776,9 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, hipStream_t stream) {
     p.kr = a.read_banks;
     p.lanes_per_head = a.head_width / CPL;
     p.heads_per_block = 256 / p.lanes_per_head;
-    if (kLazy && p.heads_per_block > kLazyHeads) p.heads_per_block = kLazyHeads;
+    // lazy kernel: 2 heads per one-wave workgroup when a head has 32 lanes, else 8 per 256 threads
+    const int lazy_hb = p.lanes_per_head == 32 ? 2 : 8;
+    if (kLazy && p.heads_per_block > lazy_hb) p.heads_per_block = lazy_hb;
     if (p.heads_per_block > a.heads) p.heads_per_block = a.heads;
     p.round_interval = a.round_interval;
     p.routed_decay = a.routed_decay;
@@ -769,9 +792,19 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, hipStream_t stream) {
     p.xcd_remap = (nseg % 8 == 0) ? 1 : 0;
     const int threads = ((p.heads_per_block * p.lanes_per_head + kWave - 1) / kWave) * kWave;
     const dim3 grid(unsigned(nseg), unsigned((a.heads + p.heads_per_block - 1) / p.heads_per_block));
+    if (a.read_banks > 0) {
+        const int64_t nt = a.batch * a.time;
+        const int64_t routes = nt * a.read_banks;
+        read_slot_kernel<<<unsigned((routes + 255) / 256), 256, 0, stream>>>(a.read_indices, routes, a.read_banks,
+                                                                              zslot);
+        if (int rc = check_launch("read_slot_kernel")) return rc;
+    }
     if constexpr (kLazy) {
-        // 256 threads always: the prep role needs one lane per (event, head, half)
-        lazy_forward_kernel<T, CPL><<<grid, 256, 0, stream>>>(p);
+        // the prep role needs one lane per (event, head, half): 32 per head
+        if (lazy_hb == 2)
+            lazy_forward_kernel<T, CPL, 2><<<grid, 64, 0, stream>>>(p);
+        else
+            lazy_forward_kernel<T, CPL, 8><<<grid, 256, 0, stream>>>(p);
         if (int rc = check_launch("lazy_forward_kernel")) return rc;
     } else {
         routed_forward_kernel<T, S, CPL><<<grid, threads, 0, stream>>>(p);
@@ -783,14 +816,14 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, hipStream_t stream) {
     if (a.read_banks > 0) {
         // 16-byte rows where the layout allows (8 BF16 or 4 FP32 columns)
         constexpr int CC = sizeof(T) == 2 ? 8 : 4;
-        if (row_width % CC == 0 && a.head_width % CC == 0) {
-            const int cthreads = min(256, max(kWave, ((row_width / CC + kWave - 1) / kWave) * kWave));
-            ordered_combine_kernel<T, CC><<<unsigned(nt), cthreads, 0, stream>>>(
-                zbuf, a.read_indices, static_cast<T *>(a.output), a.read_banks, row_width);
+        if (row_width % CC == 0) {
+            const int64_t threads = nt * (row_width / CC);
+            ordered_combine_kernel<T, CC><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
+                zbuf, static_cast<T *>(a.output), nt, a.read_banks, row_width);
         } else {
-            const int cthreads = min(256, max(kWave, ((row_width + kWave - 1) / kWave) * kWave));
-            ordered_combine_kernel<T, 1><<<unsigned(nt), cthreads, 0, stream>>>(
-                zbuf, a.read_indices, static_cast<T *>(a.output), a.read_banks, row_width);
+            const int64_t threads = nt * row_width;
+            ordered_combine_kernel<T, 1><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
+                zbuf, static_cast<T *>(a.output), nt, a.read_banks, row_width);
         }
     } else {
         const int64_t count = nt * row_width;
@@ -800,7 +833,7 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, hipStream_t stream) {
 }
 
 template <typename T>
-int dispatch_forward(const bdm_forward_args &a, T *zbuf, hipStream_t stream) {
+int dispatch_forward(const bdm_forward_args &a, T *zbuf, int *zslot, hipStream_t stream) {
     // Vector row loads need 16-byte aligned rows: aligned bases, and a state
     // batch stride that keeps them aligned.
     const bool vec = a.initial_batch_stride % 8 == 0;
@@ -812,16 +845,16 @@ int dispatch_forward(const bdm_forward_args &a, T *zbuf, hipStream_t stream) {
         const bool small_index = nt * (a.write_banks > a.read_banks ? a.write_banks : a.read_banks) < INT32_MAX;
         if (vec && a.bank_size == 8 && a.head_width % lc == 0 && a.head_width / lc <= 64 && fold == kLazyStage &&
             small_index)
-            return launch_forward<T, 8, lc, true>(a, zbuf, stream);
-        if (vec && a.head_width % 8 == 0) return launch_forward<T, 8, 8>(a, zbuf, stream);
-        return launch_forward<T, 8, 1>(a, zbuf, stream);
+            return launch_forward<T, 8, lc, true>(a, zbuf, zslot, stream);
+        if (vec && a.head_width % 8 == 0) return launch_forward<T, 8, 8>(a, zbuf, zslot, stream);
+        return launch_forward<T, 8, 1>(a, zbuf, zslot, stream);
     }
     if (a.bank_size <= 16) {
-        if (vec && a.head_width % 4 == 0) return launch_forward<T, 16, 4>(a, zbuf, stream);
-        return launch_forward<T, 16, 1>(a, zbuf, stream);
+        if (vec && a.head_width % 4 == 0) return launch_forward<T, 16, 4>(a, zbuf, zslot, stream);
+        return launch_forward<T, 16, 1>(a, zbuf, zslot, stream);
     }
-    if (vec && a.head_width % 2 == 0) return launch_forward<T, 32, 2>(a, zbuf, stream);
-    return launch_forward<T, 32, 1>(a, zbuf, stream);
+    if (vec && a.head_width % 2 == 0) return launch_forward<T, 32, 2>(a, zbuf, zslot, stream);
+    return launch_forward<T, 32, 1>(a, zbuf, zslot, stream);
 }
 
 size_t elem_size(int dtype) { return dtype == BDM_BF16 ? 2 : 4; }
@@ -829,11 +862,18 @@ size_t elem_size(int dtype) { return dtype == BDM_BF16 ? 2 : 4; }
 }  // namespace
 }  // namespace bdm
 
-extern "C" size_t bdm_forward_workspace_size(const bdm_forward_args *a) {
-    if (!a || a->batch <= 0 || a->time <= 0 || a->heads <= 0 || a->head_width <= 0 || a->read_banks < 0) return 0;
+// Workspace of bdm_forward: the read buffer (one ctrl_dtype row of H*v per
+// read event) followed by its row map (one int32 per read event).
+static size_t forward_zbuf_bytes(const bdm_forward_args *a) {
     const size_t bytes = size_t(a->batch) * size_t(a->time) * size_t(a->read_banks) * size_t(a->heads) *
                          size_t(a->head_width) * bdm::elem_size(a->ctrl_dtype);
     return (bytes + 255) / 256 * 256;
+}
+
+extern "C" size_t bdm_forward_workspace_size(const bdm_forward_args *a) {
+    if (!a || a->batch <= 0 || a->time <= 0 || a->heads <= 0 || a->head_width <= 0 || a->read_banks < 0) return 0;
+    const size_t slots = size_t(a->batch) * size_t(a->time) * size_t(a->read_banks) * sizeof(int);
+    return forward_zbuf_bytes(a) + (slots + 255) / 256 * 256;
 }
 
 extern "C" int bdm_forward(const bdm_forward_args *a, void *workspace, size_t workspace_bytes, void *stream) {
@@ -870,7 +910,10 @@ extern "C" int bdm_forward(const bdm_forward_args *a, void *workspace, size_t wo
     const size_t need = bdm_forward_workspace_size(a);
     if (need && (!workspace || workspace_bytes < need))
         return fail(BDM_ERR_WORKSPACE, "forward: workspace %zu < %zu bytes", workspace_bytes, need);
+    if (a->batch * a->time * a->read_banks > int64_t(INT32_MAX))
+        return fail(BDM_ERR_UNSUPPORTED, "forward: more than 2^31 read events");
     hipStream_t s = as_stream(stream);
-    if (a->ctrl_dtype == BDM_BF16) return dispatch_forward<bf16_t>(*a, static_cast<bf16_t *>(workspace), s);
-    return dispatch_forward<float>(*a, static_cast<float *>(workspace), s);
+    int *zslot = reinterpret_cast<int *>(static_cast<char *>(workspace) + forward_zbuf_bytes(a));
+    if (a->ctrl_dtype == BDM_BF16) return dispatch_forward<bf16_t>(*a, static_cast<bf16_t *>(workspace), zslot, s);
+    return dispatch_forward<float>(*a, static_cast<float *>(workspace), zslot, s);
 }

@@ -43,7 +43,10 @@ def test_workspace_sizes(lib):
     args = _lib.ForwardArgs()
     args.batch, args.time, args.heads, args.head_width, args.read_banks = 2, 10, 3, 16, 4
     args.ctrl_dtype = _lib.BDM_BF16
-    assert lib.bdm_forward_workspace_size(ctypes.byref(args)) == (2 * 10 * 4 * 3 * 16 * 2 + 255) // 256 * 256
+    # read rows (BF16, H*v per read event) then their row map (int32 per read event)
+    rows = (2 * 10 * 4 * 3 * 16 * 2 + 255) // 256 * 256
+    slots = (2 * 10 * 4 * 4 + 255) // 256 * 256
+    assert lib.bdm_forward_workspace_size(ctypes.byref(args)) == rows + slots
 
 
 def test_invalid_arguments_are_rejected_without_a_launch(lib):
