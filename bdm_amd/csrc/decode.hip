@@ -7,12 +7,15 @@
 //
 // One workgroup per (sequence, head).  Lane group j (head_width / CPL lanes)
 // owns write slot j and read slot j.  A step makes two dependent trips to HBM:
-// first the bank indices and controller rows (all independent of a bank id),
-// then every bank state the step touches — the write banks and the read banks
-// that are not also written — requested at once.  Writes are applied and stored (rounded
+// first the bank indices and controller rows (all independent of a bank id,
+// issued together, with no barrier behind them), then every bank state the
+// step touches — the write banks and the read banks that are not also
+// written — requested at once.  Writes are applied and stored (rounded
 // to the state dtype), and also kept in LDS, so a read of a bank written by the
 // same token sees the stored value without another trip to HBM.  The reads are
 // then combined in increasing bank id with a rounding after every add.
+#include <type_traits>
+
 #include "bdm_common.h"
 #include "recurrence_ops.h"
 
@@ -20,6 +23,18 @@ namespace bdm {
 namespace {
 
 constexpr int kMaxSlots = 16;
+
+// One token's S-element controller row: whole 16-byte vectors when the row is
+// full width and aligned, else element by element (rows >= s_real are 0).
+template <int S, bool VEC, typename E>
+__device__ __forceinline__ void load_ctrl_row(const E *p, int s_real, float (&out)[S]) {
+    if constexpr (VEC) {
+        load_row<S>(p, out);  // the launcher checked s_real == S and the alignment
+    } else {
+#pragma unroll
+        for (int r = 0; r < S; ++r) out[r] = r < s_real ? to_f32(p[r]) : 0.f;
+    }
+}
 
 template <typename T>
 struct DecodeParams {
@@ -32,11 +47,14 @@ struct DecodeParams {
     T *out;
     int heads, s_real, width, banks, kw, kr;
     int lanes_per_slot;
+    int vec_rows;  // q, k, b, g rows of S elements can be read as 16-byte vectors
     int state_dtype, routed_decay;
     float scale;
 };
 
-template <typename T, int S, int CPL>
+// SE: the state element type (bf16_t or float, the state_dtype argument);
+// KMAX >= the selected banks per role, KFIX: exactly KMAX banks in both roles.
+template <typename T, typename SE, int S, int CPL, bool VEC, int KMAX, bool KFIX>
 __global__ __launch_bounds__(512) void decode_kernel(DecodeParams<T> p) {
     extern __shared__ float smem[];
     // smem layout: written states [kw][S][width], read values [kr][width]
@@ -51,69 +69,69 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeParams<T> p) {
     const int64_t row = seq * p.heads + head;
     const bool has_write = slot < p.kw;
     const bool has_read = slot < p.kr;
+    auto clamp_bank = [&](int64_t bank) { return bank < 0 ? int64_t(0) : (bank >= p.banks ? int64_t(p.banks - 1) : bank); };
 
-    // ---- round trip 1: everything that does not depend on a bank index.  The
-    // per-token values are loaded once for the workgroup, one element per lane
-    // of the first wave(s), and shared through LDS (a conditional scalar load
-    // per value would serialise them).
-    __shared__ int64_t s_wbank[kMaxSlots], s_rbank[kMaxSlots];
-    __shared__ float s_pw[kMaxSlots], s_pr[kMaxSlots];
-    __shared__ float s_ctrl[4][32];  // k, g, b, q rows (S <= 32)
-    {
-        const int nk = p.kw + p.kr;
-        for (int t = threadIdx.x; t < nk + 4 * S; t += blockDim.x) {
-            if (t < p.kw) {
-                const int64_t bank = p.wi[seq * p.kw + t];
-                s_wbank[t] = bank < 0 ? 0 : (bank >= p.banks ? p.banks - 1 : bank);
-                s_pw[t] = to_f32(p.ww[seq * p.kw + t]);
-            } else if (t < nk) {
-                const int j = t - p.kw;
-                const int64_t bank = p.ri[seq * p.kr + j];
-                s_rbank[j] = bank < 0 ? 0 : (bank >= p.banks ? p.banks - 1 : bank);
-                s_pr[j] = to_f32(p.rw[seq * p.kr + j]);
-            } else {
-                const int e = t - nk, which = e / S, r = e % S;
-                float x = 0.f;
-                if (r < p.s_real) {
-                    const int64_t at = row * p.s_real + r;
-                    x = which == 0 ? to_f32(p.k[at])
-                                   : which == 1 ? p.g[at] : which == 2 ? to_f32(p.b[at]) : to_f32(p.q[at]);
-                }
-                s_ctrl[which][r] = x;
-            }
+    // ---- round trip 1: everything that does not depend on a bank index,
+    // issued together with no barrier behind it.  The token's bank indices,
+    // route weights and controller rows have workgroup-uniform addresses and
+    // are read by scalar loads (entry j >= K re-reads entry K-1, so every
+    // address is in bounds and the loads are unconditional); each lane group
+    // selects its own slot's entries.  The lane's value columns are vector loads.
+    const int64_t *wi = p.wi + seq * p.kw;
+    const int64_t *ri = p.ri + seq * p.kr;
+    const T *wwp = p.ww + seq * p.kw;
+    const T *rwp = p.rw + seq * p.kr;
+    int64_t wbank[KMAX], rbank[KMAX];
+    float wwt[KMAX], rwt[KMAX];
+    if constexpr (KFIX) {
+        // exactly KMAX banks per role: straight-line loads of whole rows
+#pragma unroll
+        for (int j = 0; j < KMAX; ++j) {
+            wbank[j] = clamp_bank(wi[j]);
+            rbank[j] = clamp_bank(ri[j]);
         }
+        load_row<KMAX>(wwp, wwt);
+        load_row<KMAX>(rwp, rwt);
+    } else {
+#pragma unroll
+        for (int j = 0; j < KMAX; ++j) {
+            const int jw = min(j, max(p.kw - 1, 0)), jr = min(j, max(p.kr - 1, 0));
+            wbank[j] = p.kw > 0 ? clamp_bank(wi[jw]) : 0;
+            wwt[j] = p.kw > 0 ? to_f32(wwp[jw]) : 0.f;
+            rbank[j] = p.kr > 0 ? clamp_bank(ri[jr]) : 0;
+            rwt[j] = p.kr > 0 ? to_f32(rwp[jr]) : 0.f;
+        }
+    }
+    float kk[S], gg[S], bb[S], qq[S];
+    {
+        const int64_t at = row * p.s_real;
+        load_ctrl_row<S, VEC>(p.k + at, p.s_real, kk);
+        load_ctrl_row<S, VEC>(p.g + at, p.s_real, gg);
+        load_ctrl_row<S, VEC>(p.b + at, p.s_real, bb);
+        load_ctrl_row<S, VEC>(p.q + at, p.s_real, qq);
     }
     float vv[CPL], wv[CPL];
     load_row<CPL>(p.v + row * p.width + col0, vv);
     load_row<CPL>(p.w + row * p.width + col0, wv);
-    __syncthreads();
-    float kk[S], gg[S], bb[S], qq[S];
+    int64_t my_w = 0, my_r = 0;
+    float pw = 0.f, pr = 0.f;
 #pragma unroll
-    for (int r = 0; r < S; ++r) {
-        kk[r] = s_ctrl[0][r];
-        gg[r] = s_ctrl[1][r];
-        bb[r] = s_ctrl[2][r];
-        qq[r] = s_ctrl[3][r];
+    for (int j = 0; j < KMAX; ++j) {
+        if (j == slot) {
+            my_w = wbank[j];
+            my_r = rbank[j];
+            pw = wwt[j];
+            pr = rwt[j];
+        }
     }
-    const float pw = has_write ? s_pw[slot] : 0.f;
-    const float pr = has_read ? s_pr[slot] : 0.f;
-    // this lane group's write bank and read bank; a read of a bank written by
-    // the same token is served from the stored post-write value in LDS
-    const int64_t my_w = has_write ? s_wbank[slot] : 0;
-    const int64_t my_r = has_read ? s_rbank[slot] : 0;
+    if (!has_write) pw = 0.f;
+    // a read of a bank written by the same token is served from the stored
+    // post-write value in LDS
     int read_from_write = -1;
-    if (has_read) {
-        for (int j = 0; j < p.kw; ++j)
-            if (s_wbank[j] == my_r) read_from_write = j;
-    }
-    // thread t < KR ranks read slot t by (bank id, slot)
-    if (int(threadIdx.x) < p.kr) {
-        const int t = threadIdx.x;
-        const int64_t mine = s_rbank[t];
-        int rank = 0;
-        for (int j = 0; j < p.kr; ++j) rank += (s_rbank[j] < mine) || (s_rbank[j] == mine && j < t);
-        s_rank_slot[rank] = t;
-    }
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j)
+        if (j < p.kw && wbank[j] == my_r) read_from_write = j;
+    if (!has_read) read_from_write = -1;
 
     // ---- round trip 2: the bank states this step touches
     const int64_t bank_stride = int64_t(p.heads) * p.s_real * p.width;  // elements per bank
@@ -123,27 +141,35 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeParams<T> p) {
     for (int r = 0; r < S; ++r)
 #pragma unroll
         for (int c = 0; c < CPL; ++c) hw[r][c] = hr[r][c] = 0.f;
-    if (has_write) {
-        const int64_t base = seq_base + my_w * bank_stride;
+    // Unconditional, branch-free loads (a conditional load under divergent
+    // control makes the compiler wait at the join): a lane group without a
+    // write loads bank 0, a read served from a same-step write re-reads the
+    // write bank's lines, already requested by the write load.
+    const bool load_read = has_read && read_from_write < 0;
+    {
+        const int64_t wbase = seq_base + my_w * bank_stride;
+        const int64_t rbase = load_read ? seq_base + my_r * bank_stride : wbase;
+        const SE *st = static_cast<const SE *>(p.state);
 #pragma unroll
         for (int r = 0; r < S; ++r) {
-            if (r >= p.s_real) continue;
-            if (p.state_dtype == BDM_BF16)
-                load_row<CPL>(static_cast<const bf16_t *>(p.state) + base + int64_t(r) * p.width, hw[r]);
-            else
-                load_row<CPL>(static_cast<const float *>(p.state) + base + int64_t(r) * p.width, hw[r]);
+            if (VEC || r < p.s_real) {
+                load_row<CPL>(st + wbase + int64_t(r) * p.width, hw[r]);
+                load_row<CPL>(st + rbase + int64_t(r) * p.width, hr[r]);
+            }
         }
     }
-    if (has_read && read_from_write < 0) {
-        const int64_t base = seq_base + my_r * bank_stride;
+    // thread t < KR ranks read slot t by (bank id, slot)
+    if (int(threadIdx.x) < p.kr) {
+        const int t = threadIdx.x;
+        int64_t mine = rbank[0];
 #pragma unroll
-        for (int r = 0; r < S; ++r) {
-            if (r >= p.s_real) continue;
-            if (p.state_dtype == BDM_BF16)
-                load_row<CPL>(static_cast<const bf16_t *>(p.state) + base + int64_t(r) * p.width, hr[r]);
-            else
-                load_row<CPL>(static_cast<const float *>(p.state) + base + int64_t(r) * p.width, hr[r]);
-        }
+        for (int j = 1; j < KMAX; ++j)
+            if (j == t) mine = rbank[j];
+        int rank = 0;
+#pragma unroll
+        for (int j = 0; j < KMAX; ++j)
+            if (j < p.kr) rank += (rbank[j] < mine) || (rbank[j] == mine && j < t);
+        s_rank_slot[rank] = t;
     }
 
     // ---- writes (inference.py:21-34 with the write rule of role_bank_kernel.py:40-43)
@@ -157,14 +183,12 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeParams<T> p) {
         const int64_t base = seq_base + my_w * bank_stride;
 #pragma unroll
         for (int r = 0; r < S; ++r) {
-            if (r >= p.s_real) continue;
-            if (p.state_dtype == BDM_BF16) {
+            if (!VEC && r >= p.s_real) continue;
+            if constexpr (std::is_same<SE, bf16_t>::value) {
 #pragma unroll
                 for (int c = 0; c < CPL; ++c) hw[r][c] = round_bf16(hw[r][c]);
-                store_row<CPL>(static_cast<bf16_t *>(p.state) + base + int64_t(r) * p.width, hw[r]);
-            } else {
-                store_row<CPL>(static_cast<float *>(p.state) + base + int64_t(r) * p.width, hw[r]);
             }
+            store_row<CPL>(static_cast<SE *>(p.state) + base + int64_t(r) * p.width, hw[r]);
 #pragma unroll
             for (int c = 0; c < CPL; ++c) written[(slot * S + r) * p.width + col0 + c] = hw[r][c];
         }
@@ -196,8 +220,13 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeParams<T> p) {
     // ---- ordered sum (inference.py:53-67)
     T *out = p.out + seq * int64_t(p.heads) * p.width + int64_t(head) * p.width;
     for (int c = threadIdx.x; c < p.width; c += blockDim.x) {
+        float v[kMaxSlots];
+#pragma unroll
+        for (int j = 0; j < kMaxSlots; ++j) v[j] = j < p.kr ? reads[s_rank_slot[j] * p.width + c] : 0.f;
         float total = 0.f;
-        for (int j = 0; j < p.kr; ++j) total = round_to<T>(total + reads[s_rank_slot[j] * p.width + c]);
+#pragma unroll
+        for (int j = 0; j < kMaxSlots; ++j)
+            if (j < p.kr) total = round_to<T>(total + v[j]);
         out[c] = from_f32<T>(total);
     }
 }
@@ -224,6 +253,11 @@ int launch_decode(const bdm_decode_args &a, hipStream_t stream) {
     p.kw = a.write_banks;
     p.kr = a.read_banks;
     p.lanes_per_slot = a.head_width / CPL;
+    // vector row loads need the S-element rows at 16-byte boundaries
+    p.vec_rows = (a.bank_size == S && aligned(a.q, 16) && aligned(a.k, 16) && aligned(a.b, 16) && aligned(a.g, 16) &&
+                  (S * sizeof(T)) % 16 == 0)
+                     ? 1
+                     : 0;
     p.state_dtype = a.state_dtype;
     p.routed_decay = a.routed_decay;
     p.scale = a.scale;
@@ -232,13 +266,30 @@ int launch_decode(const bdm_decode_args &a, hipStream_t stream) {
     if (threads > 512) return fail(BDM_ERR_UNSUPPORTED, "decode: %d lanes per workgroup", threads);
     const size_t lds = (size_t(a.write_banks) * S * a.head_width + size_t(a.read_banks) * a.head_width) * sizeof(float);
     if (lds > 64 * 1024) return fail(BDM_ERR_UNSUPPORTED, "decode: %zu bytes of LDS", lds);
-    decode_kernel<T, S, CPL><<<unsigned(a.batch * a.heads), threads, lds, stream>>>(p);
+    const unsigned grid = unsigned(a.batch * a.heads);
+    // the production geometry (8 banks per role, full-width aligned rows) gets
+    // straight-line loads; anything else the general form
+    const bool fast = p.vec_rows && a.write_banks == 8 && a.read_banks == 8 && aligned(a.write_weights, 16) &&
+                      aligned(a.read_weights, 16) && aligned(a.write_indices, 16) && aligned(a.read_indices, 16);
+    if (a.state_dtype == BDM_BF16) {
+        if (fast)
+            decode_kernel<T, bf16_t, S, CPL, true, 8, true><<<grid, threads, lds, stream>>>(p);
+        else
+            decode_kernel<T, bf16_t, S, CPL, false, kMaxSlots, false><<<grid, threads, lds, stream>>>(p);
+    } else {
+        if (fast)
+            decode_kernel<T, float, S, CPL, true, 8, true><<<grid, threads, lds, stream>>>(p);
+        else
+            decode_kernel<T, float, S, CPL, false, kMaxSlots, false><<<grid, threads, lds, stream>>>(p);
+    }
     return check_launch("decode_kernel");
 }
 
 template <typename T>
 int dispatch_decode(const bdm_decode_args &a, hipStream_t stream) {
     if (a.bank_size <= 8) {
+        // two columns per lane: 64 lanes per slot, more loads in flight per step
+        if (a.head_width % 2 == 0 && a.head_width / 2 <= 64) return launch_decode<T, 8, 2>(a, stream);
         if (a.head_width % 4 == 0 && a.head_width / 4 <= 64) return launch_decode<T, 8, 4>(a, stream);
         if (a.head_width % 8 == 0) return launch_decode<T, 8, 8>(a, stream);
         return launch_decode<T, 8, 1>(a, stream);
