@@ -55,7 +55,16 @@ struct ForwardParams {
     int init_dtype, final_dtype, snap_dtype;
     int xcd_remap;
     float scale;
+    // Long segments cut into pieces (prefill policy only, see lazy_forward_kernel):
+    const int4 *items;     // pieces of cut segments: (segment, piece q, pieces of the segment, state slot)
+    const int *n_items;    // [0]: number of pieces
+    int nseg;              // segments (batch * J)
+    float *pstate;         // [slots, H, S, v] FP32: zero-start end state R_q, then start state M_(q+1)
+    float *ptrans;         // [slots, H, S, S] FP32: transition P_q of piece q
 };
+
+// Events per piece when long segments are cut (a multiple of the stage size).
+constexpr int kPieceEvents = 512;
 
 // Load `S` per-row controller values of one (token, head); rows >= s_real are 0.
 template <int S, typename E>
@@ -383,7 +392,22 @@ __device__ __forceinline__ void load_vec4(const float *p, float4 &out) { out = *
 // HB heads per workgroup of 32 * HB threads (HB = 2: one wave, so its
 // barriers never wait for other waves; HB = 8 for narrow heads, where the
 // value columns of 8 heads fit in 256 lanes).
-template <typename T, int CPL, int HB>
+//
+// MODE 0 runs whole segments (one workgroup each).  Under the prefill policy
+// (no rounding inside the recurrence, no snapshots) a segment is an affine
+// map of its start state, M_end = P M_start + R, so segments longer than
+// kPieceEvents are cut into pieces to balance skewed routing:
+//   MODE 1 runs each piece q of a cut segment from a zero state, without
+//          reads, and stores its end state R_q and its transition P_q (the
+//          lanes 0..7 of a head also carry the 8 columns of P, started at
+//          the identity, through the same write updates with x = 0);
+//   piece_scan_kernel composes M_(q+1) = P_q M_q + R_q from the segment's
+//          initial state;
+//   MODE 2 runs, in one launch, the uncut segments whole (blocks below
+//          nseg, mapped as in MODE 0) and every piece from its start state
+//          M_q (blocks from nseg on), with reads; the last piece of a
+//          segment stores the final state.
+template <typename T, int CPL, int HB, int MODE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void lazy_forward_kernel(
     ForwardParams<T> p) {
     constexpr int S = 8;
@@ -404,8 +428,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     __shared__ int s_eager;
     __shared__ int s_flag[2];  // by stage parity: reset two barriers before its next use
 
-    const int nseg = gridDim.x;
-    const int seg = p.xcd_remap ? int((blockIdx.x % 8) * (nseg / 8) + blockIdx.x / 8) : int(blockIdx.x);
+    int seg, piece = 0, pieces = 1, pslot = -1;
+    const int block = int(blockIdx.x);
+    if (MODE == 0 || (MODE == 2 && block < p.nseg)) {
+        seg = p.xcd_remap ? int((block % 8) * (p.nseg / 8) + block / 8) : block;
+        // a cut segment's pieces run in the blocks from nseg on (the whole
+        // workgroup leaves together)
+        if (MODE == 2 && p.cu[seg + 1] - p.cu[seg] > kPieceEvents) return;
+    } else {
+        // the grid is an upper bound on the pieces
+        const int idx = MODE == 2 ? block - p.nseg : block;
+        if (idx >= p.n_items[0]) return;
+        const int4 it = p.items[idx];
+        seg = it.x;
+        piece = it.y;
+        pieces = it.z;
+        pslot = it.w;
+    }
     const int bank = seg % p.banks;
     const int64_t bidx = seg / p.banks;
     const int head0 = blockIdx.y * p.heads_per_block;
@@ -426,10 +465,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     const int half = (tid >> 4) & 1;
     const bool prep_head = ph < nheads;
 
-    const int64_t start = p.cu[seg], end = p.cu[seg + 1];
+    int64_t start = p.cu[seg], end = p.cu[seg + 1];
+    if constexpr (MODE != 0) {
+        if (pieces > 1) {
+            start += int64_t(piece) * kPieceEvents;
+            end = min(end, start + kPieceEvents);
+        }
+    }
     const int64_t write_events = p.nt * p.kw;
     const int64_t events = p.nt * (p.kw + p.kr);
-    const bool rounding = p.round_interval > 0;
+    const bool rounding = MODE == 0 && p.round_interval > 0;
     const int nstages = int((end - start + NE - 1) / NE);
 
     // ---- metadata of a stage from its packed order entries (lanes 0..15)
@@ -548,7 +593,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     // ---- prologue: metadata of stages 0 and 1, operands of stage 0
     float h[S][CPL];
     const int64_t state_offset = ((int64_t(bank) * p.heads + head) * S) * p.width + col0;
-    load_state<S, CPL>(p.initial, p.init_dtype, bidx * p.init_bstride + state_offset, p.width, S, h);
+    // piece-state rows of this (piece, head): [S, v] FP32
+    const int64_t pstate_offset = ((int64_t(pslot) * p.heads + head) * S) * p.width + col0;
+    if (MODE == 1) {
+#pragma unroll
+        for (int r = 0; r < S; ++r)
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) h[r][c] = 0.f;
+    } else if (MODE == 2 && piece > 0) {
+        // M_piece, stored by piece_scan_kernel in the previous piece's slot
+        load_state<S, CPL>(p.pstate, BDM_F32, pstate_offset - int64_t(p.heads) * S * p.width, p.width, S, h);
+    } else {
+        load_state<S, CPL>(p.initial, p.init_dtype, bidx * p.init_bstride + state_offset, p.width, S, h);
+    }
+    // MODE 1: lanes 0..7 of a head carry column (lane) of the piece's transition
+    const int pcol = tid % p.lanes_per_head;
+    float pc[S];
+#pragma unroll
+    for (int r = 0; r < S; ++r) pc[r] = (MODE == 1 && r == pcol) ? 1.f : 0.f;
     if (rounding) {
 #pragma unroll
         for (int r = 0; r < S; ++r)
@@ -607,6 +669,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         const bool next_has_write = st + 1 < nstages && s_nw[next_slot] > 0;
 
         auto read_event = [&](int i) {
+            if constexpr (MODE == 1) return;  // a read does not change the state
             const int64_t zrow = int64_t(__builtin_amdgcn_readfirstlane(s_route[slot][i])) * hw;
             const float *row = &s_rows[i][lh][0][0];
             float gamma[S];
@@ -652,6 +715,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
                         const float d = row[2 * S + r];
 #pragma unroll
                         for (int c = 0; c < CPL; ++c) h[r][c] *= d;
+                        if constexpr (MODE == 1) pc[r] *= d;
                     }
                 }
                 float nalpha[S], beta[S];
@@ -672,6 +736,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 #pragma unroll
                     for (int r = 0; r < S; ++r) h[r][c] = fmaf(beta[r], u, h[r][c]);
                 }
+                if constexpr (MODE == 1) {
+                    // the transition column: the same update with x = 0
+                    float u = nalpha[0] * pc[0];
+#pragma unroll
+                    for (int r = 1; r < S; ++r) u = fmaf(nalpha[r], pc[r], u);
+#pragma unroll
+                    for (int r = 0; r < S; ++r) pc[r] = fmaf(beta[r], u, pc[r]);
+                }
             }
 #pragma unroll 1
             for (; i < n; ++i) read_event(i);
@@ -683,14 +755,100 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
             const float f = s_fold[lh][r];
 #pragma unroll
             for (int c = 0; c < CPL; ++c) h[r][c] *= f;
+            if constexpr (MODE == 1) pc[r] *= f;
         }
         // metadata of stage st+2 and operands of stage st+1
         if (tid < 64) decode_order(st + 2, o2);
         if (st + 1 < nstages) finish_prep(st + 1);
     }
-    if (p.final_state) {
+    if constexpr (MODE == 1) {
+        // R_q and P_q of this piece
+        store_state<S, CPL>(p.pstate, BDM_F32, pstate_offset, p.width, S, h);
+        if (pcol < S && tid < nheads * p.lanes_per_head) {
+            float *pt = p.ptrans + ((int64_t(pslot) * p.heads + head) * S) * S;
+#pragma unroll
+            for (int r = 0; r < S; ++r) pt[r * S + pcol] = pc[r];
+        }
+    } else if (p.final_state && piece == pieces - 1) {
         const int64_t final_offset = bidx * (int64_t(p.banks) * p.heads * S * p.width) + state_offset;
         store_state<S, CPL>(p.final_state, p.final_dtype, final_offset, p.width, S, h);
+    }
+}
+
+// The piece list: a segment longer than kPieceEvents becomes
+// ceil(len / kPieceEvents) pieces with consecutive piece-state slots.  One
+// workgroup of 1024 threads; thread t handles a contiguous run of segments.
+__global__ __launch_bounds__(1024) void piece_table_kernel(const int64_t *__restrict__ cu, int nseg,
+                                                           int4 *__restrict__ items, int *__restrict__ n_items) {
+    __shared__ int s_cut[1024];
+    const int t = threadIdx.x;
+    const int per = (nseg + 1023) / 1024;
+    const int s0 = min(nseg, t * per), s1 = min(nseg, s0 + per);
+    int cut = 0;
+    for (int sg = s0; sg < s1; ++sg) {
+        const int64_t len = cu[sg + 1] - cu[sg];
+        if (len > kPieceEvents) cut += int((len + kPieceEvents - 1) / kPieceEvents);
+    }
+    s_cut[t] = cut;
+    __syncthreads();
+    // inclusive scan (Hillis-Steele over 1024 entries)
+    for (int off = 1; off < 1024; off <<= 1) {
+        const int a = t >= off ? s_cut[t - off] : 0;
+        __syncthreads();
+        s_cut[t] += a;
+        __syncthreads();
+    }
+    int pos = s_cut[t] - cut;
+    for (int sg = s0; sg < s1; ++sg) {
+        const int64_t len = cu[sg + 1] - cu[sg];
+        if (len > kPieceEvents) {
+            const int np = int((len + kPieceEvents - 1) / kPieceEvents);
+            for (int q = 0; q < np; ++q, ++pos) items[pos] = make_int4(sg, q, np, pos);
+        }
+    }
+    if (t == 0) n_items[0] = s_cut[1023];
+}
+
+// For each cut segment (its first piece's item) and head: M_0 = the
+// segment's initial state, M_(q+1) = P_q M_q + R_q in FP32, stored over R_q
+// (the slot that piece q+1 reads its start state from).  One thread per value
+// column.
+__global__ __launch_bounds__(256) void piece_scan_kernel(const int4 *__restrict__ items,
+                                                         const int *__restrict__ n_items, const void *initial,
+                                                         int init_dtype, int64_t init_bstride, int banks, int heads,
+                                                         int width, float *__restrict__ pstate,
+                                                         const float *__restrict__ ptrans) {
+    constexpr int S = 8;
+    if (int(blockIdx.x) >= n_items[0]) return;
+    const int4 it = items[blockIdx.x];
+    if (it.y != 0) return;  // not a first piece
+    const int seg = it.x, pieces = it.z, slot0 = it.w, head = blockIdx.y;
+    const int bank = seg % banks;
+    const int64_t bidx = seg / banks;
+    for (int c = threadIdx.x; c < width; c += blockDim.x) {
+        float m[S];
+        const int64_t off = bidx * init_bstride + ((int64_t(bank) * heads + head) * S) * width + c;
+#pragma unroll
+        for (int r = 0; r < S; ++r)
+            m[r] = init_dtype == BDM_BF16 ? to_f32(static_cast<const bf16_t *>(initial)[off + int64_t(r) * width])
+                                          : static_cast<const float *>(initial)[off + int64_t(r) * width];
+        for (int q = 0; q + 1 < pieces; ++q) {
+            const int64_t base = ((int64_t(slot0 + q) * heads + head) * S) * width + c;
+            const float *pt = ptrans + ((int64_t(slot0 + q) * heads + head) * S) * S;
+            float nm[S];
+#pragma unroll
+            for (int r = 0; r < S; ++r) {
+                float acc = pstate[base + int64_t(r) * width];
+#pragma unroll
+                for (int j = 0; j < S; ++j) acc = fmaf(pt[r * S + j], m[j], acc);
+                nm[r] = acc;
+            }
+#pragma unroll
+            for (int r = 0; r < S; ++r) {
+                m[r] = nm[r];
+                pstate[base + int64_t(r) * width] = nm[r];
+            }
+        }
     }
 }
 
@@ -746,8 +904,16 @@ __global__ __launch_bounds__(256) void zero_fill_kernel(T *__restrict__ out, int
     if (i < count) out[i] = from_f32<T>(0.f);
 }
 
+// Scratch of the cut-segment path, carved from the bdm_forward workspace.
+struct PieceBuffers {
+    int4 *items = nullptr;
+    int *count = nullptr;
+    float *pstate = nullptr, *ptrans = nullptr;
+    int64_t max_pieces = 0;  // 0: the path is off
+};
+
 template <typename T, int S, int CPL, bool kLazy = false>
-int launch_forward(const bdm_forward_args &a, T *zbuf, int *zslot, hipStream_t stream) {
+int launch_forward(const bdm_forward_args &a, T *zbuf, int *zslot, const PieceBuffers &pb, hipStream_t stream) {
     if (a.head_width / CPL > 256)
         return fail(BDM_ERR_UNSUPPORTED, "forward: head_width %d needs more than 256 lanes", a.head_width);
     ForwardParams<T> p{};
@@ -799,12 +965,39 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, int *zslot, hipStream_t s
                                                                               zslot);
         if (int rc = check_launch("read_slot_kernel")) return rc;
     }
+    p.nseg = int(nseg);
     if constexpr (kLazy) {
         // the prep role needs one lane per (event, head, half): 32 per head
-        if (lazy_hb == 2)
-            lazy_forward_kernel<T, CPL, 2><<<grid, 64, 0, stream>>>(p);
-        else
-            lazy_forward_kernel<T, CPL, 8><<<grid, 256, 0, stream>>>(p);
+        const int lthreads = lazy_hb == 2 ? 64 : 256;
+        if (pb.max_pieces > 0) {
+            // prefill policy: long segments run as balanced pieces
+            p.items = pb.items;
+            p.n_items = pb.count;
+            p.pstate = pb.pstate;
+            p.ptrans = pb.ptrans;
+            piece_table_kernel<<<1, 1024, 0, stream>>>(a.cu_seqlens, int(nseg), pb.items, pb.count);
+            if (int rc = check_launch("piece_table_kernel")) return rc;
+            const dim3 pgrid(unsigned(pb.max_pieces), grid.y);
+            if (lazy_hb == 2)
+                lazy_forward_kernel<T, CPL, 2, 1><<<pgrid, lthreads, 0, stream>>>(p);
+            else
+                lazy_forward_kernel<T, CPL, 8, 1><<<pgrid, lthreads, 0, stream>>>(p);
+            if (int rc = check_launch("lazy_forward_kernel")) return rc;
+            piece_scan_kernel<<<dim3(unsigned(pb.max_pieces), unsigned(a.heads)), 128, 0, stream>>>(
+                pb.items, pb.count, a.initial, a.initial_dtype, a.initial_batch_stride, a.bank_count, a.heads,
+                a.head_width, pb.pstate, pb.ptrans);
+            if (int rc = check_launch("piece_scan_kernel")) return rc;
+            const dim3 g2(unsigned(nseg + pb.max_pieces), grid.y);
+            if (lazy_hb == 2)
+                lazy_forward_kernel<T, CPL, 2, 2><<<g2, lthreads, 0, stream>>>(p);
+            else
+                lazy_forward_kernel<T, CPL, 8, 2><<<g2, lthreads, 0, stream>>>(p);
+        } else {
+            if (lazy_hb == 2)
+                lazy_forward_kernel<T, CPL, 2, 0><<<grid, lthreads, 0, stream>>>(p);
+            else
+                lazy_forward_kernel<T, CPL, 8, 0><<<grid, lthreads, 0, stream>>>(p);
+        }
         if (int rc = check_launch("lazy_forward_kernel")) return rc;
     } else {
         routed_forward_kernel<T, S, CPL><<<grid, threads, 0, stream>>>(p);
@@ -832,29 +1025,45 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, int *zslot, hipStream_t s
     return check_launch("ordered_combine_kernel");
 }
 
+// The S = 8 lazy kernel takes: 16-byte aligned state rows, 4-column lane
+// groups of at most 64 lanes per head, stages of 16 events matching the
+// rounding/snapshot interval, and token and route indices in 32 bits.
+bool lazy_path(const bdm_forward_args &a) {
+    const bool vec = a.initial_batch_stride % 8 == 0;
+    const int fold = a.round_interval > 0 ? a.round_interval : (a.snapshots ? a.snapshot_interval : kLazyStage);
+    const int64_t nt = a.batch * a.time;
+    const bool small_index = nt * (a.write_banks > a.read_banks ? a.write_banks : a.read_banks) < INT32_MAX;
+    return vec && a.bank_size == 8 && a.head_width % 4 == 0 && a.head_width / 4 <= 64 && fold == kLazyStage &&
+           small_index;
+}
+
+// Upper bound on the pieces of cut segments (0: the path is off).  It is
+// taken under the prefill policy only: no rounding inside the recurrence and
+// no snapshots, so a segment is an affine map of its start state.  A cut
+// segment has len > L events and ceil(len/L) < len/L + 1 pieces, and fewer
+// than E/L segments are cut, so the pieces number fewer than 2E/L + 1.
+int64_t max_pieces(const bdm_forward_args &a) {
+    if (!lazy_path(a) || a.round_interval > 0 || a.snapshots) return 0;
+    const int64_t events = a.batch * a.time * (int64_t(a.write_banks) + a.read_banks);
+    return 2 * (events / kPieceEvents) + 1;
+}
+
 template <typename T>
-int dispatch_forward(const bdm_forward_args &a, T *zbuf, int *zslot, hipStream_t stream) {
+int dispatch_forward(const bdm_forward_args &a, T *zbuf, int *zslot, const PieceBuffers &pb, hipStream_t stream) {
     // Vector row loads need 16-byte aligned rows: aligned bases, and a state
     // batch stride that keeps them aligned.
     const bool vec = a.initial_batch_stride % 8 == 0;
     if (a.bank_size <= 8) {
-        const int fold = a.round_interval > 0 ? a.round_interval : (a.snapshots ? a.snapshot_interval : kLazyStage);
-        constexpr int lc = 4;  // value columns per lane of the lazy kernel
-        // the lazy kernel keeps token and route indices in 32 bits
-        const int64_t nt = a.batch * a.time;
-        const bool small_index = nt * (a.write_banks > a.read_banks ? a.write_banks : a.read_banks) < INT32_MAX;
-        if (vec && a.bank_size == 8 && a.head_width % lc == 0 && a.head_width / lc <= 64 && fold == kLazyStage &&
-            small_index)
-            return launch_forward<T, 8, lc, true>(a, zbuf, zslot, stream);
-        if (vec && a.head_width % 8 == 0) return launch_forward<T, 8, 8>(a, zbuf, zslot, stream);
-        return launch_forward<T, 8, 1>(a, zbuf, zslot, stream);
+        if (lazy_path(a)) return launch_forward<T, 8, 4, true>(a, zbuf, zslot, pb, stream);
+        if (vec && a.head_width % 8 == 0) return launch_forward<T, 8, 8>(a, zbuf, zslot, pb, stream);
+        return launch_forward<T, 8, 1>(a, zbuf, zslot, pb, stream);
     }
     if (a.bank_size <= 16) {
-        if (vec && a.head_width % 4 == 0) return launch_forward<T, 16, 4>(a, zbuf, zslot, stream);
-        return launch_forward<T, 16, 1>(a, zbuf, zslot, stream);
+        if (vec && a.head_width % 4 == 0) return launch_forward<T, 16, 4>(a, zbuf, zslot, pb, stream);
+        return launch_forward<T, 16, 1>(a, zbuf, zslot, pb, stream);
     }
-    if (vec && a.head_width % 2 == 0) return launch_forward<T, 32, 2>(a, zbuf, zslot, stream);
-    return launch_forward<T, 32, 1>(a, zbuf, zslot, stream);
+    if (vec && a.head_width % 2 == 0) return launch_forward<T, 32, 2>(a, zbuf, zslot, pb, stream);
+    return launch_forward<T, 32, 1>(a, zbuf, zslot, pb, stream);
 }
 
 size_t elem_size(int dtype) { return dtype == BDM_BF16 ? 2 : 4; }
@@ -863,17 +1072,32 @@ size_t elem_size(int dtype) { return dtype == BDM_BF16 ? 2 : 4; }
 }  // namespace bdm
 
 // Workspace of bdm_forward: the read buffer (one ctrl_dtype row of H*v per
-// read event) followed by its row map (one int32 per read event).
+// read event), its row map (one int32 per read event), then, under the
+// prefill policy, the piece list, its count and the FP32 piece states and
+// transitions ([pieces, H, 8, v] and [pieces, H, 8, 8]).
+static size_t round256(size_t x) { return (x + 255) / 256 * 256; }
+
 static size_t forward_zbuf_bytes(const bdm_forward_args *a) {
-    const size_t bytes = size_t(a->batch) * size_t(a->time) * size_t(a->read_banks) * size_t(a->heads) *
-                         size_t(a->head_width) * bdm::elem_size(a->ctrl_dtype);
-    return (bytes + 255) / 256 * 256;
+    return round256(size_t(a->batch) * size_t(a->time) * size_t(a->read_banks) * size_t(a->heads) *
+                    size_t(a->head_width) * bdm::elem_size(a->ctrl_dtype));
+}
+
+static size_t forward_zslot_bytes(const bdm_forward_args *a) {
+    return round256(size_t(a->batch) * size_t(a->time) * size_t(a->read_banks) * sizeof(int));
+}
+
+static size_t forward_piece_bytes(const bdm_forward_args *a) {
+    const size_t n = size_t(bdm::max_pieces(*a));
+    if (!n) return 0;
+    return round256(n * sizeof(int4)) + 256 + round256(n * a->heads * 8 * size_t(a->head_width) * 4) +
+           round256(n * a->heads * 64 * 4);
 }
 
 extern "C" size_t bdm_forward_workspace_size(const bdm_forward_args *a) {
-    if (!a || a->batch <= 0 || a->time <= 0 || a->heads <= 0 || a->head_width <= 0 || a->read_banks < 0) return 0;
-    const size_t slots = size_t(a->batch) * size_t(a->time) * size_t(a->read_banks) * sizeof(int);
-    return forward_zbuf_bytes(a) + (slots + 255) / 256 * 256;
+    if (!a || a->batch <= 0 || a->time <= 0 || a->heads <= 0 || a->head_width <= 0 || a->read_banks < 0 ||
+        a->write_banks < 0 || a->bank_size <= 0)
+        return 0;
+    return forward_zbuf_bytes(a) + forward_zslot_bytes(a) + forward_piece_bytes(a);
 }
 
 extern "C" int bdm_forward(const bdm_forward_args *a, void *workspace, size_t workspace_bytes, void *stream) {
@@ -913,7 +1137,23 @@ extern "C" int bdm_forward(const bdm_forward_args *a, void *workspace, size_t wo
     if (a->batch * a->time * a->read_banks > int64_t(INT32_MAX))
         return fail(BDM_ERR_UNSUPPORTED, "forward: more than 2^31 read events");
     hipStream_t s = as_stream(stream);
-    int *zslot = reinterpret_cast<int *>(static_cast<char *>(workspace) + forward_zbuf_bytes(a));
-    if (a->ctrl_dtype == BDM_BF16) return dispatch_forward<bf16_t>(*a, static_cast<bf16_t *>(workspace), zslot, s);
-    return dispatch_forward<float>(*a, static_cast<float *>(workspace), zslot, s);
+    char *ws = static_cast<char *>(workspace);
+    int *zslot = reinterpret_cast<int *>(ws + forward_zbuf_bytes(a));
+    PieceBuffers pb;
+    pb.max_pieces = max_pieces(*a);
+    if (pb.max_pieces > INT32_MAX / 2) return fail(BDM_ERR_UNSUPPORTED, "forward: too many pieces");
+    if (pb.max_pieces) {
+        char *at = ws + forward_zbuf_bytes(a) + forward_zslot_bytes(a);
+        const size_t n = size_t(pb.max_pieces);
+        pb.items = reinterpret_cast<int4 *>(at);
+        at += round256(n * sizeof(int4));
+        pb.count = reinterpret_cast<int *>(at);
+        at += 256;
+        pb.pstate = reinterpret_cast<float *>(at);
+        at += round256(n * a->heads * 8 * size_t(a->head_width) * 4);
+        pb.ptrans = reinterpret_cast<float *>(at);
+    }
+    if (a->ctrl_dtype == BDM_BF16)
+        return dispatch_forward<bf16_t>(*a, static_cast<bf16_t *>(workspace), zslot, pb, s);
+    return dispatch_forward<float>(*a, static_cast<float *>(workspace), zslot, pb, s);
 }

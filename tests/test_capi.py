@@ -42,10 +42,22 @@ def test_workspace_sizes(lib):
     from bdm_amd import _lib
     args = _lib.ForwardArgs()
     args.batch, args.time, args.heads, args.head_width, args.read_banks = 2, 10, 3, 16, 4
+    args.bank_size, args.write_banks = 4, 4
     args.ctrl_dtype = _lib.BDM_BF16
+    r256 = lambda x: (x + 255) // 256 * 256  # noqa: E731
     # read rows (BF16, H*v per read event) then their row map (int32 per read event)
-    rows = (2 * 10 * 4 * 3 * 16 * 2 + 255) // 256 * 256
-    slots = (2 * 10 * 4 * 4 + 255) // 256 * 256
+    rows = r256(2 * 10 * 4 * 3 * 16 * 2)
+    slots = r256(2 * 10 * 4 * 4)
+    assert lib.bdm_forward_workspace_size(ctypes.byref(args)) == rows + slots
+    # S = 8 under the prefill policy (no rounding, no snapshots) adds the
+    # piece list of cut segments: at most 2 * (E // 512) + 1 pieces, with
+    # their FP32 start states [H, 8, v] and transitions [H, 8, 8]
+    args.bank_size, args.head_width, args.round_interval = 8, 128, 0
+    rows = r256(2 * 10 * 4 * 3 * 128 * 2)
+    pieces = 2 * ((2 * 10 * 8) // 512) + 1
+    extra = r256(pieces * 16) + 256 + r256(pieces * 3 * 8 * 128 * 4) + r256(pieces * 3 * 64 * 4)
+    assert lib.bdm_forward_workspace_size(ctypes.byref(args)) == rows + slots + extra
+    args.round_interval = 16  # the training policy rounds inside the recurrence: no pieces
     assert lib.bdm_forward_workspace_size(ctypes.byref(args)) == rows + slots
 
 

@@ -173,6 +173,42 @@ def test_forward_long_read_runs_match_oracle(device, state_dtype):
     assert rel_err(final, ref_final) < TOL, rel_err(final, ref_final)
 
 
+@pytest.mark.parametrize('decay', ['mild', 'strong'])
+def test_forward_cut_segments_match_oracle(device, decay):
+    """Prefill policy (no rounding inside the recurrence): segments longer
+    than the piece length (512 events) run as pieces whose affine summaries
+    are composed; every read and every final state must equal the per-event
+    oracle.  4 banks, one write and one read bank per token, T = 1100, so a
+    segment holds about 550 events, cut into 2 pieces (3 for the hottest)."""
+    from bdm_amd import ops
+    gen = torch.Generator().manual_seed(91)
+    batch, time, heads, s, v, j = 2, 1100, 2, 8, 128, 4
+    wi = torch.randint(0, j, (batch, time, 1), generator=gen)
+    wi[0, :400] = 0  # bank 0 of sequence 0 gets the most events
+    ri = torch.randint(0, j, (batch, time, 1), generator=gen)
+    ri[0, :400] = 0
+    ww = torch.rand(batch, time, 1, generator=gen).to(torch.bfloat16)
+    rw = torch.rand(batch, time, 1, generator=gen).to(torch.bfloat16)
+    q, k, v_, g, b, w = controllers(batch, time, heads, s, v, gen)
+    if decay == 'strong':  # stages whose scale would underflow run in eager form
+        g = g * 200.0
+    state = initial_state(j, heads, s, v, gen)
+    ref, ref_final = oracle_reads(q, k, v_, g, b, w, wi, ww, ri, rw, state, j, routed_decay=True,
+                                  state_dtype=torch.float32, interval=16, return_final=True)
+    dev = [x.to(device) for x in (q, k, v_, g, b, w, wi, ww, ri, rw, state)]
+    announce('forward cut segments', decay)
+    meta = ops.dispatch_build(dev[6], dev[8], j)
+    lengths = (meta.cu_seqlens[1:] - meta.cu_seqlens[:-1]).cpu()
+    assert int(lengths.max()) > 1024 and int((lengths > 512).sum()) >= 4  # several cut segments, one in 3 pieces
+    final = torch.empty(batch, j, heads, s, v, device=device, dtype=torch.float32)
+    y = ops.routed_forward(*dev[:10], dev[10], meta, bank_count=j, scale=s ** -0.5, routed_decay=True,
+                           round_interval=0, final_state=final)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y).all() and torch.isfinite(final).all()
+    assert rel_err(y, ref) < TOL, rel_err(y, ref)
+    assert rel_err(final, ref_final) < TOL, rel_err(final, ref_final)
+
+
 @pytest.mark.parametrize('decay', ['strong', 'mixed', 'none'])
 @pytest.mark.parametrize('state_dtype', [torch.bfloat16, torch.float32])
 def test_forward_decay_extremes_match_oracle(device, decay, state_dtype):
