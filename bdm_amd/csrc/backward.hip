@@ -5,27 +5,35 @@
 // the decay term of d(ww) and dg scaled by p) and _vjp
 // (role_bank_dispatch.py:76-132, with its BF16 rounding points).
 //
-// routed_backward_kernel: one wave per (segment, head, column tile).  A lane
-// owns CPL value columns and all S rows of them, as in the forward.  Chunks
-// of C events (the snapshot interval) are visited in reverse.  A chunk's
-// states are rebuilt exactly from its snapshot (or the initial state) by the
-// forward's own write update: for each SUB-event piece, in reverse, the
-// chunk's writes before the piece are replayed from the chunk's start state
-// and the piece's pre-event states are kept in registers, so the reverse pass
-// reads every pre-event state from registers (about 2.5x the forward's
-// writes for C = 16, no LDS or HBM history).  Per event the adjoint dM (S x CPL per lane) is
-// updated in-lane; the reductions over value columns that produce the
-// event's S-wide gradients (dk, db, dg for a write, dq for a read) do not feed
-// back into dM, so they are reduced across the wave and stored per event.
-// The write's du (one value per column) is stored in FP32; the token kernel
-// forms dv = bf(du*ew) and dw = bf(du*v) from it exactly as the reference's
-// stored BF16 products.
+// Per write event the adjoint dM (S x v) of the state after the event gives
+//   du = dM^T k;  U = dM u;  X = hd du;  P = rowsum(dM o hd)
+//   dM <- (dM - a du^T) o decay                (role_bank_kernel.py:128-138)
+// and per read event dq = scale M dy, dM += scale eq dy^T (:141-143).  U, X
+// and P (S values each) are stored per event; the token kernel forms
+// dk = U - eb X, db = -k X, dg = P - a X from them and the event's operands.
 //
-// token_vjp_kernel: one workgroup per token; each wave handles heads
-// wave, wave+4, ...  It folds a token's KW write events and KR read events
-// in route order with the reference's rounding (role_bank_dispatch.py:99-131)
-// and produces the token gradients of q,k,v,g,b,w and of both route weights.
-// Heads' route-weight gradients are added in head order in FP32.
+// chunk_backward_kernel (S = 8, replay interval 16): one wave per (segment,
+// head, column tile); a lane owns 2 value columns and all 8 rows.  Chunks of
+// 16 events are visited in reverse.  The chunk's states are rebuilt exactly
+// from its snapshot by the forward's write update, in two halves of 8 events:
+// the states before events 8..15 are kept in registers while the second half
+// is differentiated, then those before events 0..7.  Per event operands (the
+// write's k, decay, a rows and bf(w p), v columns; the read's eq*scale row
+// and dy columns) are staged in LDS one chunk ahead: the next chunk's loads
+// are issued before the current chunk's last half is differentiated.  The
+// S-wide column reductions use permlane swaps and DPP row sums
+// (reduce-scatter: each output ends in one lane, no LDS round trip).
+//
+// routed_backward_kernel: the general path (any S <= 32, intervals 4/8/16).
+// Same arithmetic; pieces of SUB events, operands loaded per event.
+//
+// token_grad_kernel: one workgroup per token, one wave per head.  Lane
+// (j, r) = (lane / 8, lane % 8) handles route slot j and state row r of the
+// S-side gradients; lanes own 2 value columns for dv, dw.  The token's KW
+// write events and KR read events are folded in route order with the
+// reference's rounding (role_bank_dispatch.py:99-131); route-weight
+// gradients add the heads' contributions in head order in FP32.
+// token_vjp_kernel: the same for shapes outside that kernel's limits.
 #include "bdm_common.h"
 #include "recurrence_ops.h"
 
@@ -45,8 +53,9 @@ struct BackwardParams {
     const void *snap;
     const T *dy;
     float *du;      // [NT*KW, H, v]
-    float *wpart;   // [tiles, 3, NT*KW, H, S]: dk, db, dg of each write slot
+    float *wpart;   // [tiles, NT*KW, H, 3, S]: U, X, P of each write slot
     float *rpart;   // [tiles, NT*KR, H, S]: dq of each read slot
+    const int4 *meta;  // [E]: token, route slot, is_read, route weight (FP32 bits)
     float *dinit;   // [batch, J, H, S, v]
     int64_t init_bstride, nt;
     int heads, s_real, width, banks, kw, kr, tiles;
@@ -140,7 +149,6 @@ __global__ __launch_bounds__(64) void routed_backward_kernel(BackwardParams<T> p
     const int64_t start = p.cu[seg], end = p.cu[seg + 1];
     const int64_t write_events = p.nt * p.kw;
     const int64_t events = p.nt * (p.kw + p.kr);
-    const int64_t hs = int64_t(p.heads) * p.s_real;
 
     float dm[S][CPL];
 #pragma unroll
@@ -259,26 +267,22 @@ __global__ __launch_bounds__(64) void routed_backward_kernel(BackwardParams<T> p
                     for (int c = 0; c < CPL; ++c)
                         if (col0 + c < p.width) du_row[col0 + c] = du[c];
                     wave_reduce<3 * S>(red);
-                    // dk = sum(dh*u) - eb*X ; db = -k*X ; dg = sum(dh*hd) - a*X
-                    // (role_bank_kernel.py:128-135, X = the contraction hd.du)
-                    float out_k = 0.f, out_b = 0.f, out_g = 0.f;
+                    // U, X, P of row `lane` (the token kernel forms dk, db, dg)
+                    float out_u = 0.f, out_x = 0.f, out_p = 0.f;
 #pragma unroll
                     for (int r = 0; r < S; ++r) {
                         if (lane == r) {
-                            const float x = red[S + r];
-                            out_k = red[r] - ev.rows.eb[r] * x;
-                            out_b = -ev.rows.key[r] * x;
-                            out_g = red[2 * S + r] - ev.rows.a[r] * x;
+                            out_u = red[r];
+                            out_x = red[S + r];
+                            out_p = red[2 * S + r];
                         }
                     }
                     if (lane < p.s_real) {
                         const int64_t nslots = p.nt * p.kw;
-                        const int64_t at = (slot * p.heads + head) * p.s_real + lane;
-                        const int64_t plane = nslots * hs;
-                        float *wp = p.wpart + int64_t(tile) * 3 * plane;
-                        wp[at] = out_k;
-                        wp[plane + at] = out_b;
-                        wp[2 * plane + at] = out_g;
+                        float *wp = p.wpart + ((int64_t(tile) * nslots + slot) * p.heads + head) * 3 * p.s_real;
+                        wp[lane] = out_u;
+                        wp[p.s_real + lane] = out_x;
+                        wp[2 * p.s_real + lane] = out_p;
                     }
                 } else {
                     const int64_t row = token * p.heads + head;
@@ -320,9 +324,446 @@ __global__ __launch_bounds__(64) void routed_backward_kernel(BackwardParams<T> p
 }
 
 
+// ------------------------------------------------- S = 8, replay interval 16
+
+// Sums over lane pairs l, l + 32: lanes 0..31 return a(l) + a(l + 32), lanes
+// 32..63 return b(l - 32) + b(l) (v_permlane32_swap exchanges a's upper half
+// with b's lower half).
+__device__ __forceinline__ float half_pair_sum(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Sums over 16-lane row pairs (0, 1) and (2, 3): rows 0 and 2 return a
+// summed with the next row, rows 1 and 3 return b summed with the previous
+// row (v_permlane16_swap exchanges a's odd rows with b's even rows).
+__device__ __forceinline__ float row_pair_sum(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float x) {
+    return x + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xF, 0xF,
+                                                                     false));
+}
+
+// Total of a 16-lane row in every lane of the row.
+__device__ __forceinline__ float row_total(float x) {
+    x = dpp_add<0xB1>(x);      // quad_perm [1,0,3,2]
+    x = dpp_add<0x4E>(x);      // quad_perm [2,3,0,1]
+    x = dpp_add<0x141>(x);     // row_half_mirror: quads 0 <-> 1, 2 <-> 3
+    return dpp_add<0x140>(x);  // row_mirror: halves of the row
+}
+
+// Sums each of N values over the 64 lanes of the wave.  Value o = (N/4) * row
+// + i (row = lane / 16) ends in the lanes of that row at position
+// lane % 16 = i < N/4, which return it; other lanes return a partial sum.
+template <int N>
+__device__ __forceinline__ float reduce_scatter(const float (&x)[N], int lane) {
+    static_assert(N % 4 == 0, "N");
+    float y[N / 2];
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) y[i] = half_pair_sum(x[i], x[i + N / 2]);
+    float z[N / 4];
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) z[i] = row_total(row_pair_sum(y[i], y[i + N / 4]));
+    const int pos = lane & 15;
+    float out = z[0];
+#pragma unroll
+    for (int i = 1; i < N / 4; ++i) out = pos == i ? z[i] : out;
+    return out;
+}
+
+// Two adjacent columns of T as loaded (BF16 pairs stay packed).
+template <typename T>
+struct Pair;
+template <>
+struct Pair<bf16_t> {
+    using raw = uint32_t;
+    static __device__ __forceinline__ raw load(const bf16_t *p) { return *reinterpret_cast<const uint32_t *>(p); }
+    static __device__ __forceinline__ float lo(raw r) { return __uint_as_float(r << 16); }
+    static __device__ __forceinline__ float hi(raw r) { return __uint_as_float(r & 0xffff0000u); }
+    // bf(x*p) of both halves, packed
+    static __device__ __forceinline__ raw scaled(raw r, float pw) { return pack_bf16x2(lo(r) * pw, hi(r) * pw); }
+    static __device__ __forceinline__ raw zero() { return 0u; }
+};
+template <>
+struct Pair<float> {
+    using raw = float2;
+    static __device__ __forceinline__ raw load(const float *p) { return *reinterpret_cast<const float2 *>(p); }
+    static __device__ __forceinline__ float lo(raw r) { return r.x; }
+    static __device__ __forceinline__ float hi(raw r) { return r.y; }
+    static __device__ __forceinline__ raw scaled(raw r, float pw) { return make_float2(r.x * pw, r.y * pw); }
+    static __device__ __forceinline__ raw zero() { return make_float2(0.f, 0.f); }
+};
+
+// One entry per event of the packed order: token, route slot, is_read and
+// the route weight (FP32 bits), shared by every head.
+template <typename T>
+__global__ __launch_bounds__(256) void event_meta_kernel(const int64_t *order, int64_t events, int64_t write_events,
+                                                         int kw, int kr, const T *ww, const T *rw, int4 *meta) {
+    const int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (e >= events) return;
+    int64_t o = order[e];
+    o = o < 0 ? 0 : (o >= events ? events - 1 : o);
+    const bool rd = o >= write_events;
+    const int64_t route = rd ? o - write_events : o;
+    const int64_t token = rd ? route / kr : route / kw;
+    const float weight = to_f32(rd ? rw[route] : ww[route]);
+    meta[e] = make_int4(int(token), int(route), rd ? 1 : 0, __float_as_int(weight));
+}
+
+template <typename T, typename SNAP>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void chunk_backward_kernel(
+    BackwardParams<T> p) {
+    constexpr int S = 8, CPL = 2, C = 16, HALF = 8;
+    using P2 = Pair<T>;
+    using Raw = typename P2::raw;
+    using SnapRaw = typename Pair<SNAP>::raw;
+    struct ColSlot {
+        Raw a, b;  // write: v, bf(w p); read: dy, unused
+    };
+    struct Staged {
+        Raw a[C], b[C];
+        Raw kq, bb;
+        float2 g;
+        SnapRaw m0[S];  // snapshot rows (chunks > 0)
+    };
+    __shared__ int4 s_meta[2][C];
+    __shared__ float4 s_rows[C][6];  // write: k, decay, ad = a*decay (2 x float4 each); read: eq*scale in [0..1]
+    __shared__ ColSlot s_cols[C][kLanes];
+    __shared__ float2 s_m0[S][kLanes];  // the chunk's start state, lane's column pair per row
+
+    const int nseg = gridDim.x;
+    const int seg = p.xcd_remap ? int((blockIdx.x % 8) * (nseg / 8) + blockIdx.x / 8) : int(blockIdx.x);
+    const int bank = seg % p.banks;
+    const int64_t bidx = seg / p.banks;
+    const int head = blockIdx.y;
+    const int tile = blockIdx.z;
+    const int lane = threadIdx.x;
+    const int col0 = (tile * kLanes + lane) * CPL;
+    const bool live = col0 < p.width;
+    const int colc = live ? col0 : p.width - CPL;  // lanes past the width load a valid pair and zero it
+    const int64_t start = p.cu[seg], end = p.cu[seg + 1];
+    const int count = int((end - start + C - 1) / C);
+    const int64_t wslots = p.nt * p.kw, rslots = p.nt * p.kr;
+
+    auto chunk_len = [&](int c) { return int(min(int64_t(C), end - (start + int64_t(c) * C))); };
+    auto load_meta = [&](int c) {
+        const int len = chunk_len(c);
+        return p.meta[start + int64_t(c) * C + (lane < len ? lane : len - 1)];
+    };
+    auto store_meta = [&](int c, const int4 &m) {
+        if (lane < C) s_meta[c & 1][lane] = m;
+    };
+    // Loads of chunk c's operands and start state (its meta is in LDS).
+    auto issue_stage = [&](int c, Staged &sg) {
+        const int len = chunk_len(c);
+        const int4 *mt = s_meta[c & 1];
+#pragma unroll
+        for (int e = 0; e < C; ++e) {
+            const int4 m = mt[e < len ? e : len - 1];
+            const int64_t row = int64_t(__builtin_amdgcn_readfirstlane(m.x)) * p.heads + head;
+            const T *src = __builtin_amdgcn_readfirstlane(m.z) ? p.dy : p.v;
+            const T *src2 = __builtin_amdgcn_readfirstlane(m.z) ? p.dy : p.w;
+            sg.a[e] = P2::load(src + row * p.width + colc);
+            sg.b[e] = P2::load(src2 + row * p.width + colc);
+        }
+        {
+            const int e = lane >> 2, rp = (lane & 3) * 2;
+            const int4 m = mt[e < len ? e : len - 1];
+            const int64_t at = (int64_t(m.x) * p.heads + head) * S + rp;
+            sg.kq = P2::load((m.z ? p.q : p.k) + at);
+            sg.bb = P2::load(p.b + at);
+            sg.g = *reinterpret_cast<const float2 *>(p.g + at);
+        }
+        if (c > 0) {
+            const SNAP *snap = static_cast<const SNAP *>(p.snap) +
+                               (((start + int64_t(c) * C) / C - 1) * p.heads + head) * S * p.width + colc;
+#pragma unroll
+            for (int r = 0; r < S; ++r) sg.m0[r] = Pair<SNAP>::load(snap + r * p.width);
+        }
+    };
+    // Operand rows, columns and the start state of chunk c into LDS.
+    auto finish_stage = [&](int c, const Staged &sg) {
+        float m0[S][CPL];
+        const int len = chunk_len(c);
+        const int4 *mt = s_meta[c & 1];
+#pragma unroll
+        for (int e = 0; e < C; ++e) {
+            const int4 m = mt[e < len ? e : len - 1];
+            const bool rd = __builtin_amdgcn_readfirstlane(m.z) != 0;
+            const float pw = __int_as_float(__builtin_amdgcn_readfirstlane(m.w));
+            ColSlot cs;
+            cs.a = live ? sg.a[e] : P2::zero();
+            cs.b = (live && !rd) ? P2::scaled(sg.b[e], pw) : P2::zero();
+            s_cols[e][lane] = cs;
+        }
+        {
+            const int e = lane >> 2, rp = (lane & 3) * 2;
+            const int4 m = mt[e < len ? e : len - 1];
+            const float pw = __int_as_float(m.w);
+            float *row = reinterpret_cast<float *>(&s_rows[e][0]);
+            const float x0 = P2::lo(sg.kq), x1 = P2::hi(sg.kq);
+            if (m.z) {
+                row[rp] = round_to<T>(x0 * pw) * p.scale;
+                row[rp + 1] = round_to<T>(x1 * pw) * p.scale;
+            } else {
+                // k, decay = exp(g p) (prepare_write_rows)
+                const float eg0 = p.routed_decay ? sg.g.x * pw : sg.g.x;
+                const float eg1 = p.routed_decay ? sg.g.y * pw : sg.g.y;
+                const float eb0 = round_to<T>(P2::lo(sg.bb) * pw), eb1 = round_to<T>(P2::hi(sg.bb) * pw);
+                row[rp] = x0;
+                row[rp + 1] = x1;
+                row[S + rp] = __expf(eg0);
+                row[S + rp + 1] = __expf(eg1);
+                // ad = a * decay, a = bf(b p) k
+                row[2 * S + rp] = eb0 * x0 * row[S + rp];
+                row[2 * S + rp + 1] = eb1 * x1 * row[S + rp + 1];
+            }
+        }
+        if (c > 0) {
+#pragma unroll
+            for (int r = 0; r < S; ++r) {
+                m0[r][0] = live ? Pair<SNAP>::lo(sg.m0[r]) : 0.f;
+                m0[r][1] = live ? Pair<SNAP>::hi(sg.m0[r]) : 0.f;
+            }
+        } else {
+            // the segment's initial state (rounded to BF16 under the rounding policy)
+            const int64_t off = bidx * p.init_bstride + (int64_t(bank) * p.heads + head) * S * p.width + colc;
+            float lo[S], hi[S];
+            if (p.init_dtype == BDM_BF16) {
+                uint32_t x[S];
+#pragma unroll
+                for (int r = 0; r < S; ++r)
+                    x[r] = Pair<bf16_t>::load(static_cast<const bf16_t *>(p.initial) + off + r * p.width);
+#pragma unroll
+                for (int r = 0; r < S; ++r) lo[r] = Pair<bf16_t>::lo(x[r]), hi[r] = Pair<bf16_t>::hi(x[r]);
+            } else {
+                float2 x[S];
+#pragma unroll
+                for (int r = 0; r < S; ++r) x[r] = Pair<float>::load(static_cast<const float *>(p.initial) + off + r * p.width);
+#pragma unroll
+                for (int r = 0; r < S; ++r) {
+                    lo[r] = x[r].x, hi[r] = x[r].y;
+                    if (p.rounding) round_pair<bf16_t>(lo[r], hi[r]);
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < S; ++r) {
+                m0[r][0] = live ? lo[r] : 0.f;
+                m0[r][1] = live ? hi[r] : 0.f;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < S; ++r) s_m0[r][lane] = make_float2(m0[r][0], m0[r][1]);
+    };
+    auto load_m0 = [&](float (&m)[S][CPL]) {
+#pragma unroll
+        for (int r = 0; r < S; ++r) {
+            const float2 x = s_m0[r][lane];
+            m[r][0] = x.x;
+            m[r][1] = x.y;
+        }
+    };
+
+    auto write_rows = [&](int e, float (&key)[S], float (&dec)[S], float (&ad)[S]) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const float4 k4 = s_rows[e][i], d4 = s_rows[e][2 + i], a4 = s_rows[e][4 + i];
+            key[4 * i] = k4.x, key[4 * i + 1] = k4.y, key[4 * i + 2] = k4.z, key[4 * i + 3] = k4.w;
+            dec[4 * i] = d4.x, dec[4 * i + 1] = d4.y, dec[4 * i + 2] = d4.z, dec[4 * i + 3] = d4.w;
+            ad[4 * i] = a4.x, ad[4 * i + 1] = a4.y, ad[4 * i + 2] = a4.z, ad[4 * i + 3] = a4.w;
+        }
+    };
+    // The write update on the lane's columns: M' = diag(decay) M + k u^T with
+    // u = bf(w p) v - (a o decay)^T M (apply_write up to FP32 rounding).
+    auto apply = [&](int e, float (&m)[S][CPL]) {
+        float key[S], dec[S], ad[S];
+        write_rows(e, key, dec, ad);
+        const ColSlot cs = s_cols[e][lane];
+        const float v[CPL] = {P2::lo(cs.a), P2::hi(cs.a)}, ew[CPL] = {P2::lo(cs.b), P2::hi(cs.b)};
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            float erase = 0.f;
+#pragma unroll
+            for (int r = 0; r < S; ++r) erase = fmaf(ad[r], m[r][c], erase);
+            const float u = fmaf(ew[c], v[c], -erase);
+#pragma unroll
+            for (int r = 0; r < S; ++r) m[r][c] = fmaf(key[r], u, m[r][c] * dec[r]);
+        }
+    };
+
+    float dm[S][CPL];
+#pragma unroll
+    for (int r = 0; r < S; ++r)
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) dm[r][c] = 0.f;
+
+    // Adjoint of write event e with pre-event state st (hd = diag(decay) st):
+    //   U = dm u, X = hd du = decay o (st du), P = rowsum(dm o hd) = decay o rowsum(dm o st)
+    auto write_back = [&](int e, int buf, const float (&st)[S][CPL]) {
+        float key[S], dec[S], ad[S];
+        write_rows(e, key, dec, ad);
+        const ColSlot cs = s_cols[e][lane];
+        const float v[CPL] = {P2::lo(cs.a), P2::hi(cs.a)}, ew[CPL] = {P2::lo(cs.b), P2::hi(cs.b)};
+        float u[CPL], du[CPL];
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+            float erase = 0.f, acc = 0.f;
+#pragma unroll
+            for (int r = 0; r < S; ++r) {
+                erase = fmaf(ad[r], st[r][c], erase);
+                acc = fmaf(dm[r][c], key[r], acc);
+            }
+            u[c] = fmaf(ew[c], v[c], -erase);
+            du[c] = acc;
+        }
+        const int64_t slot = __builtin_amdgcn_readfirstlane(s_meta[buf][e].y);
+        if (live) *reinterpret_cast<float2 *>(p.du + (slot * p.heads + head) * p.width + col0) = make_float2(du[0], du[1]);
+        float *wp = p.wpart + ((int64_t(tile) * wslots + slot) * p.heads + head) * 3 * S;
+        // rows 0..3, then 4..7: red = U[4], X'[4], P'[4] of the group
+#pragma unroll
+        for (int g = 0; g < 2; ++g) {
+            float red[12];
+#pragma unroll
+            for (int i = 0; i < 12; ++i) red[i] = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = 4 * g + i;
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) {
+                    red[i] = fmaf(dm[r][c], u[c], red[i]);
+                    red[4 + i] = fmaf(st[r][c], du[c], red[4 + i]);
+                    red[8 + i] = fmaf(dm[r][c], st[r][c], red[8 + i]);
+                    // dm <- (dm - a du^T) o decay (role_bank_kernel.py:130-138)
+                    dm[r][c] = fmaf(-ad[r], du[c], dm[r][c] * dec[r]);
+                }
+            }
+            float o = reduce_scatter<12>(red, lane);
+            const int pos = lane & 15;
+            const int at = 3 * (lane >> 4) + pos;  // kind = at / 4, row 4g + at % 4
+            if (pos < 3) {
+                const int kind = at >> 2, r = 4 * g + (at & 3);
+                if (kind > 0) o *= reinterpret_cast<const float *>(&s_rows[e][2])[r];
+                wp[kind * S + r] = o;
+            }
+        }
+    };
+    // Adjoint of read event e with state st.
+    auto read_back = [&](int e, int buf, const float (&st)[S][CPL]) {
+        const float4 q0 = s_rows[e][0], q1 = s_rows[e][1];
+        const float eq[S] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        const ColSlot cs = s_cols[e][lane];
+        const float dy[CPL] = {P2::lo(cs.a), P2::hi(cs.a)};
+        float red[S];
+#pragma unroll
+        for (int r = 0; r < S; ++r) {
+            red[r] = 0.f;
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) red[r] = fmaf(st[r][c], dy[c], red[r]);
+        }
+#pragma unroll
+        for (int r = 0; r < S; ++r)
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) dm[r][c] = fmaf(eq[r], dy[c], dm[r][c]);
+        const int64_t slot = __builtin_amdgcn_readfirstlane(s_meta[buf][e].y);
+        const float o = reduce_scatter<S>(red, lane);
+        const int pos = lane & 15;
+        if (pos < S / 4)
+            p.rpart[((int64_t(tile) * rslots + slot) * p.heads + head) * S + (S / 4) * (lane >> 4) + pos] =
+                o * p.scale;
+    };
+
+    if (count > 0) {
+        store_meta(count - 1, load_meta(count - 1));
+        int4 prev = make_int4(0, 0, 0, 0);
+        if (count > 1) prev = load_meta(count - 2);
+        __syncthreads();
+        Staged sg;
+        issue_stage(count - 1, sg);
+        if (count > 1) store_meta(count - 2, prev);
+        __syncthreads();
+        finish_stage(count - 1, sg);
+    }
+
+#pragma unroll 1
+    for (int c = count - 1; c >= 0; --c) {
+        __syncthreads();
+        const int buf = c & 1;
+        const int len = chunk_len(c);
+        const int4 mine = s_meta[buf][lane & (C - 1)];
+        const uint32_t wmask = uint32_t(__ballot(lane < len && mine.z == 0)) & 0xffffu;
+        const uint32_t rmask = uint32_t(__ballot(lane < len && mine.z != 0)) & 0xffffu;
+        float st[HALF][S][CPL];
+        if (len > HALF) {
+            float m[S][CPL];
+            load_m0(m);
+#pragma unroll
+            for (int e = 0; e < C - 1; ++e) {
+                if (e >= HALF) {
+#pragma unroll
+                    for (int r = 0; r < S; ++r)
+#pragma unroll
+                        for (int cc = 0; cc < CPL; ++cc) st[e - HALF][r][cc] = m[r][cc];
+                }
+                if (wmask & (1u << e)) apply(e, m);
+            }
+#pragma unroll
+            for (int r = 0; r < S; ++r)
+#pragma unroll
+                for (int cc = 0; cc < CPL; ++cc) st[HALF - 1][r][cc] = m[r][cc];
+#pragma unroll
+            for (int e = C - 1; e >= HALF; --e) {
+                if (wmask & (1u << e)) write_back(e, buf, st[e - HALF]);
+                else if (rmask & (1u << e)) read_back(e, buf, st[e - HALF]);
+            }
+        }
+        {
+            float m[S][CPL];
+            load_m0(m);
+#pragma unroll
+            for (int e = 0; e < HALF; ++e) {
+#pragma unroll
+                for (int r = 0; r < S; ++r)
+#pragma unroll
+                    for (int cc = 0; cc < CPL; ++cc) st[e][r][cc] = m[r][cc];
+                if (e + 1 < HALF && (wmask & (1u << e))) apply(e, m);
+            }
+        }
+#pragma unroll
+        for (int e = HALF - 1; e >= HALF / 2; --e) {
+            if (wmask & (1u << e)) write_back(e, buf, st[e]);
+            else if (rmask & (1u << e)) read_back(e, buf, st[e]);
+        }
+        // the next chunk's loads, in flight while events 3..0 are differentiated
+        int4 meta2 = make_int4(0, 0, 0, 0);
+        Staged sg;
+        if (c >= 2) meta2 = load_meta(c - 2);
+        if (c >= 1) issue_stage(c - 1, sg);
+#pragma unroll
+        for (int e = HALF / 2 - 1; e >= 0; --e) {
+            if (wmask & (1u << e)) write_back(e, buf, st[e]);
+            else if (rmask & (1u << e)) read_back(e, buf, st[e]);
+        }
+        __syncthreads();
+        if (c >= 2) store_meta(c - 2, meta2);
+        if (c >= 1) finish_stage(c - 1, sg);
+    }
+    // adjoint of the segment's initial state (FP32, per sequence)
+    if (live) {
+        const int64_t off = ((bidx * p.banks + bank) * p.heads + head) * S * p.width + col0;
+#pragma unroll
+        for (int r = 0; r < S; ++r)
+            *reinterpret_cast<float2 *>(p.dinit + off + int64_t(r) * p.width) = make_float2(dm[r][0], dm[r][1]);
+    }
+}
+
+
 template <typename T>
 struct VjpParams {
-    const T *q, *b;
+    const T *q, *k, *b;
     const float *g;
     const T *v, *w;
     const T *ww, *rw;
@@ -340,6 +781,141 @@ __device__ __forceinline__ float wave_sum(float x) {
     return x;
 }
 
+// Sum over the 8 lanes of an 8-lane group (lane % 8 varies), in every lane.
+__device__ __forceinline__ float group8_sum(float x) {
+    x += __shfl_xor(x, 1, kLanes);
+    x += __shfl_xor(x, 2, kLanes);
+    return x + __shfl_xor(x, 4, kLanes);
+}
+
+// Sum over the 8 lanes of equal lane % 8 (lane / 8 varies), in every lane.
+__device__ __forceinline__ float stride8_sum(float x) {
+    x += __shfl_xor(x, 8, kLanes);
+    x += __shfl_xor(x, 16, kLanes);
+    return x + __shfl_xor(x, 32, kLanes);
+}
+
+// One workgroup per token, one wave per head (heads <= 16); S <= 8, KW, KR
+// <= 8 and width <= 64 * CPL.  Lane (j, r) = (lane / 8, lane % 8) holds the
+// S-side gradients of route slot j, row r; lane l owns value columns
+// l*CPL .. l*CPL + CPL - 1.  The rounding points follow
+// role_bank_dispatch.py:99-131; sums over slots and rows are in FP32.
+template <typename T, int CPL>
+__global__ __launch_bounds__(1024) void token_grad_kernel(VjpParams<T> p) {
+    constexpr int MAXH = 16, MAXK = 8;
+    __shared__ float s_route[MAXH][2 * MAXK];  // per head: d(ww) of each write slot, then d(rw)
+    __shared__ float s_wv[MAXH][MAXK];         // per head: the v,w-column part of d(ww)
+    const int64_t token = blockIdx.x;
+    const int head = threadIdx.x / kLanes, lane = threadIdx.x % kLanes;
+    const int64_t row = token * p.heads + head;
+    const int64_t wslots = p.nt * p.kw, rslots = p.nt * p.kr;
+    const int j = lane >> 3, r = lane & 7;
+    const bool srow = r < p.s_real;
+    const bool wl = srow && j < p.kw, rl = srow && j < p.kr;
+    const int64_t wslot = token * p.kw + (j < p.kw ? j : p.kw - 1);
+    const int64_t rslot = token * p.kr + (j < p.kr ? j : p.kr - 1);
+    const int rr = srow ? r : 0;
+
+    // ---- S side: slot j, row r
+    const float q0 = to_f32(p.q[row * p.s_real + rr]);
+    const float k0 = to_f32(p.k[row * p.s_real + rr]);
+    const float b0 = to_f32(p.b[row * p.s_real + rr]);
+    const float g0 = p.g[row * p.s_real + rr];
+    const float pw = to_f32(p.ww[wslot]), pr = to_f32(p.rw[rslot]);
+    float su = 0.f, sx = 0.f, sp = 0.f, sq = 0.f;
+    for (int t = 0; t < p.tiles; ++t) {
+        const float *wp = p.wpart + ((int64_t(t) * wslots + wslot) * p.heads + head) * 3 * p.s_real + rr;
+        su += wp[0];
+        sx += wp[p.s_real];
+        sp += wp[2 * p.s_real];
+        sq += p.rpart[((int64_t(t) * rslots + rslot) * p.heads + head) * p.s_real + rr];
+    }
+    // dk = U - eb X ; db = -k X ; dg = P - a X (role_bank_kernel.py:128-135)
+    const float eb = round_to<T>(b0 * pw);
+    const float dk = round_to<T>(su - eb * sx);
+    const float db = round_to<T>(-k0 * sx);
+    const float dg = sp - eb * k0 * sx;
+    // routed decay: the packed gate was g*p (routed_update.py:43-47)
+    const float k_term = wl ? dk : 0.f;
+    const float g_term = wl ? (p.routed_decay ? dg * pw : dg) : 0.f;
+    const float b_term = wl ? round_to<T>(db * pw) : 0.f;
+    const float wb = round_to<T>(group8_sum(wl ? round_to<T>(db * b0) : 0.f));
+    const float dec = group8_sum(wl ? dg * g0 : 0.f);
+    const float dq = round_to<T>(sq);
+    const float q_term = rl ? round_to<T>(dq * pr) : 0.f;
+    const float wr = round_to<T>(group8_sum(rl ? round_to<T>(dq * q0) : 0.f));
+    const float kwsum = stride8_sum(k_term), gsum = stride8_sum(g_term), bsum = stride8_sum(b_term);
+    const float qsum = stride8_sum(q_term);
+    if (j == 0 && srow) {
+        const int64_t at = row * p.s_real + r;
+        p.dq[at] = from_f32<T>(qsum);
+        p.dk[at] = from_f32<T>(kwsum);
+        p.dg[at] = gsum;
+        p.db[at] = from_f32<T>(bsum);
+    }
+
+    // ---- value columns: the token's write events in route order
+    const int c0 = lane * CPL;
+    bool live[CPL];
+    float v0[CPL], w0[CPL], vwsum[CPL], wsum[CPL], wv[MAXK];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        live[c] = c0 + c < p.width;
+        v0[c] = live[c] ? to_f32(p.v[row * p.width + c0 + c]) : 0.f;
+        w0[c] = live[c] ? to_f32(p.w[row * p.width + c0 + c]) : 0.f;
+        vwsum[c] = wsum[c] = 0.f;
+    }
+#pragma unroll
+    for (int jj = 0; jj < MAXK; ++jj) {
+        wv[jj] = 0.f;
+        if (jj < p.kw) {
+            const int64_t slot = token * p.kw + jj;
+            const float pj = to_f32(p.ww[slot]);
+            const float *du = p.du + (slot * p.heads + head) * p.width + c0;
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+                const float d = live[c] ? du[c] : 0.f;
+                const float ew = round_to<T>(w0[c] * pj);
+                const float dv = round_to<T>(d * ew);
+                const float dw = round_to<T>(d * v0[c]);
+                vwsum[c] = round_to<T>(vwsum[c] + dv);
+                wsum[c] = round_to<T>(wsum[c] + round_to<T>(dw * pj));
+                wv[jj] += round_to<T>(dw * w0[c]);
+            }
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        if (live[c]) {
+            p.dv[row * p.width + c0 + c] = from_f32<T>(vwsum[c]);
+            p.dw[row * p.width + c0 + c] = from_f32<T>(wsum[c]);
+        }
+    }
+    const float wv_total = reduce_scatter<MAXK>(wv, lane);
+    if ((lane & 15) < MAXK / 4) s_wv[head][(MAXK / 4) * (lane >> 4) + (lane & 15)] = wv_total;
+    __syncthreads();
+    if (r == 0) {
+        if (j < p.kw) {
+            float dww = round_to<T>(wb + round_to<T>(s_wv[head][j]));
+            if (p.routed_decay) dww = round_to<T>(dww + dec);
+            s_route[head][j] = dww;
+        }
+        if (j < p.kr) s_route[head][MAXK + j] = wr;
+    }
+    __syncthreads();
+    // route-weight gradients: the heads' contributions added in head order
+    if (threadIdx.x < unsigned(p.kw + p.kr)) {
+        const int jj = threadIdx.x;
+        const bool wr_ = jj < p.kw;
+        const int col = wr_ ? jj : MAXK + jj - p.kw;
+        float total = 0.f;
+        for (int h = 0; h < p.heads; ++h) total += s_route[h][col];
+        if (wr_) p.dww[token * p.kw + jj] = from_f32<T>(total);
+        else p.drw[token * p.kr + (jj - p.kw)] = from_f32<T>(total);
+    }
+}
+
+
 // One workgroup (4 waves) per token.  VPL = value columns per lane.
 template <typename T, int VPL>
 __global__ __launch_bounds__(256) void token_vjp_kernel(VjpParams<T> p) {
@@ -353,6 +929,7 @@ __global__ __launch_bounds__(256) void token_vjp_kernel(VjpParams<T> p) {
         const int64_t row = token * p.heads + head;
         const bool srow = lane < p.s_real;
         const float q0 = srow ? to_f32(p.q[row * p.s_real + lane]) : 0.f;
+        const float k0 = srow ? to_f32(p.k[row * p.s_real + lane]) : 0.f;
         const float b0 = srow ? to_f32(p.b[row * p.s_real + lane]) : 0.f;
         const float g0 = srow ? p.g[row * p.s_real + lane] : 0.f;
         float v0[VPL], w0[VPL], vwsum[VPL], wsum[VPL];
@@ -370,16 +947,18 @@ __global__ __launch_bounds__(256) void token_vjp_kernel(VjpParams<T> p) {
             const float pw = to_f32(p.ww[slot]);
             float wb_part = 0.f, dec_part = 0.f;
             if (srow) {
-                const int64_t at = (slot * p.heads + head) * p.s_real + lane;
-                float dk = 0.f, db = 0.f, dg = 0.f;
+                float su = 0.f, sx = 0.f, sp = 0.f;
                 for (int t = 0; t < p.tiles; ++t) {
-                    const float *wp = p.wpart + int64_t(t) * 3 * wslots * hs;
-                    dk += wp[at];
-                    db += wp[wslots * hs + at];
-                    dg += wp[2 * wslots * hs + at];
+                    const float *wp = p.wpart + ((int64_t(t) * wslots + slot) * p.heads + head) * 3 * p.s_real;
+                    su += wp[lane];
+                    sx += wp[p.s_real + lane];
+                    sp += wp[2 * p.s_real + lane];
                 }
-                dk = round_to<T>(dk);
-                db = round_to<T>(db);
+                // dk = U - eb X ; db = -k X ; dg = P - a X (role_bank_kernel.py:128-135)
+                const float eb = round_to<T>(b0 * pw);
+                const float dk = round_to<T>(su - eb * sx);
+                const float db = round_to<T>(-k0 * sx);
+                const float dg = sp - eb * k0 * sx;
                 kwsum += dk;
                 // routed decay: the packed gate was g*p (routed_update.py:43-47)
                 gsum += p.routed_decay ? dg * pw : dg;
@@ -455,12 +1034,32 @@ __global__ __launch_bounds__(256) void token_vjp_kernel(VjpParams<T> p) {
 
 struct Workspace {
     float *du, *wpart, *rpart;
+    int4 *meta;  // per-event meta of the S = 8 chunk kernel (null otherwise)
     size_t bytes;
 };
 
 constexpr size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
 int column_lanes_per_tile(int bank_size) { return bank_size <= 8 ? 2 : 1; }
+
+int replay_interval(const bdm_backward_args &a) {
+    return a.round_interval > 0 ? a.round_interval : a.snapshot_interval;
+}
+
+// The S = 8, interval-16 chunk kernel: even head width (column pairs) and
+// token and route indices in 32 bits.
+bool chunk_path(const bdm_backward_args &a) {
+    const int64_t nt = a.batch * a.time;
+    const int64_t k = a.write_banks > a.read_banks ? a.write_banks : a.read_banks;
+    return a.bank_size == 8 && replay_interval(a) == 16 && a.head_width % 2 == 0 && a.write_banks >= 1 &&
+           a.read_banks >= 1 && nt * k < INT32_MAX;
+}
+
+// The per-token gradient kernel: one wave per head and one lane per (slot, row).
+bool token_grad_path(const bdm_backward_args &a) {
+    return a.bank_size <= 8 && a.write_banks >= 1 && a.write_banks <= 8 && a.read_banks >= 1 && a.read_banks <= 8 &&
+           a.heads <= 16 && a.head_width <= 256;
+}
 
 Workspace carve(const bdm_backward_args &a, void *base) {
     const size_t nt = size_t(a.batch) * size_t(a.time);
@@ -470,12 +1069,14 @@ Workspace carve(const bdm_backward_args &a, void *base) {
     const size_t du = align256(nt * a.write_banks * a.heads * size_t(a.head_width) * sizeof(float));
     const size_t wp = align256(tiles * 3 * nt * a.write_banks * hs * sizeof(float));
     const size_t rp = align256(tiles * nt * a.read_banks * hs * sizeof(float));
+    const size_t mt = chunk_path(a) ? align256(nt * size_t(a.write_banks + a.read_banks) * sizeof(int4)) : 0;
     char *c = static_cast<char *>(base);
     Workspace w{};
     w.du = reinterpret_cast<float *>(c);
     w.wpart = reinterpret_cast<float *>(c ? c + du : nullptr);
     w.rpart = reinterpret_cast<float *>(c ? c + du + wp : nullptr);
-    w.bytes = du + wp + rp;
+    w.meta = reinterpret_cast<int4 *>(c && mt ? c + du + wp + rp : nullptr);
+    w.bytes = du + wp + rp + mt;
     return w;
 }
 
@@ -516,11 +1117,31 @@ int launch_backward(const bdm_backward_args &a, const Workspace &ws, hipStream_t
     const int64_t nseg = a.batch * a.bank_count;
     p.xcd_remap = (nseg % 8 == 0) ? 1 : 0;
     const dim3 grid(unsigned(nseg), unsigned(a.heads), unsigned(p.tiles));
-    routed_backward_kernel<T, S, CPL, C><<<grid, kLanes, 0, stream>>>(p);
-    if (int rc = check_launch("routed_backward_kernel")) return rc;
+    if constexpr (S == 8 && C == 16) {
+        if (chunk_path(a)) {
+            const int64_t events = p.nt * (p.kw + p.kr);
+            const unsigned blocks = unsigned((events + 255) / 256);
+            event_meta_kernel<T><<<blocks, 256, 0, stream>>>(p.order, events, p.nt * p.kw, p.kw, p.kr, p.ww, p.rw,
+                                                            ws.meta);
+            if (int rc = check_launch("event_meta_kernel")) return rc;
+            p.meta = ws.meta;
+            if (a.snapshot_dtype == BDM_BF16)
+                chunk_backward_kernel<T, bf16_t><<<grid, kLanes, 0, stream>>>(p);
+            else
+                chunk_backward_kernel<T, float><<<grid, kLanes, 0, stream>>>(p);
+            if (int rc = check_launch("chunk_backward_kernel")) return rc;
+        } else {
+            routed_backward_kernel<T, S, CPL, C><<<grid, kLanes, 0, stream>>>(p);
+            if (int rc = check_launch("routed_backward_kernel")) return rc;
+        }
+    } else {
+        routed_backward_kernel<T, S, CPL, C><<<grid, kLanes, 0, stream>>>(p);
+        if (int rc = check_launch("routed_backward_kernel")) return rc;
+    }
 
     VjpParams<T> v{};
     v.q = p.q;
+    v.k = p.k;
     v.b = p.b;
     v.g = p.g;
     v.v = p.v;
@@ -546,8 +1167,18 @@ int launch_backward(const bdm_backward_args &a, const Workspace &ws, hipStream_t
     v.kr = a.read_banks;
     v.tiles = p.tiles;
     v.routed_decay = a.routed_decay;
-    const size_t lds = size_t(a.heads) * size_t(a.write_banks + a.read_banks) * sizeof(float);
     const unsigned blocks = unsigned(p.nt);
+    if (token_grad_path(a)) {
+        const unsigned threads = unsigned(a.heads) * kLanes;
+        if (a.head_width <= kLanes)
+            token_grad_kernel<T, 1><<<blocks, threads, 0, stream>>>(v);
+        else if (a.head_width <= 2 * kLanes)
+            token_grad_kernel<T, 2><<<blocks, threads, 0, stream>>>(v);
+        else
+            token_grad_kernel<T, 4><<<blocks, threads, 0, stream>>>(v);
+        return check_launch("token_grad_kernel");
+    }
+    const size_t lds = size_t(a.heads) * size_t(a.write_banks + a.read_banks) * sizeof(float);
     if (a.head_width <= kLanes)
         token_vjp_kernel<T, 1><<<blocks, 256, lds, stream>>>(v);
     else if (a.head_width <= 2 * kLanes)

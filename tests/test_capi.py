@@ -110,10 +110,14 @@ def test_backward_rejects_bad_arguments(lib):
     assert lib.bdm_backward(ctypes.byref(args), None, 0, None) == -1
     args.round_interval, args.snapshot_interval = 0, 16
     assert lib.bdm_backward(ctypes.byref(args), None, 0, None) == -1  # BF16 snapshots of an unrounded state
-    # du (NT*KW*H*v FP32) + dk/db/dg (3*NT*KW*H*S) + dq (NT*KR*H*S), each 256-byte aligned
+    # du (NT*KW*H*v FP32) + U/X/P (3*NT*KW*H*S) + dq (NT*KR*H*S), each 256-byte aligned, and for
+    # S = 8 with replay interval 16 the per-event meta (E x 16 bytes)
     args.snapshot_dtype = _lib.BDM_F32
     size = lib.bdm_backward_workspace_size(ctypes.byref(args))
     up = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    assert size == up(4 * 16 * 4) + up(3 * 4 * 8 * 4) + up(4 * 8 * 4) + up(4 * 2 * 16)
+    args.snapshot_interval = 8
+    size = lib.bdm_backward_workspace_size(ctypes.byref(args))
     assert size == up(4 * 16 * 4) + up(3 * 4 * 8 * 4) + up(4 * 8 * 4)
     assert lib.bdm_snapshot_rows(1000, 16) == 62 and lib.bdm_snapshot_rows(0, 16) == 0
 

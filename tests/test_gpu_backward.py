@@ -49,6 +49,11 @@ CASES = [
     (1, 64, 1, 8, 128, 4, 2, True, torch.bfloat16, torch.bfloat16),
     (2, 24, 2, 8, 32, 16, 4, True, torch.float32, torch.float32),
     (1, 20, 2, 8, 200, 16, 4, True, torch.bfloat16, torch.bfloat16),
+    # every token writes and reads all 4 banks: 200-event segments, 13 chunks of 16
+    (1, 100, 2, 8, 128, 4, 4, True, torch.bfloat16, torch.bfloat16),
+    (1, 100, 1, 8, 128, 4, 4, True, torch.float32, torch.bfloat16),
+    # 64 banks, 12 tokens: empty and 1..8-event segments
+    (2, 12, 2, 8, 128, 64, 2, True, torch.bfloat16, torch.bfloat16),
 ]
 
 
