@@ -348,6 +348,14 @@ __device__ __forceinline__ float dpp_add(float x) {
                                                                      false));
 }
 
+// x of the lane CTRL (a DPP row_shr / row_shl) names inside the 16-lane row,
+// 1 where that lane lies outside the row.
+template <int CTRL>
+__device__ __forceinline__ float row_shift(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, 1.f),
+                                                                 __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
+}
+
 // Total of a 16-lane row in every lane of the row.
 __device__ __forceinline__ float row_total(float x) {
     x = dpp_add<0xB1>(x);      // quad_perm [1,0,3,2]
@@ -372,6 +380,9 @@ __device__ __forceinline__ float reduce_scatter(const float (&x)[N], int lane) {
     float out = z[0];
 #pragma unroll
     for (int i = 1; i < N / 4; ++i) out = pos == i ? z[i] : out;
+    // computed in every lane: keeps the DPP adds fused when the caller stores
+    // from a subset of lanes
+    asm volatile("" : "+v"(out));
     return out;
 }
 
@@ -418,6 +429,10 @@ template <typename T, typename SNAP>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void chunk_backward_kernel(
     BackwardParams<T> p) {
     constexpr int S = 8, CPL = 2, C = 16, HALF = 8;
+    // Per-event operand row (64 floats).  Write: the adjoint's k*sigma,
+    // erase coefficient a*decay*s, update a/sigma, replay k/s', the output
+    // scales of U, X, P and the decay; read: eq*scale/sigma and dq's scale.
+    constexpr int kKey = 0, kErase = 8, kUpd = 16, kRep = 24, kScale = 32, kDecay = 56;
     using P2 = Pair<T>;
     using Raw = typename P2::raw;
     using SnapRaw = typename Pair<SNAP>::raw;
@@ -431,9 +446,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void ch
         SnapRaw m0[S];  // snapshot rows (chunks > 0)
     };
     __shared__ int4 s_meta[2][C];
-    __shared__ float4 s_rows[C][6];  // write: k, decay, ad = a*decay (2 x float4 each); read: eq*scale in [0..1]
+    __shared__ float4 s_rows[C][16];
     __shared__ ColSlot s_cols[C][kLanes];
     __shared__ float2 s_m0[S][kLanes];  // the chunk's start state, lane's column pair per row
+    __shared__ float s_fold[S];         // product of the chunk's decays per row (lazy chunks) or 1
+    __shared__ int s_eager;
 
     const int nseg = gridDim.x;
     const int seg = p.xcd_remap ? int((blockIdx.x % 8) * (nseg / 8) + blockIdx.x / 8) : int(blockIdx.x);
@@ -447,7 +464,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void ch
     const int colc = live ? col0 : p.width - CPL;  // lanes past the width load a valid pair and zero it
     const int64_t start = p.cu[seg], end = p.cu[seg + 1];
     const int count = int((end - start + C - 1) / C);
-    const int64_t wslots = p.nt * p.kw, rslots = p.nt * p.kr;
+    const uint32_t hw = uint32_t(p.heads) * uint32_t(p.width);
+    const int lane_col = head * p.width + colc;  // offset of the lane's pair in a [token] row of H*v
+    // event-uniform bases: x[slot] + per-lane offset
+    float *du_lane = p.du + head * p.width + col0;
+    float *wp_tile = p.wpart + (int64_t(tile) * p.nt * p.kw * p.heads + head) * 3 * S;
+    float *rp_tile = p.rpart + (int64_t(tile) * p.nt * p.kr * p.heads + head) * S;
 
     auto chunk_len = [&](int c) { return int(min(int64_t(C), end - (start + int64_t(c) * C))); };
     auto load_meta = [&](int c) {
@@ -464,14 +486,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void ch
 #pragma unroll
         for (int e = 0; e < C; ++e) {
             const int4 m = mt[e < len ? e : len - 1];
-            const int64_t row = int64_t(__builtin_amdgcn_readfirstlane(m.x)) * p.heads + head;
-            const T *src = __builtin_amdgcn_readfirstlane(m.z) ? p.dy : p.v;
-            const T *src2 = __builtin_amdgcn_readfirstlane(m.z) ? p.dy : p.w;
-            sg.a[e] = P2::load(src + row * p.width + colc);
-            sg.b[e] = P2::load(src2 + row * p.width + colc);
+            const uint64_t row = uint64_t(uint32_t(__builtin_amdgcn_readfirstlane(m.x))) * hw;
+            const bool rd = __builtin_amdgcn_readfirstlane(m.z) != 0;
+            sg.a[e] = P2::load((rd ? p.dy : p.v) + row + lane_col);
+            sg.b[e] = P2::load((rd ? p.dy : p.w) + row + lane_col);
         }
         {
-            const int e = lane >> 2, rp = (lane & 3) * 2;
+            const int e = lane & (C - 1), rp = (lane >> 4) * 2;
             const int4 m = mt[e < len ? e : len - 1];
             const int64_t at = (int64_t(m.x) * p.heads + head) * S + rp;
             sg.kq = P2::load((m.z ? p.q : p.k) + at);
@@ -487,7 +508,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void ch
     };
     // Operand rows, columns and the start state of chunk c into LDS.
     auto finish_stage = [&](int c, const Staged &sg) {
-        float m0[S][CPL];
         const int len = chunk_len(c);
         const int4 *mt = s_meta[c & 1];
 #pragma unroll
@@ -501,28 +521,69 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void ch
             s_cols[e][lane] = cs;
         }
         {
-            const int e = lane >> 2, rp = (lane & 3) * 2;
+            // lane = 16 j + e holds rows 2j, 2j+1 of event e: the scans over a
+            // chunk's events run inside 16-lane rows (DPP row shifts)
+            const int e = lane & (C - 1), rp = (lane >> 4) * 2;
             const int4 m = mt[e < len ? e : len - 1];
+            const bool valid = e < len;
+            const bool wr = valid && m.z == 0;
             const float pw = __int_as_float(m.w);
-            float *row = reinterpret_cast<float *>(&s_rows[e][0]);
-            const float x0 = P2::lo(sg.kq), x1 = P2::hi(sg.kq);
-            if (m.z) {
-                row[rp] = round_to<T>(x0 * pw) * p.scale;
-                row[rp + 1] = round_to<T>(x1 * pw) * p.scale;
-            } else {
-                // k, decay = exp(g p) (prepare_write_rows)
-                const float eg0 = p.routed_decay ? sg.g.x * pw : sg.g.x;
-                const float eg1 = p.routed_decay ? sg.g.y * pw : sg.g.y;
-                const float eb0 = round_to<T>(P2::lo(sg.bb) * pw), eb1 = round_to<T>(P2::hi(sg.bb) * pw);
-                row[rp] = x0;
-                row[rp + 1] = x1;
-                row[S + rp] = __expf(eg0);
-                row[S + rp + 1] = __expf(eg1);
-                // ad = a * decay, a = bf(b p) k
-                row[2 * S + rp] = eb0 * x0 * row[S + rp];
-                row[2 * S + rp + 1] = eb1 * x1 * row[S + rp + 1];
+            const float x[2] = {P2::lo(sg.kq), P2::hi(sg.kq)};  // k of a write, q of a read
+            const float bv[2] = {P2::lo(sg.bb), P2::hi(sg.bb)};
+            const float gv[2] = {sg.g.x, sg.g.y};
+            float d[2], a[2], pre[2], suf[2], pre_x[2], suf_x[2];
+            bool bad = false;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                // decay = exp(g p), a = bf(b p) k (prepare_write_rows); 1 for reads
+                d[i] = wr ? __expf(p.routed_decay ? gv[i] * pw : gv[i]) : 1.f;
+                a[i] = round_to<T>(bv[i] * pw) * x[i];
+                // inclusive prefix and suffix products of the decays over the chunk's events
+                pre[i] = d[i] * row_shift<0x111>(d[i]);
+                pre[i] *= row_shift<0x112>(pre[i]);
+                pre[i] *= row_shift<0x114>(pre[i]);
+                pre[i] *= row_shift<0x118>(pre[i]);
+                suf[i] = d[i] * row_shift<0x101>(d[i]);
+                suf[i] *= row_shift<0x102>(suf[i]);
+                suf[i] *= row_shift<0x104>(suf[i]);
+                suf[i] *= row_shift<0x108>(suf[i]);
+                pre_x[i] = row_shift<0x111>(pre[i]);
+                suf_x[i] = row_shift<0x101>(suf[i]);
+                const float lo = 0x1p-40f, hi = 0x1p40f;
+                bad |= !(pre[i] >= lo && pre[i] <= hi && suf[i] >= lo && suf[i] <= hi);
             }
+            // Lazy chunk: state diag(s) Mh with s = the decays of the chunk's earlier
+            // writes, adjoint diag(sigma) dMh with sigma = those of its later writes.
+            // Eager chunk (a product out of range): s = sigma = 1 and both are
+            // multiplied by the decay after each write.
+            const bool eager = __ballot(bad) != 0;
+            float *row = reinterpret_cast<float *>(&s_rows[e][0]);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int r = rp + i;
+                const float s = eager ? 1.f : pre_x[i];                // before the event
+                const float s1 = eager ? max(d[i], 0x1p-40f) : pre[i];  // after a write
+                const float sg_ = eager ? 1.f : suf_x[i];
+                const float inv_sg = __builtin_amdgcn_rcpf(sg_);
+                if (m.z) {
+                    const float eqs = round_to<T>(x[i] * pw) * p.scale;
+                    row[kKey + r] = eqs * inv_sg;
+                    row[kScale + r] = p.scale * s;
+                } else {
+                    row[kKey + r] = x[i] * sg_;
+                    row[kErase + r] = a[i] * d[i] * s;
+                    row[kUpd + r] = a[i] * inv_sg;
+                    row[kRep + r] = x[i] * __builtin_amdgcn_rcpf(s1);
+                    row[kScale + r] = sg_;
+                    row[kScale + S + r] = d[i] * s;
+                    row[kScale + 2 * S + r] = d[i] * s * sg_;
+                    row[kDecay + r] = s1;
+                }
+                if (e == 0) s_fold[r] = eager ? 1.f : suf[i];
+            }
+            if (lane == 0) s_eager = eager ? 1 : 0;
         }
+        float m0[S][CPL];
         if (c > 0) {
 #pragma unroll
             for (int r = 0; r < S; ++r) {
@@ -543,7 +604,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void ch
             } else {
                 float2 x[S];
 #pragma unroll
-                for (int r = 0; r < S; ++r) x[r] = Pair<float>::load(static_cast<const float *>(p.initial) + off + r * p.width);
+                for (int r = 0; r < S; ++r)
+                    x[r] = Pair<float>::load(static_cast<const float *>(p.initial) + off + r * p.width);
 #pragma unroll
                 for (int r = 0; r < S; ++r) {
                     lo[r] = x[r].x, hi[r] = x[r].y;
@@ -567,32 +629,35 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void ch
             m[r][1] = x.y;
         }
     };
-
-    auto write_rows = [&](int e, float (&key)[S], float (&dec)[S], float (&ad)[S]) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const float4 k4 = s_rows[e][i], d4 = s_rows[e][2 + i], a4 = s_rows[e][4 + i];
-            key[4 * i] = k4.x, key[4 * i + 1] = k4.y, key[4 * i + 2] = k4.z, key[4 * i + 3] = k4.w;
-            dec[4 * i] = d4.x, dec[4 * i + 1] = d4.y, dec[4 * i + 2] = d4.z, dec[4 * i + 3] = d4.w;
-            ad[4 * i] = a4.x, ad[4 * i + 1] = a4.y, ad[4 * i + 2] = a4.z, ad[4 * i + 3] = a4.w;
-        }
+    auto rows8 = [&](int e, int at, float (&x)[S]) {
+        const float4 lo = s_rows[e][at / 4], hi = s_rows[e][at / 4 + 1];
+        x[0] = lo.x, x[1] = lo.y, x[2] = lo.z, x[3] = lo.w, x[4] = hi.x, x[5] = hi.y, x[6] = hi.z, x[7] = hi.w;
     };
-    // The write update on the lane's columns: M' = diag(decay) M + k u^T with
-    // u = bf(w p) v - (a o decay)^T M (apply_write up to FP32 rounding).
+    // Replay of write e: u = bf(w p) v - sum_r (a decay s)_r Mh_r ; Mh += (k / s') u.
     auto apply = [&](int e, float (&m)[S][CPL]) {
-        float key[S], dec[S], ad[S];
-        write_rows(e, key, dec, ad);
+        float ce[S], kt[S];
+        rows8(e, kErase, ce);
+        rows8(e, kRep, kt);
         const ColSlot cs = s_cols[e][lane];
         const float v[CPL] = {P2::lo(cs.a), P2::hi(cs.a)}, ew[CPL] = {P2::lo(cs.b), P2::hi(cs.b)};
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
             float erase = 0.f;
 #pragma unroll
-            for (int r = 0; r < S; ++r) erase = fmaf(ad[r], m[r][c], erase);
+            for (int r = 0; r < S; ++r) erase = fmaf(ce[r], m[r][c], erase);
             const float u = fmaf(ew[c], v[c], -erase);
 #pragma unroll
-            for (int r = 0; r < S; ++r) m[r][c] = fmaf(key[r], u, m[r][c] * dec[r]);
+            for (int r = 0; r < S; ++r) m[r][c] = fmaf(kt[r], u, m[r][c]);
         }
+    };
+    // Eager chunks: multiply by the decay after a write.
+    auto fold = [&](int e, float (&m)[S][CPL]) {
+        float dd[S];
+        rows8(e, kDecay, dd);
+#pragma unroll
+        for (int r = 0; r < S; ++r)
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) m[r][c] *= dd[r];
     };
 
     float dm[S][CPL];
@@ -601,11 +666,15 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void ch
 #pragma unroll
         for (int c = 0; c < CPL; ++c) dm[r][c] = 0.f;
 
-    // Adjoint of write event e with pre-event state st (hd = diag(decay) st):
-    //   U = dm u, X = hd du = decay o (st du), P = rowsum(dm o hd) = decay o rowsum(dm o st)
+    // Adjoint of write e, pre-event state st = diag(s) Mh, dm = diag(sigma) dMh:
+    //   du = dMh^T (k sigma); u = x - Mh^T (a decay s)
+    //   U = sigma (dMh u); X = decay s (Mh du); P = decay s sigma rowsum(dMh o Mh)
+    //   dMh -= (a / sigma) du^T                      (role_bank_kernel.py:128-138)
     auto write_back = [&](int e, int buf, const float (&st)[S][CPL]) {
-        float key[S], dec[S], ad[S];
-        write_rows(e, key, dec, ad);
+        float kk[S], ce[S], au[S];
+        rows8(e, kKey, kk);
+        rows8(e, kErase, ce);
+        rows8(e, kUpd, au);
         const ColSlot cs = s_cols[e][lane];
         const float v[CPL] = {P2::lo(cs.a), P2::hi(cs.a)}, ew[CPL] = {P2::lo(cs.b), P2::hi(cs.b)};
         float u[CPL], du[CPL];
@@ -614,16 +683,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void ch
             float erase = 0.f, acc = 0.f;
 #pragma unroll
             for (int r = 0; r < S; ++r) {
-                erase = fmaf(ad[r], st[r][c], erase);
-                acc = fmaf(dm[r][c], key[r], acc);
+                erase = fmaf(ce[r], st[r][c], erase);
+                acc = fmaf(dm[r][c], kk[r], acc);
             }
             u[c] = fmaf(ew[c], v[c], -erase);
             du[c] = acc;
         }
-        const int64_t slot = __builtin_amdgcn_readfirstlane(s_meta[buf][e].y);
-        if (live) *reinterpret_cast<float2 *>(p.du + (slot * p.heads + head) * p.width + col0) = make_float2(du[0], du[1]);
-        float *wp = p.wpart + ((int64_t(tile) * wslots + slot) * p.heads + head) * 3 * S;
-        // rows 0..3, then 4..7: red = U[4], X'[4], P'[4] of the group
+        const uint32_t slot = uint32_t(__builtin_amdgcn_readfirstlane(s_meta[buf][e].y));
+        if (live) *reinterpret_cast<float2 *>(du_lane + uint64_t(slot) * hw) = make_float2(du[0], du[1]);
+        float *wp = wp_tile + uint64_t(slot) * uint32_t(p.heads * 3 * S);
+        // rows 0..3, then 4..7: red = U[4], X[4], P[4] of the group
 #pragma unroll
         for (int g = 0; g < 2; ++g) {
             float red[12];
@@ -637,24 +706,21 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void ch
                     red[i] = fmaf(dm[r][c], u[c], red[i]);
                     red[4 + i] = fmaf(st[r][c], du[c], red[4 + i]);
                     red[8 + i] = fmaf(dm[r][c], st[r][c], red[8 + i]);
-                    // dm <- (dm - a du^T) o decay (role_bank_kernel.py:130-138)
-                    dm[r][c] = fmaf(-ad[r], du[c], dm[r][c] * dec[r]);
+                    dm[r][c] = fmaf(-au[r], du[c], dm[r][c]);
                 }
             }
-            float o = reduce_scatter<12>(red, lane);
             const int pos = lane & 15;
-            const int at = 3 * (lane >> 4) + pos;  // kind = at / 4, row 4g + at % 4
-            if (pos < 3) {
-                const int kind = at >> 2, r = 4 * g + (at & 3);
-                if (kind > 0) o *= reinterpret_cast<const float *>(&s_rows[e][2])[r];
-                wp[kind * S + r] = o;
-            }
+            const int at = 3 * (lane >> 4) + (pos < 3 ? pos : 0);  // kind = at / 4, row 4g + at % 4
+            const int kind = at >> 2, r = 4 * g + (at & 3);
+            const float o =
+                reduce_scatter<12>(red, lane) * reinterpret_cast<const float *>(&s_rows[e][0])[kScale + kind * S + r];
+            if (pos < 3) wp[kind * S + r] = o;
         }
     };
-    // Adjoint of read event e with state st.
+    // Adjoint of read e with state st = diag(s) Mh: dq = scale s (Mh dy); dMh += (eq scale / sigma) dy^T.
     auto read_back = [&](int e, int buf, const float (&st)[S][CPL]) {
-        const float4 q0 = s_rows[e][0], q1 = s_rows[e][1];
-        const float eq[S] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        float eq[S];
+        rows8(e, kKey, eq);
         const ColSlot cs = s_cols[e][lane];
         const float dy[CPL] = {P2::lo(cs.a), P2::hi(cs.a)};
         float red[S];
@@ -668,12 +734,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void ch
         for (int r = 0; r < S; ++r)
 #pragma unroll
             for (int c = 0; c < CPL; ++c) dm[r][c] = fmaf(eq[r], dy[c], dm[r][c]);
-        const int64_t slot = __builtin_amdgcn_readfirstlane(s_meta[buf][e].y);
-        const float o = reduce_scatter<S>(red, lane);
+        const uint32_t slot = uint32_t(__builtin_amdgcn_readfirstlane(s_meta[buf][e].y));
         const int pos = lane & 15;
-        if (pos < S / 4)
-            p.rpart[((int64_t(tile) * rslots + slot) * p.heads + head) * S + (S / 4) * (lane >> 4) + pos] =
-                o * p.scale;
+        const int at = (S / 4) * (lane >> 4) + (pos < S / 4 ? pos : 0);
+        const float o = reduce_scatter<S>(red, lane) * reinterpret_cast<const float *>(&s_rows[e][0])[kScale + at];
+        if (pos < S / 4) rp_tile[uint64_t(slot) * uint32_t(p.heads * S) + at] = o;
     };
 
     if (count > 0) {
@@ -696,6 +761,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void ch
         const int4 mine = s_meta[buf][lane & (C - 1)];
         const uint32_t wmask = uint32_t(__ballot(lane < len && mine.z == 0)) & 0xffffu;
         const uint32_t rmask = uint32_t(__ballot(lane < len && mine.z != 0)) & 0xffffu;
+        const uint32_t fmask = __builtin_amdgcn_readfirstlane(s_eager) ? wmask : 0u;
         float st[HALF][S][CPL];
         if (len > HALF) {
             float m[S][CPL];
@@ -709,6 +775,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void ch
                         for (int cc = 0; cc < CPL; ++cc) st[e - HALF][r][cc] = m[r][cc];
                 }
                 if (wmask & (1u << e)) apply(e, m);
+                if (fmask & (1u << e)) fold(e, m);
             }
 #pragma unroll
             for (int r = 0; r < S; ++r)
@@ -718,6 +785,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void ch
             for (int e = C - 1; e >= HALF; --e) {
                 if (wmask & (1u << e)) write_back(e, buf, st[e - HALF]);
                 else if (rmask & (1u << e)) read_back(e, buf, st[e - HALF]);
+                if (fmask & (1u << e)) fold(e, dm);
             }
         }
         {
@@ -729,23 +797,31 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void ch
                 for (int r = 0; r < S; ++r)
 #pragma unroll
                     for (int cc = 0; cc < CPL; ++cc) st[e][r][cc] = m[r][cc];
-                if (e + 1 < HALF && (wmask & (1u << e))) apply(e, m);
+                if (e + 1 < HALF) {
+                    if (wmask & (1u << e)) apply(e, m);
+                    if (fmask & (1u << e)) fold(e, m);
+                }
             }
         }
-#pragma unroll
-        for (int e = HALF - 1; e >= HALF / 2; --e) {
-            if (wmask & (1u << e)) write_back(e, buf, st[e]);
-            else if (rmask & (1u << e)) read_back(e, buf, st[e]);
-        }
-        // the next chunk's loads, in flight while events 3..0 are differentiated
+        // the next chunk's loads, in flight while events 7..0 are differentiated
         int4 meta2 = make_int4(0, 0, 0, 0);
         Staged sg;
         if (c >= 2) meta2 = load_meta(c - 2);
         if (c >= 1) issue_stage(c - 1, sg);
 #pragma unroll
-        for (int e = HALF / 2 - 1; e >= 0; --e) {
+        for (int e = HALF - 1; e >= 0; --e) {
             if (wmask & (1u << e)) write_back(e, buf, st[e]);
             else if (rmask & (1u << e)) read_back(e, buf, st[e]);
+            if (fmask & (1u << e)) fold(e, dm);
+        }
+        // the adjoint leaves the chunk in eager form: dm = diag(sigma) dMh
+        if (!fmask) {
+#pragma unroll
+            for (int r = 0; r < S; ++r) {
+                const float f = s_fold[r];
+#pragma unroll
+                for (int cc = 0; cc < CPL; ++cc) dm[r][cc] *= f;
+            }
         }
         __syncthreads();
         if (c >= 2) store_meta(c - 2, meta2);

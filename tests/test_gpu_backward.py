@@ -57,17 +57,17 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize('case', range(len(CASES)))
-def test_backward_matches_oracle_autograd(device, case):
+def check_against_oracle(device, case, seed, gmap=None):
     from bdm_amd import bank_training, role_bank_training
-    batch, time, heads, s, v, j, kk, routed, sdt, dt = CASES[case]
-    gen = torch.Generator().manual_seed(100 + case)
+    batch, time, heads, s, v, j, kk, routed, sdt, dt = case
+    gen = torch.Generator().manual_seed(seed)
     _, ww, wi = routes(batch, time, j, kk, gen, dtype=dt)
     _, rw, ri = routes(batch, time, j, kk, gen, dtype=dt)
     q, k, val, g, b, w = controllers(batch, time, heads, s, v, gen, dtype=dt)
+    if gmap is not None:
+        g = gmap(g, gen)
     state = initial_state(j, heads, s, v, gen, scale=0.1)
     dy = torch.randn(batch, time, heads * v, generator=gen).to(dt)
-    announce('backward', CASES[case])
     ref_y, ref = oracle_grads(q, k, val, g, b, w, wi, ww, ri, rw, state, j, dy, routed_decay=routed,
                               state_dtype=sdt)
     leaves = [t.to(device).requires_grad_(True) for t in (q, k, val, g, b, w, ww, rw, state)]
@@ -84,6 +84,30 @@ def test_backward_matches_oracle_autograd(device, case):
         assert ours.shape == theirs.shape and ours.dtype == theirs.dtype, name
         err = rel_err(ours, theirs)
         assert err < tol, (name, err)
+
+
+@pytest.mark.parametrize('case', range(len(CASES)))
+def test_backward_matches_oracle_autograd(device, case):
+    announce('backward', CASES[case])
+    check_against_oracle(device, CASES[case], 100 + case)
+
+
+# Decay regimes of the S = 8 chunk kernel: products of a chunk's decays far
+# below 2^-40 (every chunk in eager form), a mix of eager and lazy chunks,
+# and decays above 1 (g > 0 on some rows).
+DECAYS = {
+    'strong': lambda g, gen: g * 100.0,
+    'mixed': lambda g, gen: g * torch.where(torch.rand(g.shape[:2], generator=gen) < 0.3, 60.0, 1.0)[..., None, None],
+    'growth': lambda g, gen: (torch.rand(g.shape, generator=gen) - 0.5) * 0.6,
+}
+
+
+@pytest.mark.parametrize('regime', sorted(DECAYS))
+@pytest.mark.parametrize('sdt', [torch.bfloat16, torch.float32], ids=['bf16', 'f32'])
+def test_backward_decay_regimes(device, regime, sdt):
+    case = (2, 48, 2, 8, 128, 16, 4, True, sdt, torch.bfloat16)
+    announce('backward decay', regime, case)
+    check_against_oracle(device, case, 300, DECAYS[regime])
 
 
 def test_backward_per_head_layout_matches_multi_head(device):
