@@ -892,14 +892,42 @@ __global__ __launch_bounds__(1024) void token_grad_kernel(VjpParams<T> p) {
     const int64_t rslot = token * p.kr + (j < p.kr ? j : p.kr - 1);
     const int rr = srow ? r : 0;
 
-    // ---- S side: slot j, row r
+    // ---- every load first: the S side (slot j, row r), then the value columns
     const float q0 = to_f32(p.q[row * p.s_real + rr]);
     const float k0 = to_f32(p.k[row * p.s_real + rr]);
     const float b0 = to_f32(p.b[row * p.s_real + rr]);
     const float g0 = p.g[row * p.s_real + rr];
     const float pw = to_f32(p.ww[wslot]), pr = to_f32(p.rw[rslot]);
-    float su = 0.f, sx = 0.f, sp = 0.f, sq = 0.f;
-    for (int t = 0; t < p.tiles; ++t) {
+    const float *wp0 = p.wpart + (wslot * p.heads + head) * 3 * p.s_real + rr;
+    float su = wp0[0], sx = wp0[p.s_real], sp = wp0[2 * p.s_real];
+    float sq = p.rpart[(rslot * p.heads + head) * p.s_real + rr];
+    const int c0 = lane * CPL;
+    bool live[CPL];
+    float v0[CPL], w0[CPL], vwsum[CPL], wsum[CPL], wv[MAXK];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+        live[c] = c0 + c < p.width;
+        const int cc = min(c0 + c, p.width - 1);
+        const float vx = to_f32(p.v[row * p.width + cc]), wx = to_f32(p.w[row * p.width + cc]);
+        v0[c] = live[c] ? vx : 0.f;
+        w0[c] = live[c] ? wx : 0.f;
+        vwsum[c] = wsum[c] = 0.f;
+    }
+    // every slot's du and weight requested up front (slots >= KW re-read slot
+    // KW-1: straight-line loads, all in flight together)
+    float dus[MAXK][CPL], pws[MAXK];
+    int cols[CPL];  // clamped columns: lanes past the width re-read the last one and drop it
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) cols[c] = min(c0 + c, p.width - 1);
+#pragma unroll
+    for (int jj = 0; jj < MAXK; ++jj) {
+        const int64_t slot = token * p.kw + (jj < p.kw ? jj : p.kw - 1);
+        pws[jj] = to_f32(p.ww[slot]);
+        const float *du = p.du + (slot * p.heads + head) * p.width;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) dus[jj][c] = du[cols[c]];
+    }
+    for (int t = 1; t < p.tiles; ++t) {  // column tiles past the first
         const float *wp = p.wpart + ((int64_t(t) * wslots + wslot) * p.heads + head) * 3 * p.s_real + rr;
         su += wp[0];
         sx += wp[p.s_real];
@@ -931,26 +959,14 @@ __global__ __launch_bounds__(1024) void token_grad_kernel(VjpParams<T> p) {
     }
 
     // ---- value columns: the token's write events in route order
-    const int c0 = lane * CPL;
-    bool live[CPL];
-    float v0[CPL], w0[CPL], vwsum[CPL], wsum[CPL], wv[MAXK];
-#pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-        live[c] = c0 + c < p.width;
-        v0[c] = live[c] ? to_f32(p.v[row * p.width + c0 + c]) : 0.f;
-        w0[c] = live[c] ? to_f32(p.w[row * p.width + c0 + c]) : 0.f;
-        vwsum[c] = wsum[c] = 0.f;
-    }
 #pragma unroll
     for (int jj = 0; jj < MAXK; ++jj) {
         wv[jj] = 0.f;
         if (jj < p.kw) {
-            const int64_t slot = token * p.kw + jj;
-            const float pj = to_f32(p.ww[slot]);
-            const float *du = p.du + (slot * p.heads + head) * p.width + c0;
+            const float pj = pws[jj];
 #pragma unroll
             for (int c = 0; c < CPL; ++c) {
-                const float d = live[c] ? du[c] : 0.f;
+                const float d = live[c] ? dus[jj][c] : 0.f;
                 const float ew = round_to<T>(w0[c] * pj);
                 const float dv = round_to<T>(d * ew);
                 const float dw = round_to<T>(d * v0[c]);
