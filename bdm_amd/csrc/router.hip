@@ -2,16 +2,19 @@
 // FP32 softmax of the selected pair sums.
 //
 // Reference: product_key_route, implementation/bdm/gdn2_banks.py:74-114.
-// Selection is by rank, with one lane per score (a 32- or 64-lane group per
-// row), so a row costs a few dozen compares per lane instead of a serial
-// insertion sort.  The order is (value desc, index asc): that is the pinned
-// tie rule, equal values keep the lower index first.
+// One lane per row: the row's scores stream through two sorted top-s lists
+// held in registers (one per factor), then the candidate pairs through a
+// third; no LDS and no barriers.  Order is (value desc, index asc), the pinned
+// tie rule: entries arrive in increasing index and an arrival goes behind
+// every equal entry, so equal values keep the lower index first.
+// Values are compared as order-preserving 32-bit keys (NaN as -inf, -0 as
+// +0), with key 0 marking an empty slot below every score.
 //
 // Only pairs (i, l) of the two sorted factor lists with (i+1)(l+1) <= B can
 // reach the top B: the (i+1)(l+1)-1 pairs (i', l') <= (i, l) are all at least
 // as large (rounding is monotone) and come earlier in the flattened
 // i*s + l order, so they all precede (i, l).  Only those candidates are
-// formed, numbered in increasing flattened index.
+// formed, in increasing flattened index.
 #include <cfloat>
 
 #include "bdm_common.h"
@@ -19,155 +22,259 @@
 namespace bdm {
 namespace {
 
-template <int N>
-__device__ __forceinline__ void insert_sorted(float (&val)[N], int (&idx)[N], float x, int i) {
-#pragma unroll
-    for (int p = 0; p < N; ++p) {
-        const bool before = (x > val[p]) || (x == val[p] && i < idx[p]);
-        const float tv = before ? val[p] : x;
-        const int ti = before ? idx[p] : i;
-        val[p] = before ? x : val[p];
-        idx[p] = before ? i : idx[p];
-        x = tv;
-        i = ti;
-    }
-}
-
-// One lane per score (a G-lane group per row, G = 32 or 64), selection by
-// rank: an entry of a factor list is kept at position
-//   rank = #{entries before it in (value desc, index asc) order}
-// when rank < s.  NaN scores order as -inf (ties among them by index), so the
-// ranks always form a permutation.  The candidate pairs (i, l) with
-// (i+1)(l+1) <= count are enumerated in increasing flattened index i*s + l
-// and ranked the same way among themselves; the softmax sums the selected
-// exponentials in selection order, one lane per output.
-constexpr int kRouterBlock = 256;
 constexpr int kRouterMaxScores = 256;  // J1 + J2 per row
 constexpr int kRouterMaxSel = 16;
-constexpr int kRouterMaxCand = 64;     // pairs with (i+1)(l+1) <= 16: 50
 
-__device__ __forceinline__ float order_key(float x) { return x != x ? -INFINITY : x; }
-
-// a (value va, index ia) precedes b (value vb, index ib)
-__device__ __forceinline__ bool precedes(float va, int ia, float vb, int ib) {
-    return va > vb || (va == vb && ia < ib);
+// Order-preserving key of a score: NaN orders as -inf, -0 as +0; keys of real
+// values are >= 0x007FFFFF, so 0 can mark an empty slot.
+__device__ __forceinline__ uint32_t score_key(float x) {
+    if (x != x) x = -INFINITY;
+    uint32_t b = __float_as_uint(x);
+    if (b == 0x80000000u) b = 0u;
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
-template <typename T, int G>
-__global__ __launch_bounds__(kRouterBlock) void router_rank_kernel(const T *__restrict__ scores, int64_t rows,
-                                                                   int64_t stride, int j1, int j2, int selected,
-                                                                   T *__restrict__ weights,
-                                                                   int64_t *__restrict__ indices) {
-    constexpr int RB = kRouterBlock / G;  // rows per workgroup
-    __shared__ float s_val[RB][kRouterMaxScores];
-    __shared__ float s_sv[RB][2][kRouterMaxSel];  // sorted factor lists: values
-    __shared__ int s_si[RB][2][kRouterMaxSel];    // ... and indices
-    __shared__ float s_cand[RB][kRouterMaxCand];
-    __shared__ float s_pv[RB][kRouterMaxSel];     // selected pair sums, in order
-    __shared__ int s_pc[RB][kRouterMaxSel];       // ... and their candidate numbers
-    __shared__ float s_pe[RB][kRouterMaxSel];     // exp(selected - top)
+__device__ __forceinline__ float key_value(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k ^ 0x80000000u) : ~k);
+}
 
-    const int g = threadIdx.x / G, lane = threadIdx.x % G;
-    const int64_t row = int64_t(blockIdx.x) * RB + g;
-    const bool live = row < rows;
-    const int jt = j1 + j2;
+// Insert (k, id) into a list sorted by key desc, behind every entry with an
+// equal or larger key; the entries after it move down one slot and the last
+// one falls off.  c[p] = key[p] >= k is true on a prefix of the list, so slot
+// p keeps its entry (c[p]), takes the new one (first p with !c[p]) or takes
+// the entry of slot p-1.
+template <int N>
+__device__ __forceinline__ void insert_key(uint32_t (&key)[N], int (&id)[N], uint32_t k, int i) {
+    bool c[N];
+#pragma unroll
+    for (int p = 0; p < N; ++p) c[p] = key[p] >= k;
+#pragma unroll
+    for (int p = N - 1; p >= 0; --p) {
+        const bool prev = p == 0 ? true : c[p - 1];
+        const uint32_t nk = prev ? k : key[p > 0 ? p - 1 : 0];
+        const int ni = prev ? i : id[p > 0 ? p - 1 : 0];
+        key[p] = c[p] ? key[p] : nk;
+        id[p] = c[p] ? id[p] : ni;
+    }
+}
+
+// BF16 scores have 16-bit keys: an entry packs key16 << 16 | (0xffff - id),
+// so the larger entry is the earlier one in (value desc, index asc) order
+// and insertion is a max/min compare-exchange chain.  0 is an empty slot.
+__device__ __forceinline__ uint32_t pack_entry(float bf16_value, int id) {
+    return (score_key(bf16_value) & 0xffff0000u) | uint32_t(0xffff - id);
+}
+
+__device__ __forceinline__ float entry_value(uint32_t e) {
+    const uint32_t k = e >> 16;
+    return key_value((k << 16) | ((k & 0x8000u) ? 0u : 0xffffu));
+}
+
+__device__ __forceinline__ int entry_id(uint32_t e) { return 0xffff - int(e & 0xffffu); }
+
+// Slot p of the list with x inserted is the (p+1)-th largest of list + {x}:
+// max(list[p], min(list[p-1], x)) (entries are distinct).  Every slot is
+// independent of the others, so the insertion has no serial chain.
+template <int N>
+__device__ __forceinline__ void insert_entry(uint32_t (&list)[N], uint32_t x) {
+#pragma unroll
+    for (int p = N - 1; p > 0; --p) list[p] = max(list[p], min(list[p - 1], x));
+    list[0] = max(list[0], x);
+}
+
+// Eight scores of a row starting at element e0 (vector loads when VEC: the
+// row is 16-byte aligned; elements past the row repeat its last score).
+template <typename T, bool VEC>
+__device__ __forceinline__ void load_block(const T *z, int e0, int n, float (&x)[8]) {
+    if constexpr (VEC && sizeof(T) == 2) {
+        const uint4 raw = *reinterpret_cast<const uint4 *>(z + e0);
+        const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            x[2 * q] = __uint_as_float(w[q] << 16);
+            x[2 * q + 1] = __uint_as_float(w[q] & 0xffff0000u);
+        }
+    } else if constexpr (VEC) {
+        const float4 a = *reinterpret_cast<const float4 *>(z + e0), b = *reinterpret_cast<const float4 *>(z + e0 + 4);
+        x[0] = a.x, x[1] = a.y, x[2] = a.z, x[3] = a.w, x[4] = b.x, x[5] = b.y, x[6] = b.z, x[7] = b.w;
+    } else {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) x[q] = to_f32(z[min(e0 + q, n - 1)]);
+    }
+}
+
+// SM: list slots (>= selected); VEC: rows are 16-byte aligned and hold a
+// multiple of 8 scores.
+template <typename T, int SM, bool VEC>
+__global__ __launch_bounds__(64) void router_lane_kernel(const T *__restrict__ scores, int64_t rows, int64_t stride,
+                                                         int j1, int j2, int selected, T *__restrict__ weights,
+                                                         int64_t *__restrict__ indices) {
+    const int64_t row = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (row >= rows) return;
+    const T *z = scores + row * stride;
     const int s = min(selected, min(j1, j2));
     const int count = min(selected, s * s);
-    const T *z = scores + (live ? row : 0) * stride;
+    const int n = j1 + j2;
 
-    // (1) the row's scores
-    for (int e = lane; e < jt; e += G) s_val[g][e] = live ? order_key(to_f32(z[e])) : 0.f;
-    __syncthreads();
-    // (2) rank of each score within its factor; the top s form the sorted lists
-    for (int e = lane; e < jt; e += G) {
-        const int f = e < j1 ? 0 : 1;
-        const int lo = f ? j1 : 0, n = f ? j2 : j1, i = e - lo;
-        const float x = s_val[g][e];
-        int rank = 0;
-#pragma unroll 8
-        for (int jj = 0; jj < n; ++jj) rank += precedes(s_val[g][lo + jj], jj, x, i) ? 1 : 0;
-        if (rank < s) {
-            s_sv[g][f][rank] = x;
-            s_si[g][f][rank] = i;
-        }
-    }
-    __syncthreads();
-    // (3) candidate pairs in increasing flattened index; their pair sums are
-    // formed in the score dtype (gdn2_banks.py:106)
-    int ci = -1, cl = -1;
-    {
-        int c = 0;
-        for (int i = 0; i < s; ++i) {
-            const int nl = min(s, count / (i + 1));
-            if (lane >= c && lane < c + nl) {
-                ci = i;
-                cl = lane - c;
+    // blocks e0 + 8 and e0 + 16 are in flight while block e0 is inserted
+    const int last = ((n - 1) / 8) * 8;  // start of the row's last block
+    float x0[8], x1[8], x2[8];
+    load_block<T, VEC>(z, 0, n, x0);
+    load_block<T, VEC>(z, min(8, last), n, x1);
+    T *wout = weights + row * count;
+    int64_t *iout = indices + row * count;
+    float ex[SM];
+    int bank[SM];
+
+    if constexpr (sizeof(T) == 2) {
+        // (1) top-s of each factor, packed entries; a block of 8 scores is
+        // branch-free unless it straddles the factor boundary
+        uint32_t f0[SM], f1[SM];
+#pragma unroll
+        for (int p = 0; p < SM; ++p) f0[p] = f1[p] = 0u;
+        for (int e0 = 0; e0 < n; e0 += 8) {
+            load_block<T, VEC>(z, min(e0 + 16, last), n, x2);
+            if (e0 + 8 <= j1) {
+                uint32_t en[8];
+#pragma unroll
+                for (int q = 0; q < 8; ++q) en[q] = pack_entry(x0[q], e0 + q);
+#pragma unroll
+                for (int q = 0; q < 8; ++q) insert_entry<SM>(f0, en[q]);
+            } else if (e0 >= j1 && e0 + 8 <= n) {
+                uint32_t en[8];
+#pragma unroll
+                for (int q = 0; q < 8; ++q) en[q] = pack_entry(x0[q], e0 + q - j1);
+#pragma unroll
+                for (int q = 0; q < 8; ++q) insert_entry<SM>(f1, en[q]);
+            } else {
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const int e = e0 + q;
+                    if (e < j1)
+                        insert_entry<SM>(f0, pack_entry(x0[q], e));
+                    else if (e < n)
+                        insert_entry<SM>(f1, pack_entry(x0[q], e - j1));
+                }
             }
-            c += nl;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) x0[q] = x1[q], x1[q] = x2[q];
+        }
+        float v0[SM], v1[SM];
+        int i0[SM], i1[SM];
+#pragma unroll
+        for (int p = 0; p < SM; ++p) {
+            v0[p] = entry_value(f0[p]), v1[p] = entry_value(f1[p]);
+            i0[p] = entry_id(f0[p]), i1[p] = entry_id(f1[p]);
+        }
+        // (2) candidate pairs (i+1)(l+1) <= count, packed with id i*SM + l
+        // (increasing flattened index); pair sums formed in BF16
+        // (gdn2_banks.py:106)
+        uint32_t pl[SM];
+#pragma unroll
+        for (int p = 0; p < SM; ++p) pl[p] = 0u;
+        auto candidate = [&](int i, int l) { insert_entry<SM>(pl, pack_entry(round_to<T>(v0[i] + v1[l]), i * SM + l)); };
+        if (s == SM && count == SM) {  // every (i+1)(l+1) <= SM pair: straight-line
+#pragma unroll
+            for (int i = 0; i < SM; ++i)
+#pragma unroll
+                for (int l = 0; l < SM / (i + 1); ++l) candidate(i, l);
+        } else {
+#pragma unroll
+            for (int i = 0; i < SM; ++i)
+#pragma unroll
+                for (int l = 0; l < SM / (i + 1); ++l)
+                    if (i < s && l < s && (i + 1) * (l + 1) <= count) candidate(i, l);
+        }
+        // the selected pairs' bank ids through a per-lane table of the two lists' ids
+        __shared__ int s_ids[64][2 * SM];
+        const int lane = threadIdx.x;
+#pragma unroll
+        for (int p = 0; p < SM; ++p) s_ids[lane][p] = i0[p], s_ids[lane][SM + p] = i1[p];
+        const float top = entry_value(pl[0]);
+#pragma unroll
+        for (int p = 0; p < SM; ++p) {
+            ex[p] = expf(entry_value(pl[p]) - top);
+            const int c = entry_id(pl[p]) & (SM * SM - 1);  // empty slots (past count) stay in the table
+            bank[p] = s_ids[lane][c / SM] * j2 + s_ids[lane][SM + c % SM];
+        }
+    } else {
+        // (1) top-s of each factor: FP32 keys with the index alongside
+        uint32_t k0[SM], k1[SM];
+        int i0[SM], i1[SM];
+#pragma unroll
+        for (int p = 0; p < SM; ++p) k0[p] = k1[p] = 0u, i0[p] = i1[p] = 0;
+        for (int e0 = 0; e0 < n; e0 += 8) {
+            load_block<T, VEC>(z, min(e0 + 16, last), n, x2);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const int e = e0 + q;
+                if (e < j1)
+                    insert_key<SM>(k0, i0, score_key(x0[q]), e);
+                else if (e < n)
+                    insert_key<SM>(k1, i1, score_key(x0[q]), e - j1);
+            }
+#pragma unroll
+            for (int q = 0; q < 8; ++q) x0[q] = x1[q], x1[q] = x2[q];
+        }
+        float v0[SM], v1[SM];
+#pragma unroll
+        for (int p = 0; p < SM; ++p) v0[p] = key_value(k0[p]), v1[p] = key_value(k1[p]);
+        // (2) candidate pairs in increasing flattened index, carrying the bank
+        uint32_t kp[SM];
+#pragma unroll
+        for (int p = 0; p < SM; ++p) kp[p] = 0u, bank[p] = 0;
+#pragma unroll
+        for (int i = 0; i < SM; ++i) {
+#pragma unroll
+            for (int l = 0; l < SM / (i + 1); ++l) {  // (i+1)(l+1) <= SM
+                if (i < s && l < s && (i + 1) * (l + 1) <= count)
+                    insert_key<SM>(kp, bank, score_key(round_to<T>(v0[i] + v1[l])), i0[i] * j2 + i1[l]);
+            }
+        }
+        const float top = key_value(kp[0]);
+#pragma unroll
+        for (int p = 0; p < SM; ++p) ex[p] = expf(key_value(kp[p]) - top);
+    }
+
+    // (3) softmax over the selected sums in FP32, cast to the score dtype
+    // (:114); the exponentials are summed in selection order
+    float total = 0.f;
+#pragma unroll
+    for (int p = 0; p < SM; ++p)
+        if (p < count) total += ex[p];
+#pragma unroll
+    for (int p = 0; p < SM; ++p) {
+        if (p < count) {
+            wout[p] = from_f32<T>(ex[p] / total);
+            iout[p] = int64_t(bank[p]);
         }
     }
-    const bool cand = ci >= 0;
-    float pair = 0.f;
-    if (cand) {
-        pair = order_key(round_to<T>(s_sv[g][0][ci] + s_sv[g][1][cl]));
-        s_cand[g][lane] = pair;
-    }
-    int ncand = 0;
-    for (int i = 0; i < s; ++i) ncand += min(s, count / (i + 1));
-    __syncthreads();
-    if (cand) {
-        int rank = 0;
-#pragma unroll 8
-        for (int c = 0; c < ncand; ++c) rank += precedes(s_cand[g][c], c, pair, lane) ? 1 : 0;
-        if (rank < count) {
-            s_pv[g][rank] = pair;
-            s_pc[g][rank] = lane;
-        }
-    }
-    __syncthreads();
-    // (4) softmax over the selected sums in FP32, cast to the score dtype (:114);
-    // the exponentials are summed in selection order
-    const bool out = live && lane < count;
-    float mine = 0.f;
-    if (out) {
-        mine = expf(s_pv[g][lane] - s_pv[g][0]);
-        s_pe[g][lane] = mine;
-    }
-    __syncthreads();
-    if (out) {
-        float total = 0.f;
-        for (int p = 0; p < count; ++p) total += s_pe[g][p];
-        // candidate number -> (i, l): candidates are numbered row by row of i
-        const int c = s_pc[g][lane];
-        int i = 0, base = 0;
-        while (i + 1 < s && c >= base + min(s, count / (i + 1))) {
-            base += min(s, count / (i + 1));
-            ++i;
-        }
-        const int l = c - base;
-        weights[row * count + lane] = from_f32<T>(mine / total);
-        indices[row * count + lane] = int64_t(s_si[g][0][i]) * j2 + s_si[g][1][l];
-    }
+}
+
+template <typename T, int SM>
+void launch_router_sm(const T *scores, int64_t rows, int64_t stride, int j1, int j2, int selected, T *weights,
+                      int64_t *indices, hipStream_t stream) {
+    // one lane per row, 64-lane workgroups spread over the CUs
+    const dim3 grid(unsigned((rows + 63) / 64));
+    const int n = j1 + j2;
+    const bool vec = aligned(scores, 16) && (stride * int64_t(sizeof(T))) % 16 == 0 && n % 8 == 0;
+    if (vec)
+        router_lane_kernel<T, SM, true><<<grid, 64, 0, stream>>>(scores, rows, stride, j1, j2, selected, weights,
+                                                                 indices);
+    else
+        router_lane_kernel<T, SM, false><<<grid, 64, 0, stream>>>(scores, rows, stride, j1, j2, selected, weights,
+                                                                  indices);
 }
 
 template <typename T>
 int launch_router(const void *scores, int64_t rows, int64_t stride, int j1, int j2, int selected,
                   void *weights, int64_t *indices, hipStream_t stream) {
-    // one lane per score and per candidate pair: 32-lane groups (8 rows per
-    // workgroup) when both fit in 32, else 64-lane groups (4 rows)
-    const int s = min(selected, min(j1, j2)), count = min(selected, s * s);
-    int ncand = 0;
-    for (int i = 0; i < s; ++i) ncand += min(s, count / (i + 1));
-    if (j1 + j2 <= 32 && ncand <= 32) {
-        const dim3 grid(unsigned((rows + 7) / 8));
-        router_rank_kernel<T, 32><<<grid, kRouterBlock, 0, stream>>>(
-            static_cast<const T *>(scores), rows, stride, j1, j2, selected, static_cast<T *>(weights), indices);
-    } else {
-        const dim3 grid(unsigned((rows + 3) / 4));
-        router_rank_kernel<T, 64><<<grid, kRouterBlock, 0, stream>>>(
-            static_cast<const T *>(scores), rows, stride, j1, j2, selected, static_cast<T *>(weights), indices);
-    }
-    return check_launch("router_rank_kernel");
+    const T *z = static_cast<const T *>(scores);
+    if (selected <= 8)
+        launch_router_sm<T, 8>(z, rows, stride, j1, j2, selected, static_cast<T *>(weights), indices, stream);
+    else
+        launch_router_sm<T, 16>(z, rows, stride, j1, j2, selected, static_cast<T *>(weights), indices, stream);
+    return check_launch("router_lane_kernel");
 }
 
 }  // namespace
@@ -189,7 +296,7 @@ extern "C" int bdm_router_select(const void *scores, int32_t score_dtype, int64_
     if (rows == 0) return BDM_OK;
     if (!scores || !weights || !indices) return fail(BDM_ERR_INVALID, "router: null pointer");
     if (!aligned(scores, 16)) return fail(BDM_ERR_INVALID, "router: scores must be 16-byte aligned");
-    if (rows > int64_t(INT32_MAX) * 4) return fail(BDM_ERR_UNSUPPORTED, "router: too many rows");
+    if (rows > int64_t(INT32_MAX) * 32) return fail(BDM_ERR_UNSUPPORTED, "router: too many rows");
     switch (score_dtype) {
         case BDM_BF16:
             return launch_router<bf16_t>(scores, rows, row_stride, factor_first, factor_second, selected, weights,
