@@ -60,6 +60,9 @@ def parse_args():
     ap.add_argument('--cpu-tokens', type=int, default=512,
                     help='tokens of sequence 0 the CPU oracle runs (0 skips the CPU baseline)')
     ap.add_argument('--no-extras', action='store_true', help='skip the full-layer and decode measurements')
+    ap.add_argument('--only', choices=('c3', 'c4', 'c5'),
+                    help='run one named workload alone (C3 decode, C4 skewed forward, C5 training) and print '
+                         'its figures as one JSON line; used to profile a workload on its own')
     return ap.parse_args()
 
 
@@ -177,6 +180,7 @@ def decode_bench(layer, device, steps, seed=1):
         eager_sec, _ = timed(lambda: [launch(i) for i in range(steps)], 1, 0)
         # full step: controllers, routes, decode kernel and output interface
         sec, _ = timed(lambda: [layer.step(xs[i], state) for i in range(steps)], 1, 1)
+        full_graph_us, graph_check = full_step_graph(layer, xs, state, steps)
     bank_bytes = cfg.num_heads * cfg.bank_size * cfg.head_value_width * 2
     # BASELINE's figure: every step reads and writes KW banks and reads KR banks
     state_bytes = batch * (2 * cfg.selected_banks + cfg.selected_banks) * bank_bytes
@@ -193,9 +197,56 @@ def decode_bench(layer, device, steps, seed=1):
             'touched_state_bytes_per_step': round(touched),
             'touched_state_GBps': round(touched / (kernel_us * 1e-6) / 1e9, 1),
             'eager_launch_us_per_step': round(eager_sec * 1e6 / steps, 2),
-            'full_step_us_eager': round(sec * 1e6 / steps, 2), 'state_bytes_per_step': state_bytes,
+            'full_step_us_eager': round(sec * 1e6 / steps, 2), 'full_step_us_graph': full_graph_us,
+            'full_step_graph_check': graph_check, 'state_bytes_per_step': state_bytes,
             'state_GBps': round(state_bytes / (kernel_us * 1e-6) / 1e9, 1),
             'state_frac_of_hbm_peak': round(state_bytes / (kernel_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
+
+
+def full_step_graph(layer, xs, state, steps):
+    """The full decode step (controllers, both routes, decode kernel, output
+    projection) of every step captured in one HIP graph and replayed.  Before
+    it is timed, one replay from a copy of the state is checked against the
+    same steps run eagerly: the final states and the last outputs must be
+    identical.  Returns (us per step or None, check result)."""
+    import torch
+    device = state.device
+    try:
+        with torch.no_grad():
+            start_state = state.clone()
+            eager_state = start_state.clone()
+            for i in range(steps):
+                eager_out, _ = layer.step(xs[i], eager_state)
+            graph_state = start_state.clone()
+            side = torch.cuda.Stream(device)
+            side.wait_stream(torch.cuda.current_stream(device))
+            with torch.cuda.stream(side):  # warm the allocator and libraries on the capture stream
+                scratch = start_state.clone()
+                for i in range(3):
+                    layer.step(xs[i], scratch)
+            torch.cuda.current_stream(device).wait_stream(side)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.stream(side):
+                with torch.cuda.graph(graph, stream=side):
+                    outs = [layer.step(xs[i], graph_state)[0] for i in range(steps)]
+            torch.cuda.current_stream(device).wait_stream(side)
+            graph_state.copy_(start_state)
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            same = bool(torch.equal(graph_state, eager_state)) and bool(torch.equal(outs[-1], eager_out))
+            if not same:
+                return None, 'graph replay differs from the eager steps'
+            stream = torch.cuda.current_stream(device)
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            graph.replay()
+            b.record(stream)
+            torch.cuda.synchronize()
+            return round(a.elapsed_time(b) * 1e3 / steps, 2), 'replay equals eager'
+    except RuntimeError as exc:  # a step that cannot be captured is reported, not hidden
+        return None, f'capture failed: {str(exc)[:120]}'
 
 
 def c4_forward(device, steps=3):
@@ -336,6 +387,12 @@ def main():
     cfg = c2_config()
     batch, time_ = args.batch, args.time
     layer = BankedDeltaMemory(cfg, layer_id=0, seed=0).to(device=device, dtype=torch.bfloat16)
+    if args.only:
+        run = {'c3': lambda: decode_bench(layer, device, args.decode_steps), 'c4': lambda: c4_forward(device),
+               'c5': lambda: c5_training(device)}[args.only]
+        progress('workload', args.only)
+        print(json.dumps({'workload': args.only, 'result': run()}), flush=True)
+        return
     x, (q, k, v, g, b, w), (read_scores, write_scores), initial = make_inputs(layer, batch, time_, device)
     final = torch.empty(batch, cfg.bank_count, cfg.num_heads, cfg.bank_size, cfg.head_value_width,
                         device=device, dtype=torch.bfloat16)
