@@ -184,8 +184,10 @@ typedef struct bdm_backward_args {
     float scale;
 } bdm_backward_args;
 
-/* Scratch of bdm_backward: per-event du (FP32, NT*KW*H*v) and per-event
- * S-wide partial gradients; the workspace must be 256-byte aligned. */
+/* Scratch of bdm_backward: per-event du (FP32, NT*KW*H*v), per-event S-wide
+ * partials (U, X, P of each write and dq of each read, per 128-column tile)
+ * and, for S = 8 with replay interval 16, a 16-byte meta entry per event; the
+ * workspace must be 256-byte aligned. */
 size_t bdm_backward_workspace_size(const bdm_backward_args *args);
 int bdm_backward(const bdm_backward_args *args, void *workspace, size_t workspace_bytes, void *stream);
 
