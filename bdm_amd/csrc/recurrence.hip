@@ -875,7 +875,7 @@ __global__ __launch_bounds__(256) void read_slot_kernel(const int64_t *__restric
 // y[token, :] = fold over the token's reads in increasing bank id of
 // bf(total + z) (role_bank_dispatch.py:209-215): the token's KR rows of the
 // read buffer are already in that order.  One thread per (token, CPL columns).
-template <typename T, int CPL>
+template <typename T, int CPL, int KFIX>
 __global__ __launch_bounds__(256) void ordered_combine_kernel(const T *__restrict__ zbuf, T *__restrict__ y,
                                                               int64_t nt, int kr, int row_width) {
     const int chunks = row_width / CPL;
@@ -887,12 +887,31 @@ __global__ __launch_bounds__(256) void ordered_combine_kernel(const T *__restric
     float total[CPL];
 #pragma unroll
     for (int c = 0; c < CPL; ++c) total[c] = 0.f;
-#pragma unroll 8
-    for (int j = 0; j < kr; ++j) {
-        float v[CPL];
-        load_row<CPL>(z + int64_t(j) * row_width, v);
+    if constexpr (KFIX > 0 && sizeof(T) == 2 && CPL == 8) {
+        // exactly KFIX rows: 16-byte nontemporal loads (the rows are used
+        // once), all in flight before the fold
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        u32x4 raw[KFIX];
 #pragma unroll
-        for (int c = 0; c < CPL; ++c) total[c] = round_to<T>(total[c] + v[c]);
+        for (int j = 0; j < KFIX; ++j)
+            raw[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(z + int64_t(j) * row_width));
+#pragma unroll
+        for (int j = 0; j < KFIX; ++j) {
+            const uint32_t w[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                total[2 * q] = round_to<T>(total[2 * q] + __uint_as_float(w[q] << 16));
+                total[2 * q + 1] = round_to<T>(total[2 * q + 1] + __uint_as_float(w[q] & 0xffff0000u));
+            }
+        }
+    } else {
+#pragma unroll 8
+        for (int j = 0; j < kr; ++j) {
+            float v[CPL];
+            load_row<CPL>(z + int64_t(j) * row_width, v);
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) total[c] = round_to<T>(total[c] + v[c]);
+        }
     }
     store_row<CPL>(y + token * row_width + col0, total);
 }
@@ -1011,11 +1030,15 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, int *zslot, const PieceBu
         constexpr int CC = sizeof(T) == 2 ? 8 : 4;
         if (row_width % CC == 0) {
             const int64_t threads = nt * (row_width / CC);
-            ordered_combine_kernel<T, CC><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
-                zbuf, static_cast<T *>(a.output), nt, a.read_banks, row_width);
+            if (a.read_banks == 8)
+                ordered_combine_kernel<T, CC, 8><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
+                    zbuf, static_cast<T *>(a.output), nt, a.read_banks, row_width);
+            else
+                ordered_combine_kernel<T, CC, 0><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
+                    zbuf, static_cast<T *>(a.output), nt, a.read_banks, row_width);
         } else {
             const int64_t threads = nt * row_width;
-            ordered_combine_kernel<T, 1><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
+            ordered_combine_kernel<T, 1, 0><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
                 zbuf, static_cast<T *>(a.output), nt, a.read_banks, row_width);
         }
     } else {
