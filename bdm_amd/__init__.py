@@ -2,16 +2,19 @@
 
 Public surface mirrors the reference packages ``bdm`` and ``bsdm``:
 ``BDMConfig``/``BSDMConfig``, the ``BankedDeltaMemory`` module (alias
-``BlockSparseDeltaMemory``), the routed operator ``bank_training`` and the
-router ``product_key_route``.  Kernels live in ``libbdm_hip.so``.
+``BlockSparseDeltaMemory``), the routed operator ``bank_training``, the
+router ``product_key_route`` and ``GraphDecoder`` (a layer's decode step
+replayed from a HIP graph).  Kernels live in ``libbdm_hip.so``.
 """
 
 from .config import BDMConfig, BSDMConfig, near_square_factors, replay_interval
+from .graphs import GraphDecoder
 from .model import BankedDeltaMemory
 from .routed_update import bank_training, role_bank_training
 from .routing import SharedResidualRouter, product_key_route
 
 BlockSparseDeltaMemory = BankedDeltaMemory
 
-__all__ = ['BDMConfig', 'BSDMConfig', 'BankedDeltaMemory', 'BlockSparseDeltaMemory', 'SharedResidualRouter',
-           'bank_training', 'role_bank_training', 'product_key_route', 'near_square_factors', 'replay_interval']
+__all__ = ['BDMConfig', 'BSDMConfig', 'BankedDeltaMemory', 'BlockSparseDeltaMemory', 'GraphDecoder',
+           'SharedResidualRouter', 'bank_training', 'role_bank_training', 'product_key_route', 'near_square_factors',
+           'replay_interval']

@@ -60,9 +60,9 @@ def parse_args():
     ap.add_argument('--cpu-tokens', type=int, default=512,
                     help='tokens of sequence 0 the CPU oracle runs (0 skips the CPU baseline)')
     ap.add_argument('--no-extras', action='store_true', help='skip the full-layer and decode measurements')
-    ap.add_argument('--only', choices=('c3', 'c4', 'c5'),
-                    help='run one named workload alone (C3 decode, C4 skewed forward, C5 training) and print '
-                         'its figures as one JSON line; used to profile a workload on its own')
+    ap.add_argument('--only', choices=('c3', 'c4', 'c5', 'prefill'),
+                    help='run one named workload alone (C3 decode, C4 skewed forward, C5 training, C2 full-layer '
+                         'prefill) and print its figures as one JSON line; used to profile a workload on its own')
     return ap.parse_args()
 
 
@@ -203,48 +203,48 @@ def decode_bench(layer, device, steps, seed=1):
             'state_frac_of_hbm_peak': round(state_bytes / (kernel_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
 
 
+def full_layer_prefill(layer, device, batch, time_, steps):
+    """C2 geometry through the whole layer: controllers, route projections,
+    routers, dispatch, recurrence, combine and the output interface (LN x gate,
+    o_proj), from x ~ N(0, 1)."""
+    import torch
+    gen = torch.Generator().manual_seed(3)
+    x = torch.randn(batch, time_, layer.hidden_size, generator=gen).to(torch.bfloat16).to(device)
+    with torch.no_grad():
+        sec, _ = timed(lambda: layer.prefill(x), steps, 1)
+    return {'tokens_per_s': round(batch * time_ / sec, 1), 'ms_per_step': round(sec * 1e3, 3)}
+
+
 def full_step_graph(layer, xs, state, steps):
     """The full decode step (controllers, both routes, decode kernel, output
-    projection) of every step captured in one HIP graph and replayed.  Before
-    it is timed, one replay from a copy of the state is checked against the
-    same steps run eagerly: the final states and the last outputs must be
-    identical.  Returns (us per step or None, check result)."""
+    projection) replayed per token from a HIP graph (bdm_amd.GraphDecoder: one
+    input copy and one replay per token).  Before it is timed, the replays of
+    all steps from a copy of the state are checked against the same steps run
+    eagerly: every output and the final state must be identical.  Returns
+    (us per step or None, check result)."""
     import torch
+    from bdm_amd import GraphDecoder
     device = state.device
     try:
         with torch.no_grad():
-            start_state = state.clone()
-            eager_state = start_state.clone()
+            eager_state = state.clone()
+            graph_state = state.clone()
+            decoder = GraphDecoder(layer, graph_state)
             for i in range(steps):
-                eager_out, _ = layer.step(xs[i], eager_state)
-            graph_state = start_state.clone()
-            side = torch.cuda.Stream(device)
-            side.wait_stream(torch.cuda.current_stream(device))
-            with torch.cuda.stream(side):  # warm the allocator and libraries on the capture stream
-                scratch = start_state.clone()
-                for i in range(3):
-                    layer.step(xs[i], scratch)
-            torch.cuda.current_stream(device).wait_stream(side)
+                want, _ = layer.step(xs[i], eager_state)
+                if not torch.equal(decoder.step(xs[i]), want):
+                    return None, f'graph replay differs from the eager step {i}'
+            if not torch.equal(graph_state, eager_state):
+                return None, 'graph replays leave a different state'
             torch.cuda.synchronize()
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.stream(side):
-                with torch.cuda.graph(graph, stream=side):
-                    outs = [layer.step(xs[i], graph_state)[0] for i in range(steps)]
-            torch.cuda.current_stream(device).wait_stream(side)
-            graph_state.copy_(start_state)
-            torch.cuda.synchronize()
-            graph.replay()
-            torch.cuda.synchronize()
-            same = bool(torch.equal(graph_state, eager_state)) and bool(torch.equal(outs[-1], eager_out))
-            if not same:
-                return None, 'graph replay differs from the eager steps'
             stream = torch.cuda.current_stream(device)
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record(stream)
-            graph.replay()
+            for i in range(steps):
+                decoder.step(xs[i])
             b.record(stream)
             torch.cuda.synchronize()
-            return round(a.elapsed_time(b) * 1e3 / steps, 2), 'replay equals eager'
+            return round(a.elapsed_time(b) * 1e3 / steps, 2), 'replays equal the eager steps'
     except RuntimeError as exc:  # a step that cannot be captured is reported, not hidden
         return None, f'capture failed: {str(exc)[:120]}'
 
@@ -389,7 +389,8 @@ def main():
     layer = BankedDeltaMemory(cfg, layer_id=0, seed=0).to(device=device, dtype=torch.bfloat16)
     if args.only:
         run = {'c3': lambda: decode_bench(layer, device, args.decode_steps), 'c4': lambda: c4_forward(device),
-               'c5': lambda: c5_training(device)}[args.only]
+               'c5': lambda: c5_training(device),
+               'prefill': lambda: full_layer_prefill(layer, device, batch, time_, max(3, args.steps // 4))}[args.only]
         progress('workload', args.only)
         print(json.dumps({'workload': args.only, 'result': run()}), flush=True)
         return
@@ -454,9 +455,8 @@ def main():
     }
     if not args.no_extras:
         progress('full layer prefill')
-        with torch.no_grad():
-            layer_sec, _ = timed(lambda: layer.prefill(x), max(3, args.steps // 4), 1)
-        result['full_layer_prefill_tokens_per_s'] = round(tokens / layer_sec, 1)
+        result['full_layer_prefill_tokens_per_s'] = full_layer_prefill(layer, device, batch, time_,
+                                                                       max(3, args.steps // 4))['tokens_per_s']
         progress('decode C3')
         result['decode_c3'] = decode_bench(layer, device, args.decode_steps)
         progress('skewed forward C4')
