@@ -20,7 +20,7 @@ BDM_ROUTE_DUPLICATE = 2
 EXPORTED_SYMBOLS = (
     'bdm_version', 'bdm_last_error_string', 'bdm_router_select', 'bdm_dispatch_workspace_size',
     'bdm_dispatch_build', 'bdm_forward_workspace_size', 'bdm_forward', 'bdm_snapshot_rows',
-    'bdm_backward_workspace_size', 'bdm_backward', 'bdm_decode',
+    'bdm_backward_workspace_size', 'bdm_backward', 'bdm_decode', 'bdm_controller_epilogue', 'bdm_output_epilogue',
 )
 
 _i32, _i64, _f32, _vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
@@ -70,6 +70,27 @@ class DecodeArgs(ctypes.Structure):
     ]
 
 
+class ControllerArgs(ctypes.Structure):
+    """Mirror of ``bdm_controller_args``."""
+    _fields_ = [
+        ('proj', _vp), ('f', _vp), ('a_log', _vp), ('dt_bias', _vp),
+        ('q', _vp), ('k', _vp), ('v', _vp), ('b', _vp), ('w', _vp), ('g', _vp),
+        ('tokens', _i64), ('proj_stride', _i64), ('f_stride', _i64),
+        ('q_col', _i32), ('k_col', _i32), ('v_col', _i32), ('b_col', _i32), ('w_col', _i32),
+        ('heads', _i32), ('bank_size', _i32), ('head_width', _i32),
+        ('ctrl_dtype', _i32), ('param_dtype', _i32), ('qk_norm', _i32),
+    ]
+
+
+class OutputArgs(ctypes.Structure):
+    """Mirror of ``bdm_output_args``."""
+    _fields_ = [
+        ('raw', _vp), ('gate', _vp), ('norm_weight', _vp), ('norm_bias', _vp), ('out', _vp),
+        ('tokens', _i64), ('gate_stride', _i64),
+        ('width', _i32), ('ctrl_dtype', _i32), ('param_dtype', _i32), ('norm_kind', _i32), ('eps', _f32),
+    ]
+
+
 class BDMError(RuntimeError):
     """A call into libbdm_hip returned a non-zero status."""
 
@@ -101,6 +122,10 @@ def library() -> ctypes.CDLL:
     lib.bdm_backward.restype = _i32
     lib.bdm_decode.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
     lib.bdm_decode.restype = _i32
+    lib.bdm_controller_epilogue.argtypes = [ctypes.POINTER(ControllerArgs), _vp]
+    lib.bdm_controller_epilogue.restype = _i32
+    lib.bdm_output_epilogue.argtypes = [ctypes.POINTER(OutputArgs), _vp]
+    lib.bdm_output_epilogue.restype = _i32
     return lib
 
 

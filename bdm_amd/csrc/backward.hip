@@ -562,7 +562,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void ch
             for (int i = 0; i < 2; ++i) {
                 const int r = rp + i;
                 const float s = eager ? 1.f : pre_x[i];                // before the event
-                const float s1 = eager ? max(d[i], 0x1p-40f) : pre[i];  // after a write
+                const float s1 = eager ? fmaxf(d[i], 0x1p-40f) : pre[i];  // after a write
                 const float sg_ = eager ? 1.f : suf_x[i];
                 const float inv_sg = __builtin_amdgcn_rcpf(sg_);
                 if (m.z) {

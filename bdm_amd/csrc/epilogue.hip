@@ -1,0 +1,366 @@
+// Controller and output epilogues of the inference path: the elementwise and
+// per-head work around the projection GEMMs, one pass each over the GEMM
+// outputs instead of a dozen elementwise kernels.
+//
+// Reference: heads.controllers (implementation/bdm/heads.py:11-22) with
+// _normalize_qk (_parameters.py:214-220), and _project_bank_output
+// (_parameters.py:222-232).  Every intermediate that torch materialises in
+// the controller dtype is rounded to it at the same point here (silu before
+// the l2 normalization, sigmoid of the gate before the product, ...); the
+// arithmetic between those points is FP32 as in torch's opmath.
+#include "bdm_common.h"
+
+namespace bdm {
+namespace {
+
+// silu and sigmoid with the hardware exp and reciprocal (v_exp_f32,
+// v_rcp_f32): a few FP32 ulps, below the BF16 rounding every result gets
+__device__ __forceinline__ float sigmoid_f(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
+__device__ __forceinline__ float silu_f(float x) { return x * sigmoid_f(x); }
+// F.softplus with beta 1 and threshold 20
+__device__ __forceinline__ float softplus_f(float x) { return x > 20.f ? x : log1pf(expf(x)); }
+
+__device__ __forceinline__ float param_at(const void *p, int dtype, int64_t i) {
+    return dtype == BDM_BF16 ? to_f32(static_cast<const bf16_t *>(p)[i]) : static_cast<const float *>(p)[i];
+}
+
+// Eight consecutive elements of T (FP32 or BF16 parameters given by dtype
+// for param8) widened to FP32: 16-byte vector loads when VEC (the caller
+// checked 16-byte alignment of every such group), element loads otherwise.
+template <typename T, bool VEC>
+__device__ __forceinline__ void load8(const T *p, float (&x)[8]) {
+    if constexpr (VEC && sizeof(T) == 2) {
+        const uint4 r = *reinterpret_cast<const uint4 *>(p);
+        const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            x[2 * q] = __uint_as_float(w[q] << 16);
+            x[2 * q + 1] = __uint_as_float(w[q] & 0xffff0000u);
+        }
+    } else if constexpr (VEC) {
+        const float4 a = *reinterpret_cast<const float4 *>(p), b = *reinterpret_cast<const float4 *>(p + 4);
+        x[0] = a.x, x[1] = a.y, x[2] = a.z, x[3] = a.w, x[4] = b.x, x[5] = b.y, x[6] = b.z, x[7] = b.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = to_f32(p[j]);
+    }
+}
+
+template <bool VEC>
+__device__ __forceinline__ void param8(const void *p, int dtype, int64_t at, float (&x)[8]) {
+    if (dtype == BDM_BF16)
+        load8<bf16_t, VEC>(static_cast<const bf16_t *>(p) + at, x);
+    else
+        load8<float, VEC>(static_cast<const float *>(p) + at, x);
+}
+
+template <typename T>
+struct ControllerParams {
+    const T *proj, *f;
+    const void *a_log, *dt_bias;
+    T *q, *k, *v, *b, *w;
+    float *g;
+    int64_t tokens, proj_stride, f_stride;
+    int q_col, k_col, v_col, b_col, w_col;
+    int heads, hv, param_dtype, qk_norm;
+};
+
+// One thread per (token, item): items 0..4H-1 are the q, k, b, g rows of one
+// head (S values, 8 at a time), the rest 8-column chunks of v then w.  VEC:
+// every 8-element group of the inputs and outputs is 16-byte aligned.
+template <typename T, int S, bool VEC>
+__global__ __launch_bounds__(64) void controller_epilogue_kernel(ControllerParams<T> p) {
+    static_assert(S % 8 == 0, "S");
+    const int chunks = p.heads * p.hv / 8;
+    const int items = 4 * p.heads + 2 * chunks;
+    const int64_t token = blockIdx.x;  // grid: (tokens, item blocks of 64)
+    const int it = int(blockIdx.y) * 64 + int(threadIdx.x);
+    if (it >= items) return;
+    const T *row = p.proj + token * p.proj_stride;
+    const int64_t hs = int64_t(p.heads) * S;
+    if (it < 2 * p.heads) {
+        // q or k: silu, rounded, then the l2 normalization over the head's S values
+        const int h = it % p.heads;
+        const T *src = row + (it < p.heads ? p.q_col : p.k_col) + h * S;
+        float x[S], ss = 0.f;
+#pragma unroll
+        for (int r0 = 0; r0 < S; r0 += 8) {
+            float t[8];
+            load8<T, VEC>(src + r0, t);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                x[r0 + j] = round_to<T>(silu_f(t[j]));
+                ss = fmaf(x[r0 + j], x[r0 + j], ss);
+            }
+        }
+        T *dst = (it < p.heads ? p.q : p.k) + token * hs + h * S;
+        const float inv = p.qk_norm == 1 ? rsqrtf(ss + 1e-6f) : 0.f;
+        const float norm = fmaxf(sqrtf(ss), 1e-12f);
+#pragma unroll
+        for (int r0 = 0; r0 < S; r0 += 8) {
+            float y[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) y[j] = p.qk_norm == 1 ? x[r0 + j] * inv : x[r0 + j] / norm;
+            if constexpr (VEC)
+                store_row<8>(dst + r0, y);
+            else
+#pragma unroll
+                for (int j = 0; j < 8; ++j) dst[r0 + j] = from_f32<T>(y[j]);
+        }
+    } else if (it < 3 * p.heads) {
+        const int h = it - 2 * p.heads;
+        const T *src = row + p.b_col + h * S;
+        T *dst = p.b + token * hs + h * S;
+#pragma unroll
+        for (int r0 = 0; r0 < S; r0 += 8) {
+            float t[8];
+            load8<T, VEC>(src + r0, t);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) t[j] = sigmoid_f(t[j]);
+            if constexpr (VEC)
+                store_row<8>(dst + r0, t);
+            else
+#pragma unroll
+                for (int j = 0; j < 8; ++j) dst[r0 + j] = from_f32<T>(t[j]);
+        }
+    } else if (it < 4 * p.heads) {
+        // g = -exp(A_log[h]) * softplus(f + dt_bias), FP32
+        const int h = it - 3 * p.heads;
+        const T *src = p.f + token * p.f_stride + h * S;
+        const float a = -expf(param_at(p.a_log, p.param_dtype, h));
+        float *dst = p.g + token * hs + h * S;
+#pragma unroll
+        for (int r0 = 0; r0 < S; r0 += 8) {
+            float t[8], bias[8];
+            load8<T, VEC>(src + r0, t);
+            param8<VEC>(p.dt_bias, p.param_dtype, int64_t(h) * S + r0, bias);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) t[j] = a * softplus_f(t[j] + bias[j]);
+            if constexpr (VEC)
+                store_row<8>(dst + r0, t);
+            else
+#pragma unroll
+                for (int j = 0; j < 8; ++j) dst[r0 + j] = t[j];
+        }
+    } else {
+        const int c = it - 4 * p.heads;
+        const bool is_v = c < chunks;
+        const int col = (is_v ? c : c - chunks) * 8;
+        const T *src = row + (is_v ? p.v_col : p.w_col) + col;
+        T *dst = (is_v ? p.v : p.w) + token * int64_t(p.heads) * p.hv + col;
+        float x[8];
+        load8<T, VEC>(src, x);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = is_v ? silu_f(x[j]) : sigmoid_f(x[j]);
+        store_row<8>(dst, x);
+    }
+}
+
+template <typename T>
+struct OutputParams {
+    const T *raw, *gate;
+    const void *weight, *bias;
+    T *out;
+    int64_t tokens, gate_stride;
+    int width, param_dtype, norm_kind;
+    float eps;
+};
+
+template <int N>
+__device__ __forceinline__ float wave_total(float x) {
+#pragma unroll
+    for (int m = N / 2; m >= 1; m >>= 1) x += __shfl_xor(x, m, N);
+    return x;
+}
+
+// One wave per token; a lane owns 8-column chunks lane*8, lane*8 + 512, ...
+// VEC: raw, gate and the parameters are read as 16-byte groups.
+template <typename T, int MAXC, bool VEC>
+__global__ __launch_bounds__(256) void output_epilogue_kernel(OutputParams<T> p) {
+    const int lane = threadIdx.x % kWave;
+    const int64_t token = int64_t(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
+    if (token >= p.tokens) return;
+    const T *raw = p.raw + token * p.width;
+    const T *gate = p.gate + token * p.gate_stride;
+    float x[MAXC][8], gs[MAXC][8];
+    float sum = 0.f, sq = 0.f;
+#pragma unroll
+    for (int i = 0; i < MAXC; ++i) {
+        const int c = min((lane + i * kWave) * 8, p.width - 8);  // chunks past the width re-read the last
+        load8<T, VEC>(raw + c, x[i]);
+        load8<T, VEC>(gate + c, gs[i]);
+        const bool live = (lane + i * kWave) * 8 < p.width;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            x[i][j] = live ? x[i][j] : 0.f;
+            sum += x[i][j];
+            sq = fmaf(x[i][j], x[i][j], sq);
+        }
+    }
+    const float inv_n = 1.f / float(p.width);
+    float mean = 0.f, scale = 0.f;
+    if (p.norm_kind == 1) {
+        // layer norm: mean, then the centred second moment
+        mean = wave_total<kWave>(sum) * inv_n;
+        float var = 0.f;
+#pragma unroll
+        for (int i = 0; i < MAXC; ++i) {
+            const bool live = (lane + i * kWave) * 8 < p.width;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float d = x[i][j] - mean;
+                var = live ? fmaf(d, d, var) : var;
+            }
+        }
+        scale = rsqrtf(wave_total<kWave>(var) * inv_n + p.eps);
+    } else {
+        scale = round_to<T>(rsqrtf(wave_total<kWave>(sq) * inv_n + p.eps));
+    }
+    T *out = p.out + token * p.width;
+#pragma unroll
+    for (int i = 0; i < MAXC; ++i) {
+        const int c = (lane + i * kWave) * 8;
+        if (c >= p.width) continue;
+        float wt[8], bs[8], y[8];
+        param8<VEC>(p.weight, p.param_dtype, c, wt);
+        if (p.norm_kind == 1) param8<VEC>(p.bias, p.param_dtype, c, bs);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            float n;
+            if (p.norm_kind == 1) {
+                n = round_to<T>((x[i][j] - mean) * scale * wt[j] + bs[j]);
+            } else {
+                n = round_to<T>(x[i][j] * scale);
+                n = round_to<T>(n * round_to<T>(wt[j]));
+            }
+            y[j] = n * round_to<T>(sigmoid_f(gs[i][j]));
+        }
+        store_row<8>(out + c, y);
+    }
+}
+
+template <typename T>
+int launch_controller(const bdm_controller_args &a, hipStream_t stream) {
+    ControllerParams<T> p{};
+    p.proj = static_cast<const T *>(a.proj);
+    p.f = static_cast<const T *>(a.f);
+    p.a_log = a.a_log;
+    p.dt_bias = a.dt_bias;
+    p.q = static_cast<T *>(a.q);
+    p.k = static_cast<T *>(a.k);
+    p.v = static_cast<T *>(a.v);
+    p.b = static_cast<T *>(a.b);
+    p.w = static_cast<T *>(a.w);
+    p.g = a.g;
+    p.tokens = a.tokens;
+    p.proj_stride = a.proj_stride;
+    p.f_stride = a.f_stride;
+    p.q_col = a.q_col;
+    p.k_col = a.k_col;
+    p.v_col = a.v_col;
+    p.b_col = a.b_col;
+    p.w_col = a.w_col;
+    p.heads = a.heads;
+    p.hv = a.head_width;
+    p.param_dtype = a.param_dtype;
+    p.qk_norm = a.qk_norm;
+    const int64_t items = 4 * int64_t(a.heads) + 2 * (int64_t(a.heads) * a.head_width / 8);
+    const dim3 blocks(unsigned(a.tokens), unsigned((items + 63) / 64));
+    // 16-byte groups everywhere: aligned bases, strides and column offsets in multiples of 8 elements
+    const bool vec = aligned(a.proj, 16) && aligned(a.f, 16) && aligned(a.q, 16) && aligned(a.k, 16) &&
+                     aligned(a.b, 16) && aligned(a.g, 16) && aligned(a.dt_bias, 16) && a.proj_stride % 8 == 0 &&
+                     a.f_stride % 8 == 0 && a.q_col % 8 == 0 && a.k_col % 8 == 0 && a.v_col % 8 == 0 &&
+                     a.b_col % 8 == 0 && a.w_col % 8 == 0;
+#define BDM_CTRL(S) (vec ? (controller_epilogue_kernel<T, S, true><<<blocks, 64, 0, stream>>>(p), 0) \
+                         : (controller_epilogue_kernel<T, S, false><<<blocks, 64, 0, stream>>>(p), 0))
+    switch (a.bank_size) {
+        case 8: BDM_CTRL(8); break;
+        case 16: BDM_CTRL(16); break;
+        case 32: BDM_CTRL(32); break;
+        default: return fail(BDM_ERR_UNSUPPORTED, "controller epilogue: bank_size %d", a.bank_size);
+    }
+#undef BDM_CTRL
+    return check_launch("controller_epilogue_kernel");
+}
+
+template <typename T>
+int launch_output(const bdm_output_args &a, hipStream_t stream) {
+    OutputParams<T> p{};
+    p.raw = static_cast<const T *>(a.raw);
+    p.gate = static_cast<const T *>(a.gate);
+    p.weight = a.norm_weight;
+    p.bias = a.norm_bias;
+    p.out = static_cast<T *>(a.out);
+    p.tokens = a.tokens;
+    p.gate_stride = a.gate_stride;
+    p.width = a.width;
+    p.param_dtype = a.param_dtype;
+    p.norm_kind = a.norm_kind;
+    p.eps = a.eps;
+    const unsigned blocks = unsigned((a.tokens + 3) / 4);
+    const int chunks = (a.width / 8 + kWave - 1) / kWave;  // 8-column chunks per lane
+    const bool vec = aligned(a.raw, 16) && aligned(a.gate, 16) && aligned(a.norm_weight, 16) &&
+                     (!a.norm_bias || aligned(a.norm_bias, 16)) && a.gate_stride % 8 == 0;
+#define BDM_OUT(C) (vec ? (output_epilogue_kernel<T, C, true><<<blocks, 256, 0, stream>>>(p), 0) \
+                        : (output_epilogue_kernel<T, C, false><<<blocks, 256, 0, stream>>>(p), 0))
+    if (chunks <= 1)
+        BDM_OUT(1);
+    else if (chunks <= 2)
+        BDM_OUT(2);
+    else if (chunks <= 4)
+        BDM_OUT(4);
+    else if (chunks <= 8)
+        BDM_OUT(8);
+    else
+        return fail(BDM_ERR_UNSUPPORTED, "output epilogue: width %d > 4096", a.width);
+#undef BDM_OUT
+    return check_launch("output_epilogue_kernel");
+}
+
+}  // namespace
+}  // namespace bdm
+
+extern "C" int bdm_controller_epilogue(const bdm_controller_args *a, void *stream) {
+    using namespace bdm;
+    if (!a) return fail(BDM_ERR_INVALID, "controller epilogue: null args");
+    if (a->tokens < 0 || a->heads <= 0 || a->bank_size <= 0 || a->head_width <= 0)
+        return fail(BDM_ERR_INVALID, "controller epilogue: bad geometry");
+    if ((int64_t(a->heads) * a->head_width) % 8 != 0)
+        return fail(BDM_ERR_UNSUPPORTED, "controller epilogue: value width not a multiple of 8");
+    if (a->tokens > int64_t(INT32_MAX) || 4 * int64_t(a->heads) + 2 * int64_t(a->heads) * a->head_width / 8 > 64 * 65535)
+        return fail(BDM_ERR_UNSUPPORTED, "controller epilogue: grid too large");
+    if (a->ctrl_dtype != BDM_BF16 && a->ctrl_dtype != BDM_F32) return fail(BDM_ERR_INVALID, "controller: dtype");
+    if (a->param_dtype != BDM_BF16 && a->param_dtype != BDM_F32) return fail(BDM_ERR_INVALID, "controller: params");
+    const int64_t hs = int64_t(a->heads) * a->bank_size, vw = int64_t(a->heads) * a->head_width;
+    const int64_t cols[5] = {a->q_col, a->k_col, a->b_col, a->v_col, a->w_col};
+    const int64_t widths[5] = {hs, hs, hs, vw, vw};
+    for (int i = 0; i < 5; ++i)
+        if (cols[i] < 0 || cols[i] + widths[i] > a->proj_stride)
+            return fail(BDM_ERR_INVALID, "controller epilogue: slice %d outside the projection row", i);
+    if (a->f_stride < hs) return fail(BDM_ERR_INVALID, "controller epilogue: f row shorter than H*S");
+    if (a->tokens == 0) return BDM_OK;
+    if (!a->proj || !a->f || !a->a_log || !a->dt_bias || !a->q || !a->k || !a->v || !a->b || !a->w || !a->g)
+        return fail(BDM_ERR_INVALID, "controller epilogue: null pointer");
+    if (!aligned(a->v, 16) || !aligned(a->w, 16))
+        return fail(BDM_ERR_INVALID, "controller epilogue: v and w must be 16-byte aligned");
+    hipStream_t s = as_stream(stream);
+    if (a->ctrl_dtype == BDM_BF16) return launch_controller<bf16_t>(*a, s);
+    return launch_controller<float>(*a, s);
+}
+
+extern "C" int bdm_output_epilogue(const bdm_output_args *a, void *stream) {
+    using namespace bdm;
+    if (!a) return fail(BDM_ERR_INVALID, "output epilogue: null args");
+    if (a->tokens < 0 || a->width <= 0 || a->width % 8 != 0 || a->gate_stride < a->width)
+        return fail(BDM_ERR_INVALID, "output epilogue: bad geometry");
+    if (a->norm_kind != 0 && a->norm_kind != 1) return fail(BDM_ERR_INVALID, "output epilogue: norm kind");
+    if (a->ctrl_dtype != BDM_BF16 && a->ctrl_dtype != BDM_F32) return fail(BDM_ERR_INVALID, "output: dtype");
+    if (a->param_dtype != BDM_BF16 && a->param_dtype != BDM_F32) return fail(BDM_ERR_INVALID, "output: params");
+    if (a->tokens == 0) return BDM_OK;
+    if (!a->raw || !a->gate || !a->norm_weight || !a->out || (a->norm_kind == 1 && !a->norm_bias))
+        return fail(BDM_ERR_INVALID, "output epilogue: null pointer");
+    if (!aligned(a->out, 16)) return fail(BDM_ERR_INVALID, "output epilogue: out must be 16-byte aligned");
+    hipStream_t s = as_stream(stream);
+    if (a->ctrl_dtype == BDM_BF16) return launch_output<bf16_t>(*a, s);
+    return launch_output<float>(*a, s);
+}

@@ -76,6 +76,7 @@ class BankedDeltaMemory(nn.Module):
         if config.output_normalization == 'layer':
             self.output_norm_bias = nn.Parameter(torch.zeros(config.value_width))
         self.o_proj = nn.Linear(config.value_width, config.dim, bias=config.output_bias)
+        self._fused_cache = None  # concatenated inference projection, keyed by the parameters' storage
         self.init_weights(initialization_seed=self.initialization_seed)
 
     # -- geometry helpers (_parameters.py:11-38) ------------------------------------
@@ -187,6 +188,82 @@ class BankedDeltaMemory(nn.Module):
         w = self.w_proj(hidden).sigmoid().reshape(*shape, self.head_value_width)
         return q, k, v, g, b, w
 
+    # -- fused inference path -----------------------------------------------------------
+    def _fused_weights(self):
+        """One weight and bias for every linear map of ``hidden`` the layer makes
+        (q, k, v, the first f_proj factor, b, w, both route roles, the output
+        gate), concatenated along the outputs and cached while the parameters
+        keep their storage and version.  Returns (weight, bias, column offsets)."""
+        router = self.shared_router
+        parts = [self.q_proj.weight, self.k_proj.weight, self.v_proj.weight, self.f_proj[0].weight,
+                 self.b_proj.weight, self.w_proj.weight]
+        tracked = parts + [router.base.weight, router.base.bias, router.read_residual.weight,
+                           router.read_residual.bias, router.write_residual.weight, router.write_residual.bias,
+                           self.output_gate.weight, self.output_gate.bias]
+        key = tuple((t.data_ptr(), t._version, t.dtype) for t in tracked)
+        if self._fused_cache is None or self._fused_cache[0] != key:
+            with torch.no_grad():
+                read_w = router.base.weight + router.read_residual.weight
+                write_w = router.base.weight + router.write_residual.weight
+                weight = torch.cat(parts + [read_w, write_w, self.output_gate.weight], 0).contiguous()
+                plain = sum(t.shape[0] for t in parts)
+                bias = torch.cat([torch.zeros(plain, device=weight.device, dtype=weight.dtype),
+                                  router.base.bias + router.read_residual.bias,
+                                  router.base.bias + router.write_residual.bias, self.output_gate.bias])
+            names = ('q', 'k', 'v', 'f', 'b', 'w', 'read', 'write', 'gate')
+            widths = [t.shape[0] for t in parts] + [read_w.shape[0], write_w.shape[0], self.output_gate.weight.shape[0]]
+            columns, at = {}, 0
+            for name, width in zip(names, widths):
+                columns[name] = at
+                at += width
+            self._fused_cache = (key, weight, bias, columns)
+        return self._fused_cache[1:]
+
+    def _fused_supported(self, hidden: Tensor) -> bool:
+        return (hidden.dtype in (torch.bfloat16, torch.float32) and self.A_log.dtype == self.dt_bias.dtype
+                and self.bank_size in (8, 16, 32) and self.value_width % 8 == 0 and self.value_width <= 4096
+                and self.output_norm_weight.dtype in (torch.bfloat16, torch.float32))
+
+    def _fused_controllers(self, hidden: Tensor):
+        """Inference controllers, route scores and the output-gate projection from
+        one projection GEMM and the controller epilogue (heads.py:11-22)."""
+        weight, bias, cols = self._fused_weights()
+        lead = hidden.shape[:-1]
+        proj = F.linear(hidden.reshape(-1, self.hidden_size), weight, bias)
+        hv, rw = self.head_value_width, self.factor_route_width
+        f = F.linear(proj[:, cols['f']:cols['f'] + hv], self.f_proj[1].weight)
+        q, k, v, g, b, w = ops.controller_epilogue(proj, f, cols, self.A_log, self.dt_bias, heads=self.num_heads,
+                                                   bank_size=self.bank_size, head_width=hv,
+                                                   qk_norm=self.config.qk_normalization)
+        heads = (*lead, self.num_heads)
+        controllers = (q.view(*heads, self.bank_size), k.view(*heads, self.bank_size), v.view(*heads, hv),
+                       g.view(*heads, self.bank_size), b.view(*heads, self.bank_size), w.view(*heads, hv))
+        read_scores = proj[:, cols['read']:cols['read'] + rw].view(*lead, rw)
+        write_scores = proj[:, cols['write']:cols['write'] + rw].view(*lead, rw)
+        gate = proj[:, cols['gate']:cols['gate'] + self.value_width]
+        return controllers, (read_scores, write_scores), gate
+
+    def _inference_inputs(self, hidden: Tensor):
+        """The controllers and route scores prefill and step use: the fused
+        projection and epilogue where the geometry allows, the torch ops
+        otherwise.  Returns ((q, k, v, g, b, w), (read scores, write scores),
+        the output-gate projection or None)."""
+        if self._fused_supported(hidden):
+            return self._fused_controllers(hidden)
+        return self._controllers(hidden), self._route_projections(hidden), None
+
+    def _inference_output(self, hidden: Tensor, gate, raw: Tensor) -> Tensor:
+        return self._fused_output(gate, raw) if gate is not None else self._project_bank_output(hidden, raw)
+
+    def _fused_output(self, gate: Tensor, raw: Tensor) -> Tensor:
+        """_project_bank_output (_parameters.py:222-232) with the normalization
+        and gate in one epilogue kernel, then o_proj."""
+        layer = self.config.output_normalization == 'layer'
+        normalized = ops.output_epilogue(raw.reshape(-1, self.value_width), gate, self.output_norm_weight,
+                                         self.output_norm_bias if layer else None, eps=self.norm_eps,
+                                         kind='layer' if layer else 'rms')
+        return self.o_proj(normalized).view(*raw.shape[:-1], -1)
+
     def _project_bank_output(self, hidden: Tensor, raw: Tensor) -> Tensor:
         """LN (or RMS) x sigmoid gate -> o_proj (_parameters.py:222-232)."""
         if self.config.output_normalization == 'layer':
@@ -263,8 +340,7 @@ class BankedDeltaMemory(nn.Module):
             state = self.create_state(hidden.shape[0], dtype=work)
         elif state_dtype is not None and state_dtype != state.dtype:
             raise ValueError('state_dtype must match the supplied cache')
-        q, k, v, g, b, w = self._controllers(hidden)
-        read_routes, write_routes = self._route_projections(hidden)
+        (q, k, v, g, b, w), (read_routes, write_routes), gate = self._inference_inputs(hidden)
         ww, wi = self._route(write_routes, self.num_writes)
         rw, ri = self._route(read_routes, self.num_reads)
         meta = ops.dispatch_build(wi, ri, self.bank_count)
@@ -276,15 +352,14 @@ class BankedDeltaMemory(nn.Module):
                                  final_state=heads_view)
         if state.dtype != cache_dtype:
             state = state.to(cache_dtype)
-        return self._project_bank_output(hidden, raw), state
+        return self._inference_output(hidden, gate, raw), state
 
     def step(self, hidden: Tensor, state: Tensor):
         """Advance an existing bank state by one token (inference only)."""
         self._validate_stateful(hidden, state)
         if torch.is_grad_enabled() or hidden.shape[1] != 1:
             raise ValueError('step requires one token under no_grad/inference_mode')
-        q, k, v, g, b, w = self._controllers(hidden)
-        read_routes, write_routes = self._route_projections(hidden)
+        (q, k, v, g, b, w), (read_routes, write_routes), gate = self._inference_inputs(hidden)
         ww, wi = self._route(write_routes, self.num_writes)
         rw, ri = self._route(read_routes, self.num_reads)
         batch = hidden.shape[0]
@@ -292,4 +367,4 @@ class BankedDeltaMemory(nn.Module):
         raw = ops.decode_step(q[:, 0], k[:, 0], v[:, 0], g[:, 0], b[:, 0], w[:, 0], wi[:, 0], ww[:, 0],
                               ri[:, 0], rw[:, 0], heads_view, bank_count=self.bank_count,
                               scale=self.bank_size ** -0.5, routed_decay=self.config.routed_decay)
-        return self._project_bank_output(hidden, raw.unsqueeze(1)), state
+        return self._inference_output(hidden, gate, raw.unsqueeze(1)), state

@@ -73,16 +73,34 @@ def router_select(projected: Tensor, *, bank_count: int, selected_banks: int) ->
     if not 1 <= selected_banks <= bank_count:
         raise ValueError('selected bank count is outside the bank table')
     _require_gpu(projected)
-    scores = _aligned(projected)
+    row_stride = _row_stride(projected)
+    scores = projected if row_stride else _aligned(projected)
+    row_stride = row_stride or scores.shape[-1]
     s = min(selected_banks, j1, j2)
     count = min(selected_banks, s * s)
     rows = scores.numel() // scores.shape[-1]
     weights = torch.empty((*scores.shape[:-1], count), device=scores.device, dtype=scores.dtype)
     indices = torch.empty((*scores.shape[:-1], count), device=scores.device, dtype=torch.int64)
     _lib.check(_lib.library().bdm_router_select(
-        _ptr(scores), _dtype_code(scores.dtype), rows, scores.shape[-1], j1, j2, selected_banks,
+        _ptr(scores), _dtype_code(scores.dtype), rows, row_stride, j1, j2, selected_banks,
         _ptr(weights), _ptr(indices), _stream(scores.device)), 'bdm_router_select')
     return weights, indices
+
+
+def _row_stride(t: Tensor) -> int:
+    """Row stride of a view whose rows are contiguous and evenly spaced from a
+    16-byte aligned start (a column slice of a wider matrix), else 0."""
+    if t.ndim < 1 or t.numel() == 0 or t.stride(-1) != 1 or t.data_ptr() % 16:
+        return 0
+    if t.ndim == 1:
+        return t.shape[-1]
+    stride = t.stride(-2)
+    expect = stride
+    for d in range(t.ndim - 2, -1, -1):
+        if t.shape[d] != 1 and t.stride(d) != expect:
+            return 0
+        expect *= t.shape[d]
+    return stride if stride >= t.shape[-1] else 0
 
 
 # ---------------------------------------------------------------------------
@@ -356,3 +374,60 @@ def decode_step(q, k, v, g, b, w, wi, ww, ri, rw, state: Tensor, *, bank_count: 
     args.scale = float(scale)
     _lib.check(_lib.library().bdm_decode(ctypes.byref(args), _stream(device)), 'bdm_decode')
     return output
+
+
+# ---------------------------------------------------------------------------
+# inference epilogues (the controller activations and the output interface)
+
+def controller_epilogue(proj: Tensor, f: Tensor, columns: dict, a_log: Tensor, dt_bias: Tensor, *, heads: int,
+                        bank_size: int, head_width: int, qk_norm: str):
+    """Controllers of heads.controllers (heads.py:11-22) from one projection
+    matrix ``proj`` [N, P] (the q, k, v, b, w slices at ``columns``) and the
+    f_proj output ``f`` [N, H*S]: returns q, k, b [N, H, S], v, w [N, H, v]
+    in the projection dtype and g [N, H, S] FP32."""
+    _require_gpu(proj, f, a_log, dt_bias)
+    if proj.ndim != 2 or proj.stride(-1) != 1 or f.ndim != 2 or f.stride(-1) != 1:
+        raise ValueError('proj and f must be row-major matrices')
+    if a_log.dtype != dt_bias.dtype:
+        raise ValueError('A_log and dt_bias must share a dtype')
+    n = proj.shape[0]
+    dev, dt = proj.device, proj.dtype
+    q = torch.empty(n, heads, bank_size, device=dev, dtype=dt)
+    k, b = torch.empty_like(q), torch.empty_like(q)
+    g = torch.empty(n, heads, bank_size, device=dev, dtype=torch.float32)
+    v = torch.empty(n, heads, head_width, device=dev, dtype=dt)
+    w = torch.empty_like(v)
+    a_log, dt_bias = a_log.contiguous(), dt_bias.contiguous()  # kept alive until the launch is enqueued
+    args = _lib.ControllerArgs()
+    args.proj, args.f, args.a_log, args.dt_bias = (t.data_ptr() for t in (proj, f, a_log, dt_bias))
+    args.q, args.k, args.v, args.b, args.w, args.g = (t.data_ptr() for t in (q, k, v, b, w, g))
+    args.tokens, args.proj_stride, args.f_stride = n, proj.stride(0), f.stride(0)
+    args.q_col, args.k_col, args.v_col = columns['q'], columns['k'], columns['v']
+    args.b_col, args.w_col = columns['b'], columns['w']
+    args.heads, args.bank_size, args.head_width = heads, bank_size, head_width
+    args.ctrl_dtype, args.param_dtype = _dtype_code(dt), _dtype_code(a_log.dtype)
+    args.qk_norm = 1 if qk_norm == 'nvidia' else 0
+    _lib.check(_lib.library().bdm_controller_epilogue(ctypes.byref(args), _stream(dev)), 'bdm_controller_epilogue')
+    return q, k, v, g, b, w
+
+
+def output_epilogue(raw: Tensor, gate: Tensor, weight: Tensor, bias: Tensor | None, *, eps: float,
+                    kind: str) -> Tensor:
+    """norm(raw) * sigmoid(gate) of _project_bank_output (_parameters.py:222-232),
+    before o_proj: ``kind`` 'layer' (LayerNorm with weight, bias) or 'rms'."""
+    _require_gpu(raw, gate, weight, bias)
+    if raw.ndim != 2 or gate.ndim != 2 or gate.stride(-1) != 1 or gate.shape != raw.shape:
+        raise ValueError('raw and gate must be [tokens, width] with contiguous rows')
+    raw, weight = raw.contiguous(), weight.contiguous()
+    bias = None if bias is None else bias.contiguous()
+    out = torch.empty_like(raw)
+    args = _lib.OutputArgs()
+    args.raw, args.gate, args.out = raw.data_ptr(), gate.data_ptr(), out.data_ptr()
+    args.norm_weight = weight.data_ptr()
+    args.norm_bias = None if bias is None else bias.data_ptr()
+    args.tokens, args.gate_stride, args.width = raw.shape[0], gate.stride(0), raw.shape[1]
+    args.ctrl_dtype, args.param_dtype = _dtype_code(raw.dtype), _dtype_code(weight.dtype)
+    args.norm_kind = 1 if kind == 'layer' else 0
+    args.eps = float(eps)
+    _lib.check(_lib.library().bdm_output_epilogue(ctypes.byref(args), _stream(raw.device)), 'bdm_output_epilogue')
+    return out

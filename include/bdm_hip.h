@@ -219,6 +219,57 @@ typedef struct bdm_decode_args {
 
 int bdm_decode(const bdm_decode_args *args, void *stream);
 
+/*
+ * Controller epilogue of the inference path.  Replaces the activations of
+ * heads.controllers (implementation/bdm/heads.py:11-22) applied to the
+ * outputs of one concatenated projection GEMM:
+ *   q = l2norm(silu(P_q)), k = l2norm(silu(P_k)) per head of S values
+ *     (qk_norm 1: x * rsqrt(sum x^2 + 1e-6); 0: x / max(|x|_2, 1e-12),
+ *      _parameters.py:214-220), rounded to ctrl_dtype after silu and after
+ *     the normalization;
+ *   v = silu(P_v), b = sigmoid(P_b), w = sigmoid(P_w), rounded to ctrl_dtype;
+ *   g = -exp(A_log[h]) * softplus(f + dt_bias) in FP32, f the f_proj output.
+ * proj is [tokens, proj_stride] ctrl_dtype with the q, k, v, b, w slices at
+ * the given column offsets; f is [tokens, f_stride].  Outputs are contiguous
+ * [tokens, H, S] (q, k, b; g FP32) and [tokens, H, head_width] (v, w).
+ */
+typedef struct bdm_controller_args {
+    const void *proj;
+    const void *f;
+    const void *a_log;         /* [H], param_dtype */
+    const void *dt_bias;       /* [H*S], param_dtype */
+    void *q, *k, *v, *b, *w;
+    float *g;
+    int64_t tokens, proj_stride, f_stride;
+    int32_t q_col, k_col, v_col, b_col, w_col;
+    int32_t heads, bank_size, head_width;
+    int32_t ctrl_dtype, param_dtype, qk_norm;
+} bdm_controller_args;
+
+int bdm_controller_epilogue(const bdm_controller_args *args, void *stream);
+
+/*
+ * Output epilogue of the inference path: the normalization and gate of
+ * _project_bank_output (_parameters.py:222-232) before o_proj.
+ *   norm_kind 1 (layer): layer_norm(raw, weight, bias, eps) in FP32, rounded;
+ *   norm_kind 0 (rms):   raw * bf(rsqrt(mean(raw^2) + eps)), rounded, then
+ *                        times bf(weight), rounded;
+ * then times bf(sigmoid(gate)), rounded to ctrl_dtype.  raw is [tokens, width],
+ * gate [tokens, gate_stride] (the output_gate projection with its bias), out
+ * [tokens, width]; norm_bias may be null for rms.
+ */
+typedef struct bdm_output_args {
+    const void *raw;
+    const void *gate;
+    const void *norm_weight, *norm_bias;   /* [width], param_dtype */
+    void *out;
+    int64_t tokens, gate_stride;
+    int32_t width, ctrl_dtype, param_dtype, norm_kind;
+    float eps;
+} bdm_output_args;
+
+int bdm_output_epilogue(const bdm_output_args *args, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -132,7 +132,8 @@ def test_struct_layouts_match_the_header(tmp_path):
     if gcc is None:
         pytest.skip('no host C compiler')
     mirrors = {'bdm_forward_args': _lib.ForwardArgs, 'bdm_backward_args': _lib.BackwardArgs,
-               'bdm_decode_args': _lib.DecodeArgs}
+               'bdm_decode_args': _lib.DecodeArgs, 'bdm_controller_args': _lib.ControllerArgs,
+               'bdm_output_args': _lib.OutputArgs}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', 'int main(void) {']
     for struct, mirror in mirrors.items():
         lines.append(f'printf("{struct} size %zu\\n", sizeof({struct}));')
@@ -149,3 +150,26 @@ def test_struct_layouts_match_the_header(tmp_path):
         assert got[(struct, 'size')] == ctypes.sizeof(mirror), struct
         for field, _ in mirror._fields_:
             assert got[(struct, field)] == getattr(mirror, field).offset, (struct, field)
+
+
+def test_epilogues_reject_bad_arguments(lib):
+    from bdm_amd import _lib
+    assert lib.bdm_controller_epilogue(None, None) == -1
+    args = _lib.ControllerArgs()
+    args.tokens, args.heads, args.bank_size, args.head_width = 4, 2, 8, 64
+    args.proj_stride, args.f_stride = 100, 16
+    args.ctrl_dtype = args.param_dtype = _lib.BDM_BF16
+    args.q_col, args.k_col, args.b_col, args.v_col, args.w_col = 0, 16, 32, 48, 60  # w runs past the row
+    assert lib.bdm_controller_epilogue(ctypes.byref(args), None) == -1
+    assert b'outside the projection row' in lib.bdm_last_error_string()
+    args.proj_stride = 300
+    assert lib.bdm_controller_epilogue(ctypes.byref(args), None) == -1  # null operands
+    args.bank_size = 12
+    args.proj_stride = 400
+    assert lib.bdm_controller_epilogue(ctypes.byref(args), None) == -1  # null checked before the S template
+    out = _lib.OutputArgs()
+    out.tokens, out.width, out.gate_stride = 4, 100, 100  # width not a multiple of 8
+    out.ctrl_dtype = out.param_dtype = _lib.BDM_BF16
+    assert lib.bdm_output_epilogue(ctypes.byref(out), None) == -1
+    out.width, out.gate_stride, out.norm_kind = 128, 128, 2
+    assert lib.bdm_output_epilogue(ctypes.byref(out), None) == -1

@@ -324,8 +324,10 @@ def test_prefill_and_step_match_oracle(device):
         announce('prefill', cache_dtype)
         with torch.no_grad():
             out, state = layer.prefill(x.to(device), state_dtype=cache_dtype)
-            q, k, v, g, b, w = (t.cpu() for t in layer._controllers(x.to(device)))
-            rr, wr = (t.cpu() for t in layer._route_projections(x.to(device)))
+            # the controllers and scores prefill used (fused projection + epilogue)
+            ctrl, scores, _ = layer._inference_inputs(x.to(device))
+            q, k, v, g, b, w = (t.cpu() for t in ctrl)
+            rr, wr = (t.cpu() for t in scores)
             ww, wi = O.product_key_route(wr, bank_count=cfg.bank_count, selected_banks=cfg.selected_banks)
             rw, ri = O.product_key_route(rr, bank_count=cfg.bank_count, selected_banks=cfg.selected_banks)
             init = oracle.create_state(2, torch.float32)
@@ -337,8 +339,9 @@ def test_prefill_and_step_match_oracle(device):
             cpu_state = state.cpu().clone()
             out1, state = layer.step(nxt.to(device), state)
             # oracle step on the same controllers/routes as the GPU step
-            q1, k1, v1, g1, b1, w1 = (t.cpu() for t in layer._controllers(nxt.to(device)))
-            rr1, wr1 = (t.cpu() for t in layer._route_projections(nxt.to(device)))
+            ctrl1, scores1, _ = layer._inference_inputs(nxt.to(device))
+            q1, k1, v1, g1, b1, w1 = (t.cpu() for t in ctrl1)
+            rr1, wr1 = (t.cpu() for t in scores1)
             ww1, wi1 = O.product_key_route(wr1, bank_count=cfg.bank_count, selected_banks=cfg.selected_banks)
             rw1, ri1 = O.product_key_route(rr1, bank_count=cfg.bank_count, selected_banks=cfg.selected_banks)
             oracle_state = cpu_state
