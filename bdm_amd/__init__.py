@@ -3,18 +3,20 @@
 Public surface mirrors the reference packages ``bdm`` and ``bsdm``:
 ``BDMConfig``/``BSDMConfig``, the ``BankedDeltaMemory`` module (alias
 ``BlockSparseDeltaMemory``), the routed operator ``bank_training``, the
-router ``product_key_route`` and ``GraphDecoder`` (a layer's decode step
-replayed from a HIP graph).  Kernels live in ``libbdm_hip.so``.
+router ``product_key_route``, ``bank_occupancy`` (the bank-union
+regularizer) and ``GraphDecoder`` (a layer's decode step replayed from a HIP
+graph).  Kernels live in ``libbdm_hip.so``.
 """
 
 from .config import BDMConfig, BSDMConfig, near_square_factors, replay_interval
 from .graphs import GraphDecoder
 from .model import BankedDeltaMemory
+from .occupancy import bank_occupancy
 from .routed_update import bank_training, role_bank_training
 from .routing import SharedResidualRouter, product_key_route
 
 BlockSparseDeltaMemory = BankedDeltaMemory
 
 __all__ = ['BDMConfig', 'BSDMConfig', 'BankedDeltaMemory', 'BlockSparseDeltaMemory', 'GraphDecoder',
-           'SharedResidualRouter', 'bank_training', 'role_bank_training', 'product_key_route', 'near_square_factors',
-           'replay_interval']
+           'SharedResidualRouter', 'bank_occupancy', 'bank_training', 'role_bank_training', 'product_key_route',
+           'near_square_factors', 'replay_interval']

@@ -431,3 +431,26 @@ def output_epilogue(raw: Tensor, gate: Tensor, weight: Tensor, bias: Tensor | No
     args.eps = float(eps)
     _lib.check(_lib.library().bdm_output_epilogue(ctypes.byref(args), _stream(raw.device)), 'bdm_output_epilogue')
     return out
+
+
+# ---------------------------------------------------------------------------
+# bank occupancy
+
+def bank_occupancy_totals(weights: Tensor, indices: Tensor, bank_count: int, valid: Tensor | None = None):
+    """Per (sequence, bank): the sum of log1p(-clamp(p, 0, 1-1e-6)) over its
+    writes (FP32) and their number, over the segments of a write-only dispatch
+    (elastic_bank_regularizer.py:10-25).  weights [B, T, K], int64 indices
+    [B, T, K], valid [B, T] or None.  Returns (totals [B, J], counts [B, J])."""
+    if weights.ndim != 3 or indices.shape != weights.shape or indices.dtype != torch.long:
+        raise ValueError('weights and int64 indices must both be [batch, time, selected]')
+    device = _require_gpu(weights, indices, valid)
+    batch, time, k = weights.shape
+    meta = dispatch_build(indices, indices[..., :0], bank_count)
+    w = _aligned(weights)
+    mask = None if valid is None else valid.reshape(batch * time).to(torch.uint8).contiguous()
+    totals = torch.empty(batch, bank_count, device=device, dtype=torch.float32)
+    counts = torch.empty(batch, bank_count, device=device, dtype=torch.int32)
+    _lib.check(_lib.library().bdm_bank_occupancy(
+        _ptr(w), _dtype_code(w.dtype), _ptr(mask), _ptr(meta.order), _ptr(meta.cu_seqlens), batch, time, k,
+        bank_count, _ptr(totals), _ptr(counts), _stream(device)), 'bdm_bank_occupancy')
+    return totals, counts

@@ -270,6 +270,22 @@ typedef struct bdm_output_args {
 
 int bdm_output_epilogue(const bdm_output_args *args, void *stream);
 
+/*
+ * Bank occupancy of a write-route table: the Elastic-SDM final-union
+ * regularizer applied to banks (reproduction/experiments/
+ * elastic_bank_regularizer.py:10-25), reduced over the (sequence, bank)
+ * segments of a write-only dispatch (bdm_dispatch_build with read_banks = 0)
+ * instead of a scatter over [batch, J].  For segment s = b*J + bank:
+ *   totals[s] = sum over its writes of valid tokens of
+ *               log1p(-clamp(p, 0, 1 - 1e-6)) in FP32,
+ *   counts[s] = the number of those writes.
+ * valid ([batch*time] bytes, nonzero = valid) may be null.  The sum of a
+ * segment is a fixed wave reduction: deterministic.
+ */
+int bdm_bank_occupancy(const void *write_weights, int32_t weight_dtype, const uint8_t *valid,
+                       const int64_t *order, const int64_t *cu_seqlens, int64_t batch, int64_t time,
+                       int32_t write_banks, int32_t bank_count, float *totals, int32_t *counts, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

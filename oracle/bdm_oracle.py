@@ -393,6 +393,30 @@ def bank_forward(q, k, v, g, b, w, wi, ww, ri, rw, state, bank_count: int, scale
 # ---------------------------------------------------------------------------
 # initialisation (_parameters.py:69-177, routing.py:37-68)
 
+def bank_occupancy(weights: Tensor, indices: Tensor, banks: int, valid: Tensor | None = None):
+    """Elastic-SDM final-union occupancy over banks
+    (reproduction/experiments/elastic_bank_regularizer.py:10-25).
+
+    Per sequence: ``hard`` = fraction of banks written at least once (valid
+    tokens only); ``soft`` = mean over banks of the noisy OR
+    1 - prod(1 - p) = -expm1(sum log1p(-p)), p clamped to [0, 1 - 1e-6];
+    returns ``(hard - soft.detach() + soft, hard, soft)`` (straight-through).
+    The token axis is collapsed before the scatter, as the reference does."""
+    batch = weights.shape[0]
+    addresses = indices.reshape(batch, -1)
+    event_mask = torch.ones_like(indices, dtype=torch.int32)
+    if valid is not None:
+        event_mask = valid[..., None].expand_as(indices).to(torch.int32)
+    log_survival = torch.log1p(-weights.float().clamp(0, 1 - 1e-6)) * event_mask
+    totals = torch.zeros(batch, banks, dtype=torch.float32)
+    totals = totals.scatter_add(1, addresses, log_survival.reshape(batch, -1))
+    soft = -torch.expm1(totals).mean(-1)
+    counts = torch.zeros(batch, banks, dtype=torch.int32)
+    counts.scatter_add_(1, addresses, event_mask.reshape(batch, -1))
+    hard = (counts > 0).float().mean(-1)
+    return hard.detach() - soft.detach() + soft, hard, soft
+
+
 def role_generator(layer_id: int, role: str, seed: int) -> torch.Generator:
     """Seed ``(seed XOR blake2b_8('bank_sparse_gdn2.{layer}.{role}')) mod 2^63``
     (_parameters.py:69-84)."""

@@ -216,3 +216,54 @@ def test_serial_and_packed_oracles_agree_in_fp32(routed):
                                      scale=s ** -0.5, routed_decay=routed)
     assert torch.allclose(packed, serial, rtol=1e-5, atol=1e-6)
     assert math.isfinite(float(packed.abs().max()))
+
+
+# ------------------------------------------------------------------ bank occupancy
+
+def _occupancy_inputs(seed=3, batch=3, time=11, banks=20, k=4):
+    gen = torch.Generator().manual_seed(seed)
+    indices = torch.stack([torch.stack([torch.randperm(banks, generator=gen)[:k] for _ in range(time)])
+                           for _ in range(batch)])
+    weights = torch.rand(batch, time, k, generator=gen, dtype=torch.float64).float()
+    valid = torch.rand(batch, time, generator=gen) < 0.7
+    return weights, indices, banks, valid
+
+
+@pytest.mark.parametrize('masked', [False, True])
+def test_bank_occupancy_matches_sets_and_products(masked):
+    """hard: the written-bank union by brute force; soft: mean over banks of
+    1 - prod(1 - p) by the direct product in FP64 (the closed form of the
+    reference's expm1(sum log1p))."""
+    weights, indices, banks, valid = _occupancy_inputs()
+    value, hard, soft = O.bank_occupancy(weights, indices, banks, valid if masked else None)
+    for b in range(weights.shape[0]):
+        seen, survive = set(), [1.0] * banks
+        for t in range(weights.shape[1]):
+            if masked and not bool(valid[b, t]):
+                continue
+            for j in range(indices.shape[-1]):
+                bank = int(indices[b, t, j])
+                seen.add(bank)
+                survive[bank] *= 1.0 - min(max(float(weights[b, t, j]), 0.0), 1 - 1e-6)
+        assert float(hard[b]) == pytest.approx(len(seen) / banks, abs=1e-7)
+        assert float(soft[b]) == pytest.approx(sum(1 - s for s in survive) / banks, rel=1e-5)
+    assert torch.allclose(value, hard)  # straight-through: the value is the hard union
+
+
+def test_bank_occupancy_gradient_is_the_soft_union_gradient():
+    """d value / d p_e = prod(1 - p) over the other writes to that bank / J."""
+    weights, indices, banks, _ = _occupancy_inputs(seed=4)
+    w = weights.clone().requires_grad_(True)
+    value, _, _ = O.bank_occupancy(w, indices, banks)
+    value.sum().backward()
+    for b in range(weights.shape[0]):
+        for t in range(weights.shape[1]):
+            for j in range(indices.shape[-1]):
+                bank = int(indices[b, t, j])
+                others = 1.0
+                for t2 in range(weights.shape[1]):
+                    for j2 in range(indices.shape[-1]):
+                        if (t2, j2) != (t, j) and int(indices[b, t2, j2]) == bank:
+                            others *= 1.0 - float(weights[b, t2, j2])
+                # FP32 log-space sums: 1 - p loses digits for p near 1, hence 1e-2
+                assert float(w.grad[b, t, j]) == pytest.approx(others / banks, rel=1e-2)
