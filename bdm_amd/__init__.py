@@ -4,14 +4,15 @@ Public surface mirrors the reference packages ``bdm`` and ``bsdm``:
 ``BDMConfig``/``BSDMConfig``, the ``BankedDeltaMemory`` module (alias
 ``BlockSparseDeltaMemory``), the routed operator ``bank_training``, the
 router ``product_key_route``, ``bank_occupancy`` (the bank-union
-regularizer) and ``GraphDecoder`` (a layer's decode step replayed from a HIP
+regularizer), ``written_banks`` (the copy-on-write state count at nested
+prefixes) and ``GraphDecoder`` (a layer's decode step replayed from a HIP
 graph).  Kernels live in ``libbdm_hip.so``.
 """
 
 from .config import BDMConfig, BSDMConfig, near_square_factors, replay_interval
 from .graphs import GraphDecoder
 from .model import BankedDeltaMemory
-from .occupancy import bank_occupancy
+from .occupancy import bank_occupancy, written_banks
 from .routed_update import bank_training, role_bank_training
 from .routing import SharedResidualRouter, product_key_route
 
@@ -19,4 +20,4 @@ BlockSparseDeltaMemory = BankedDeltaMemory
 
 __all__ = ['BDMConfig', 'BSDMConfig', 'BankedDeltaMemory', 'BlockSparseDeltaMemory', 'GraphDecoder',
            'SharedResidualRouter', 'bank_occupancy', 'bank_training', 'role_bank_training', 'product_key_route',
-           'near_square_factors', 'replay_interval']
+           'near_square_factors', 'replay_interval', 'written_banks']

@@ -22,6 +22,7 @@ EXPORTED_SYMBOLS = (
     'bdm_dispatch_build', 'bdm_forward_workspace_size', 'bdm_forward', 'bdm_snapshot_rows',
     'bdm_backward_workspace_size', 'bdm_backward', 'bdm_decode', 'bdm_controller_epilogue', 'bdm_output_epilogue',
     'bdm_bank_occupancy',
+    'bdm_written_bank_curve',
 )
 
 _i32, _i64, _f32, _vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
@@ -127,8 +128,10 @@ def library() -> ctypes.CDLL:
     lib.bdm_controller_epilogue.restype = _i32
     lib.bdm_output_epilogue.argtypes = [ctypes.POINTER(OutputArgs), _vp]
     lib.bdm_output_epilogue.restype = _i32
-    lib.bdm_bank_occupancy.argtypes = [_vp, _i32, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp]
+    lib.bdm_bank_occupancy.argtypes = [_vp, _i32, _vp, _vp, _vp, _i64, _i64, _i32, _i32, _vp, _vp, _vp, _vp]
     lib.bdm_bank_occupancy.restype = _i32
+    lib.bdm_written_bank_curve.argtypes = [_vp, _i64, _i32, _vp, _i32, _vp, _vp]
+    lib.bdm_written_bank_curve.restype = _i32
     return lib
 
 

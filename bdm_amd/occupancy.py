@@ -51,3 +51,47 @@ def bank_occupancy(weights: Tensor, indices: Tensor, banks: int, valid: Tensor |
     soft = -torch.expm1(totals).mean(-1)
     hard = (counts > 0).float().mean(-1)
     return hard.detach() - soft.detach() + soft, hard, soft
+
+
+# ---------------------------------------------------------------------------
+# copy-on-write state accounting (APPENDIX.md:511-584; the byte arithmetic is
+# the one scripts/verify_results.py:190-235 checks)
+#
+# A bank holds private state from its first write on; an unwritten bank reads
+# the layer's shared initial state.  The state a request holds after n
+# positions is therefore its written banks times the bytes of one bank.
+
+def written_banks(indices: Tensor, banks: int, prefixes, valid: Tensor | None = None) -> Tensor:
+    """Written banks after each prefix: [B, len(prefixes)] int32, where entry
+    (b, i) counts the banks that sequence b writes within its first
+    ``prefixes[i]`` positions (valid tokens only).  indices [B, T, K] int64
+    write routes.  One pass over the write-only dispatch finds each bank's
+    first write; the curve counts first writes below each prefix end."""
+    _, _, first = ops.bank_occupancy_totals(None, indices, banks, valid, first_write=True)
+    return ops.written_bank_curve(first, prefixes)
+
+
+def state_value_bytes(written, bank_size: int, width: int, element_bytes: int = 2):
+    """Copy-on-write state bytes of ``written`` banks (a count, or the sum of
+    counts over layers): written * bank_size * width * element_bytes
+    (verify_results.py:207)."""
+    return written * bank_size * width * element_bytes
+
+
+def dense_state_bytes(layers: int, memory_rows: int, width: int, element_bytes: int = 2) -> int:
+    """Fully allocated state: L * N * D * b (verify_results.py:194)."""
+    return layers * memory_rows * width * element_bytes
+
+
+def cow_worst_case_bytes(memory_rows: int, accessed_rows: int, history: int, layers: int, width: int,
+                         element_bytes: int = 2) -> int:
+    """Copy-on-write ceiling after ``history`` positions: each position writes
+    at most ``accessed_rows`` = selected_banks * bank_size new rows, capped at
+    the N rows of a layer: min(N, K * n) * L * D * b (verify_results.py:220)."""
+    return min(memory_rows, accessed_rows * history) * layers * width * element_bytes
+
+
+def attention_kv_bytes(history: int, layers: int, width: int, element_bytes: int = 2) -> int:
+    """The attention KV cache compared against: 2 * n * L * D * b
+    (verify_results.py:218)."""
+    return 2 * history * layers * width * element_bytes

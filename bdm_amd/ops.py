@@ -436,21 +436,48 @@ def output_epilogue(raw: Tensor, gate: Tensor, weight: Tensor, bias: Tensor | No
 # ---------------------------------------------------------------------------
 # bank occupancy
 
-def bank_occupancy_totals(weights: Tensor, indices: Tensor, bank_count: int, valid: Tensor | None = None):
+def bank_occupancy_totals(weights: Tensor, indices: Tensor, bank_count: int, valid: Tensor | None = None,
+                          first_write: bool = False):
     """Per (sequence, bank): the sum of log1p(-clamp(p, 0, 1-1e-6)) over its
     writes (FP32) and their number, over the segments of a write-only dispatch
     (elastic_bank_regularizer.py:10-25).  weights [B, T, K], int64 indices
-    [B, T, K], valid [B, T] or None.  Returns (totals [B, J], counts [B, J])."""
-    if weights.ndim != 3 or indices.shape != weights.shape or indices.dtype != torch.long:
+    [B, T, K] or None (totals are then 0), valid [B, T] or None.  Returns
+    (totals [B, J], counts [B, J]), and with ``first_write`` also the first
+    written position of each bank ([B, J] int32, 2**31 - 1 when the bank is
+    never written)."""
+    if indices.ndim != 3 or indices.dtype != torch.long or (weights is not None and weights.shape != indices.shape):
         raise ValueError('weights and int64 indices must both be [batch, time, selected]')
     device = _require_gpu(weights, indices, valid)
-    batch, time, k = weights.shape
+    batch, time, k = indices.shape
     meta = dispatch_build(indices, indices[..., :0], bank_count)
-    w = _aligned(weights)
+    w = None if weights is None else _aligned(weights)
     mask = None if valid is None else valid.reshape(batch * time).to(torch.uint8).contiguous()
     totals = torch.empty(batch, bank_count, device=device, dtype=torch.float32)
     counts = torch.empty(batch, bank_count, device=device, dtype=torch.int32)
+    first = torch.empty(batch, bank_count, device=device, dtype=torch.int32) if first_write else None
     _lib.check(_lib.library().bdm_bank_occupancy(
-        _ptr(w), _dtype_code(w.dtype), _ptr(mask), _ptr(meta.order), _ptr(meta.cu_seqlens), batch, time, k,
-        bank_count, _ptr(totals), _ptr(counts), _stream(device)), 'bdm_bank_occupancy')
+        _ptr(w), _lib.BDM_BF16 if w is None else _dtype_code(w.dtype), _ptr(mask), _ptr(meta.order), _ptr(meta.cu_seqlens), batch, time, k,
+        bank_count, _ptr(totals), _ptr(counts), _ptr(first), _stream(device)), 'bdm_bank_occupancy')
+    if first_write:
+        return totals, counts, first
     return totals, counts
+
+
+def written_bank_curve(first_write: Tensor, prefixes) -> Tensor:
+    """Banks written before each prefix end, per sequence: [B, len(prefixes)]
+    int32 from the first-write positions [B, J] of ``bank_occupancy_totals``."""
+    if first_write.ndim != 2 or first_write.dtype != torch.int32:
+        raise ValueError('first_write must be [batch, banks] int32')
+    device = _require_gpu(first_write)
+    ends = torch.as_tensor(prefixes, dtype=torch.long).reshape(-1).to(device).contiguous()
+    if ends.numel() == 0:
+        raise ValueError('at least one prefix is needed')
+    if int(ends.numel()) > 2**31 - 1:
+        raise ValueError('too many prefixes')
+    batch, banks = first_write.shape
+    first = first_write.contiguous()
+    written = torch.empty(batch, ends.numel(), device=device, dtype=torch.int32)
+    _lib.check(_lib.library().bdm_written_bank_curve(
+        _ptr(first), batch, banks, _ptr(ends), ends.numel(), _ptr(written), _stream(device)),
+        'bdm_written_bank_curve')
+    return written

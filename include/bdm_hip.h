@@ -278,13 +278,27 @@ int bdm_output_epilogue(const bdm_output_args *args, void *stream);
  * instead of a scatter over [batch, J].  For segment s = b*J + bank:
  *   totals[s] = sum over its writes of valid tokens of
  *               log1p(-clamp(p, 0, 1 - 1e-6)) in FP32,
- *   counts[s] = the number of those writes.
- * valid ([batch*time] bytes, nonzero = valid) may be null.  The sum of a
- * segment is a fixed wave reduction: deterministic.
+ *   counts[s] = the number of those writes,
+ *   first_write[s] = the first position t of such a write, or INT32_MAX
+ *               when the bank is never written (first_write may be null).
+ * valid ([batch*time] bytes, nonzero = valid) may be null.  write_weights
+ * may be null when only counts and first writes are wanted (totals are then
+ * 0).  The sum of a segment is a fixed wave reduction: deterministic.
  */
 int bdm_bank_occupancy(const void *write_weights, int32_t weight_dtype, const uint8_t *valid,
                        const int64_t *order, const int64_t *cu_seqlens, int64_t batch, int64_t time,
-                       int32_t write_banks, int32_t bank_count, float *totals, int32_t *counts, void *stream);
+                       int32_t write_banks, int32_t bank_count, float *totals, int32_t *counts,
+                       int32_t *first_write, void *stream);
+
+/* Written banks at nested prefixes: the copy-on-write state count of the
+ * reference's memory study (APPENDIX.md:511-584; the byte arithmetic is
+ * checked by scripts/verify_results.py:190-235).  A bank holds private state
+ * from its first write on, so after the first t positions of sequence b
+ *   written[b*prefix_count + i] = #{bank : first_write[b*J + bank] < prefixes[i]}
+ * first_write [batch, J] int32 from bdm_bank_occupancy; prefixes [prefix_count]
+ * int64 on the device. */
+int bdm_written_bank_curve(const int32_t *first_write, int64_t batch, int32_t bank_count,
+                           const int64_t *prefixes, int32_t prefix_count, int32_t *written, void *stream);
 
 #ifdef __cplusplus
 }

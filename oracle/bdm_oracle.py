@@ -645,3 +645,25 @@ class OracleBankedDeltaMemory(nn.Module):
             heads.append(total.to(vh.dtype))
         raw = torch.cat(heads, dim=-1).unsqueeze(1)
         return self.project_output(hidden, raw), state
+
+
+def first_write_positions(indices: Tensor, banks: int, valid: Tensor | None = None) -> Tensor:
+    """Per (sequence, bank): the first position that writes the bank, valid
+    tokens only, or 2**31 - 1 when none does.  The copy-on-write state of the
+    reference's memory study holds exactly the banks whose first write came
+    before the measured prefix (APPENDIX.md:511-584)."""
+    batch, time, _ = indices.shape
+    pos = torch.arange(time).view(1, time, 1).expand_as(indices)
+    if valid is not None:
+        pos = torch.where(valid[..., None].bool(), pos, torch.full_like(pos, 2**31 - 1))
+    first = torch.full((batch, banks), 2**31 - 1, dtype=torch.int64)
+    first.scatter_reduce_(1, indices.reshape(batch, -1), pos.reshape(batch, -1), reduce='amin')
+    return first.to(torch.int32)
+
+
+def written_bank_curve(indices: Tensor, banks: int, prefixes, valid: Tensor | None = None) -> Tensor:
+    """[B, P] int32: distinct banks written within the first prefixes[i]
+    positions of each sequence (valid tokens only)."""
+    first = first_write_positions(indices, banks, valid).to(torch.int64)
+    ends = torch.as_tensor(prefixes, dtype=torch.int64).view(1, 1, -1)
+    return (first[..., None] < ends).sum(1).to(torch.int32)

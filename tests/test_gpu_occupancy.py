@@ -51,3 +51,40 @@ def test_bank_occupancy_is_deterministic(device):
     announce('occupancy determinism')
     runs = [ops.bank_occupancy_totals(weights.to(device), indices.to(device), 2048) for _ in range(2)]
     assert torch.equal(runs[0][0], runs[1][0]) and torch.equal(runs[0][1], runs[1][1])
+
+
+@pytest.mark.parametrize('masked', [False, True], ids=['all', 'valid'])
+def test_written_banks_match_oracle(device, masked):
+    """First-write positions and the written-bank curve (the copy-on-write
+    state count) equal the oracle exactly, prefixes past the end included."""
+    from bdm_amd import ops, written_banks
+    gen = torch.Generator().manual_seed(19)
+    batch, time, banks, k = 3, 300, 256, 8
+    _, weights, indices = routes(batch, time, banks, k, gen)
+    valid = torch.rand(batch, time, generator=gen) < 0.5 if masked else None
+    prefixes = [0, 1, 7, 150, 299, 300, 1000]
+    announce('written banks', masked)
+    vd = None if valid is None else valid.to(device)
+    _, counts, first = ops.bank_occupancy_totals(weights.to(device), indices.to(device), banks, vd, first_write=True)
+    curve = written_banks(indices.to(device), banks, prefixes, vd)
+    torch.cuda.synchronize()
+    assert torch.equal(first.cpu(), O.first_write_positions(indices, banks, valid))
+    assert torch.equal(curve.cpu(), O.written_bank_curve(indices, banks, prefixes, valid))
+    assert torch.equal(curve[:, -1].cpu(), (counts > 0).sum(1).int().cpu())
+
+
+def test_written_banks_memory_study_shape(device):
+    """The reference memory study's geometry (J = 2048, K = 8, 16k positions)
+    at its measured prefixes: exact against the oracle, K banks after one
+    token, never above min(J, K t)."""
+    from bdm_amd import written_banks
+    gen = torch.Generator().manual_seed(20)
+    batch, time, banks, k = 4, 16384, 2048, 8
+    _, _, indices = routes(batch, time, banks, k, gen)
+    prefixes = [1, 8, 32, 128, 512, 1008, 1024, 4096, 16368, 16384]
+    announce('written banks 16k')
+    curve = written_banks(indices.to(device), banks, prefixes).cpu()
+    assert torch.equal(curve, O.written_bank_curve(indices, banks, prefixes))
+    assert torch.all(curve[:, 0] == k)
+    for i, t in enumerate(prefixes):
+        assert torch.all(curve[:, i] <= min(banks, k * t))

@@ -267,3 +267,43 @@ def test_bank_occupancy_gradient_is_the_soft_union_gradient():
                             others *= 1.0 - float(weights[b, t2, j2])
                 # FP32 log-space sums: 1 - p loses digits for p near 1, hence 1e-2
                 assert float(w.grad[b, t, j]) == pytest.approx(others / banks, rel=1e-2)
+
+
+# ------------------------------------------------------------------ copy-on-write state count
+
+@pytest.mark.parametrize('masked', [False, True])
+def test_written_bank_curve_matches_sets(masked):
+    """Written banks after each prefix, by brute force over the token sets,
+    and the first-write positions by a scan in time order."""
+    _, indices, banks, valid = _occupancy_inputs(seed=9, batch=3, time=13)
+    mask = valid if masked else None
+    prefixes = [0, 1, 2, 5, 12, 13, 40]
+    curve = O.written_bank_curve(indices, banks, prefixes, mask)
+    first = O.first_write_positions(indices, banks, mask)
+    for b in range(indices.shape[0]):
+        seen_at = {}
+        for t in range(indices.shape[1]):
+            if masked and not bool(valid[b, t]):
+                continue
+            for bank in indices[b, t].tolist():
+                seen_at.setdefault(bank, t)
+        for bank in range(banks):
+            assert int(first[b, bank]) == seen_at.get(bank, 2**31 - 1)
+        for i, end in enumerate(prefixes):
+            assert int(curve[b, i]) == sum(1 for t in seen_at.values() if t < end)
+
+
+def test_written_bank_curve_boundaries():
+    """Known answers: nothing before position 0; the first token writes its K
+    distinct banks (the reference's memory data records K / J for one token in
+    every layer); the count never decreases, never exceeds min(J, K * t), and
+    at the full length equals the hard union of bank_occupancy."""
+    weights, indices, banks, _ = _occupancy_inputs(seed=10, batch=4, time=30, banks=64, k=6)
+    prefixes = list(range(0, 31))
+    curve = O.written_bank_curve(indices, banks, prefixes)
+    _, hard, _ = O.bank_occupancy(weights, indices, banks)
+    assert torch.all(curve[:, 0] == 0) and torch.all(curve[:, 1] == 6)
+    assert torch.all(curve[:, 1:] >= curve[:, :-1])
+    for i, t in enumerate(prefixes):
+        assert torch.all(curve[:, i] <= min(banks, 6 * t))
+    assert torch.equal(curve[:, -1].float() / banks, hard)
