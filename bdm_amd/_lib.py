@@ -23,6 +23,8 @@ EXPORTED_SYMBOLS = (
     'bdm_backward_workspace_size', 'bdm_backward', 'bdm_decode', 'bdm_controller_epilogue', 'bdm_output_epilogue',
     'bdm_bank_occupancy',
     'bdm_written_bank_curve',
+    'bdm_rms_norm',
+    'bdm_swiglu',
 )
 
 _i32, _i64, _f32, _vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
@@ -132,6 +134,10 @@ def library() -> ctypes.CDLL:
     lib.bdm_bank_occupancy.restype = _i32
     lib.bdm_written_bank_curve.argtypes = [_vp, _i64, _i32, _vp, _i32, _vp, _vp]
     lib.bdm_written_bank_curve.restype = _i32
+    lib.bdm_rms_norm.argtypes = [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _f32, _vp]
+    lib.bdm_rms_norm.restype = _i32
+    lib.bdm_swiglu.argtypes = [_vp, _vp, _i64, _i32, _i32, _vp]
+    lib.bdm_swiglu.restype = _i32
     return lib
 
 

@@ -5,8 +5,10 @@
 // the reference supports one head with eight rows only (:88-104), this kernel
 // any head count and bank size <= 32.
 //
-// One workgroup per (sequence, head).  Lane group j (head_width / CPL lanes)
-// owns write slot j and read slot j.  A step makes two dependent trips to HBM:
+// One workgroup per (sequence, head, column span).  Value columns are
+// independent in both the write rule and the read, so a wide head is split
+// into spans that keep a workgroup within 512 lanes and 64 KiB of LDS.  Lane
+// group j (span / CPL lanes) owns write slot j and read slot j.  A step makes two dependent trips to HBM:
 // first the bank indices and controller rows (all independent of a bank id,
 // issued together, with no barrier behind them), then every bank state the
 // step touches — the write banks and the read banks that are not also
@@ -46,6 +48,7 @@ struct DecodeParams {
     void *state;
     T *out;
     int heads, s_real, width, banks, kw, kr;
+    int span, spans;  // columns per workgroup and workgroups per (sequence, head)
     int lanes_per_slot;
     int vec_rows;  // q, k, b, g rows of S elements can be read as 16-byte vectors
     int state_dtype, routed_decay;
@@ -57,15 +60,17 @@ struct DecodeParams {
 template <typename T, typename SE, int S, int CPL, bool VEC, int KMAX, bool KFIX>
 __global__ __launch_bounds__(512) void decode_kernel(DecodeParams<T> p) {
     extern __shared__ float smem[];
-    // smem layout: written states [kw][S][width], read values [kr][width]
+    // smem layout: written states [kw][S][span], read values [kr][span]
     float *written = smem;
-    float *reads = smem + p.kw * S * p.width;
+    float *reads = smem + p.kw * S * p.span;
     __shared__ int s_rank_slot[kMaxSlots];
 
-    const int64_t seq = blockIdx.x / p.heads;
-    const int head = blockIdx.x % p.heads;
+    const int64_t seq = blockIdx.x / (p.heads * p.spans);
+    const int head = (blockIdx.x / p.spans) % p.heads;
+    const int span0 = (blockIdx.x % p.spans) * p.span;
     const int slot = threadIdx.x / p.lanes_per_slot;
-    const int col0 = (threadIdx.x % p.lanes_per_slot) * CPL;
+    const int lc = (threadIdx.x % p.lanes_per_slot) * CPL;  // column within the span
+    const int col0 = span0 + lc;
     const int64_t row = seq * p.heads + head;
     const bool has_write = slot < p.kw;
     const bool has_read = slot < p.kr;
@@ -190,7 +195,7 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeParams<T> p) {
             }
             store_row<CPL>(static_cast<SE *>(p.state) + base + int64_t(r) * p.width, hw[r]);
 #pragma unroll
-            for (int c = 0; c < CPL; ++c) written[(slot * S + r) * p.width + col0 + c] = hw[r][c];
+            for (int c = 0; c < CPL; ++c) written[(slot * S + r) * p.span + lc + c] = hw[r][c];
         }
     }
     __syncthreads();
@@ -202,7 +207,7 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeParams<T> p) {
             for (int r = 0; r < S; ++r)
 #pragma unroll
                 for (int c = 0; c < CPL; ++c)
-                    hr[r][c] = r < p.s_real ? written[(read_from_write * S + r) * p.width + col0 + c] : 0.f;
+                    hr[r][c] = r < p.s_real ? written[(read_from_write * S + r) * p.span + lc + c] : 0.f;
         }
         float qr[S];
 #pragma unroll
@@ -212,17 +217,17 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeParams<T> p) {
             float acc = 0.f;
 #pragma unroll
             for (int r = 0; r < S; ++r) acc = fmaf(qr[r], hr[r][c], acc);
-            reads[slot * p.width + col0 + c] = round_to<T>(acc * p.scale);
+            reads[slot * p.span + lc + c] = round_to<T>(acc * p.scale);
         }
     }
     __syncthreads();
 
     // ---- ordered sum (inference.py:53-67)
-    T *out = p.out + seq * int64_t(p.heads) * p.width + int64_t(head) * p.width;
-    for (int c = threadIdx.x; c < p.width; c += blockDim.x) {
+    T *out = p.out + seq * int64_t(p.heads) * p.width + int64_t(head) * p.width + span0;
+    for (int c = threadIdx.x; c < p.span; c += blockDim.x) {
         float v[kMaxSlots];
 #pragma unroll
-        for (int j = 0; j < kMaxSlots; ++j) v[j] = j < p.kr ? reads[s_rank_slot[j] * p.width + c] : 0.f;
+        for (int j = 0; j < kMaxSlots; ++j) v[j] = j < p.kr ? reads[s_rank_slot[j] * p.span + c] : 0.f;
         float total = 0.f;
 #pragma unroll
         for (int j = 0; j < kMaxSlots; ++j)
@@ -252,7 +257,18 @@ int launch_decode(const bdm_decode_args &a, hipStream_t stream) {
     p.banks = a.bank_count;
     p.kw = a.write_banks;
     p.kr = a.read_banks;
-    p.lanes_per_slot = a.head_width / CPL;
+    // the widest span (a divisor of the head width, a multiple of CPL) that
+    // fits 512 lanes and 64 KiB of LDS
+    const int slots = a.write_banks > a.read_banks ? a.write_banks : a.read_banks;
+    auto lds_bytes = [&](int span) {
+        return (size_t(a.write_banks) * S * span + size_t(a.read_banks) * span) * sizeof(float);
+    };
+    int span = a.head_width;
+    while ((slots * (span / CPL) > 512 || lds_bytes(span) > 64 * 1024) && span % 2 == 0 && (span / 2) % CPL == 0)
+        span /= 2;
+    p.span = span;
+    p.spans = a.head_width / span;
+    p.lanes_per_slot = span / CPL;
     // vector row loads need the S-element rows at 16-byte boundaries
     p.vec_rows = (a.bank_size == S && aligned(a.q, 16) && aligned(a.k, 16) && aligned(a.b, 16) && aligned(a.g, 16) &&
                   (S * sizeof(T)) % 16 == 0)
@@ -261,12 +277,12 @@ int launch_decode(const bdm_decode_args &a, hipStream_t stream) {
     p.state_dtype = a.state_dtype;
     p.routed_decay = a.routed_decay;
     p.scale = a.scale;
-    const int slots = a.write_banks > a.read_banks ? a.write_banks : a.read_banks;
     const int threads = ((slots * p.lanes_per_slot + kWave - 1) / kWave) * kWave;
     if (threads > 512) return fail(BDM_ERR_UNSUPPORTED, "decode: %d lanes per workgroup", threads);
-    const size_t lds = (size_t(a.write_banks) * S * a.head_width + size_t(a.read_banks) * a.head_width) * sizeof(float);
+    const size_t lds = lds_bytes(span);
     if (lds > 64 * 1024) return fail(BDM_ERR_UNSUPPORTED, "decode: %zu bytes of LDS", lds);
-    const unsigned grid = unsigned(a.batch * a.heads);
+    if (a.batch * a.heads * p.spans > int64_t(UINT32_MAX)) return fail(BDM_ERR_UNSUPPORTED, "decode: grid too large");
+    const unsigned grid = unsigned(a.batch * a.heads * p.spans);
     // the production geometry (8 banks per role, full-width aligned rows) gets
     // straight-line loads; anything else the general form
     const bool fast = p.vec_rows && a.write_banks == 8 && a.read_banks == 8 && aligned(a.write_weights, 16) &&
@@ -288,8 +304,10 @@ int launch_decode(const bdm_decode_args &a, hipStream_t stream) {
 template <typename T>
 int dispatch_decode(const bdm_decode_args &a, hipStream_t stream) {
     if (a.bank_size <= 8) {
-        // two columns per lane: 64 lanes per slot, more loads in flight per step
-        if (a.head_width % 2 == 0 && a.head_width / 2 <= 64) return launch_decode<T, 8, 2>(a, stream);
+        // two columns per lane: 64 lanes per slot, more loads in flight per
+        // step (wide heads run as spans of 128 columns)
+        if (a.head_width % 2 == 0 && (a.head_width / 2 <= 64 || a.head_width % 128 == 0))
+            return launch_decode<T, 8, 2>(a, stream);
         if (a.head_width % 4 == 0 && a.head_width / 4 <= 64) return launch_decode<T, 8, 4>(a, stream);
         if (a.head_width % 8 == 0) return launch_decode<T, 8, 8>(a, stream);
         return launch_decode<T, 8, 1>(a, stream);

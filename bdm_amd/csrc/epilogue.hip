@@ -8,6 +8,11 @@
 // the controller dtype is rounded to it at the same point here (silu before
 // the l2 normalization, sigmoid of the gate before the product, ...); the
 // arithmetic between those points is FP32 as in torch's opmath.
+//
+// The language-model shell around the layer adds two more: the residual add
+// fused with RMSNorm (_shell.py:10-35) and the SwiGLU product
+// silu(w1 x) * (w3 x) (_shell.py:86-91) over one GEMM of the concatenated
+// w1 | w3 weights.
 #include "bdm_common.h"
 
 namespace bdm {
@@ -317,6 +322,71 @@ int launch_output(const bdm_output_args &a, hipStream_t stream) {
     return check_launch("output_epilogue_kernel");
 }
 
+// RMSNorm of the shell (_shell.py:29-35): out = (x * rsqrt(mean(x^2) + eps))
+// * weight in FP32, rounded once to T.  With a residual, x = round(a + r) is
+// the block's new hidden state: written to sum_out and normalized.  One wave
+// per row; lane l owns the 8-column chunks l*8, l*8 + 512, ...
+template <typename T, int MAXC, bool VEC>
+__global__ __launch_bounds__(256) void rms_norm_kernel(const T *__restrict__ x, const T *__restrict__ residual,
+                                                       const void *__restrict__ weight, int weight_dtype,
+                                                       T *__restrict__ sum_out, T *__restrict__ out, int64_t rows,
+                                                       int width, float eps) {
+    const int lane = threadIdx.x % kWave;
+    const int64_t row = int64_t(blockIdx.x) * (blockDim.x / kWave) + threadIdx.x / kWave;
+    if (row >= rows) return;
+    const int64_t base = row * width;
+    float h[MAXC][8];
+    float sq = 0.f;
+#pragma unroll
+    for (int i = 0; i < MAXC; ++i) {
+        const int c = min((lane + i * kWave) * 8, width - 8);  // chunks past the width re-read the last
+        const bool live = (lane + i * kWave) * 8 < width;
+        load8<T, VEC>(x + base + c, h[i]);
+        if (residual) {
+            float r[8];
+            load8<T, VEC>(residual + base + c, r);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) h[i][j] = round_to<T>(h[i][j] + r[j]);
+            if (live) store_row<8>(sum_out + base + c, h[i]);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) sq = live ? fmaf(h[i][j], h[i][j], sq) : sq;
+    }
+    const float scale = rsqrtf(wave_total<kWave>(sq) / float(width) + eps);
+#pragma unroll
+    for (int i = 0; i < MAXC; ++i) {
+        const int c = (lane + i * kWave) * 8;
+        if (c >= width) continue;
+        float wt[8], y[8];
+        param8<VEC>(weight, weight_dtype, c, wt);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) y[j] = h[i][j] * scale * wt[j];
+        store_row<8>(out + base + c, y);
+    }
+}
+
+// SwiGLU of the shell's feed-forward (_shell.py:86-91) over the output of one
+// GEMM with the concatenated w1 | w3 weights: row r holds x1 = w1 x in columns
+// [0, hidden) and x3 = w3 x in [hidden, 2 hidden).  out = round(round(silu(x1))
+// * x3), the two roundings torch makes in the module's dtype; silu is
+// x / (1 + exp(-x)) with IEEE division, as torch evaluates it.
+template <typename T, bool VEC>
+__global__ __launch_bounds__(256) void swiglu_kernel(const T *__restrict__ gate_up, T *__restrict__ out,
+                                                     int64_t rows, int hidden) {
+    const int64_t groups = int64_t(hidden) / 8;
+    const int64_t item = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (item >= rows * groups) return;
+    const int64_t row = item / groups;
+    const int c = int(item % groups) * 8;
+    const T *in = gate_up + row * 2 * hidden;
+    float a[8], b[8], y[8];
+    load8<T, VEC>(in + c, a);
+    load8<T, VEC>(in + hidden + c, b);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) y[j] = round_to<T>(a[j] / (1.f + expf(-a[j]))) * b[j];
+    store_row<8>(out + row * hidden + c, y);
+}
+
 }  // namespace
 }  // namespace bdm
 
@@ -363,4 +433,76 @@ extern "C" int bdm_output_epilogue(const bdm_output_args *a, void *stream) {
     hipStream_t s = as_stream(stream);
     if (a->ctrl_dtype == BDM_BF16) return launch_output<bf16_t>(*a, s);
     return launch_output<float>(*a, s);
+}
+
+extern "C" int bdm_rms_norm(const void *x, const void *residual, const void *weight, void *sum_out, void *out,
+                            int64_t rows, int32_t width, int32_t dtype, int32_t weight_dtype, float eps,
+                            void *stream) {
+    using namespace bdm;
+    if (rows < 0 || width <= 0 || width % 8 != 0) return fail(BDM_ERR_INVALID, "rms_norm: bad geometry");
+    if (width > 8192) return fail(BDM_ERR_UNSUPPORTED, "rms_norm: width %d > 8192", width);
+    if (dtype != BDM_BF16 && dtype != BDM_F32) return fail(BDM_ERR_INVALID, "rms_norm: dtype");
+    if (weight_dtype != BDM_BF16 && weight_dtype != BDM_F32) return fail(BDM_ERR_INVALID, "rms_norm: weight dtype");
+    if (rows == 0) return BDM_OK;
+    if (!x || !weight || !out || (residual && !sum_out)) return fail(BDM_ERR_INVALID, "rms_norm: null pointer");
+    if ((rows + 3) / 4 > int64_t(INT32_MAX)) return fail(BDM_ERR_UNSUPPORTED, "rms_norm: too many rows");
+    const bool vec = aligned(x, 16) && aligned(weight, 16) && aligned(out, 16) &&
+                     (!residual || (aligned(residual, 16) && aligned(sum_out, 16)));
+    const unsigned blocks = unsigned((rows + 3) / 4);
+    const int chunks = (width / 8 + kWave - 1) / kWave;
+    hipStream_t s = as_stream(stream);
+    auto go = [&](auto tag) {
+        using T = decltype(tag);
+        const T *xp = static_cast<const T *>(x), *rp = static_cast<const T *>(residual);
+        T *sp = static_cast<T *>(sum_out), *op = static_cast<T *>(out);
+#define BDM_RMS(C)                                                                                           \
+    (vec ? (rms_norm_kernel<T, C, true><<<blocks, 256, 0, s>>>(xp, rp, weight, weight_dtype, sp, op, rows, width, eps), 0) \
+         : (rms_norm_kernel<T, C, false><<<blocks, 256, 0, s>>>(xp, rp, weight, weight_dtype, sp, op, rows, width, eps), 0))
+        if (chunks <= 1)
+            BDM_RMS(1);
+        else if (chunks <= 2)
+            BDM_RMS(2);
+        else if (chunks <= 4)
+            BDM_RMS(4);
+        else if (chunks <= 8)
+            BDM_RMS(8);
+        else
+            BDM_RMS(16);
+#undef BDM_RMS
+    };
+    if (dtype == BDM_BF16)
+        go(bf16_t{});
+    else
+        go(0.f);
+    return check_launch("rms_norm_kernel");
+}
+
+extern "C" int bdm_swiglu(const void *gate_up, void *out, int64_t rows, int32_t hidden, int32_t dtype,
+                          void *stream) {
+    using namespace bdm;
+    if (rows < 0 || hidden <= 0 || hidden % 8 != 0) return fail(BDM_ERR_INVALID, "swiglu: bad geometry");
+    if (dtype != BDM_BF16 && dtype != BDM_F32) return fail(BDM_ERR_INVALID, "swiglu: dtype");
+    if (rows == 0) return BDM_OK;
+    if (!gate_up || !out) return fail(BDM_ERR_INVALID, "swiglu: null pointer");
+    const int64_t items = rows * (hidden / 8);
+    if ((items + 255) / 256 > int64_t(INT32_MAX)) return fail(BDM_ERR_UNSUPPORTED, "swiglu: too many rows");
+    const bool vec = aligned(gate_up, 16) && aligned(out, 16);
+    const unsigned blocks = unsigned((items + 255) / 256);
+    hipStream_t s = as_stream(stream);
+    if (dtype == BDM_BF16) {
+        auto *in = static_cast<const bf16_t *>(gate_up);
+        auto *o = static_cast<bf16_t *>(out);
+        if (vec)
+            swiglu_kernel<bf16_t, true><<<blocks, 256, 0, s>>>(in, o, rows, hidden);
+        else
+            swiglu_kernel<bf16_t, false><<<blocks, 256, 0, s>>>(in, o, rows, hidden);
+    } else {
+        auto *in = static_cast<const float *>(gate_up);
+        auto *o = static_cast<float *>(out);
+        if (vec)
+            swiglu_kernel<float, true><<<blocks, 256, 0, s>>>(in, o, rows, hidden);
+        else
+            swiglu_kernel<float, false><<<blocks, 256, 0, s>>>(in, o, rows, hidden);
+    }
+    return check_launch("swiglu_kernel");
 }

@@ -1,0 +1,221 @@
+"""The language-model shell around the BDM layer.
+
+``BDMLanguageModel`` keeps the reference shell's configuration, module tree,
+parameter names and seeded initialisation (implementation/bdm/model.py:143-216,
+_shell.py:10-118), so state dicts interchange with the reference and
+``forward(tokens, target=None)`` returns the same logits or loss.  Its
+``prefill``/``step`` pair follows the reference's whole-model inference
+harness (reproduction/experiments/perf_inference_case.py:15-56): each block
+runs ``attention.prefill``/``attention.step`` on its own bank cache and the
+head projects only the last position.
+
+Under no_grad the shell's elementwise work runs in ``libbdm_hip.so``
+(``bdm_rms_norm``, ``bdm_swiglu``) and the feed-forward's two input
+projections are one GEMM over their concatenated weights; with autograd the
+modules run as the reference writes them.
+"""
+
+from __future__ import annotations
+
+from dataclasses import asdict, dataclass, field
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from . import ops
+from .config import BDMConfig
+from .model import BankedDeltaMemory
+
+Tensor = torch.Tensor
+
+
+@dataclass(frozen=True)
+class LanguageModelConfig:
+    """model.py:143-161."""
+    memory: BDMConfig = field(default_factory=BDMConfig)
+    vocab_size: int = 192
+    layers: int = 8
+    ffn_multiple_of: int = 256
+    seed: int = 0
+    recompute_ffn: bool = True
+    compact_replay: bool | None = None
+
+    def __post_init__(self):
+        if min(self.vocab_size, self.layers, self.ffn_multiple_of) <= 0 or self.seed < 0:
+            raise ValueError('invalid language-model geometry or seed')
+        if self.compact_replay is not None and type(self.compact_replay) is not bool:
+            raise ValueError('compact_replay must be None, True, or False')
+
+    def record(self):
+        return dict(asdict(self), memory=self.memory.record())
+
+
+class RMSNorm(nn.Module):
+    """x * rsqrt(mean(x^2) + eps) * weight in FP32, cast back (_shell.py:10-35)."""
+
+    def __init__(self, dim: int, eps: float = 1e-6):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(dim))
+
+    def forward(self, x: Tensor) -> Tensor:
+        if not torch.is_grad_enabled() and ops.rms_norm_supported(x):
+            return ops.rms_norm(x, self.weight, self.eps)
+        output = x.float() * torch.rsqrt((x.float() * x.float()).mean(-1, keepdim=True) + self.eps)
+        return (output * self.weight.float()).type_as(x)
+
+    def add_norm(self, x: Tensor, residual: Tensor):
+        """(residual + x, its norm): a block's residual add followed by the
+        next normalization, one kernel under no_grad."""
+        if not torch.is_grad_enabled() and ops.rms_norm_supported(x):
+            return ops.rms_norm(x, self.weight, self.eps, residual=residual)
+        total = residual + x
+        return total, self(total)
+
+    def reset_parameters(self):
+        nn.init.ones_(self.weight)
+
+
+class FeedForward(nn.Module):
+    """SwiGLU w2(silu(w1 x) * w3 x) with the reference's hidden width rule
+    (_shell.py:37-118)."""
+
+    def __init__(self, dim: int, hidden_dim: int, multiple_of: int, ffn_dim_multiplier: float | None,
+                 mp_size: int = 1, recompute_activations: bool = False):
+        super().__init__()
+        hidden_dim = int(2 * hidden_dim / 3)
+        if ffn_dim_multiplier is not None:
+            hidden_dim = int(ffn_dim_multiplier * hidden_dim)
+        hidden_dim = multiple_of * ((hidden_dim + multiple_of - 1) // multiple_of)
+        if hidden_dim % mp_size:
+            raise ValueError('hidden width must divide over mp_size')
+        self.dim, self.hidden_dim = dim, hidden_dim
+        self.recompute_activations = recompute_activations
+        self.w1 = nn.Linear(dim, hidden_dim, bias=False)
+        self.w3 = nn.Linear(dim, hidden_dim, bias=False)
+        self.w2 = nn.Linear(hidden_dim, dim, bias=False)
+        self._fused_cache = None
+
+    def _fused_input_weight(self) -> Tensor:
+        key = tuple((p.data_ptr(), p._version, p.dtype) for p in (self.w1.weight, self.w3.weight))
+        if self._fused_cache is None or self._fused_cache[0] != key:
+            self._fused_cache = (key, torch.cat([self.w1.weight, self.w3.weight], 0).contiguous())
+        return self._fused_cache[1]
+
+    def forward(self, x: Tensor) -> Tensor:
+        if not torch.is_grad_enabled() and x.is_cuda and self.hidden_dim % 8 == 0:
+            gated = ops.swiglu(F.linear(x, self._fused_input_weight()), self.hidden_dim)
+            return self.w2(gated)
+        if (self.recompute_activations and torch.is_grad_enabled() and x.is_cuda and x.dtype == torch.bfloat16
+                and x.numel() // self.dim >= 1024):
+            return torch.utils.checkpoint.checkpoint(self._forward, x, use_reentrant=False,
+                                                     preserve_rng_state=False)
+        return self._forward(x)
+
+    def _forward(self, x: Tensor) -> Tensor:
+        return self.w2(F.silu(self.w1(x)) * self.w3(x))
+
+    def reset_parameters(self, init_std=None, factor=1.0):
+        in_std = init_std or self.dim ** -0.5
+        out_std = (init_std or self.hidden_dim ** -0.5) / factor
+        for w in (self.w1, self.w3):
+            nn.init.trunc_normal_(w.weight, mean=0.0, std=in_std, a=-3 * in_std, b=3 * in_std)
+        nn.init.trunc_normal_(self.w2.weight, mean=0.0, std=out_std, a=-3 * out_std, b=3 * out_std)
+
+
+class BDMBlock(nn.Module):
+    """Pre-norm residual block: memory layer then SwiGLU (model.py:164-176)."""
+
+    def __init__(self, config: LanguageModelConfig, index: int, backend: str):
+        super().__init__()
+        dim = config.memory.dim
+        self.attention = BankedDeltaMemory(config.memory, layer_id=index, seed=config.seed, backend=backend,
+                                           compact_replay=config.compact_replay)
+        self.feed_forward = FeedForward(dim, 4 * dim, config.ffn_multiple_of, None,
+                                        recompute_activations=config.recompute_ffn)
+        self.attention_norm = RMSNorm(dim, eps=config.memory.norm_eps)
+        self.ffn_norm = RMSNorm(dim, eps=config.memory.norm_eps)
+
+    def forward(self, hidden: Tensor) -> Tensor:
+        hidden = hidden + self.attention(self.attention_norm(hidden))
+        return hidden + self.feed_forward(self.ffn_norm(hidden))
+
+
+class BDMLanguageModel(nn.Module):
+    """Checkpoint-compatible all-bank shell with independent width and depth
+    (model.py:179-216)."""
+
+    def __init__(self, config: LanguageModelConfig, *, backend='hip'):
+        super().__init__()
+        self.config = config
+        self.dim = config.memory.dim
+        self.layers = nn.ModuleList([BDMBlock(config, i, backend) for i in range(config.layers)])
+        self.tok_embeddings = nn.Embedding(config.vocab_size, self.dim)
+        self.norm = RMSNorm(self.dim, eps=config.memory.norm_eps)
+        self.output = nn.Linear(self.dim, config.vocab_size, bias=False)
+        base, std = config.seed * 100_000, self.dim ** -.5
+        with torch.random.fork_rng(devices=[]):
+            torch.manual_seed(base + 100)
+            for parameter in (self.tok_embeddings.weight, self.output.weight):
+                nn.init.trunc_normal_(parameter, mean=0, std=std, a=-3 * std, b=3 * std)
+        for i, block in enumerate(self.layers):
+            block.attention.init_weights(initialization_seed=base + 6000 + i)
+            with torch.random.fork_rng(devices=[]):
+                torch.manual_seed(base + 1000 + i)
+                block.feed_forward.reset_parameters()
+
+    def _hidden(self, tokens: Tensor) -> Tensor:
+        hidden = self.tok_embeddings(tokens)
+        for block in self.layers:
+            hidden = block(hidden)
+        return hidden
+
+    def forward(self, tokens: Tensor, target: Tensor | None = None):
+        logits = self.output(self.norm(self._hidden(tokens)))
+        if target is not None:
+            return F.cross_entropy(logits.float().flatten(0, -2), target.flatten())
+        return logits
+
+    # -- stateful inference (perf_inference_case.py:15-56) ---------------------------
+    def empty_cache(self) -> list:
+        return [None] * len(self.layers)
+
+    def prefill(self, tokens: Tensor, caches: list | None = None):
+        """Run a prompt through every block, each prefilling its bank cache
+        ([B, J, H, S, v] per layer); returns (logits of the last position
+        [B, 1, vocab], caches).  No autograd."""
+        if torch.is_grad_enabled():
+            raise RuntimeError('Stateful inference requires no_grad or inference_mode')
+        caches = list(caches) if caches is not None else self.empty_cache()
+        if len(caches) != len(self.layers):
+            raise ValueError('one cache per layer is required')
+        return self._run(tokens, caches, decode=False)
+
+    def step(self, tokens: Tensor, caches: list):
+        """One decode position ([B, 1] tokens) against prefilled caches,
+        advanced in place; returns (logits [B, 1, vocab], caches)."""
+        if torch.is_grad_enabled():
+            raise RuntimeError('Stateful inference requires no_grad or inference_mode')
+        if tokens.ndim != 2 or tokens.shape[1] != 1:
+            raise ValueError('step takes [batch, 1] tokens')
+        if len(caches) != len(self.layers) or any(c is None for c in caches):
+            raise ValueError('step needs the caches returned by prefill')
+        return self._run(tokens, list(caches), decode=True)
+
+    def _run(self, tokens: Tensor, caches: list, decode: bool):
+        # Each residual add is fused with the normalization that reads its
+        # result: the block's ffn_norm, then the next block's attention_norm
+        # (the final norm after the last block).
+        hidden = self.tok_embeddings(tokens)
+        normed = self.layers[0].attention_norm(hidden)
+        for i, block in enumerate(self.layers):
+            run = block.attention.step if decode else block.attention.prefill
+            out, caches[i] = run(normed, caches[i])
+            hidden, normed = block.ffn_norm.add_norm(out, hidden)
+            after = self.layers[i + 1].attention_norm if i + 1 < len(self.layers) else self.norm
+            hidden, normed = after.add_norm(block.feed_forward(normed), hidden)
+        return self.output(normed[:, -1:]), caches
+
+
+BSDMLanguageModel = BDMLanguageModel

@@ -434,6 +434,48 @@ def output_epilogue(raw: Tensor, gate: Tensor, weight: Tensor, bias: Tensor | No
 
 
 # ---------------------------------------------------------------------------
+# language-model shell
+
+def rms_norm_supported(x: Tensor) -> bool:
+    return x.is_cuda and x.dtype in (torch.bfloat16, torch.float32) and x.shape[-1] % 8 == 0 and x.shape[-1] <= 8192
+
+
+def rms_norm(x: Tensor, weight: Tensor, eps: float, residual: Tensor | None = None):
+    """RMSNorm of the shell (_shell.py:29-35) in one pass: FP32 arithmetic,
+    one rounding.  With ``residual``, returns (x + residual rounded, its norm),
+    the block's residual add fused in; otherwise the norm of x."""
+    _require_gpu(x, weight, residual)
+    if not rms_norm_supported(x):
+        raise ValueError('rms_norm takes BF16/FP32 rows whose width is a multiple of 8, at most 8192')
+    if residual is not None and (residual.shape != x.shape or residual.dtype != x.dtype):
+        raise ValueError('residual must match x')
+    if weight.shape != (x.shape[-1],):
+        raise ValueError('weight must be [width]')
+    x, weight = _aligned(x), _aligned(weight)
+    res = None if residual is None else _aligned(residual)
+    out = torch.empty_like(x)
+    total = None if res is None else torch.empty_like(x)
+    width = x.shape[-1]
+    _lib.check(_lib.library().bdm_rms_norm(
+        _ptr(x), _ptr(res), _ptr(weight), _ptr(total), _ptr(out), x.numel() // width, width, _dtype_code(x.dtype),
+        _dtype_code(weight.dtype), float(eps), _stream(x.device)), 'bdm_rms_norm')
+    return out if res is None else (total, out)
+
+
+def swiglu(gate_up: Tensor, hidden: int) -> Tensor:
+    """silu(x1) * x3 of the shell's feed-forward (_shell.py:86-91) from the
+    output [..., 2*hidden] of one GEMM with the concatenated w1 | w3 weights."""
+    _require_gpu(gate_up)
+    if gate_up.shape[-1] != 2 * hidden or hidden % 8:
+        raise ValueError('gate_up must be [..., 2*hidden] with hidden a multiple of 8')
+    gate_up = _aligned(gate_up)
+    out = torch.empty(*gate_up.shape[:-1], hidden, device=gate_up.device, dtype=gate_up.dtype)
+    _lib.check(_lib.library().bdm_swiglu(_ptr(gate_up), _ptr(out), gate_up.numel() // (2 * hidden), hidden,
+                                         _dtype_code(gate_up.dtype), _stream(gate_up.device)), 'bdm_swiglu')
+    return out
+
+
+# ---------------------------------------------------------------------------
 # bank occupancy
 
 def bank_occupancy_totals(weights: Tensor, indices: Tensor, bank_count: int, valid: Tensor | None = None,

@@ -60,9 +60,12 @@ def parse_args():
     ap.add_argument('--cpu-tokens', type=int, default=512,
                     help='tokens of sequence 0 the CPU oracle runs (0 skips the CPU baseline)')
     ap.add_argument('--no-extras', action='store_true', help='skip the full-layer and decode measurements')
-    ap.add_argument('--only', choices=('c3', 'c4', 'c5', 'prefill'),
+    ap.add_argument('--only', choices=('c3', 'c4', 'c5', 'prefill', 'lm'),
                     help='run one named workload alone (C3 decode, C4 skewed forward, C5 training, C2 full-layer '
-                         'prefill) and print its figures as one JSON line; used to profile a workload on its own')
+                         'prefill, whole-model prefill and decode) and print its figures as one JSON line; used to '
+                         'profile a workload on its own')
+    ap.add_argument('--lm-context', type=int, default=8192,
+                    help='prompt length T (= memory rows N) of the whole-model L16/D2048 measurement')
     return ap.parse_args()
 
 
@@ -249,6 +252,67 @@ def full_step_graph(layer, xs, state, steps):
         return None, f'capture failed: {str(exc)[:120]}'
 
 
+# Published H200 whole-model figures for L16/D2048/FFN5632, batch 1, N = T
+# (data/inference-performance.json:2497,2656,2868; data/decode-performance.json:851)
+H200_PREFILL_SECONDS = {8192: 0.0504, 65536: 0.3757, 1048576: 6.709}
+H200_DECODE_MS = {8192: 2.523}
+
+
+def whole_model(device, context, timed_runs=3, decode_tokens=16):
+    """The reference's whole-model inference case (perf_inference_case.py:15-56,
+    80-160): BDMLanguageModel L16/D2048/FFN5632, vocab 50,257, one head of width
+    2,048, N = T memory rows (J = T/8 banks of 8), K = 8, BF16 weights, batch
+    1.  Prefill = embedding, every block's prefill from a fresh cache (the
+    caches are created inside, as the reference's run does) and the head on
+    the last position; decode = one eager step per token through all blocks
+    and the full-vocabulary head.  Random-init weights, token ids uniform."""
+    import torch
+    from bdm_amd import BSDMConfig
+    from bdm_amd.lm import BDMLanguageModel, LanguageModelConfig
+    memory = BSDMConfig(dim=2048, bank_count=context // 8, bank_size=8, selected_banks=8, value_width=2048,
+                        num_heads=1)
+    config = LanguageModelConfig(memory=memory, vocab_size=50257, layers=16, seed=0)
+    with torch.device(device):
+        model = BDMLanguageModel(config)
+    model = model.to(torch.bfloat16).eval()
+    gen = torch.Generator().manual_seed(5)
+    tokens = torch.randint(0, config.vocab_size, (1, context + 64), generator=gen).to(device)
+    prompt = tokens[:, :context]
+    samples = []
+    with torch.inference_mode():
+        for i in range(timed_runs + 1):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            logits, caches = model.prefill(prompt)
+            torch.cuda.synchronize()
+            if i:  # the first run warms up the GEMM and kernel caches
+                samples.append(time.perf_counter() - t0)
+        if not bool(torch.isfinite(logits).all()):
+            raise RuntimeError('whole-model prefill produced non-finite logits')
+        for i in range(4):
+            logits, caches = model.step(tokens[:, context + i:context + i + 1], caches)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(decode_tokens):
+            pos = context + 4 + i
+            logits, caches = model.step(tokens[:, pos:pos + 1], caches)
+        torch.cuda.synchronize()
+        decode_ms = (time.perf_counter() - t0) * 1e3 / decode_tokens
+    prefill_s = statistics.mean(samples)
+    out = {'context': context, 'layers': 16, 'd_model': 2048, 'ffn': model.layers[0].feed_forward.hidden_dim,
+           'bank_count': memory.bank_count, 'prefill_seconds': round(prefill_s, 5),
+           'prefill_tokens_per_s': round(context / prefill_s, 1), 'decode_ms_per_token_eager': round(decode_ms, 3),
+           'cache_bytes': sum(c.numel() * c.element_size() for c in caches)}
+    if context in H200_PREFILL_SECONDS:
+        out['h200_prefill_seconds'] = H200_PREFILL_SECONDS[context]
+        out['prefill_speedup_vs_h200'] = round(H200_PREFILL_SECONDS[context] / prefill_s, 3)
+    if context in H200_DECODE_MS:
+        out['h200_decode_ms_per_token'] = H200_DECODE_MS[context]
+    del model, caches
+    torch.cuda.empty_cache()
+    return out
+
+
 def c4_forward(device, steps=3):
     """C4: batch 4, T8192, J2048 (32x64), Zipf s=1.1 bias on the factor scores,
     hot-path prefill forward (router x2, dispatch, recurrence + combine, final
@@ -390,7 +454,8 @@ def main():
     if args.only:
         run = {'c3': lambda: decode_bench(layer, device, args.decode_steps), 'c4': lambda: c4_forward(device),
                'c5': lambda: c5_training(device),
-               'prefill': lambda: full_layer_prefill(layer, device, batch, time_, max(3, args.steps // 4))}[args.only]
+               'prefill': lambda: full_layer_prefill(layer, device, batch, time_, max(3, args.steps // 4)),
+               'lm': lambda: whole_model(device, args.lm_context)}[args.only]
         progress('workload', args.only)
         print(json.dumps({'workload': args.only, 'result': run()}), flush=True)
         return
@@ -463,6 +528,8 @@ def main():
         result['forward_c4'] = c4_forward(device)
         progress('training C5')
         result['training_c5'] = c5_training(device)
+        progress('whole model L16/D2048', args.lm_context)
+        result['whole_model'] = whole_model(device, args.lm_context)
     progress('copy probe')
     result['hbm_copy_GBps'] = round(copy_probe(device), 1)
     if args.cpu_tokens > 0:

@@ -300,6 +300,22 @@ int bdm_bank_occupancy(const void *write_weights, int32_t weight_dtype, const ui
 int bdm_written_bank_curve(const int32_t *first_write, int64_t batch, int32_t bank_count,
                            const int64_t *prefixes, int32_t prefix_count, int32_t *written, void *stream);
 
+/* RMSNorm of the language-model shell (implementation/bdm/_shell.py:29-35,
+ * RMSNorm.forward): out = (x * rsqrt(mean(x^2) + eps)) * weight, in FP32,
+ * rounded once to dtype.  x, out [rows, width] of dtype (BDM_BF16 or
+ * BDM_F32); weight [width] of weight_dtype.  With residual non-null the
+ * block's residual add comes first (model.py:174-176): sum_out = round(x +
+ * residual) is written and normalized.  width: a multiple of 8, at most 8192. */
+int bdm_rms_norm(const void *x, const void *residual, const void *weight, void *sum_out, void *out,
+                 int64_t rows, int32_t width, int32_t dtype, int32_t weight_dtype, float eps, void *stream);
+
+/* SwiGLU of the shell's feed-forward (_shell.py:86-91, FeedForward._forward:
+ * silu(w1 x) * w3 x) applied to the output of one GEMM with the concatenated
+ * weights [w1; w3]: gate_up [rows, 2*hidden] (x1 in the first hidden columns,
+ * x3 in the rest), out [rows, hidden] = round(round(silu(x1)) * x3), the
+ * roundings torch makes in dtype.  hidden: a multiple of 8. */
+int bdm_swiglu(const void *gate_up, void *out, int64_t rows, int32_t hidden, int32_t dtype, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

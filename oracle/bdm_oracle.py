@@ -667,3 +667,107 @@ def written_bank_curve(indices: Tensor, banks: int, prefixes, valid: Tensor | No
     first = first_write_positions(indices, banks, valid).to(torch.int64)
     ends = torch.as_tensor(prefixes, dtype=torch.int64).view(1, 1, -1)
     return (first[..., None] < ends).sum(1).to(torch.int32)
+
+
+# ---------------------------------------------------------------------------
+# language-model shell (model.py:143-216, _shell.py:10-118)
+
+class OracleRMSNorm(nn.Module):
+    """_shell.py:10-35: FP32 x * rsqrt(mean(x^2) + eps) * weight, cast back."""
+
+    def __init__(self, dim: int, eps: float):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(dim))
+
+    def forward(self, x: Tensor) -> Tensor:
+        out = x.float() * torch.rsqrt((x.float() * x.float()).mean(-1, keepdim=True) + self.eps)
+        return (out * self.weight.float()).type_as(x)
+
+
+class OracleFeedForward(nn.Module):
+    """_shell.py:37-118: hidden = multiple_of * ceil(int(2 * 4d / 3) / multiple_of),
+    w2(silu(w1 x) * w3 x), truncated-normal init with stds d^-1/2 and hidden^-1/2."""
+
+    def __init__(self, dim: int, multiple_of: int):
+        super().__init__()
+        hidden = int(2 * (4 * dim) / 3)
+        hidden = multiple_of * ((hidden + multiple_of - 1) // multiple_of)
+        self.dim, self.hidden_dim = dim, hidden
+        self.w1 = nn.Linear(dim, hidden, bias=False)
+        self.w3 = nn.Linear(dim, hidden, bias=False)
+        self.w2 = nn.Linear(hidden, dim, bias=False)
+
+    @torch.no_grad()
+    def reset(self):
+        s_in, s_out = self.dim ** -0.5, self.hidden_dim ** -0.5
+        for w in (self.w1, self.w3):
+            nn.init.trunc_normal_(w.weight, mean=0.0, std=s_in, a=-3 * s_in, b=3 * s_in)
+        nn.init.trunc_normal_(self.w2.weight, mean=0.0, std=s_out, a=-3 * s_out, b=3 * s_out)
+
+    def forward(self, x: Tensor) -> Tensor:
+        return self.w2(F.silu(self.w1(x)) * self.w3(x))
+
+
+class OracleBlock(nn.Module):
+    def __init__(self, memory, index: int, seed: int, multiple_of: int):
+        super().__init__()
+        self.attention = OracleBankedDeltaMemory(memory, layer_id=index, seed=seed)
+        self.feed_forward = OracleFeedForward(memory.dim, multiple_of)
+        self.attention_norm = OracleRMSNorm(memory.dim, memory.norm_eps)
+        self.ffn_norm = OracleRMSNorm(memory.dim, memory.norm_eps)
+
+
+class OracleLanguageModel(nn.Module):
+    """BDMLanguageModel (model.py:179-216): embeddings, pre-norm blocks of
+    memory layer + SwiGLU, final RMSNorm, untied head.  Seeds: embeddings and
+    head from manual_seed(100000 s + 100) in that order, block i's
+    feed-forward from manual_seed(100000 s + 1000 + i), the memory layers from
+    their role generators."""
+
+    def __init__(self, memory, *, vocab_size: int, layers: int, multiple_of: int = 256, seed: int = 0):
+        super().__init__()
+        d = memory.dim
+        self.layers = nn.ModuleList([OracleBlock(memory, i, seed, multiple_of) for i in range(layers)])
+        self.tok_embeddings = nn.Embedding(vocab_size, d)
+        self.norm = OracleRMSNorm(d, memory.norm_eps)
+        self.output = nn.Linear(d, vocab_size, bias=False)
+        base, std = seed * 100_000, d ** -0.5
+        with torch.no_grad(), torch.random.fork_rng(devices=[]):
+            torch.manual_seed(base + 100)
+            for p in (self.tok_embeddings.weight, self.output.weight):
+                nn.init.trunc_normal_(p, mean=0, std=std, a=-3 * std, b=3 * std)
+        for i, block in enumerate(self.layers):
+            with torch.random.fork_rng(devices=[]):
+                torch.manual_seed(base + 1000 + i)
+                block.feed_forward.reset()
+
+    def forward(self, tokens: Tensor, target: Tensor | None = None):
+        hidden = self.tok_embeddings(tokens)
+        for block in self.layers:
+            hidden = hidden + block.attention(block.attention_norm(hidden))
+            hidden = hidden + block.feed_forward(block.ffn_norm(hidden))
+        logits = self.output(self.norm(hidden))
+        if target is not None:
+            return F.cross_entropy(logits.float().flatten(0, -2), target.flatten())
+        return logits
+
+    def prefill(self, tokens: Tensor, caches=None):
+        """perf_inference_case.py:26-56: per-block attention.prefill on its own
+        cache; logits of the last position."""
+        caches = list(caches) if caches is not None else [None] * len(self.layers)
+        hidden = self.tok_embeddings(tokens)
+        for i, block in enumerate(self.layers):
+            out, caches[i] = block.attention.prefill(block.attention_norm(hidden), caches[i])
+            hidden = hidden + out
+            hidden = hidden + block.feed_forward(block.ffn_norm(hidden))
+        return self.output(self.norm(hidden[:, -1:])), caches
+
+    def step(self, tokens: Tensor, caches):
+        caches = list(caches)
+        hidden = self.tok_embeddings(tokens)
+        for i, block in enumerate(self.layers):
+            out, caches[i] = block.attention.step(block.attention_norm(hidden), caches[i])
+            hidden = hidden + out
+            hidden = hidden + block.feed_forward(block.ffn_norm(hidden))
+        return self.output(self.norm(hidden)), caches

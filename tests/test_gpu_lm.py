@@ -1,0 +1,143 @@
+"""The language-model shell on the GPU.
+
+* ``bdm_rms_norm`` and ``bdm_swiglu`` against torch's FP32 formulas of
+  _shell.py:29-35 and :86-91 (tolerances in each test).
+* The whole model (FP32 weights) against the reference's logits, loss and
+  gradients in tests/golden/lm_small.pt.
+* Stateful inference: ``prefill`` then ``step`` against the oracle shell's,
+  FP32 weights and caches (routes on FP32 scores have no near-ties).
+"""
+
+import os
+import sys
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from _inputs import rel_err
+from conftest import ROOT
+from oracle import bdm_oracle as O
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(ROOT, 'tests', 'golden', 'lm_small.pt')
+
+
+def announce(*what):
+    print('CASE', *what, flush=True)
+    sys.stdout.flush()
+
+
+def close_rows(out, ref, dtype):
+    """BF16: each element within one BF16 ulp of torch's (ulp <= 2^-7 of the
+    value); FP32: within 1e-5 relative."""
+    tol = 2 ** -7 if dtype == torch.bfloat16 else 1e-5
+    return float(((out.float() - ref.float()).abs() / ref.float().abs().clamp_min(1e-3)).max()) <= tol
+
+
+def torch_rms(x, weight, eps):
+    out = x.float() * torch.rsqrt((x.float() * x.float()).mean(-1, keepdim=True) + eps)
+    return (out * weight.float()).to(x.dtype)
+
+
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float32], ids=['bf16', 'f32'])
+@pytest.mark.parametrize('width', [32, 520, 2048, 5120])
+def test_rms_norm_matches_torch(device, dtype, width):
+    """FP32 sums in another order: BF16 results within one ulp, FP32 within
+    1e-5 relative; the residual sum is exact (one rounding)."""
+    from bdm_amd import ops
+    gen = torch.Generator().manual_seed(width)
+    x = (torch.randn(37, width, generator=gen) * 3).to(dtype).to(device)
+    r = torch.randn(37, width, generator=gen).to(dtype).to(device)
+    weight = (1 + 0.1 * torch.randn(width, generator=gen)).to(device)
+    announce('rms_norm', dtype, width)
+    for wdt in (torch.float32, torch.bfloat16):
+        w = weight.to(wdt)
+        out = ops.rms_norm(x, w, 1e-5)
+        ref = torch_rms(x, w, 1e-5)
+        assert close_rows(out, ref, dtype)
+        total, normed = ops.rms_norm(x, w, 1e-5, residual=r)
+        assert torch.equal(total, r + x)
+        ref = torch_rms(r + x, w, 1e-5)
+        assert close_rows(normed, ref, dtype)
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float32], ids=['bf16', 'f32'])
+def test_swiglu_matches_torch(device, dtype):
+    """silu(x1) * x3 with torch's rounding points: BF16 equal but for
+    one-ulp exp differences (checked as at most 1 % of elements, each within
+    one ulp), FP32 within 1e-6."""
+    from bdm_amd import ops
+    gen = torch.Generator().manual_seed(5)
+    hidden = 5632
+    gate_up = (torch.randn(19, 2 * hidden, generator=gen) * 4).to(dtype).to(device)
+    announce('swiglu', dtype)
+    out = ops.swiglu(gate_up, hidden)
+    ref = F.silu(gate_up[:, :hidden]) * gate_up[:, hidden:]
+    torch.cuda.synchronize()
+    if dtype == torch.float32:
+        assert rel_err(out, ref) < 1e-6
+    else:
+        diff = (out.float() - ref.float()).abs()
+        ulp = ref.float().abs() * 2 ** -7
+        assert bool((diff <= ulp).all())
+        assert float((diff > 0).float().mean()) < 0.01
+
+
+def _golden_model(device):
+    from bdm_amd import BSDMConfig
+    from bdm_amd.lm import BDMLanguageModel, LanguageModelConfig
+    golden = torch.load(GOLDEN, weights_only=True)
+    dim, j, s, k, v, h, vocab, layers, multiple, seed = golden['geometry'].tolist()
+    memory = BSDMConfig(dim=dim, bank_count=j, bank_size=s, selected_banks=k, value_width=v, num_heads=h)
+    config = LanguageModelConfig(memory=memory, vocab_size=vocab, layers=layers, ffn_multiple_of=multiple,
+                                 seed=seed)
+    model = BDMLanguageModel(config)
+    model.load_state_dict(golden['state'])
+    return golden, memory, config, model.to(device)
+
+
+def test_lm_matches_reference_fixture(device):
+    """FP32 weights; the layer rounds its training state to BF16 every 16
+    events as the reference does.  Logits within 1e-4 of the largest, loss
+    within 1e-5, gradients of the loss within 2e-2 per tensor."""
+    golden, _, _, model = _golden_model(device)
+    tokens, target = golden['tokens'].to(device), golden['target'].to(device)
+    announce('lm fixture forward')
+    logits = model(tokens)
+    assert rel_err(logits, golden['logits']) < 1e-4, rel_err(logits, golden['logits'])
+    loss = model(tokens, target)
+    assert float(loss.detach()) == pytest.approx(float(golden['loss']), rel=1e-5)
+    announce('lm fixture backward')
+    loss.backward()
+    torch.cuda.synchronize()
+    params = dict(model.named_parameters())
+    for name, grad in golden['grads'].items():
+        assert rel_err(params[name].grad, grad) < 2e-2, (name, rel_err(params[name].grad, grad))
+
+
+def test_lm_prefill_and_step_match_oracle(device):
+    """FP32 weights and caches; our prefill (fused projections, shell
+    kernels, HIP recurrence) and steps against the oracle shell's.  Logits
+    within 1e-3 of the largest, caches within 1e-3."""
+    golden, memory, config, model = _golden_model(device)
+    oracle = O.OracleLanguageModel(memory, vocab_size=config.vocab_size, layers=config.layers,
+                                   multiple_of=config.ffn_multiple_of, seed=config.seed)
+    oracle.load_state_dict(golden['state'])
+    tokens = golden['tokens']
+    with torch.no_grad():
+        announce('lm prefill')
+        caches = [block.attention.create_state(2, dtype=torch.float32) for block in model.layers]
+        ref_caches = [block.attention.create_state(2, torch.float32) for block in oracle.layers]
+        logits, caches = model.prefill(tokens[:, :14].to(device), caches)
+        ref, ref_caches = oracle.prefill(tokens[:, :14], ref_caches)
+        assert rel_err(logits, ref) < 1e-3, rel_err(logits, ref)
+        for c, rc in zip(caches, ref_caches):
+            assert rel_err(c, rc) < 1e-3
+        for t in range(14, 18):
+            announce('lm step', t)
+            logits, caches = model.step(tokens[:, t:t + 1].to(device), caches)
+            ref, ref_caches = oracle.step(tokens[:, t:t + 1], ref_caches)
+            assert rel_err(logits, ref) < 1e-3, (t, rel_err(logits, ref))
+        torch.cuda.synchronize()

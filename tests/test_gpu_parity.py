@@ -375,10 +375,13 @@ def test_prefill_and_step_match_oracle(device):
             assert rel_err(out1, ref_out1) < 2e-2
 
 
-def test_decode_kernel_matches_oracle(device):
+@pytest.mark.parametrize('heads,v', [(3, 128), (2, 384), (1, 2048)], ids=['h3v128', 'h2v384', 'h1v2048'])
+def test_decode_kernel_matches_oracle(device, heads, v):
+    """Wide heads run as column spans (v = 384: 4 spans of 96, v = 2048: 16
+    spans of 128); the state and output must not depend on the split."""
     from bdm_amd import ops
     gen = torch.Generator().manual_seed(21)
-    batch, heads, s, v, j, kk = 6, 3, 8, 128, 64, 8
+    batch, s, j, kk = 6, 8, 64, 8
     _, ww, wi = routes(batch, 1, j, kk, gen)
     _, rw, ri = routes(batch, 1, j, kk, gen)
     ri[0, 0, :3] = wi[0, 0, :3]  # reads of banks written by the same token
@@ -404,7 +407,7 @@ def test_decode_kernel_matches_oracle(device):
             for jj in range(kk):
                 total = (total + vals[rows, order[:, jj]].float()).to(torch.bfloat16).float()
             ys.append(total)
-        announce('decode', state_dtype)
+        announce('decode', heads, v, state_dtype)
         dstate = state.to(device)
         y = ops.decode_step(*(t[:, 0].to(device) for t in (q, k, v_, g, b, w, wi, ww, ri, rw)), dstate,
                             bank_count=j, scale=s ** -0.5, routed_decay=True)
