@@ -50,6 +50,12 @@ struct ForwardParams {
     int64_t nt, time;
     int heads, s_real, width, banks, kw, kr;
     int lanes_per_head, heads_per_block;
+    // Column split of wide heads (lazy kernel): `heads` and `width` above are
+    // then virtual heads of `width` columns, `split` of them per real head;
+    // q, k, g, b rows are per real head (s_heads of them), and the state,
+    // snapshot and final-state rows of a real head are row_stride elements.
+    int split, s_heads;
+    int64_t row_stride;
     int round_interval, routed_decay;
     int snap_interval;  // events between snapshots (0: none); equals round_interval when rounding
     int init_dtype, final_dtype, snap_dtype;
@@ -513,7 +519,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         const int slot = stage % 3;
         if (stage >= nstages || !prep_head || pe >= s_n[slot]) return;
         const bool rd = (s_rmask[slot] >> pe) & 1u;
-        const int64_t row = (int64_t(s_tok[slot][pe]) * p.heads + head0 + ph) * S + 4 * half;
+        const int64_t row = (int64_t(s_tok[slot][pe]) * p.s_heads + (head0 + ph) / p.split) * S + 4 * half;
         const int route = s_route[slot][pe];
         if (rd) {
             if (tid < NE) pl.zrow = p.zslot[route];
@@ -592,7 +598,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 
     // ---- prologue: metadata of stages 0 and 1, operands of stage 0
     float h[S][CPL];
-    const int64_t state_offset = ((int64_t(bank) * p.heads + head) * S) * p.width + col0;
+    // state rows of this (bank, head, columns): a real head's S rows of
+    // row_stride elements, this virtual head's span of them
+    const int64_t head_cols = int64_t(head / p.split) * S * p.row_stride + int64_t(head % p.split) * p.width + col0;
+    const int64_t state_offset = int64_t(bank) * p.s_heads * S * p.row_stride + head_cols;
     // piece-state rows of this (piece, head): [S, v] FP32
     const int64_t pstate_offset = ((int64_t(pslot) * p.heads + head) * S) * p.width + col0;
     if (MODE == 1) {
@@ -604,7 +613,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         // M_piece, stored by piece_scan_kernel in the previous piece's slot
         load_state<S, CPL>(p.pstate, BDM_F32, pstate_offset - int64_t(p.heads) * S * p.width, p.width, S, h);
     } else {
-        load_state<S, CPL>(p.initial, p.init_dtype, bidx * p.init_bstride + state_offset, p.width, S, h);
+        load_state<S, CPL>(p.initial, p.init_dtype, bidx * p.init_bstride + state_offset, p.row_stride, S, h);
     }
     // MODE 1: lanes 0..7 of a head carry column (lane) of the piece's transition
     const int pcol = tid % p.lanes_per_head;
@@ -657,8 +666,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
             if (p.snap) {
                 // stage starts are the multiples of snap_interval = kLazyStage
                 const int64_t sslot = (start / NE) + st - 1;
-                store_state<S, CPL>(p.snap, p.snap_dtype, ((sslot * p.heads + head) * S) * p.width + col0, p.width,
-                                    S, h);
+                store_state<S, CPL>(p.snap, p.snap_dtype, sslot * p.s_heads * S * p.row_stride + head_cols,
+                                    p.row_stride, S, h);
             }
         }
 
@@ -770,8 +779,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
             for (int r = 0; r < S; ++r) pt[r * S + pcol] = pc[r];
         }
     } else if (p.final_state && piece == pieces - 1) {
-        const int64_t final_offset = bidx * (int64_t(p.banks) * p.heads * S * p.width) + state_offset;
-        store_state<S, CPL>(p.final_state, p.final_dtype, final_offset, p.width, S, h);
+        const int64_t final_offset = bidx * (int64_t(p.banks) * p.s_heads * S * p.row_stride) + state_offset;
+        store_state<S, CPL>(p.final_state, p.final_dtype, final_offset, p.row_stride, S, h);
     }
 }
 
@@ -816,7 +825,8 @@ __global__ __launch_bounds__(1024) void piece_table_kernel(const int64_t *__rest
 __global__ __launch_bounds__(256) void piece_scan_kernel(const int4 *__restrict__ items,
                                                          const int *__restrict__ n_items, const void *initial,
                                                          int init_dtype, int64_t init_bstride, int banks, int heads,
-                                                         int width, float *__restrict__ pstate,
+                                                         int width, int split, int64_t row_stride,
+                                                         float *__restrict__ pstate,
                                                          const float *__restrict__ ptrans) {
     constexpr int S = 8;
     if (int(blockIdx.x) >= n_items[0]) return;
@@ -827,11 +837,13 @@ __global__ __launch_bounds__(256) void piece_scan_kernel(const int4 *__restrict_
     const int64_t bidx = seg / banks;
     for (int c = threadIdx.x; c < width; c += blockDim.x) {
         float m[S];
-        const int64_t off = bidx * init_bstride + ((int64_t(bank) * heads + head) * S) * width + c;
+        // heads, width: virtual heads of the column split (split per real head)
+        const int64_t off = bidx * init_bstride + ((int64_t(bank) * (heads / split) + head / split) * S) * row_stride +
+                            int64_t(head % split) * width + c;
 #pragma unroll
         for (int r = 0; r < S; ++r)
-            m[r] = init_dtype == BDM_BF16 ? to_f32(static_cast<const bf16_t *>(initial)[off + int64_t(r) * width])
-                                          : static_cast<const float *>(initial)[off + int64_t(r) * width];
+            m[r] = init_dtype == BDM_BF16 ? to_f32(static_cast<const bf16_t *>(initial)[off + int64_t(r) * row_stride])
+                                          : static_cast<const float *>(initial)[off + int64_t(r) * row_stride];
         for (int q = 0; q + 1 < pieces; ++q) {
             const int64_t base = ((int64_t(slot0 + q) * heads + head) * S) * width + c;
             const float *pt = ptrans + ((int64_t(slot0 + q) * heads + head) * S) * S;
@@ -923,6 +935,17 @@ __global__ __launch_bounds__(256) void zero_fill_kernel(T *__restrict__ out, int
     if (i < count) out[i] = from_f32<T>(0.f);
 }
 
+// Virtual heads per real head on the lazy path: 1 for heads of at most 256
+// columns (4 per lane, 64 lanes); a wider head whose width is a multiple of
+// 128 runs as width/128 heads of 128 columns (value columns are independent
+// in the recurrence, and 128-column heads are the kernel's two-heads-per-wave
+// shape); 0 when neither applies.
+int lazy_split(const bdm_forward_args &a) {
+    if (a.head_width % 4 != 0) return 0;
+    if (a.head_width / 4 <= 64) return 1;
+    return a.head_width % 128 == 0 ? a.head_width / 128 : 0;
+}
+
 // Scratch of the cut-segment path, carved from the bdm_forward workspace.
 struct PieceBuffers {
     int4 *items = nullptr;
@@ -933,7 +956,8 @@ struct PieceBuffers {
 
 template <typename T, int S, int CPL, bool kLazy = false>
 int launch_forward(const bdm_forward_args &a, T *zbuf, int *zslot, const PieceBuffers &pb, hipStream_t stream) {
-    if (a.head_width / CPL > 256)
+    const int split = kLazy ? lazy_split(a) : 1;
+    if (a.head_width / split / CPL > 256)
         return fail(BDM_ERR_UNSUPPORTED, "forward: head_width %d needs more than 256 lanes", a.head_width);
     ForwardParams<T> p{};
     p.q = static_cast<const T *>(a.q);
@@ -953,18 +977,21 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, int *zslot, const PieceBu
     p.init_bstride = a.initial_batch_stride;
     p.nt = a.batch * a.time;
     p.time = a.time;
-    p.heads = a.heads;
+    p.heads = a.heads * split;
     p.s_real = a.bank_size;
-    p.width = a.head_width;
+    p.width = a.head_width / split;
+    p.split = split;
+    p.s_heads = a.heads;
+    p.row_stride = a.head_width;
     p.banks = a.bank_count;
     p.kw = a.write_banks;
     p.kr = a.read_banks;
-    p.lanes_per_head = a.head_width / CPL;
+    p.lanes_per_head = p.width / CPL;
     p.heads_per_block = 256 / p.lanes_per_head;
     // lazy kernel: 2 heads per one-wave workgroup when a head has 32 lanes, else 8 per 256 threads
     const int lazy_hb = p.lanes_per_head == 32 ? 2 : 8;
     if (kLazy && p.heads_per_block > lazy_hb) p.heads_per_block = lazy_hb;
-    if (p.heads_per_block > a.heads) p.heads_per_block = a.heads;
+    if (p.heads_per_block > p.heads) p.heads_per_block = p.heads;
     p.round_interval = a.round_interval;
     p.routed_decay = a.routed_decay;
     p.snap = a.snapshots;
@@ -976,7 +1003,7 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, int *zslot, const PieceBu
     const int64_t nseg = a.batch * a.bank_count;
     p.xcd_remap = (nseg % 8 == 0) ? 1 : 0;
     const int threads = ((p.heads_per_block * p.lanes_per_head + kWave - 1) / kWave) * kWave;
-    const dim3 grid(unsigned(nseg), unsigned((a.heads + p.heads_per_block - 1) / p.heads_per_block));
+    const dim3 grid(unsigned(nseg), unsigned((p.heads + p.heads_per_block - 1) / p.heads_per_block));
     if (a.read_banks > 0) {
         const int64_t nt = a.batch * a.time;
         const int64_t routes = nt * a.read_banks;
@@ -1002,9 +1029,9 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, int *zslot, const PieceBu
             else
                 lazy_forward_kernel<T, CPL, 8, 1><<<pgrid, lthreads, 0, stream>>>(p);
             if (int rc = check_launch("lazy_forward_kernel")) return rc;
-            piece_scan_kernel<<<dim3(unsigned(pb.max_pieces), unsigned(a.heads)), 128, 0, stream>>>(
-                pb.items, pb.count, a.initial, a.initial_dtype, a.initial_batch_stride, a.bank_count, a.heads,
-                a.head_width, pb.pstate, pb.ptrans);
+            piece_scan_kernel<<<dim3(unsigned(pb.max_pieces), unsigned(p.heads)), 128, 0, stream>>>(
+                pb.items, pb.count, a.initial, a.initial_dtype, a.initial_batch_stride, a.bank_count, p.heads,
+                p.width, p.split, p.row_stride, pb.pstate, pb.ptrans);
             if (int rc = check_launch("piece_scan_kernel")) return rc;
             const dim3 g2(unsigned(nseg + pb.max_pieces), grid.y);
             if (lazy_hb == 2)
@@ -1056,8 +1083,7 @@ bool lazy_path(const bdm_forward_args &a) {
     const int fold = a.round_interval > 0 ? a.round_interval : (a.snapshots ? a.snapshot_interval : kLazyStage);
     const int64_t nt = a.batch * a.time;
     const bool small_index = nt * (a.write_banks > a.read_banks ? a.write_banks : a.read_banks) < INT32_MAX;
-    return vec && a.bank_size == 8 && a.head_width % 4 == 0 && a.head_width / 4 <= 64 && fold == kLazyStage &&
-           small_index;
+    return vec && a.bank_size == 8 && lazy_split(a) > 0 && fold == kLazyStage && small_index;
 }
 
 // Upper bound on the pieces of cut segments (0: the path is off).  It is
@@ -1112,8 +1138,9 @@ static size_t forward_zslot_bytes(const bdm_forward_args *a) {
 static size_t forward_piece_bytes(const bdm_forward_args *a) {
     const size_t n = size_t(bdm::max_pieces(*a));
     if (!n) return 0;
+    // transitions per virtual head of the column split
     return round256(n * sizeof(int4)) + 256 + round256(n * a->heads * 8 * size_t(a->head_width) * 4) +
-           round256(n * a->heads * 64 * 4);
+           round256(n * a->heads * size_t(bdm::lazy_split(*a)) * 64 * 4);
 }
 
 extern "C" size_t bdm_forward_workspace_size(const bdm_forward_args *a) {

@@ -111,6 +111,9 @@ FORWARD_CASES = [
     (1, 60, 4, 8, 128, 256, 8, torch.bfloat16, True, torch.bfloat16),
     (1, 30, 1, 32, 8, 16, 4, torch.bfloat16, True, torch.bfloat16),
     (3, 17, 2, 8, 12, 16, 4, torch.bfloat16, True, torch.bfloat16),
+    # heads wider than 256 columns run as 128-column virtual heads on the S = 8 path
+    (1, 40, 1, 8, 2048, 16, 4, torch.bfloat16, True, torch.bfloat16),
+    (2, 36, 2, 8, 384, 16, 4, torch.bfloat16, True, torch.float32),
 ]
 
 
@@ -173,16 +176,18 @@ def test_forward_long_read_runs_match_oracle(device, state_dtype):
     assert rel_err(final, ref_final) < TOL, rel_err(final, ref_final)
 
 
+@pytest.mark.parametrize('heads,v', [(2, 128), (1, 512)], ids=['h2v128', 'h1v512'])
 @pytest.mark.parametrize('decay', ['mild', 'strong'])
-def test_forward_cut_segments_match_oracle(device, decay):
+def test_forward_cut_segments_match_oracle(device, decay, heads, v):
     """Prefill policy (no rounding inside the recurrence): segments longer
     than the piece length (512 events) run as pieces whose affine summaries
     are composed; every read and every final state must equal the per-event
     oracle.  4 banks, one write and one read bank per token, T = 1100, so a
-    segment holds about 550 events, cut into 2 pieces (3 for the hottest)."""
+    segment holds about 550 events, cut into 2 pieces (3 for the hottest).
+    v = 512 runs as four 128-column virtual heads."""
     from bdm_amd import ops
     gen = torch.Generator().manual_seed(91)
-    batch, time, heads, s, v, j = 2, 1100, 2, 8, 128, 4
+    batch, time, s, j = 2, 1100, 8, 4
     wi = torch.randint(0, j, (batch, time, 1), generator=gen)
     wi[0, :400] = 0  # bank 0 of sequence 0 gets the most events
     ri = torch.randint(0, j, (batch, time, 1), generator=gen)
@@ -196,7 +201,7 @@ def test_forward_cut_segments_match_oracle(device, decay):
     ref, ref_final = oracle_reads(q, k, v_, g, b, w, wi, ww, ri, rw, state, j, routed_decay=True,
                                   state_dtype=torch.float32, interval=16, return_final=True)
     dev = [x.to(device) for x in (q, k, v_, g, b, w, wi, ww, ri, rw, state)]
-    announce('forward cut segments', decay)
+    announce('forward cut segments', decay, heads, v)
     meta = ops.dispatch_build(dev[6], dev[8], j)
     lengths = (meta.cu_seqlens[1:] - meta.cu_seqlens[:-1]).cpu()
     assert int(lengths.max()) > 1024 and int((lengths > 512).sum()) >= 4  # several cut segments, one in 3 pieces
