@@ -10,7 +10,7 @@ graph).  Kernels live in ``libbdm_hip.so``.
 """
 
 from .config import BDMConfig, BSDMConfig, near_square_factors, replay_interval
-from .graphs import GraphDecoder
+from .graphs import GraphDecoder, LanguageModelGraphDecoder
 from .model import BankedDeltaMemory
 from .occupancy import bank_occupancy, written_banks
 from .routed_update import bank_training, role_bank_training
@@ -19,5 +19,6 @@ from .routing import SharedResidualRouter, product_key_route
 BlockSparseDeltaMemory = BankedDeltaMemory
 
 __all__ = ['BDMConfig', 'BSDMConfig', 'BankedDeltaMemory', 'BlockSparseDeltaMemory', 'GraphDecoder',
+           'LanguageModelGraphDecoder',
            'SharedResidualRouter', 'bank_occupancy', 'bank_training', 'role_bank_training', 'product_key_route',
            'near_square_factors', 'replay_interval', 'written_banks']

@@ -58,3 +58,48 @@ class GraphDecoder:
         self.input.copy_(x)
         self.graph.replay()
         return self.output
+
+
+class LanguageModelGraphDecoder:
+    """Replays a whole ``BDMLanguageModel.step`` (embedding, every block's
+    norms, memory-layer step and feed-forward, final norm and the vocabulary
+    head) from one HIP graph.
+
+    The reference times this loop eagerly under torch.compile
+    (reproduction/experiments/perf_inference_case.py:140-160); here the ~250
+    kernels of one token are recorded once.  ``caches`` (one per layer, from
+    ``model.prefill``) are advanced in place by every replay.  ``step(tokens)``
+    copies ``tokens`` [batch, 1] into the static input, replays, and returns
+    the static logits [batch, 1, vocab], overwritten by the next call.
+    """
+
+    def __init__(self, model, caches, *, warmup: int = 2) -> None:
+        if not caches or any(c is None or not c.is_cuda for c in caches):
+            raise ValueError('LanguageModelGraphDecoder needs the per-layer caches on a ROCm device')
+        self.model = model
+        self.caches = list(caches)
+        device = self.caches[0].device
+        batch = self.caches[0].shape[0]
+        self.input = torch.zeros(batch, 1, device=device, dtype=torch.long)
+        side = torch.cuda.Stream(device)
+        side.wait_stream(torch.cuda.current_stream(device))
+        with torch.no_grad():
+            scratch = [c.clone() for c in self.caches]
+            with torch.cuda.stream(side):
+                for _ in range(warmup):
+                    model.step(self.input, scratch)
+            torch.cuda.current_stream(device).wait_stream(side)
+            torch.cuda.synchronize(device)
+            del scratch
+            self.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.stream(side):
+                with torch.cuda.graph(self.graph, stream=side):
+                    self.output, _ = model.step(self.input, self.caches)
+            torch.cuda.current_stream(device).wait_stream(side)
+
+    def step(self, tokens: Tensor) -> Tensor:
+        if tuple(tokens.shape) != tuple(self.input.shape):
+            raise ValueError(f'tokens must be {tuple(self.input.shape)}')
+        self.input.copy_(tokens)
+        self.graph.replay()
+        return self.output

@@ -258,6 +258,34 @@ H200_PREFILL_SECONDS = {8192: 0.0504, 65536: 0.3757, 1048576: 6.709}
 H200_DECODE_MS = {8192: 2.523}
 
 
+def lm_graph_decode(model, tokens, caches, pos, count):
+    """Whole-model decode replayed from one HIP graph
+    (bdm_amd.LanguageModelGraphDecoder).  The replays of the first 4 tokens
+    are checked against eager steps on a copy of the caches (logits and caches
+    identical), then `count` more replays are timed.  Returns (ms per token or
+    None, check result)."""
+    import torch
+    from bdm_amd import LanguageModelGraphDecoder
+    try:
+        eager = [c.clone() for c in caches]
+        decoder = LanguageModelGraphDecoder(model, caches)
+        for i in range(4):
+            want, eager = model.step(tokens[:, pos + i:pos + i + 1], eager)
+            if not torch.equal(decoder.step(tokens[:, pos + i:pos + i + 1]), want):
+                return None, f'graph replay differs from the eager step {i}'
+        if not all(torch.equal(a, b) for a, b in zip(decoder.caches, eager)):
+            return None, 'graph replays leave different caches'
+        del eager
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(count):
+            decoder.step(tokens[:, pos + 4 + i:pos + 5 + i])
+        torch.cuda.synchronize()
+        return round((time.perf_counter() - t0) * 1e3 / count, 3), 'replays equal the eager steps'
+    except RuntimeError as exc:  # a step that cannot be captured is reported, not hidden
+        return None, f'capture failed: {str(exc)[:120]}'
+
+
 def whole_model(device, context, timed_runs=3, decode_tokens=16):
     """The reference's whole-model inference case (perf_inference_case.py:15-56,
     80-160): BDMLanguageModel L16/D2048/FFN5632, vocab 50,257, one head of width
@@ -276,7 +304,7 @@ def whole_model(device, context, timed_runs=3, decode_tokens=16):
         model = BDMLanguageModel(config)
     model = model.to(torch.bfloat16).eval()
     gen = torch.Generator().manual_seed(5)
-    tokens = torch.randint(0, config.vocab_size, (1, context + 64), generator=gen).to(device)
+    tokens = torch.randint(0, config.vocab_size, (1, context + 128), generator=gen).to(device)
     prompt = tokens[:, :context]
     samples = []
     with torch.inference_mode():
@@ -298,16 +326,20 @@ def whole_model(device, context, timed_runs=3, decode_tokens=16):
             logits, caches = model.step(tokens[:, pos:pos + 1], caches)
         torch.cuda.synchronize()
         decode_ms = (time.perf_counter() - t0) * 1e3 / decode_tokens
+        graph_ms, graph_check = lm_graph_decode(model, tokens, caches, context + 4 + decode_tokens, decode_tokens)
     prefill_s = statistics.mean(samples)
     out = {'context': context, 'layers': 16, 'd_model': 2048, 'ffn': model.layers[0].feed_forward.hidden_dim,
            'bank_count': memory.bank_count, 'prefill_seconds': round(prefill_s, 5),
            'prefill_tokens_per_s': round(context / prefill_s, 1), 'decode_ms_per_token_eager': round(decode_ms, 3),
+           'decode_ms_per_token_graph': graph_ms, 'decode_graph_check': graph_check,
            'cache_bytes': sum(c.numel() * c.element_size() for c in caches)}
     if context in H200_PREFILL_SECONDS:
         out['h200_prefill_seconds'] = H200_PREFILL_SECONDS[context]
         out['prefill_speedup_vs_h200'] = round(H200_PREFILL_SECONDS[context] / prefill_s, 3)
     if context in H200_DECODE_MS:
         out['h200_decode_ms_per_token'] = H200_DECODE_MS[context]
+        if graph_ms:
+            out['decode_speedup_vs_h200'] = round(H200_DECODE_MS[context] / graph_ms, 3)
     del model, caches
     torch.cuda.empty_cache()
     return out

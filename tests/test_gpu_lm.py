@@ -141,3 +141,30 @@ def test_lm_prefill_and_step_match_oracle(device):
             ref, ref_caches = oracle.step(tokens[:, t:t + 1], ref_caches)
             assert rel_err(logits, ref) < 1e-3, (t, rel_err(logits, ref))
         torch.cuda.synchronize()
+
+
+def test_lm_graph_decoder_matches_eager_steps(device):
+    """The whole model's decode step replayed from one HIP graph equals the
+    eager steps bit for bit, logits and every layer's cache, with unrelated
+    eager work and synchronizations between replays."""
+    from bdm_amd import LanguageModelGraphDecoder
+    golden, _, _, model = _golden_model(device)
+    model = model.to(torch.bfloat16)
+    tokens = golden['tokens'].to(device)
+    announce('lm graph decoder')
+    with torch.no_grad():
+        _, caches = model.prefill(tokens[:, :10])
+        eager = [c.clone() for c in caches]
+        graph = [c.clone() for c in caches]
+        decoder = LanguageModelGraphDecoder(model, graph)
+        for a, b in zip(graph, caches):
+            assert torch.equal(a, b)  # building the graph leaves the caches untouched
+        noise = torch.randn(1 << 20, device=device)
+        for t in range(10, 18):
+            want, eager = model.step(tokens[:, t:t + 1], eager)
+            got = decoder.step(tokens[:, t:t + 1])
+            assert torch.equal(got, want), t
+            for a, b in zip(graph, eager):
+                assert torch.equal(a, b), t
+            noise.mul_(0.5).add_(1.0)
+            torch.cuda.synchronize()
