@@ -25,6 +25,7 @@ EXPORTED_SYMBOLS = (
     'bdm_written_bank_curve',
     'bdm_rms_norm',
     'bdm_swiglu',
+    'bdm_gemv',
 )
 
 _i32, _i64, _f32, _vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
@@ -138,6 +139,8 @@ def library() -> ctypes.CDLL:
     lib.bdm_rms_norm.restype = _i32
     lib.bdm_swiglu.argtypes = [_vp, _vp, _i64, _i32, _i32, _vp]
     lib.bdm_swiglu.restype = _i32
+    lib.bdm_gemv.argtypes = [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp]
+    lib.bdm_gemv.restype = _i32
     return lib
 
 

@@ -105,8 +105,8 @@ class FeedForward(nn.Module):
 
     def forward(self, x: Tensor) -> Tensor:
         if not torch.is_grad_enabled() and x.is_cuda and self.hidden_dim % 8 == 0:
-            gated = ops.swiglu(F.linear(x, self._fused_input_weight()), self.hidden_dim)
-            return self.w2(gated)
+            gated = ops.swiglu(ops.linear(x, self._fused_input_weight()), self.hidden_dim)
+            return ops.linear(gated, self.w2.weight)
         if (self.recompute_activations and torch.is_grad_enabled() and x.is_cuda and x.dtype == torch.bfloat16
                 and x.numel() // self.dim >= 1024):
             return torch.utils.checkpoint.checkpoint(self._forward, x, use_reentrant=False,
@@ -215,7 +215,7 @@ class BDMLanguageModel(nn.Module):
             hidden, normed = block.ffn_norm.add_norm(out, hidden)
             after = self.layers[i + 1].attention_norm if i + 1 < len(self.layers) else self.norm
             hidden, normed = after.add_norm(block.feed_forward(normed), hidden)
-        return self.output(normed[:, -1:]), caches
+        return ops.linear(normed[:, -1:], self.output.weight), caches
 
 
 BSDMLanguageModel = BDMLanguageModel

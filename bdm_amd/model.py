@@ -229,9 +229,9 @@ class BankedDeltaMemory(nn.Module):
         one projection GEMM and the controller epilogue (heads.py:11-22)."""
         weight, bias, cols = self._fused_weights()
         lead = hidden.shape[:-1]
-        proj = F.linear(hidden.reshape(-1, self.hidden_size), weight, bias)
+        proj = ops.linear(hidden.reshape(-1, self.hidden_size), weight, bias)
         hv, rw = self.head_value_width, self.factor_route_width
-        f = F.linear(proj[:, cols['f']:cols['f'] + hv], self.f_proj[1].weight)
+        f = ops.linear(proj[:, cols['f']:cols['f'] + hv], self.f_proj[1].weight)
         q, k, v, g, b, w = ops.controller_epilogue(proj, f, cols, self.A_log, self.dt_bias, heads=self.num_heads,
                                                    bank_size=self.bank_size, head_width=hv,
                                                    qk_norm=self.config.qk_normalization)
@@ -262,7 +262,7 @@ class BankedDeltaMemory(nn.Module):
         normalized = ops.output_epilogue(raw.reshape(-1, self.value_width), gate, self.output_norm_weight,
                                          self.output_norm_bias if layer else None, eps=self.norm_eps,
                                          kind='layer' if layer else 'rms')
-        return self.o_proj(normalized).view(*raw.shape[:-1], -1)
+        return ops.linear(normalized, self.o_proj.weight, self.o_proj.bias).view(*raw.shape[:-1], -1)
 
     def _project_bank_output(self, hidden: Tensor, raw: Tensor) -> Tensor:
         """LN (or RMS) x sigmoid gate -> o_proj (_parameters.py:222-232)."""
@@ -322,9 +322,13 @@ class BankedDeltaMemory(nn.Module):
             raise ValueError('cache dtype must be FP32 or BF16')
         with torch.no_grad():
             total = (self.initial_row_factor[:, None, :] + self.initial_column_factor[None, :, :])
-            initial = total.to(self.initial_row_factor.dtype).float().to(dtype)
-            initial = initial.reshape(self._cache_shape(1)[1:])
-            return initial.unsqueeze(0).repeat(batch, *([1] * initial.ndim)).contiguous()
+            # the sum is in parameter dtype; widening BF16 to FP32 and back is
+            # exact, so only a change of dtype converts
+            initial = total if total.dtype == dtype else total.float().to(dtype)
+            initial = initial.reshape(self._cache_shape(1)[1:]).unsqueeze(0)
+            if batch == 1:
+                return initial.contiguous()
+            return initial.expand(batch, *initial.shape[1:]).contiguous()
 
     def prefill(self, hidden: Tensor, state: Tensor | None = None, *, state_dtype=None):
         """Process a prefix; BF16 cache storage (the default) rounds at handoff.

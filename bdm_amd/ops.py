@@ -12,6 +12,7 @@ import ctypes
 from dataclasses import dataclass
 
 import torch
+import torch.nn.functional as F
 
 from . import _lib
 from .config import near_square_factors
@@ -431,6 +432,44 @@ def output_epilogue(raw: Tensor, gate: Tensor, weight: Tensor, bias: Tensor | No
     args.eps = float(eps)
     _lib.check(_lib.library().bdm_output_epilogue(ctypes.byref(args), _stream(raw.device)), 'bdm_output_epilogue')
     return out
+
+
+# ---------------------------------------------------------------------------
+# skinny linear maps (decode)
+
+GEMV_MAX_ROWS = 4
+
+
+def gemv_supported(x: Tensor, weight: Tensor, bias: Tensor | None) -> bool:
+    rows = x.numel() // max(x.shape[-1], 1)
+    return (x.is_cuda and 1 <= rows <= GEMV_MAX_ROWS and x.dtype in (torch.bfloat16, torch.float32)
+            and weight.dtype == x.dtype and weight.ndim == 2 and weight.is_contiguous()
+            and x.shape[-1] == weight.shape[1] and x.shape[-1] % 8 == 0 and weight.data_ptr() % 16 == 0
+            and (bias is None or (bias.dtype == x.dtype and bias.shape == (weight.shape[0],))))
+
+
+def gemv(x: Tensor, weight: Tensor, bias: Tensor | None = None) -> Tensor:
+    """F.linear(x, weight, bias) for 1 to 4 rows of x, streaming the weight
+    once at HBM bandwidth (FP32 accumulation, one rounding)."""
+    _require_gpu(x, weight, bias)
+    if not gemv_supported(x, weight, bias):
+        raise ValueError('gemv takes 1-4 BF16/FP32 rows, a contiguous aligned [N, K] weight and K % 8 == 0')
+    lead, k = x.shape[:-1], x.shape[-1]
+    rows, n = x.numel() // k, weight.shape[0]
+    x2 = _aligned(x.reshape(rows, k))
+    b = None if bias is None else bias.contiguous()
+    y = torch.empty(rows, n, device=x.device, dtype=x.dtype)
+    _lib.check(_lib.library().bdm_gemv(_ptr(x2), _ptr(weight), _ptr(b), _ptr(y), rows, n, k,
+                                       _dtype_code(x.dtype), _stream(x.device)), 'bdm_gemv')
+    return y.view(*lead, n)
+
+
+def linear(x: Tensor, weight: Tensor, bias: Tensor | None = None) -> Tensor:
+    """Inference F.linear: the HBM-streaming GEMV for the few rows of a
+    decode step, the library GEMM otherwise (and under autograd)."""
+    if not torch.is_grad_enabled() and gemv_supported(x, weight, bias):
+        return gemv(x, weight, bias)
+    return F.linear(x, weight, bias)
 
 
 # ---------------------------------------------------------------------------

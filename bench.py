@@ -39,6 +39,7 @@ import math
 import os
 import statistics
 import sys
+import tempfile
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -303,6 +304,13 @@ def whole_model(device, context, timed_runs=3, decode_tokens=16):
     with torch.device(device):
         model = BDMLanguageModel(config)
     model = model.to(torch.bfloat16).eval()
+    # GEMM selection by measurement (PyTorch TunableOp over the hipBLASLt and
+    # rocBLAS solutions): each shape is tuned on its first call, in the warmup
+    tunable = torch.cuda.tunable
+    tunable.enable(True)
+    tunable.tuning_enable(True)
+    tunable.set_max_tuning_duration(30)
+    tunable.set_filename(os.path.join(tempfile.gettempdir(), f'bdm_tunableop_{os.getpid()}_%d.csv'))
     gen = torch.Generator().manual_seed(5)
     tokens = torch.randint(0, config.vocab_size, (1, context + 128), generator=gen).to(device)
     prompt = tokens[:, :context]
@@ -313,8 +321,12 @@ def whole_model(device, context, timed_runs=3, decode_tokens=16):
             t0 = time.perf_counter()
             logits, caches = model.prefill(prompt)
             torch.cuda.synchronize()
-            if i:  # the first run warms up the GEMM and kernel caches
+            if i:  # the first run warms up (and tunes) the GEMMs and kernel caches
                 samples.append(time.perf_counter() - t0)
+            else:
+                for j in range(2):  # tune the decode shapes too, then only look up
+                    model.step(tokens[:, context + 100 + j:context + 101 + j], [c.clone() for c in caches])
+                tunable.tuning_enable(False)
         if not bool(torch.isfinite(logits).all()):
             raise RuntimeError('whole-model prefill produced non-finite logits')
         for i in range(4):
@@ -340,6 +352,8 @@ def whole_model(device, context, timed_runs=3, decode_tokens=16):
         out['h200_decode_ms_per_token'] = H200_DECODE_MS[context]
         if graph_ms:
             out['decode_speedup_vs_h200'] = round(H200_DECODE_MS[context] / graph_ms, 3)
+    out['gemm_selection'] = 'PyTorch TunableOp (hipBLASLt and rocBLAS solutions, tuned in the warmup run)'
+    tunable.enable(False)
     del model, caches
     torch.cuda.empty_cache()
     return out

@@ -316,6 +316,15 @@ int bdm_rms_norm(const void *x, const void *residual, const void *weight, void *
  * roundings torch makes in dtype.  hidden: a multiple of 8. */
 int bdm_swiglu(const void *gate_up, void *out, int64_t rows, int32_t hidden, int32_t dtype, void *stream);
 
+/* y[m] = W x[m] + bias for the few rows of a decode step: torch's F.linear
+ * (nn.Linear.forward, used by every projection of implementation/bdm/
+ * _parameters.py:189-232 and _shell.py:86-91) when the batch of rows is 1 to
+ * 4.  x [rows, k], W [n, k] row-major, bias [n] or null, y [rows, n], all of
+ * dtype (BDM_BF16 or BDM_F32); FP32 accumulation, bias added in FP32, one
+ * rounding.  k: a multiple of 8; x and W 16-byte aligned. */
+int bdm_gemv(const void *x, const void *weight, const void *bias, void *y, int64_t rows, int64_t n, int64_t k,
+             int32_t dtype, void *stream);
+
 #ifdef __cplusplus
 }
 #endif
