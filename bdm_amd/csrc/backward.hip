@@ -1275,8 +1275,14 @@ int launch_backward(const bdm_backward_args &a, const Workspace &ws, hipStream_t
         token_vjp_kernel<T, 1><<<blocks, 256, lds, stream>>>(v);
     else if (a.head_width <= 2 * kLanes)
         token_vjp_kernel<T, 2><<<blocks, 256, lds, stream>>>(v);
-    else
+    else if (a.head_width <= 4 * kLanes)
         token_vjp_kernel<T, 4><<<blocks, 256, lds, stream>>>(v);
+    else if (a.head_width <= 8 * kLanes)
+        token_vjp_kernel<T, 8><<<blocks, 256, lds, stream>>>(v);
+    else if (a.head_width <= 16 * kLanes)
+        token_vjp_kernel<T, 16><<<blocks, 256, lds, stream>>>(v);
+    else
+        token_vjp_kernel<T, 32><<<blocks, 256, lds, stream>>>(v);
     return check_launch("token_vjp_kernel");
 }
 
@@ -1312,7 +1318,7 @@ extern "C" int bdm_backward(const bdm_backward_args *a, void *workspace, size_t 
     if (a->batch <= 0 || a->time <= 0 || a->heads <= 0 || a->bank_size <= 0 || a->head_width <= 0 ||
         a->bank_count <= 0 || a->write_banks < 0 || a->read_banks < 0 || a->write_banks + a->read_banks == 0)
         return fail(BDM_ERR_INVALID, "backward: bad geometry");
-    if (a->head_width > 4 * kLanes) return fail(BDM_ERR_UNSUPPORTED, "backward: head_width %d > 256", a->head_width);
+    if (a->head_width > 32 * kLanes) return fail(BDM_ERR_UNSUPPORTED, "backward: head_width %d > 2048", a->head_width);
     if (a->ctrl_dtype != BDM_BF16 && a->ctrl_dtype != BDM_F32)
         return fail(BDM_ERR_INVALID, "backward: ctrl dtype %d", a->ctrl_dtype);
     if ((a->initial_dtype != BDM_BF16 && a->initial_dtype != BDM_F32) ||

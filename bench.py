@@ -61,7 +61,7 @@ def parse_args():
     ap.add_argument('--cpu-tokens', type=int, default=512,
                     help='tokens of sequence 0 the CPU oracle runs (0 skips the CPU baseline)')
     ap.add_argument('--no-extras', action='store_true', help='skip the full-layer and decode measurements')
-    ap.add_argument('--only', choices=('c3', 'c4', 'c5', 'prefill', 'lm'),
+    ap.add_argument('--only', choices=('c3', 'c4', 'c5', 'prefill', 'lm', 'lm-train'),
                     help='run one named workload alone (C3 decode, C4 skewed forward, C5 training, C2 full-layer '
                          'prefill, whole-model prefill and decode) and print its figures as one JSON line; used to '
                          'profile a workload on its own')
@@ -359,6 +359,71 @@ def whole_model(device, context, timed_runs=3, decode_tokens=16):
     return out
 
 
+H200_TRAIN_MS = {8192: 342.8}  # data/training-performance.json:1640-1643
+
+
+def whole_model_training(device, context, timed_steps=3, warmup=2):
+    """One full optimizer update of the reference's training case
+    (reproduction/experiments/profile_final.py:30-80 with optim.py:7-50):
+    BDMLanguageModel L16/D2048/FFN5632, vocab 50,257, batch 1, N = T, BF16
+    weights with FP32 master copies; forward to the cross-entropy loss,
+    backward, gradient-norm clipping at 1.0, fused AdamW on the FP32 masters
+    (weight decay 0.01 except the no-decay parameters), masters copied back
+    to the BF16 weights.  Random-init weights and token ids."""
+    import torch
+    from bdm_amd import BSDMConfig
+    from bdm_amd.lm import BDMLanguageModel, LanguageModelConfig
+    memory = BSDMConfig(dim=2048, bank_count=context // 8, bank_size=8, selected_banks=8, value_width=2048,
+                        num_heads=1)
+    config = LanguageModelConfig(memory=memory, vocab_size=50257, layers=16, seed=0)
+    with torch.device(device):
+        model = BDMLanguageModel(config)
+    model = model.to(torch.bfloat16).train()
+    params = list(model.parameters())
+    masters = [torch.nn.Parameter(p.detach().float().clone()) for p in params]
+    groups = [{'params': [m for m, p in zip(masters, params) if bool(getattr(p, '_no_weight_decay', False)) == nd],
+               'weight_decay': 0.0 if nd else 0.01} for nd in (False, True)]
+    optimizer = torch.optim.AdamW(groups, lr=0.0, betas=(0.9, 0.95), eps=1e-8, fused=True)
+    gen = torch.Generator().manual_seed(7)
+    tokens = torch.randint(0, config.vocab_size, (1, context + 1), generator=gen).to(device)
+    x, y = tokens[:, :-1], tokens[:, 1:]
+
+    def step():
+        for p in params:
+            p.grad = None
+        optimizer.zero_grad(set_to_none=True)
+        loss = model(x, y)
+        loss.backward()
+        with torch.no_grad():
+            norm = torch.nn.utils.clip_grad_norm_(params, 1.0)
+            for p, m in zip(params, masters):
+                m.grad = None if p.grad is None else p.grad.float()
+            optimizer.step()
+            for p, m in zip(params, masters):
+                p.copy_(m)
+        return loss.detach(), norm
+
+    for _ in range(warmup):
+        loss, norm = step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(timed_steps):
+        loss, norm = step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / timed_steps
+    if not (math.isfinite(float(loss)) and math.isfinite(float(norm))):
+        raise RuntimeError('whole-model training produced a non-finite loss or gradient norm')
+    out = {'context': context, 'ms_per_step': round(ms, 2), 'tokens_per_s': round(context / ms * 1e3, 1),
+           'loss': round(float(loss), 4), 'grad_norm': round(float(norm), 4),
+           'peak_allocated_GiB': round(torch.cuda.max_memory_allocated() / 2 ** 30, 2)}
+    if context in H200_TRAIN_MS:
+        out['h200_ms_per_step'] = H200_TRAIN_MS[context]
+        out['speedup_vs_h200'] = round(H200_TRAIN_MS[context] / ms, 3)
+    del model, optimizer, masters, params
+    torch.cuda.empty_cache()
+    return out
+
+
 def c4_forward(device, steps=3):
     """C4: batch 4, T8192, J2048 (32x64), Zipf s=1.1 bias on the factor scores,
     hot-path prefill forward (router x2, dispatch, recurrence + combine, final
@@ -501,7 +566,8 @@ def main():
         run = {'c3': lambda: decode_bench(layer, device, args.decode_steps), 'c4': lambda: c4_forward(device),
                'c5': lambda: c5_training(device),
                'prefill': lambda: full_layer_prefill(layer, device, batch, time_, max(3, args.steps // 4)),
-               'lm': lambda: whole_model(device, args.lm_context)}[args.only]
+               'lm': lambda: whole_model(device, args.lm_context),
+               'lm-train': lambda: whole_model_training(device, args.lm_context)}[args.only]
         progress('workload', args.only)
         print(json.dumps({'workload': args.only, 'result': run()}), flush=True)
         return

@@ -54,6 +54,9 @@ CASES = [
     (1, 100, 1, 8, 128, 4, 4, True, torch.float32, torch.bfloat16),
     # 64 banks, 12 tokens: empty and 1..8-event segments
     (2, 12, 2, 8, 128, 64, 2, True, torch.bfloat16, torch.bfloat16),
+    # heads wider than 256 columns: 128-column virtual heads forward, column tiles backward
+    (1, 24, 1, 8, 2048, 8, 4, True, torch.bfloat16, torch.bfloat16),
+    (1, 20, 2, 8, 384, 16, 4, True, torch.float32, torch.bfloat16),
 ]
 
 
