@@ -848,6 +848,7 @@ struct VjpParams {
     float *dg;
     int64_t nt;
     int heads, s_real, width, kw, kr, tiles;
+    int wph;  // token_grad_kernel: waves per head (each owns 64 * CPL value columns)
     int routed_decay;
 };
 
@@ -878,11 +879,14 @@ __device__ __forceinline__ float stride8_sum(float x) {
 // role_bank_dispatch.py:99-131; sums over slots and rows are in FP32.
 template <typename T, int CPL>
 __global__ __launch_bounds__(1024) void token_grad_kernel(VjpParams<T> p) {
-    constexpr int MAXH = 16, MAXK = 8;
+    constexpr int MAXH = 16, MAXK = 8, MAXW = 16;
     __shared__ float s_route[MAXH][2 * MAXK];  // per head: d(ww) of each write slot, then d(rw)
-    __shared__ float s_wv[MAXH][MAXK];         // per head: the v,w-column part of d(ww)
+    __shared__ float s_wv[MAXW][MAXK];         // per wave: its columns' part of d(ww)
     const int64_t token = blockIdx.x;
-    const int head = threadIdx.x / kLanes, lane = threadIdx.x % kLanes;
+    const int wave = threadIdx.x / kLanes, lane = threadIdx.x % kLanes;
+    // a head's columns are split over p.wph waves; every wave of a head
+    // computes the head's S-side terms, its first wave stores them
+    const int head = wave / p.wph, hw = wave % p.wph;
     const int64_t row = token * p.heads + head;
     const int64_t wslots = p.nt * p.kw, rslots = p.nt * p.kr;
     const int j = lane >> 3, r = lane & 7;
@@ -901,7 +905,7 @@ __global__ __launch_bounds__(1024) void token_grad_kernel(VjpParams<T> p) {
     const float *wp0 = p.wpart + (wslot * p.heads + head) * 3 * p.s_real + rr;
     float su = wp0[0], sx = wp0[p.s_real], sp = wp0[2 * p.s_real];
     float sq = p.rpart[(rslot * p.heads + head) * p.s_real + rr];
-    const int c0 = lane * CPL;
+    const int c0 = (hw * kLanes + lane) * CPL;
     bool live[CPL];
     float v0[CPL], w0[CPL], vwsum[CPL], wsum[CPL], wv[MAXK];
 #pragma unroll
@@ -950,7 +954,7 @@ __global__ __launch_bounds__(1024) void token_grad_kernel(VjpParams<T> p) {
     const float wr = round_to<T>(group8_sum(rl ? round_to<T>(dq * q0) : 0.f));
     const float kwsum = stride8_sum(k_term), gsum = stride8_sum(g_term), bsum = stride8_sum(b_term);
     const float qsum = stride8_sum(q_term);
-    if (j == 0 && srow) {
+    if (hw == 0 && j == 0 && srow) {
         const int64_t at = row * p.s_real + r;
         p.dq[at] = from_f32<T>(qsum);
         p.dk[at] = from_f32<T>(kwsum);
@@ -984,11 +988,13 @@ __global__ __launch_bounds__(1024) void token_grad_kernel(VjpParams<T> p) {
         }
     }
     const float wv_total = reduce_scatter<MAXK>(wv, lane);
-    if ((lane & 15) < MAXK / 4) s_wv[head][(MAXK / 4) * (lane >> 4) + (lane & 15)] = wv_total;
+    if ((lane & 15) < MAXK / 4) s_wv[wave][(MAXK / 4) * (lane >> 4) + (lane & 15)] = wv_total;
     __syncthreads();
-    if (r == 0) {
+    if (hw == 0 && r == 0) {
         if (j < p.kw) {
-            float dww = round_to<T>(wb + round_to<T>(s_wv[head][j]));
+            float cols = 0.f;  // the head's waves in column order
+            for (int w = 0; w < p.wph; ++w) cols += s_wv[wave + w][j];
+            float dww = round_to<T>(wb + round_to<T>(cols));
             if (p.routed_decay) dww = round_to<T>(dww + dec);
             s_route[head][j] = dww;
         }
@@ -1148,9 +1154,15 @@ bool chunk_path(const bdm_backward_args &a) {
 }
 
 // The per-token gradient kernel: one wave per head and one lane per (slot, row).
+// A head wider than 256 columns takes ceil(width / 256) waves (4 columns per
+// lane); the workgroup holds at most 16 waves.
+int token_grad_waves(const bdm_backward_args &a) {
+    return a.head_width <= 256 ? 1 : (a.head_width + 255) / 256;
+}
+
 bool token_grad_path(const bdm_backward_args &a) {
     return a.bank_size <= 8 && a.write_banks >= 1 && a.write_banks <= 8 && a.read_banks >= 1 && a.read_banks <= 8 &&
-           a.heads <= 16 && a.head_width <= 256;
+           a.heads * token_grad_waves(a) <= 16;
 }
 
 Workspace carve(const bdm_backward_args &a, void *base) {
@@ -1259,10 +1271,13 @@ int launch_backward(const bdm_backward_args &a, const Workspace &ws, hipStream_t
     v.kr = a.read_banks;
     v.tiles = p.tiles;
     v.routed_decay = a.routed_decay;
+    v.wph = token_grad_waves(a);
     const unsigned blocks = unsigned(p.nt);
     if (token_grad_path(a)) {
-        const unsigned threads = unsigned(a.heads) * kLanes;
-        if (a.head_width <= kLanes)
+        const unsigned threads = unsigned(a.heads * v.wph) * kLanes;
+        if (v.wph > 1)
+            token_grad_kernel<T, 4><<<blocks, threads, 0, stream>>>(v);
+        else if (a.head_width <= kLanes)
             token_grad_kernel<T, 1><<<blocks, threads, 0, stream>>>(v);
         else if (a.head_width <= 2 * kLanes)
             token_grad_kernel<T, 2><<<blocks, threads, 0, stream>>>(v);
