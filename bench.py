@@ -381,6 +381,8 @@ def whole_model_training(device, context, timed_steps=3, warmup=2):
     model = model.to(torch.bfloat16).train()
     params = list(model.parameters())
     masters = [torch.nn.Parameter(p.detach().float().clone()) for p in params]
+    for m in masters:  # FP32 gradient buffers of the masters, filled by one foreach copy per step
+        m.grad = torch.empty_like(m)
     groups = [{'params': [m for m, p in zip(masters, params) if bool(getattr(p, '_no_weight_decay', False)) == nd],
                'weight_decay': 0.0 if nd else 0.01} for nd in (False, True)]
     optimizer = torch.optim.AdamW(groups, lr=0.0, betas=(0.9, 0.95), eps=1e-8, fused=True)
@@ -391,20 +393,21 @@ def whole_model_training(device, context, timed_steps=3, warmup=2):
     def step():
         for p in params:
             p.grad = None
-        optimizer.zero_grad(set_to_none=True)
         loss = model(x, y)
         loss.backward()
         with torch.no_grad():
             norm = torch.nn.utils.clip_grad_norm_(params, 1.0)
-            for p, m in zip(params, masters):
-                m.grad = None if p.grad is None else p.grad.float()
+            if any(p.grad is None for p in params):
+                raise RuntimeError('a parameter received no gradient')
+            torch._foreach_copy_([m.grad for m in masters], [p.grad for p in params])
             optimizer.step()
-            for p, m in zip(params, masters):
-                p.copy_(m)
+            torch._foreach_copy_(params, masters)
         return loss.detach(), norm
 
-    for _ in range(warmup):
+    for i in range(warmup):
         loss, norm = step()
+        torch.cuda.synchronize()
+        progress('training warmup step', i + 1)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(timed_steps):
@@ -642,6 +645,8 @@ def main():
         result['training_c5'] = c5_training(device)
         progress('whole model L16/D2048', args.lm_context)
         result['whole_model'] = whole_model(device, args.lm_context)
+        progress('whole model training step', args.lm_context)
+        result['whole_model_training'] = whole_model_training(device, args.lm_context)
     progress('copy probe')
     result['hbm_copy_GBps'] = round(copy_probe(device), 1)
     if args.cpu_tokens > 0:
