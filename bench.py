@@ -61,12 +61,15 @@ def parse_args():
     ap.add_argument('--cpu-tokens', type=int, default=512,
                     help='tokens of sequence 0 the CPU oracle runs (0 skips the CPU baseline)')
     ap.add_argument('--no-extras', action='store_true', help='skip the full-layer and decode measurements')
-    ap.add_argument('--only', choices=('c3', 'c4', 'c5', 'prefill', 'lm', 'lm-train'),
+    ap.add_argument('--only', choices=('c3', 'c4', 'c5', 'prefill', 'lm', 'lm-prefill', 'lm-train'),
                     help='run one named workload alone (C3 decode, C4 skewed forward, C5 training, C2 full-layer '
                          'prefill, whole-model prefill and decode) and print its figures as one JSON line; used to '
                          'profile a workload on its own')
     ap.add_argument('--lm-context', type=int, default=8192,
                     help='prompt length T (= memory rows N) of the whole-model L16/D2048 measurement')
+    ap.add_argument('--lm-gemm-tuning', choices=('on', 'off'), default='on',
+                    help='whole-model inference: pick GEMM solutions with PyTorch TunableOp (on) or take the '
+                         "library's heuristic choice (off, e.g. under a profiler)")
     return ap.parse_args()
 
 
@@ -287,14 +290,16 @@ def lm_graph_decode(model, tokens, caches, pos, count):
         return None, f'capture failed: {str(exc)[:120]}'
 
 
-def whole_model(device, context, timed_runs=3, decode_tokens=16):
+def whole_model(device, context, timed_runs=3, decode_tokens=16, tune=True, decode=True):
     """The reference's whole-model inference case (perf_inference_case.py:15-56,
     80-160): BDMLanguageModel L16/D2048/FFN5632, vocab 50,257, one head of width
     2,048, N = T memory rows (J = T/8 banks of 8), K = 8, BF16 weights, batch
     1.  Prefill = embedding, every block's prefill from a fresh cache (the
     caches are created inside, as the reference's run does) and the head on
     the last position; decode = one eager step per token through all blocks
-    and the full-vocabulary head.  Random-init weights, token ids uniform."""
+    and the full-vocabulary head.  Random-init weights, token ids uniform.
+    ``tune``: GEMM selection by TunableOp in the warmup run (the library's
+    heuristic otherwise); ``decode``: also time the eager and graph decode."""
     import torch
     from bdm_amd import BSDMConfig
     from bdm_amd.lm import BDMLanguageModel, LanguageModelConfig
@@ -307,8 +312,8 @@ def whole_model(device, context, timed_runs=3, decode_tokens=16):
     # GEMM selection by measurement (PyTorch TunableOp over the hipBLASLt and
     # rocBLAS solutions): each shape is tuned on its first call, in the warmup
     tunable = torch.cuda.tunable
-    tunable.enable(True)
-    tunable.tuning_enable(True)
+    tunable.enable(tune)
+    tunable.tuning_enable(tune)
     tunable.set_max_tuning_duration(30)
     tunable.set_filename(os.path.join(tempfile.gettempdir(), f'bdm_tunableop_{os.getpid()}_%d.csv'))
     gen = torch.Generator().manual_seed(5)
@@ -323,12 +328,27 @@ def whole_model(device, context, timed_runs=3, decode_tokens=16):
             torch.cuda.synchronize()
             if i:  # the first run warms up (and tunes) the GEMMs and kernel caches
                 samples.append(time.perf_counter() - t0)
-            else:
+            elif decode:
                 for j in range(2):  # tune the decode shapes too, then only look up
                     model.step(tokens[:, context + 100 + j:context + 101 + j], [c.clone() for c in caches])
-                tunable.tuning_enable(False)
+            tunable.tuning_enable(False)
         if not bool(torch.isfinite(logits).all()):
             raise RuntimeError('whole-model prefill produced non-finite logits')
+        prefill_s = statistics.mean(samples)
+        out = {'context': context, 'layers': 16, 'd_model': 2048, 'ffn': model.layers[0].feed_forward.hidden_dim,
+               'bank_count': memory.bank_count, 'prefill_seconds': round(prefill_s, 5),
+               'prefill_tokens_per_s': round(context / prefill_s, 1),
+               'cache_bytes': sum(c.numel() * c.element_size() for c in caches)}
+        if context in H200_PREFILL_SECONDS:
+            out['h200_prefill_seconds'] = H200_PREFILL_SECONDS[context]
+            out['prefill_speedup_vs_h200'] = round(H200_PREFILL_SECONDS[context] / prefill_s, 3)
+        out['gemm_selection'] = ('PyTorch TunableOp (hipBLASLt and rocBLAS solutions, tuned in the warmup run)'
+                                 if tune else 'library heuristic')
+        if not decode:
+            tunable.enable(False)
+            del model, caches
+            torch.cuda.empty_cache()
+            return out
         for i in range(4):
             logits, caches = model.step(tokens[:, context + i:context + i + 1], caches)
         torch.cuda.synchronize()
@@ -339,20 +359,12 @@ def whole_model(device, context, timed_runs=3, decode_tokens=16):
         torch.cuda.synchronize()
         decode_ms = (time.perf_counter() - t0) * 1e3 / decode_tokens
         graph_ms, graph_check = lm_graph_decode(model, tokens, caches, context + 4 + decode_tokens, decode_tokens)
-    prefill_s = statistics.mean(samples)
-    out = {'context': context, 'layers': 16, 'd_model': 2048, 'ffn': model.layers[0].feed_forward.hidden_dim,
-           'bank_count': memory.bank_count, 'prefill_seconds': round(prefill_s, 5),
-           'prefill_tokens_per_s': round(context / prefill_s, 1), 'decode_ms_per_token_eager': round(decode_ms, 3),
-           'decode_ms_per_token_graph': graph_ms, 'decode_graph_check': graph_check,
-           'cache_bytes': sum(c.numel() * c.element_size() for c in caches)}
-    if context in H200_PREFILL_SECONDS:
-        out['h200_prefill_seconds'] = H200_PREFILL_SECONDS[context]
-        out['prefill_speedup_vs_h200'] = round(H200_PREFILL_SECONDS[context] / prefill_s, 3)
+    out.update({'decode_ms_per_token_eager': round(decode_ms, 3), 'decode_ms_per_token_graph': graph_ms,
+                'decode_graph_check': graph_check})
     if context in H200_DECODE_MS:
         out['h200_decode_ms_per_token'] = H200_DECODE_MS[context]
         if graph_ms:
             out['decode_speedup_vs_h200'] = round(H200_DECODE_MS[context] / graph_ms, 3)
-    out['gemm_selection'] = 'PyTorch TunableOp (hipBLASLt and rocBLAS solutions, tuned in the warmup run)'
     tunable.enable(False)
     del model, caches
     torch.cuda.empty_cache()
@@ -569,7 +581,9 @@ def main():
         run = {'c3': lambda: decode_bench(layer, device, args.decode_steps), 'c4': lambda: c4_forward(device),
                'c5': lambda: c5_training(device),
                'prefill': lambda: full_layer_prefill(layer, device, batch, time_, max(3, args.steps // 4)),
-               'lm': lambda: whole_model(device, args.lm_context),
+               'lm': lambda: whole_model(device, args.lm_context, tune=args.lm_gemm_tuning == 'on'),
+               'lm-prefill': lambda: whole_model(device, args.lm_context, tune=args.lm_gemm_tuning == 'on',
+                                                 decode=False),
                'lm-train': lambda: whole_model_training(device, args.lm_context)}[args.only]
         progress('workload', args.only)
         print(json.dumps({'workload': args.only, 'result': run()}), flush=True)
@@ -644,7 +658,7 @@ def main():
         progress('training C5')
         result['training_c5'] = c5_training(device)
         progress('whole model L16/D2048', args.lm_context)
-        result['whole_model'] = whole_model(device, args.lm_context)
+        result['whole_model'] = whole_model(device, args.lm_context, tune=args.lm_gemm_tuning == 'on')
         progress('whole model training step', args.lm_context)
         result['whole_model_training'] = whole_model_training(device, args.lm_context)
     progress('copy probe')
