@@ -26,6 +26,7 @@ EXPORTED_SYMBOLS = (
     'bdm_rms_norm',
     'bdm_swiglu',
     'bdm_gemv',
+    'bdm_gemv_ex',
 )
 
 _i32, _i64, _f32, _vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
@@ -96,6 +97,19 @@ class OutputArgs(ctypes.Structure):
     ]
 
 
+GEMV_PLAIN, GEMV_RMS, GEMV_SWIGLU, GEMV_OUT_LAYER, GEMV_OUT_RMS = 0, 1, 2, 3, 4
+
+
+class GemvArgs(ctypes.Structure):
+    """Mirror of ``bdm_gemv_args``."""
+    _fields_ = [
+        ('x', _vp), ('weight', _vp), ('bias', _vp), ('y', _vp), ('residual', _vp), ('sum_out', _vp),
+        ('norm_weight', _vp), ('norm_bias', _vp), ('gate', _vp),
+        ('rows', _i64), ('n', _i64), ('k', _i64), ('gate_stride', _i64),
+        ('dtype', _i32), ('param_dtype', _i32), ('prologue', _i32), ('eps', _f32),
+    ]
+
+
 class BDMError(RuntimeError):
     """A call into libbdm_hip returned a non-zero status."""
 
@@ -141,6 +155,8 @@ def library() -> ctypes.CDLL:
     lib.bdm_swiglu.restype = _i32
     lib.bdm_gemv.argtypes = [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp]
     lib.bdm_gemv.restype = _i32
+    lib.bdm_gemv_ex.argtypes = [_vp, _vp]
+    lib.bdm_gemv_ex.restype = _i32
     return lib
 
 

@@ -13,51 +13,10 @@
 // fused with RMSNorm (_shell.py:10-35) and the SwiGLU product
 // silu(w1 x) * (w3 x) (_shell.py:86-91) over one GEMM of the concatenated
 // w1 | w3 weights.
-#include "bdm_common.h"
+#include "epilogue_ops.h"
 
 namespace bdm {
 namespace {
-
-// silu and sigmoid with the hardware exp and reciprocal (v_exp_f32,
-// v_rcp_f32): a few FP32 ulps, below the BF16 rounding every result gets
-__device__ __forceinline__ float sigmoid_f(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
-__device__ __forceinline__ float silu_f(float x) { return x * sigmoid_f(x); }
-// F.softplus with beta 1 and threshold 20
-__device__ __forceinline__ float softplus_f(float x) { return x > 20.f ? x : log1pf(expf(x)); }
-
-__device__ __forceinline__ float param_at(const void *p, int dtype, int64_t i) {
-    return dtype == BDM_BF16 ? to_f32(static_cast<const bf16_t *>(p)[i]) : static_cast<const float *>(p)[i];
-}
-
-// Eight consecutive elements of T (FP32 or BF16 parameters given by dtype
-// for param8) widened to FP32: 16-byte vector loads when VEC (the caller
-// checked 16-byte alignment of every such group), element loads otherwise.
-template <typename T, bool VEC>
-__device__ __forceinline__ void load8(const T *p, float (&x)[8]) {
-    if constexpr (VEC && sizeof(T) == 2) {
-        const uint4 r = *reinterpret_cast<const uint4 *>(p);
-        const uint32_t w[4] = {r.x, r.y, r.z, r.w};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            x[2 * q] = __uint_as_float(w[q] << 16);
-            x[2 * q + 1] = __uint_as_float(w[q] & 0xffff0000u);
-        }
-    } else if constexpr (VEC) {
-        const float4 a = *reinterpret_cast<const float4 *>(p), b = *reinterpret_cast<const float4 *>(p + 4);
-        x[0] = a.x, x[1] = a.y, x[2] = a.z, x[3] = a.w, x[4] = b.x, x[5] = b.y, x[6] = b.z, x[7] = b.w;
-    } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) x[j] = to_f32(p[j]);
-    }
-}
-
-template <bool VEC>
-__device__ __forceinline__ void param8(const void *p, int dtype, int64_t at, float (&x)[8]) {
-    if (dtype == BDM_BF16)
-        load8<bf16_t, VEC>(static_cast<const bf16_t *>(p) + at, x);
-    else
-        load8<float, VEC>(static_cast<const float *>(p) + at, x);
-}
 
 template <typename T>
 struct ControllerParams {
@@ -171,13 +130,6 @@ struct OutputParams {
     float eps;
 };
 
-template <int N>
-__device__ __forceinline__ float wave_total(float x) {
-#pragma unroll
-    for (int m = N / 2; m >= 1; m >>= 1) x += __shfl_xor(x, m, N);
-    return x;
-}
-
 // One wave per token; a lane owns 8-column chunks lane*8, lane*8 + 512, ...
 // VEC: raw, gate and the parameters are read as 16-byte groups.
 template <typename T, int MAXC, bool VEC>
@@ -217,9 +169,9 @@ __global__ __launch_bounds__(256) void output_epilogue_kernel(OutputParams<T> p)
                 var = live ? fmaf(d, d, var) : var;
             }
         }
-        scale = rsqrtf(wave_total<kWave>(var) * inv_n + p.eps);
+        scale = rsqrtf(fmaf(wave_total<kWave>(var), inv_n, p.eps));
     } else {
-        scale = round_to<T>(rsqrtf(wave_total<kWave>(sq) * inv_n + p.eps));
+        scale = round_to<T>(rsqrtf(fmaf(wave_total<kWave>(sq), inv_n, p.eps)));
     }
     T *out = p.out + token * p.width;
 #pragma unroll
@@ -233,7 +185,8 @@ __global__ __launch_bounds__(256) void output_epilogue_kernel(OutputParams<T> p)
         for (int j = 0; j < 8; ++j) {
             float n;
             if (p.norm_kind == 1) {
-                n = round_to<T>((x[i][j] - mean) * scale * wt[j] + bs[j]);
+                // the multiply-adds spelled out: the fused GEMV prologue rounds identically
+                n = round_to<T>(fmaf((x[i][j] - mean) * scale, wt[j], bs[j]));
             } else {
                 n = round_to<T>(x[i][j] * scale);
                 n = round_to<T>(n * round_to<T>(wt[j]));
@@ -383,7 +336,7 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const T *__restrict__ gate_
     load8<T, VEC>(in + c, a);
     load8<T, VEC>(in + hidden + c, b);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) y[j] = round_to<T>(a[j] / (1.f + expf(-a[j]))) * b[j];
+    for (int j = 0; j < 8; ++j) y[j] = swiglu_value<T>(a[j], b[j]);
     store_row<8>(out + row * hidden + c, y);
 }
 

@@ -203,11 +203,42 @@ class BDMLanguageModel(nn.Module):
             raise ValueError('step needs the caches returned by prefill')
         return self._run(tokens, list(caches), decode=True)
 
+    def _fused_decode_supported(self, hidden: Tensor) -> bool:
+        ffn = self.layers[0].feed_forward
+        return (hidden.shape[0] <= ops.GEMV_MAX_ROWS and ffn.hidden_dim % 8 == 0 and self.dim % 8 == 0
+                and max(ffn.hidden_dim, self.dim) <= ops.GEMV_PROLOGUE_MAX_K
+                and all(block.attention.step_fused_norm_supported(hidden, block.attention_norm.weight)
+                        for block in self.layers))
+
+    def _decode_fused(self, hidden: Tensor, caches: list):
+        # One decode token with every one-row elementwise kernel formed inside
+        # the GEMV that consumes it: the residual add + attention_norm inside
+        # the memory layer's projection, the output interface inside o_proj,
+        # the residual add + ffn_norm inside w1|w3, SwiGLU inside w2, and the
+        # last residual add + final norm inside the vocabulary head.
+        rows = hidden.shape[0]
+        delta = None
+        for i, block in enumerate(self.layers):
+            out, hidden = block.attention.step_fused_norm(hidden, delta, block.attention_norm.weight,
+                                                          block.attention_norm.eps, caches[i])
+            ffn = block.feed_forward
+            gate_up, hidden = ops.gemv_fused(out.reshape(rows, self.dim), ffn._fused_input_weight(), prologue='rms',
+                                             residual=hidden.reshape(rows, self.dim),
+                                             norm_weight=block.ffn_norm.weight, eps=block.ffn_norm.eps)
+            delta = ops.gemv_fused(gate_up, ffn.w2.weight, prologue='swiglu')
+            hidden = hidden.view(rows, 1, self.dim)
+        logits, _ = ops.gemv_fused(delta.reshape(rows, self.dim), self.output.weight, prologue='rms',
+                                   residual=hidden.reshape(rows, self.dim), norm_weight=self.norm.weight,
+                                   eps=self.norm.eps)
+        return logits.view(rows, 1, -1), caches
+
     def _run(self, tokens: Tensor, caches: list, decode: bool):
         # Each residual add is fused with the normalization that reads its
         # result: the block's ffn_norm, then the next block's attention_norm
         # (the final norm after the last block).
         hidden = self.tok_embeddings(tokens)
+        if decode and self._fused_decode_supported(hidden):
+            return self._decode_fused(hidden, caches)
         normed = self.layers[0].attention_norm(hidden)
         for i, block in enumerate(self.layers):
             run = block.attention.step if decode else block.attention.prefill

@@ -224,12 +224,15 @@ class BankedDeltaMemory(nn.Module):
                 and self.bank_size in (8, 16, 32) and self.value_width % 8 == 0 and self.value_width <= 4096
                 and self.output_norm_weight.dtype in (torch.bfloat16, torch.float32))
 
-    def _fused_controllers(self, hidden: Tensor):
+    def _fused_controllers(self, hidden: Tensor, proj: Tensor | None = None):
         """Inference controllers, route scores and the output-gate projection from
-        one projection GEMM and the controller epilogue (heads.py:11-22)."""
+        one projection GEMM and the controller epilogue (heads.py:11-22).
+        ``proj``: the projection already computed (hidden then only gives the
+        leading shape)."""
         weight, bias, cols = self._fused_weights()
         lead = hidden.shape[:-1]
-        proj = ops.linear(hidden.reshape(-1, self.hidden_size), weight, bias)
+        if proj is None:
+            proj = ops.linear(hidden.reshape(-1, self.hidden_size), weight, bias)
         hv, rw = self.head_value_width, self.factor_route_width
         f = ops.linear(proj[:, cols['f']:cols['f'] + hv], self.f_proj[1].weight)
         q, k, v, g, b, w = ops.controller_epilogue(proj, f, cols, self.A_log, self.dt_bias, heads=self.num_heads,
@@ -364,11 +367,50 @@ class BankedDeltaMemory(nn.Module):
         if torch.is_grad_enabled() or hidden.shape[1] != 1:
             raise ValueError('step requires one token under no_grad/inference_mode')
         (q, k, v, g, b, w), (read_routes, write_routes), gate = self._inference_inputs(hidden)
+        raw = self._decode_banks((q, k, v, g, b, w), (read_routes, write_routes), hidden.shape[0], state)
+        return self._inference_output(hidden, gate, raw.unsqueeze(1)), state
+
+    def _decode_banks(self, controllers, scores, batch: int, state: Tensor) -> Tensor:
+        """Both routes and the decode kernel of one step: the bank reads [B, V]."""
+        q, k, v, g, b, w = controllers
+        read_routes, write_routes = scores
         ww, wi = self._route(write_routes, self.num_writes)
         rw, ri = self._route(read_routes, self.num_reads)
-        batch = hidden.shape[0]
         heads_view = state.view(batch, self.bank_count, self.num_heads, self.bank_size, self.head_value_width)
-        raw = ops.decode_step(q[:, 0], k[:, 0], v[:, 0], g[:, 0], b[:, 0], w[:, 0], wi[:, 0], ww[:, 0],
-                              ri[:, 0], rw[:, 0], heads_view, bank_count=self.bank_count,
-                              scale=self.bank_size ** -0.5, routed_decay=self.config.routed_decay)
-        return self._inference_output(hidden, gate, raw.unsqueeze(1)), state
+        return ops.decode_step(q[:, 0], k[:, 0], v[:, 0], g[:, 0], b[:, 0], w[:, 0], wi[:, 0], ww[:, 0],
+                               ri[:, 0], rw[:, 0], heads_view, bank_count=self.bank_count,
+                               scale=self.bank_size ** -0.5, routed_decay=self.config.routed_decay)
+
+    def step_fused_norm(self, hidden: Tensor, delta: Tensor | None, norm_weight: Tensor, norm_eps: float,
+                        state: Tensor):
+        """The memory sublayer of a pre-norm block for one decode token, with the
+        block's residual add and RMSNorm formed inside the projection GEMV and
+        the output interface inside the o_proj GEMV (``bdm_gemv_ex``):
+        h = hidden + delta (delta None: h = hidden), out = step(RMSNorm(h)).
+        Returns (out, h); results equal the unfused kernels bit for bit."""
+        weight, bias, _ = self._fused_weights()
+        rows = hidden.shape[0]
+        flat = hidden.reshape(rows, self.hidden_size)
+        if delta is None:
+            proj = ops.gemv_fused(flat, weight, bias, prologue='rms', norm_weight=norm_weight, eps=norm_eps)
+            new_hidden = hidden
+        else:
+            proj, total = ops.gemv_fused(delta.reshape(rows, self.hidden_size), weight, bias, prologue='rms',
+                                         residual=flat, norm_weight=norm_weight, eps=norm_eps)
+            new_hidden = total.view_as(hidden)
+        controllers, scores, gate = self._fused_controllers(new_hidden, proj=proj)
+        raw = self._decode_banks(controllers, scores, rows, state)
+        layer = self.config.output_normalization == 'layer'
+        out = ops.gemv_fused(raw, self.o_proj.weight, self.o_proj.bias,
+                             prologue='out_layer' if layer else 'out_rms', norm_weight=self.output_norm_weight,
+                             norm_bias=self.output_norm_bias if layer else None, gate=gate, eps=self.norm_eps)
+        return out.view(rows, 1, self.hidden_size), new_hidden
+
+    def step_fused_norm_supported(self, hidden: Tensor, norm_weight: Tensor) -> bool:
+        rows = hidden.shape[0]
+        return (hidden.is_cuda and hidden.dim() == 3 and hidden.shape[1] == 1 and 1 <= rows <= ops.GEMV_MAX_ROWS
+                and self._fused_supported(hidden) and self.hidden_size % 8 == 0
+                and max(self.hidden_size, self.value_width) <= ops.GEMV_PROLOGUE_MAX_K
+                and self.o_proj.weight.dtype == hidden.dtype and self.q_proj.weight.dtype == hidden.dtype
+                and norm_weight.dtype in (torch.bfloat16, torch.float32)
+                and (self.o_proj.bias is None or self.o_proj.bias.dtype == hidden.dtype))

@@ -58,6 +58,10 @@ def _ptr(t: Tensor | None):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
+def _addr(t: Tensor | None):
+    return None if t is None else t.data_ptr()
+
+
 # ---------------------------------------------------------------------------
 # router
 
@@ -438,6 +442,7 @@ def output_epilogue(raw: Tensor, gate: Tensor, weight: Tensor, bias: Tensor | No
 # skinny linear maps (decode)
 
 GEMV_MAX_ROWS = 4
+GEMV_PROLOGUE_MAX_K = 6144
 
 
 def gemv_supported(x: Tensor, weight: Tensor, bias: Tensor | None) -> bool:
@@ -462,6 +467,55 @@ def gemv(x: Tensor, weight: Tensor, bias: Tensor | None = None) -> Tensor:
     _lib.check(_lib.library().bdm_gemv(_ptr(x2), _ptr(weight), _ptr(b), _ptr(y), rows, n, k,
                                        _dtype_code(x.dtype), _stream(x.device)), 'bdm_gemv')
     return y.view(*lead, n)
+
+
+_PROLOGUES = {'rms': _lib.GEMV_RMS, 'swiglu': _lib.GEMV_SWIGLU, 'out_layer': _lib.GEMV_OUT_LAYER,
+              'out_rms': _lib.GEMV_OUT_RMS}
+
+
+def gemv_fused(x: Tensor, weight: Tensor, bias: Tensor | None = None, *, prologue: str,
+               residual: Tensor | None = None, norm_weight: Tensor | None = None, norm_bias: Tensor | None = None,
+               gate: Tensor | None = None, eps: float = 1e-5):
+    """F.linear of 1-4 rows whose input is formed inside the GEMV, bit-identical
+    to running the elementwise kernel first:
+      'rms'       RMSNorm(x [+ residual]) * norm_weight; with ``residual``
+                  returns (y, x + residual rounded) -- the block's new hidden;
+      'swiglu'    silu(a) * b of x = [rows, 2K] (a | b);
+      'out_layer' / 'out_rms'  the layer's output interface: norm(x) * sigmoid(gate)."""
+    _require_gpu(x, weight, bias, residual, norm_weight, norm_bias, gate)
+    kind = _PROLOGUES[prologue]
+    k = weight.shape[1]
+    rows = x.numel() // x.shape[-1]
+    if not (1 <= rows <= GEMV_MAX_ROWS) or x.dtype not in (torch.bfloat16, torch.float32) or weight.dtype != x.dtype:
+        raise ValueError('gemv_fused takes 1-4 BF16/FP32 rows of the weight dtype')
+    if x.shape[-1] != (2 * k if prologue == 'swiglu' else k) or k % 8 or k > GEMV_PROLOGUE_MAX_K:
+        raise ValueError('x does not match the weight (K % 8 == 0, K <= 6144; 2K columns for swiglu)')
+    x2 = _aligned(x.reshape(rows, x.shape[-1]))
+    res = None if residual is None else _aligned(residual.reshape(rows, k))
+    total = None if res is None else torch.empty_like(res)
+    g = None
+    if gate is not None:
+        g = gate.reshape(rows, -1) if gate.stride(-1) == 1 else gate.reshape(rows, -1).contiguous()
+        if g.data_ptr() % 16 or g.stride(0) % 8:
+            g = g.contiguous().clone()
+    nw = None if norm_weight is None else _aligned(norm_weight)
+    nb = None if norm_bias is None else _aligned(norm_bias)
+    b = None if bias is None else bias.contiguous()
+    y = torch.empty(rows, weight.shape[0], device=x.device, dtype=x.dtype)
+    args = _lib.GemvArgs()
+    args.x, args.weight, args.bias, args.y = _addr(x2), _addr(weight), _addr(b), _addr(y)
+    args.residual, args.sum_out, args.norm_weight, args.norm_bias, args.gate = (
+        _addr(res), _addr(total), _addr(nw), _addr(nb), _addr(g))
+    args.rows, args.n, args.k = rows, weight.shape[0], k
+    args.gate_stride = 0 if g is None else g.stride(0)
+    args.dtype = _dtype_code(x.dtype)
+    args.param_dtype = _dtype_code(nw.dtype) if nw is not None else _lib.BDM_F32
+    args.prologue, args.eps = kind, float(eps)
+    _lib.check(_lib.library().bdm_gemv_ex(ctypes.byref(args), _stream(x.device)), 'bdm_gemv_ex')
+    y = y.view(*x.shape[:-1], weight.shape[0])
+    if total is not None:
+        return y, total.view(residual.shape)
+    return y
 
 
 def linear(x: Tensor, weight: Tensor, bias: Tensor | None = None) -> Tensor:

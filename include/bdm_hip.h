@@ -325,6 +325,44 @@ int bdm_swiglu(const void *gate_up, void *out, int64_t rows, int32_t hidden, int
 int bdm_gemv(const void *x, const void *weight, const void *bias, void *y, int64_t rows, int64_t n, int64_t k,
              int32_t dtype, void *stream);
 
+/* bdm_gemv with an input prologue: the elementwise kernel that would produce
+ * the GEMV's input row, fused (no counterpart of its own in the reference; it
+ * replaces the pair "elementwise kernel, then F.linear" of a decode step with
+ * bit-identical results):
+ *   BDM_GEMV_RMS        x' = RMSNorm(x [+ residual]) * norm_weight, the shell's
+ *                       RMSNorm (_shell.py:29-35); with a residual,
+ *                       sum_out = round(x + residual) is also stored
+ *                       (model.py:174-176);
+ *   BDM_GEMV_SWIGLU     x [rows, 2k] = (a | b), x' = silu(a) * b (_shell.py:86-91);
+ *   BDM_GEMV_OUT_LAYER  x' = LayerNorm(x; norm_weight, norm_bias) * sigmoid(gate)
+ *   BDM_GEMV_OUT_RMS    x' = RMSNorm(x) * norm_weight * sigmoid(gate)
+ *                       (_project_bank_output, _parameters.py:222-232), the
+ *                       rounding points of bdm_output_epilogue.
+ * A prologue takes k <= 6144.  sum_out must not alias x or residual. */
+#define BDM_GEMV_PLAIN 0
+#define BDM_GEMV_RMS 1
+#define BDM_GEMV_SWIGLU 2
+#define BDM_GEMV_OUT_LAYER 3
+#define BDM_GEMV_OUT_RMS 4
+
+typedef struct bdm_gemv_args {
+    const void *x;            /* [rows, k] ([rows, 2k] for BDM_GEMV_SWIGLU) of dtype */
+    const void *weight;       /* [n, k] of dtype, row-major */
+    const void *bias;         /* [n] of dtype or NULL */
+    void *y;                  /* [rows, n] of dtype */
+    const void *residual;     /* BDM_GEMV_RMS: [rows, k] or NULL */
+    void *sum_out;            /* BDM_GEMV_RMS with a residual: [rows, k] */
+    const void *norm_weight;  /* [k] of param_dtype (norm prologues) */
+    const void *norm_bias;    /* [k] of param_dtype (BDM_GEMV_OUT_LAYER) */
+    const void *gate;         /* [rows, gate_stride] of dtype (output prologues) */
+    int64_t rows, n, k, gate_stride;
+    int32_t dtype, param_dtype;
+    int32_t prologue;
+    float eps;
+} bdm_gemv_args;
+
+int bdm_gemv_ex(const bdm_gemv_args *args, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -133,7 +133,7 @@ def test_struct_layouts_match_the_header(tmp_path):
         pytest.skip('no host C compiler')
     mirrors = {'bdm_forward_args': _lib.ForwardArgs, 'bdm_backward_args': _lib.BackwardArgs,
                'bdm_decode_args': _lib.DecodeArgs, 'bdm_controller_args': _lib.ControllerArgs,
-               'bdm_output_args': _lib.OutputArgs}
+               'bdm_output_args': _lib.OutputArgs, 'bdm_gemv_args': _lib.GemvArgs}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', 'int main(void) {']
     for struct, mirror in mirrors.items():
         lines.append(f'printf("{struct} size %zu\\n", sizeof({struct}));')

@@ -53,3 +53,80 @@ def test_linear_dispatch(device):
             y = ops.linear(x, w)
         ref = torch.nn.functional.linear(x.float(), w.float())
         assert rel_err(y, ref) < 1e-2
+
+
+def _rows(rows, k, gen, dtype, device, scale=1.0):
+    return (torch.randn(rows, k, generator=gen) * scale).to(dtype).to(device)
+
+
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float32], ids=['bf16', 'f32'])
+@pytest.mark.parametrize('rows', [1, 3])
+@pytest.mark.parametrize('k', [520, 2048])
+def test_gemv_prologues_equal_the_unfused_kernels(device, dtype, rows, k):
+    """Each prologue of bdm_gemv_ex gives exactly the output of its standalone
+    kernel followed by the plain GEMV (and the RMS prologue's residual sum
+    equals rms_norm's); the one exception, FP32 layer norm, is within an
+    FP32 ulp of it."""
+    from bdm_amd import ops
+    gen = torch.Generator().manual_seed(k + rows)
+    n = 1000
+    w = _rows(n, k, gen, dtype, device, k ** -0.5)
+    bias = _rows(1, n, gen, dtype, device)[0]
+    x = _rows(rows, k, gen, dtype, device, 2.0)
+    res = _rows(rows, k, gen, dtype, device)
+    for pdt in (torch.float32, torch.bfloat16):
+        nw = (1 + 0.1 * torch.randn(k, generator=gen)).to(pdt).to(device)
+        nb = (0.1 * torch.randn(k, generator=gen)).to(pdt).to(device)
+        announce('gemv prologues', dtype, rows, k, pdt)
+        # RMSNorm, plain and after a residual add
+        y = ops.gemv_fused(x, w, bias, prologue='rms', norm_weight=nw, eps=1e-5)
+        assert torch.equal(y, ops.gemv(ops.rms_norm(x, nw, 1e-5), w, bias))
+        y, total = ops.gemv_fused(x, w, bias, prologue='rms', residual=res, norm_weight=nw, eps=1e-5)
+        want_total, normed = ops.rms_norm(x, nw, 1e-5, residual=res)
+        assert torch.equal(total, want_total) and torch.equal(y, ops.gemv(normed, w, bias))
+        # the output interface: layer norm or RMS norm, times sigmoid(gate); the gate a strided slice
+        wide = _rows(rows, 3 * k, gen, dtype, device)
+        gate = wide[:, k:2 * k]
+        for kind in ('layer', 'rms'):
+            y = ops.gemv_fused(x, w, bias, prologue='out_' + kind, norm_weight=nw,
+                               norm_bias=nb if kind == 'layer' else None, gate=gate, eps=1e-5)
+            normed = ops.output_epilogue(x, gate, nw, nb if kind == 'layer' else None, eps=1e-5, kind=kind)
+            want = ops.gemv(normed, w, bias)
+            if kind == 'layer' and dtype == torch.float32:
+                # FP32 layer norm: the row mean may differ in its last bit from the standalone
+                # kernel's (widths not a multiple of 512), so the input within one FP32 ulp
+                assert rel_err(y, want) < 1e-6, (kind, rel_err(y, want))
+            else:
+                assert torch.equal(y, want), kind
+    # SwiGLU of a [rows, 2k] row
+    gu = _rows(rows, 2 * k, gen, dtype, device, 3.0)
+    y = ops.gemv_fused(gu, w, None, prologue='swiglu')
+    assert torch.equal(y, ops.gemv(ops.swiglu(gu, k), w))
+    torch.cuda.synchronize()
+
+
+def test_lm_fused_decode_equals_unfused(device):
+    """The whole model's decode step with the elementwise kernels fused into
+    the GEMVs equals the unfused step bit for bit (logits and caches)."""
+    from bdm_amd import BSDMConfig
+    from bdm_amd.lm import BDMLanguageModel, LanguageModelConfig
+    memory = BSDMConfig(dim=256, bank_count=64, bank_size=8, selected_banks=4, value_width=512, num_heads=2)
+    config = LanguageModelConfig(memory=memory, vocab_size=1000, layers=3, seed=2)
+    model = BDMLanguageModel(config).to(device=device, dtype=torch.bfloat16).eval()
+    gen = torch.Generator().manual_seed(4)
+    tokens = torch.randint(0, 1000, (2, 30), generator=gen).to(device)
+    announce('lm fused decode')
+    with torch.no_grad():
+        _, caches = model.prefill(tokens[:, :20])
+        fused = [c.clone() for c in caches]
+        plain = [c.clone() for c in caches]
+        assert model._fused_decode_supported(model.tok_embeddings(tokens[:, :1]))
+        for t in range(20, 26):
+            got, fused = model.step(tokens[:, t:t + 1], fused)
+            model._fused_decode_supported = lambda h: False  # the unfused kernels, for comparison
+            want, plain = model.step(tokens[:, t:t + 1], plain)
+            del model._fused_decode_supported
+            assert torch.equal(got, want), t
+            for a, b in zip(fused, plain):
+                assert torch.equal(a, b), t
+        torch.cuda.synchronize()
