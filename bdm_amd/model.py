@@ -374,8 +374,18 @@ class BankedDeltaMemory(nn.Module):
         """Both routes and the decode kernel of one step: the bank reads [B, V]."""
         q, k, v, g, b, w = controllers
         read_routes, write_routes = scores
-        ww, wi = self._route(write_routes, self.num_writes)
-        rw, ri = self._route(read_routes, self.num_reads)
+        width = read_routes.shape[-1]
+        if (batch == 1 and self.num_reads == self.num_writes and read_routes.stride(-1) == 1
+                and write_routes.data_ptr() == read_routes.data_ptr() + width * read_routes.element_size()):
+            # one token: its read and write scores are adjacent slices of the
+            # projection row, so both roles route in one launch, as two rows
+            pair = torch.as_strided(read_routes, (1, 2, width), (2 * width, width, 1))
+            weights, indices = self._route(pair, self.num_reads)
+            rw, ww = weights[:, 0:1], weights[:, 1:2]
+            ri, wi = indices[:, 0:1], indices[:, 1:2]
+        else:
+            ww, wi = self._route(write_routes, self.num_writes)
+            rw, ri = self._route(read_routes, self.num_reads)
         heads_view = state.view(batch, self.bank_count, self.num_heads, self.bank_size, self.head_value_width)
         return ops.decode_step(q[:, 0], k[:, 0], v[:, 0], g[:, 0], b[:, 0], w[:, 0], wi[:, 0], ww[:, 0],
                                ri[:, 0], rw[:, 0], heads_view, bank_count=self.bank_count,

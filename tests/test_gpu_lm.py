@@ -117,19 +117,21 @@ def test_lm_matches_reference_fixture(device):
         assert rel_err(params[name].grad, grad) < 2e-2, (name, rel_err(params[name].grad, grad))
 
 
-def test_lm_prefill_and_step_match_oracle(device):
+@pytest.mark.parametrize('batch', [2, 1])
+def test_lm_prefill_and_step_match_oracle(device, batch):
     """FP32 weights and caches; our prefill (fused projections, shell
-    kernels, HIP recurrence) and steps against the oracle shell's.  Logits
-    within 1e-3 of the largest, caches within 1e-3."""
+    kernels, HIP recurrence) and steps (decode GEMVs with fused prologues; at
+    batch 1 both route roles in one launch) against the oracle shell's.
+    Logits within 1e-3 of the largest, caches within 1e-3."""
     golden, memory, config, model = _golden_model(device)
     oracle = O.OracleLanguageModel(memory, vocab_size=config.vocab_size, layers=config.layers,
                                    multiple_of=config.ffn_multiple_of, seed=config.seed)
     oracle.load_state_dict(golden['state'])
-    tokens = golden['tokens']
+    tokens = golden['tokens'][:batch]
     with torch.no_grad():
-        announce('lm prefill')
-        caches = [block.attention.create_state(2, dtype=torch.float32) for block in model.layers]
-        ref_caches = [block.attention.create_state(2, torch.float32) for block in oracle.layers]
+        announce('lm prefill', batch)
+        caches = [block.attention.create_state(batch, dtype=torch.float32) for block in model.layers]
+        ref_caches = [block.attention.create_state(batch, torch.float32) for block in oracle.layers]
         logits, caches = model.prefill(tokens[:, :14].to(device), caches)
         ref, ref_caches = oracle.prefill(tokens[:, :14], ref_caches)
         assert rel_err(logits, ref) < 1e-3, rel_err(logits, ref)
