@@ -47,6 +47,12 @@ def test_router_bit_exact(device, bank_count, selected, dtype):
         diff = (w.cpu().float() - wr.float()).abs()
         ulp = wr.float().abs() * (2 ** -7 if dtype == torch.bfloat16 else 1e-6)
         assert bool((diff <= ulp + 1e-12).all()), float(diff.max())
+        # few rows (a decode step) take the one-wave-per-row kernel for BF16
+        # scores: identical weights and indices to the one-lane-per-row kernel
+        few = scores[:1, :37]
+        wf, idf = ops.router_select(few.to(device), bank_count=bank_count, selected_banks=selected)
+        torch.cuda.synchronize()
+        assert torch.equal(idf.cpu(), i.cpu()[:1, :37]) and torch.equal(wf.cpu(), w.cpu()[:1, :37]), kind
 
 
 def test_router_module_autograd(device):
