@@ -22,7 +22,7 @@
 namespace bdm {
 namespace {
 
-constexpr int kRouterMaxScores = 256;  // J1 + J2 per row
+constexpr int kRouterMaxScores = 4096;  // J1 + J2 per row (entries pack 16-bit factor ids)
 constexpr int kRouterMaxSel = 16;
 
 // Order-preserving key of a score: NaN orders as -inf, -0 as +0; keys of real

@@ -24,7 +24,8 @@ def announce(*what):
 
 # ---------------------------------------------------------------------------- router
 
-@pytest.mark.parametrize('bank_count,selected', [(16, 4), (256, 8), (2048, 8), (12, 3), (6, 2), (256, 16)])
+@pytest.mark.parametrize('bank_count,selected', [(16, 4), (256, 8), (2048, 8), (12, 3), (6, 2), (256, 16),
+                                                  (131072, 8)])
 @pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float32])
 def test_router_bit_exact(device, bank_count, selected, dtype):
     from bdm_amd import ops
