@@ -27,6 +27,7 @@ EXPORTED_SYMBOLS = (
     'bdm_swiglu',
     'bdm_gemv',
     'bdm_gemv_ex',
+    'bdm_adamw_step',
 )
 
 _i32, _i64, _f32, _vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
@@ -110,6 +111,22 @@ class GemvArgs(ctypes.Structure):
     ]
 
 
+class AdamwTensor(ctypes.Structure):
+    """Mirror of ``bdm_adamw_tensor`` (40 bytes)."""
+    _fields_ = [('param', _vp), ('grad', _vp), ('offset', _i64), ('numel', _i64), ('weight_decay', ctypes.c_double)]
+
+
+class AdamwArgs(ctypes.Structure):
+    """Mirror of ``bdm_adamw_args``."""
+    _fields_ = [
+        ('tensors', _vp), ('block_tensor', _vp), ('block_start', _vp),
+        ('tensor_count', _i64), ('blocks', _i64), ('chunk', _i64),
+        ('master', _vp), ('exp_avg', _vp), ('exp_avg_sq', _vp), ('grad_scale', _vp),
+        ('lr', ctypes.c_double), ('beta1', ctypes.c_double), ('beta2', ctypes.c_double),
+        ('eps', ctypes.c_double), ('step', ctypes.c_double),
+    ]
+
+
 class BDMError(RuntimeError):
     """A call into libbdm_hip returned a non-zero status."""
 
@@ -157,6 +174,8 @@ def library() -> ctypes.CDLL:
     lib.bdm_gemv.restype = _i32
     lib.bdm_gemv_ex.argtypes = [_vp, _vp]
     lib.bdm_gemv_ex.restype = _i32
+    lib.bdm_adamw_step.argtypes = [_vp, _vp]
+    lib.bdm_adamw_step.restype = _i32
     return lib
 
 

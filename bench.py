@@ -379,12 +379,15 @@ def whole_model_training(device, context, timed_steps=3, warmup=2):
     (reproduction/experiments/profile_final.py:30-80 with optim.py:7-50):
     BDMLanguageModel L16/D2048/FFN5632, vocab 50,257, batch 1, N = T, BF16
     weights with FP32 master copies; forward to the cross-entropy loss,
-    backward, gradient-norm clipping at 1.0, fused AdamW on the FP32 masters
+    backward, gradient-norm clipping at 1.0, AdamW on the FP32 masters
     (weight decay 0.01 except the no-decay parameters), masters copied back
-    to the BF16 weights.  Random-init weights and token ids."""
+    to the BF16 weights.  The clip scaling, the update and the copy back run
+    as one pass (``MasterAdamW``, bit-identical to the reference's four).
+    Random-init weights and token ids."""
     import torch
     from bdm_amd import BSDMConfig
     from bdm_amd.lm import BDMLanguageModel, LanguageModelConfig
+    from bdm_amd.optim import MasterAdamW
     memory = BSDMConfig(dim=2048, bank_count=context // 8, bank_size=8, selected_banks=8, value_width=2048,
                         num_heads=1)
     config = LanguageModelConfig(memory=memory, vocab_size=50257, layers=16, seed=0)
@@ -392,12 +395,7 @@ def whole_model_training(device, context, timed_steps=3, warmup=2):
         model = BDMLanguageModel(config)
     model = model.to(torch.bfloat16).train()
     params = list(model.parameters())
-    masters = [torch.nn.Parameter(p.detach().float().clone()) for p in params]
-    for m in masters:  # FP32 gradient buffers of the masters, filled by one foreach copy per step
-        m.grad = torch.empty_like(m)
-    groups = [{'params': [m for m, p in zip(masters, params) if bool(getattr(p, '_no_weight_decay', False)) == nd],
-               'weight_decay': 0.0 if nd else 0.01} for nd in (False, True)]
-    optimizer = torch.optim.AdamW(groups, lr=0.0, betas=(0.9, 0.95), eps=1e-8, fused=True)
+    optimizer = MasterAdamW(params, lr=0.0, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.01, max_norm=1.0)
     gen = torch.Generator().manual_seed(7)
     tokens = torch.randint(0, config.vocab_size, (1, context + 1), generator=gen).to(device)
     x, y = tokens[:, :-1], tokens[:, 1:]
@@ -407,13 +405,7 @@ def whole_model_training(device, context, timed_steps=3, warmup=2):
             p.grad = None
         loss = model(x, y)
         loss.backward()
-        with torch.no_grad():
-            norm = torch.nn.utils.clip_grad_norm_(params, 1.0)
-            if any(p.grad is None for p in params):
-                raise RuntimeError('a parameter received no gradient')
-            torch._foreach_copy_([m.grad for m in masters], [p.grad for p in params])
-            optimizer.step()
-            torch._foreach_copy_(params, masters)
+        norm = optimizer.step()  # raises if a parameter received no gradient
         return loss.detach(), norm
 
     for i in range(warmup):
@@ -434,7 +426,7 @@ def whole_model_training(device, context, timed_steps=3, warmup=2):
     if context in H200_TRAIN_MS:
         out['h200_ms_per_step'] = H200_TRAIN_MS[context]
         out['speedup_vs_h200'] = round(H200_TRAIN_MS[context] / ms, 3)
-    del model, optimizer, masters, params
+    del model, optimizer, params
     torch.cuda.empty_cache()
     return out
 

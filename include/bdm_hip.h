@@ -363,6 +363,39 @@ typedef struct bdm_gemv_args {
 
 int bdm_gemv_ex(const bdm_gemv_args *args, void *stream);
 
+/* One AdamW step of the shell's training recipe with FP32 masters
+ * (reproduction/experiments/optim.py:30-50, AdamW.step for "wiki"): the
+ * gradient-clipping scale, torch's fused AdamW update of the masters and both
+ * moments, and the masters' copy back into the BF16 weights, fused into one
+ * pass.  Tensor i's master and moments are elements [offset, offset + numel)
+ * of the flat FP32 buffers master, exp_avg, exp_avg_sq (16-byte aligned).
+ * Each of the `blocks` workgroups updates elements [block_start[b],
+ * block_start[b] + chunk) of tensor block_tensor[b] (chunk a multiple of 4).
+ * grad_scale (device, may be NULL) multiplies every gradient, rounded to
+ * BF16 as clip_grad_norm_'s in-place scaling rounds it; the gradients
+ * themselves are not written.  step: the step count after this update's
+ * increment (>= 1).  tensors, block_tensor and block_start are device
+ * arrays. */
+typedef struct bdm_adamw_tensor {
+    void *param;          /* [numel] BF16 weight, overwritten with round(master) */
+    const void *grad;     /* [numel] BF16 gradient */
+    int64_t offset;       /* first element in the flat FP32 buffers */
+    int64_t numel;
+    double weight_decay;  /* 0 for the no-decay group */
+} bdm_adamw_tensor;
+
+typedef struct bdm_adamw_args {
+    const bdm_adamw_tensor *tensors;
+    const int32_t *block_tensor;
+    const int64_t *block_start;
+    int64_t tensor_count, blocks, chunk;
+    float *master, *exp_avg, *exp_avg_sq;
+    const float *grad_scale;
+    double lr, beta1, beta2, eps, step;
+} bdm_adamw_args;
+
+int bdm_adamw_step(const bdm_adamw_args *args, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

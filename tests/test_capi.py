@@ -133,7 +133,8 @@ def test_struct_layouts_match_the_header(tmp_path):
         pytest.skip('no host C compiler')
     mirrors = {'bdm_forward_args': _lib.ForwardArgs, 'bdm_backward_args': _lib.BackwardArgs,
                'bdm_decode_args': _lib.DecodeArgs, 'bdm_controller_args': _lib.ControllerArgs,
-               'bdm_output_args': _lib.OutputArgs, 'bdm_gemv_args': _lib.GemvArgs}
+               'bdm_output_args': _lib.OutputArgs, 'bdm_gemv_args': _lib.GemvArgs,
+               'bdm_adamw_tensor': _lib.AdamwTensor, 'bdm_adamw_args': _lib.AdamwArgs}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', 'int main(void) {']
     for struct, mirror in mirrors.items():
         lines.append(f'printf("{struct} size %zu\\n", sizeof({struct}));')
@@ -150,6 +151,20 @@ def test_struct_layouts_match_the_header(tmp_path):
         assert got[(struct, 'size')] == ctypes.sizeof(mirror), struct
         for field, _ in mirror._fields_:
             assert got[(struct, field)] == getattr(mirror, field).offset, (struct, field)
+
+
+def test_adamw_rejects_bad_arguments(lib):
+    from bdm_amd import _lib
+    assert lib.bdm_adamw_step(None, None) == -1
+    args = _lib.AdamwArgs()
+    args.blocks, args.chunk, args.tensor_count, args.step = 1, 6, 1, 1.0  # chunk not a multiple of 4
+    assert lib.bdm_adamw_step(ctypes.byref(args), None) == -1
+    assert b'block table' in lib.bdm_last_error_string()
+    args.chunk = 8
+    assert lib.bdm_adamw_step(ctypes.byref(args), None) == -1
+    assert b'null pointer' in lib.bdm_last_error_string()
+    args.blocks = 0
+    assert lib.bdm_adamw_step(ctypes.byref(args), None) == 0  # nothing to update: no launch
 
 
 def test_epilogues_reject_bad_arguments(lib):

@@ -1,0 +1,66 @@
+"""The fused AdamW step against the reference's recipe run with torch
+(reproduction/experiments/optim.py:30-50, "wiki"): clip_grad_norm_(1.0),
+FP32 master gradients, torch's fused AdamW on the masters, masters copied
+into the BF16 weights.  Bit-exact on weights, masters and both moments over
+several steps, with the clip active and inactive and a ragged tensor tail."""
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+SIZES = [(5,), (4099,), (64, 33), (3,), (128, 256), (70000,)]
+
+
+def make_params(device, seed):
+    gen = torch.Generator().manual_seed(seed)
+    params = []
+    for i, shape in enumerate(SIZES):
+        p = torch.nn.Parameter((torch.randn(shape, generator=gen) * 0.05).to(torch.bfloat16).to(device))
+        if i % 3 == 1:
+            p._no_weight_decay = True
+        params.append(p)
+    return params
+
+
+def reference_step(params, masters, optimizer, lr):
+    for group in optimizer.param_groups:
+        group['lr'] = lr
+    norm = torch.nn.utils.clip_grad_norm_(params, 1.0)
+    for p, m in zip(params, masters):
+        m.grad = p.grad.float()
+    optimizer.step()
+    for p, m in zip(params, masters):
+        p.data.copy_(m)
+    return norm
+
+
+def test_fused_adamw_matches_the_reference_recipe():
+    from bdm_amd.optim import MasterAdamW
+    device = torch.device('cuda', 0)
+    ours = make_params(device, 0)
+    ref = make_params(device, 0)
+    masters = [torch.nn.Parameter(p.detach().float().clone()) for p in ref]
+    groups = [{'params': [m for m, p in zip(masters, ref) if bool(getattr(p, '_no_weight_decay', False)) == nd],
+               'weight_decay': 0.0 if nd else 0.01} for nd in (False, True)]
+    optimizer = torch.optim.AdamW(groups, lr=3e-4, betas=(0.9, 0.95), eps=1e-8, fused=True)
+    fused = MasterAdamW(ours, lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.01)
+    gen = torch.Generator().manual_seed(1)
+    # gradient scales: clipped (norm >> 1), unclipped (norm < 1), clipped again
+    for step, (scale, lr) in enumerate([(1.0, 3e-4), (1e-4, 2e-4), (0.3, 1e-3), (2e-5, 5e-4)]):
+        for p, q in zip(ours, ref):
+            g = (torch.randn(p.shape, generator=gen) * scale).to(torch.bfloat16).to(device)
+            p.grad = g.clone()
+            q.grad = g.clone()
+        n_ref = reference_step(ref, masters, optimizer, lr)
+        n_ours = fused.step(lr)
+        torch.cuda.synchronize()
+        assert torch.equal(n_ours, n_ref), step
+        for i, (p, q, m) in enumerate(zip(ours, ref, masters)):
+            state = optimizer.state[m]
+            ea, eas = fused.moments_of(i)
+            assert torch.equal(fused.master_of(i), m.detach()), (step, i, 'master')
+            assert torch.equal(ea, state['exp_avg']), (step, i, 'exp_avg')
+            assert torch.equal(eas, state['exp_avg_sq']), (step, i, 'exp_avg_sq')
+            assert torch.equal(p.detach(), q.detach()), (step, i, 'weight')
+        fused.zero_grad()
