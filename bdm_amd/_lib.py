@@ -28,6 +28,8 @@ EXPORTED_SYMBOLS = (
     'bdm_gemv',
     'bdm_gemv_ex',
     'bdm_adamw_step',
+    'bdm_rms_norm_backward_partials',
+    'bdm_rms_norm_backward',
 )
 
 _i32, _i64, _f32, _vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
@@ -176,6 +178,10 @@ def library() -> ctypes.CDLL:
     lib.bdm_gemv_ex.restype = _i32
     lib.bdm_adamw_step.argtypes = [_vp, _vp]
     lib.bdm_adamw_step.restype = _i32
+    lib.bdm_rms_norm_backward_partials.argtypes = [_i64]
+    lib.bdm_rms_norm_backward_partials.restype = _i64
+    lib.bdm_rms_norm_backward.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _f32, _vp]
+    lib.bdm_rms_norm_backward.restype = _i32
     return lib
 
 

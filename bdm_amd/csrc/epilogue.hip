@@ -318,6 +318,102 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const T *__restrict__ x, 
     }
 }
 
+// Gradients of rms_norm_kernel's normalization (no residual) for training.
+// With xh = x * s, s = rsqrt(mean(x^2) + eps) and y = xh * w in FP32:
+//   dxh = dy * w,  dx = dxh * s - x * s^3 * sum(dxh * x) / width,
+//   dw = sum over rows of dy * xh,
+// the derivative of the FP32 chain of RMSNorm.forward (_shell.py:29-35) that
+// autograd forms op by op.  One wave per row; the 4 waves of a workgroup take
+// kRmsRowsPerBlock consecutive rows and each wave keeps an FP32 partial of dw
+// for its columns; the workgroup adds its waves' partials in LDS and stores
+// one partial row, and rms_norm_weight_grad_kernel sums the partial rows.
+constexpr int kRmsRowsPerBlock = 32;
+
+template <typename T, int MAXC, bool VEC>
+__global__ __launch_bounds__(256) void rms_norm_backward_kernel(const T *__restrict__ x, const T *__restrict__ dy,
+                                                                const void *__restrict__ weight, int weight_dtype,
+                                                                T *__restrict__ dx, float *__restrict__ dw_part,
+                                                                int64_t rows, int width, float eps) {
+    const int lane = threadIdx.x % kWave;
+    const int wave = threadIdx.x / kWave;
+    const int64_t first = int64_t(blockIdx.x) * kRmsRowsPerBlock;
+    const int64_t last = min(rows, first + kRmsRowsPerBlock);
+    float acc[MAXC][8];
+#pragma unroll
+    for (int i = 0; i < MAXC; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = 0.f;
+    for (int64_t row = first + wave; row < last; row += blockDim.x / kWave) {
+        const int64_t base = row * width;
+        float h[MAXC][8], g[MAXC][8];
+        float sq = 0.f;
+#pragma unroll
+        for (int i = 0; i < MAXC; ++i) {
+            const int c = min((lane + i * kWave) * 8, width - 8);
+            const bool live = (lane + i * kWave) * 8 < width;
+            load8<T, VEC>(x + base + c, h[i]);
+            load8<T, VEC>(dy + base + c, g[i]);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) sq = live ? fmaf(h[i][j], h[i][j], sq) : sq;
+        }
+        const float s = rsqrtf(wave_total<kWave>(sq) / float(width) + eps);
+        float dot = 0.f;
+#pragma unroll
+        for (int i = 0; i < MAXC; ++i) {
+            const int c = (lane + i * kWave) * 8;
+            if (c >= width) continue;
+            float wt[8];
+            param8<VEC>(weight, weight_dtype, c, wt);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                acc[i][j] = fmaf(g[i][j], h[i][j] * s, acc[i][j]);
+                g[i][j] *= wt[j];  // dxh
+                dot = fmaf(g[i][j], h[i][j], dot);
+            }
+        }
+        const float coef = wave_total<kWave>(dot) * s * s * s / float(width);
+#pragma unroll
+        for (int i = 0; i < MAXC; ++i) {
+            const int c = (lane + i * kWave) * 8;
+            if (c >= width) continue;
+            float d[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) d[j] = g[i][j] * s - h[i][j] * coef;
+            store_row<8>(dx + base + c, d);
+        }
+    }
+    // the workgroup's partial row: its waves' partials added in wave order
+    extern __shared__ float red[];  // [waves][width]
+#pragma unroll
+    for (int i = 0; i < MAXC; ++i) {
+        const int c = (lane + i * kWave) * 8;
+        if (c < width)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) red[wave * width + c + j] = acc[i][j];
+    }
+    __syncthreads();
+    float *part = dw_part + int64_t(blockIdx.x) * width;
+    for (int c = threadIdx.x; c < width; c += blockDim.x) {
+        float total = red[c];
+        for (int w = 1; w < int(blockDim.x / kWave); ++w) total += red[w * width + c];
+        part[c] = total;
+    }
+}
+
+// dw[c] = sum of the partial rows' column c (in partial-row order), rounded
+// once to the weight's dtype.
+__global__ __launch_bounds__(256) void rms_norm_weight_grad_kernel(const float *__restrict__ dw_part, int64_t parts,
+                                                                   int width, void *__restrict__ dw, int dw_dtype) {
+    const int c = int(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (c >= width) return;
+    float total = 0.f;
+    for (int64_t p = 0; p < parts; ++p) total += dw_part[p * width + c];
+    if (dw_dtype == BDM_BF16)
+        static_cast<bf16_t *>(dw)[c] = from_f32<bf16_t>(total);
+    else
+        static_cast<float *>(dw)[c] = total;
+}
+
 // SwiGLU of the shell's feed-forward (_shell.py:86-91) over the output of one
 // GEMM with the concatenated w1 | w3 weights: row r holds x1 = w1 x in columns
 // [0, hidden) and x3 = w3 x in [hidden, 2 hidden).  out = round(round(silu(x1))
@@ -428,6 +524,65 @@ extern "C" int bdm_rms_norm(const void *x, const void *residual, const void *wei
     else
         go(0.f);
     return check_launch("rms_norm_kernel");
+}
+
+extern "C" int64_t bdm_rms_norm_backward_partials(int64_t rows) {
+    return rows <= 0 ? 0 : (rows + bdm::kRmsRowsPerBlock - 1) / bdm::kRmsRowsPerBlock;
+}
+
+extern "C" int bdm_rms_norm_backward(const void *x, const void *grad_out, const void *weight, void *grad_x,
+                                     void *grad_weight, float *partials, int64_t rows, int32_t width, int32_t dtype,
+                                     int32_t weight_dtype, float eps, void *stream) {
+    using namespace bdm;
+    if (rows < 0 || width <= 0 || width % 8 != 0) return fail(BDM_ERR_INVALID, "rms_norm_backward: bad geometry");
+    if (width > 4096) return fail(BDM_ERR_UNSUPPORTED, "rms_norm_backward: width %d > 4096", width);
+    if (dtype != BDM_BF16 && dtype != BDM_F32) return fail(BDM_ERR_INVALID, "rms_norm_backward: dtype");
+    if (weight_dtype != BDM_BF16 && weight_dtype != BDM_F32)
+        return fail(BDM_ERR_INVALID, "rms_norm_backward: weight dtype");
+    if (!x || !grad_out || !weight || !grad_x || !grad_weight || (rows > 0 && !partials))
+        return fail(BDM_ERR_INVALID, "rms_norm_backward: null pointer");
+    const int64_t parts = bdm_rms_norm_backward_partials(rows);
+    if (parts > int64_t(INT32_MAX)) return fail(BDM_ERR_UNSUPPORTED, "rms_norm_backward: too many rows");
+    hipStream_t s = as_stream(stream);
+    if (rows > 0) {
+        const bool vec = aligned(x, 16) && aligned(grad_out, 16) && aligned(weight, 16) && aligned(grad_x, 16) &&
+                         aligned(partials, 16);
+        const int chunks = (width / 8 + kWave - 1) / kWave;
+        const size_t lds = size_t(4) * width * sizeof(float);
+        auto go = [&](auto tag) {
+            using T = decltype(tag);
+            const T *xp = static_cast<const T *>(x), *gp = static_cast<const T *>(grad_out);
+            T *dp = static_cast<T *>(grad_x);
+#define BDM_RMS_BWD(C)                                                                                        \
+    (vec ? (rms_norm_backward_kernel<T, C, true><<<unsigned(parts), 256, lds, s>>>(xp, gp, weight, weight_dtype, dp, \
+                                                                                   partials, rows, width, eps), \
+            0)                                                                                                 \
+         : (rms_norm_backward_kernel<T, C, false><<<unsigned(parts), 256, lds, s>>>(                          \
+                xp, gp, weight, weight_dtype, dp, partials, rows, width, eps),                                 \
+            0))
+            if (chunks <= 1)
+                BDM_RMS_BWD(1);
+            else if (chunks <= 2)
+                BDM_RMS_BWD(2);
+            else if (chunks <= 4)
+                BDM_RMS_BWD(4);
+            else
+                BDM_RMS_BWD(8);
+#undef BDM_RMS_BWD
+        };
+        if (dtype == BDM_BF16)
+            go(bf16_t{});
+        else
+            go(0.f);
+        if (int rc = check_launch("rms_norm_backward_kernel")) return rc;
+        rms_norm_weight_grad_kernel<<<unsigned((width + 63) / 64), 64, 0, s>>>(partials, parts, width, grad_weight,
+                                                                              weight_dtype);
+    } else {
+        // no rows: the weight gradient is zero
+        rms_norm_weight_grad_kernel<<<unsigned((width + 63) / 64), 64, 0, s>>>(nullptr, 0, width, grad_weight,
+                                                                              weight_dtype);
+    }
+    return check_launch("rms_norm_weight_grad_kernel");
 }
 
 extern "C" int bdm_swiglu(const void *gate_up, void *out, int64_t rows, int32_t hidden, int32_t dtype,

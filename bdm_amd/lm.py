@@ -11,8 +11,10 @@ head projects only the last position.
 
 Under no_grad the shell's elementwise work runs in ``libbdm_hip.so``
 (``bdm_rms_norm``, ``bdm_swiglu``) and the feed-forward's two input
-projections are one GEMM over their concatenated weights; with autograd the
-modules run as the reference writes them.
+projections are one GEMM over their concatenated weights.  With autograd on a
+ROCm device RMSNorm runs as ``bdm_rms_norm`` forward and
+``bdm_rms_norm_backward``; the other modules run as the reference writes
+them.
 """
 
 from __future__ import annotations
@@ -51,8 +53,31 @@ class LanguageModelConfig:
         return dict(asdict(self), memory=self.memory.record())
 
 
+class _RMSNormFunction(torch.autograd.Function):
+    """RMSNorm with HIP forward and backward kernels: one pass each instead
+    of the ~14 FP32 elementwise kernels autograd runs for the torch chain."""
+
+    @staticmethod
+    def forward(ctx, x, weight, eps):
+        ctx.save_for_backward(x, weight)
+        ctx.eps = eps
+        return ops.rms_norm(x, weight, eps)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        x, weight = ctx.saved_tensors
+        grad_x, grad_weight = ops.rms_norm_backward(x, grad_out.contiguous(), weight, ctx.eps)
+        return grad_x, grad_weight, None
+
+
+def _rms_norm_trainable(x: Tensor, weight: Tensor) -> bool:
+    return ops.rms_norm_supported(x) and x.shape[-1] <= 4096 and weight.dtype in (torch.bfloat16, torch.float32)
+
+
 class RMSNorm(nn.Module):
-    """x * rsqrt(mean(x^2) + eps) * weight in FP32, cast back (_shell.py:10-35)."""
+    """x * rsqrt(mean(x^2) + eps) * weight in FP32, cast back (_shell.py:10-35).
+    On a ROCm device the norm and, under autograd, its gradients run in HIP
+    kernels; elsewhere the torch chain of the reference."""
 
     def __init__(self, dim: int, eps: float = 1e-6):
         super().__init__()
@@ -62,7 +87,10 @@ class RMSNorm(nn.Module):
     def forward(self, x: Tensor) -> Tensor:
         if not torch.is_grad_enabled() and ops.rms_norm_supported(x):
             return ops.rms_norm(x, self.weight, self.eps)
-        output = x.float() * torch.rsqrt((x.float() * x.float()).mean(-1, keepdim=True) + self.eps)
+        if _rms_norm_trainable(x, self.weight):
+            return _RMSNormFunction.apply(x.contiguous(), self.weight, self.eps)
+        xf = x.float()
+        output = xf * torch.rsqrt((xf * xf).mean(-1, keepdim=True) + self.eps)
         return (output * self.weight.float()).type_as(x)
 
     def add_norm(self, x: Tensor, residual: Tensor):

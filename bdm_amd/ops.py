@@ -555,6 +555,29 @@ def rms_norm(x: Tensor, weight: Tensor, eps: float, residual: Tensor | None = No
     return out if res is None else (total, out)
 
 
+def rms_norm_backward(x: Tensor, grad_out: Tensor, weight: Tensor, eps: float):
+    """Gradients (grad_x, grad_weight) of ``rms_norm(x, weight, eps)``: the
+    derivative of the shell's FP32 RMSNorm (_shell.py:29-35), one pass over
+    the rows and a column sum for the weight.  width <= 4096."""
+    _require_gpu(x, grad_out, weight)
+    width = x.shape[-1]
+    if not rms_norm_supported(x) or width > 4096:
+        raise ValueError('rms_norm_backward takes BF16/FP32 rows whose width is a multiple of 8, at most 4096')
+    if grad_out.shape != x.shape or grad_out.dtype != x.dtype or weight.shape != (width,):
+        raise ValueError('grad_out must match x and weight must be [width]')
+    x, grad_out, weight = _aligned(x), _aligned(grad_out), _aligned(weight)
+    rows = x.numel() // width
+    lib = _lib.library()
+    partials = torch.empty(max(int(lib.bdm_rms_norm_backward_partials(rows)), 1) * width, device=x.device,
+                           dtype=torch.float32)
+    grad_x = torch.empty_like(x)
+    grad_weight = torch.empty_like(weight)
+    _lib.check(lib.bdm_rms_norm_backward(
+        _ptr(x), _ptr(grad_out), _ptr(weight), _ptr(grad_x), _ptr(grad_weight), _ptr(partials), rows, width,
+        _dtype_code(x.dtype), _dtype_code(weight.dtype), float(eps), _stream(x.device)), 'bdm_rms_norm_backward')
+    return grad_x, grad_weight
+
+
 def swiglu(gate_up: Tensor, hidden: int) -> Tensor:
     """silu(x1) * x3 of the shell's feed-forward (_shell.py:86-91) from the
     output [..., 2*hidden] of one GEMM with the concatenated w1 | w3 weights."""

@@ -316,6 +316,17 @@ int bdm_rms_norm(const void *x, const void *residual, const void *weight, void *
  * roundings torch makes in dtype.  hidden: a multiple of 8. */
 int bdm_swiglu(const void *gate_up, void *out, int64_t rows, int32_t hidden, int32_t dtype, void *stream);
 
+/* Gradients of bdm_rms_norm without a residual, for training: the derivative
+ * of the FP32 chain of RMSNorm.forward (_shell.py:29-35) that autograd forms.
+ * grad_x [rows, width] of dtype, grad_weight [width] of weight_dtype (FP32
+ * sum over rows, one rounding).  partials: FP32 scratch of
+ * bdm_rms_norm_backward_partials(rows) * width elements, 16-byte aligned.
+ * width: a multiple of 8, at most 4096. */
+int64_t bdm_rms_norm_backward_partials(int64_t rows);
+int bdm_rms_norm_backward(const void *x, const void *grad_out, const void *weight, void *grad_x, void *grad_weight,
+                          float *partials, int64_t rows, int32_t width, int32_t dtype, int32_t weight_dtype,
+                          float eps, void *stream);
+
 /* y[m] = W x[m] + bias for the few rows of a decode step: torch's F.linear
  * (nn.Linear.forward, used by every projection of implementation/bdm/
  * _parameters.py:189-232 and _shell.py:86-91) when the batch of rows is 1 to

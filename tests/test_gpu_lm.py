@@ -64,6 +64,37 @@ def test_rms_norm_matches_torch(device, dtype, width):
 
 
 @pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float32], ids=['bf16', 'f32'])
+@pytest.mark.parametrize('width', [8, 520, 2048, 4096])
+def test_rms_norm_backward_matches_float64(device, dtype, width):
+    """Gradients of the shell's RMSNorm from ``bdm_rms_norm_backward`` against
+    the exact (float64) derivative, with torch's autograd of the reference's
+    chain in the same dtype as the yardstick: our error at most twice torch's
+    plus an FP32 rounding.  100 rows: a ragged last block of 32 rows."""
+    from bdm_amd import ops
+    gen = torch.Generator().manual_seed(width + 1)
+    x = (torch.randn(100, width, generator=gen) * 2).to(dtype)
+    dy = torch.randn(100, width, generator=gen).to(dtype)
+    for wdt in (torch.float32, torch.bfloat16):
+        weight = (1 + 0.1 * torch.randn(width, generator=gen)).to(wdt)
+        x64 = x.double().requires_grad_(True)
+        w64 = weight.double().requires_grad_(True)
+        y64 = x64 * torch.rsqrt((x64 * x64).mean(-1, keepdim=True) + 1e-5) * w64
+        dx64, dw64 = torch.autograd.grad(y64, (x64, w64), dy.double())
+        xt = x.to(device).requires_grad_(True)
+        wt = weight.to(device).requires_grad_(True)
+        dxt, dwt = torch.autograd.grad(torch_rms(xt, wt, 1e-5), (xt, wt), dy.to(device))
+        announce('rms_norm_backward', dtype, width, wdt)
+        dx, dw = ops.rms_norm_backward(x.to(device), dy.to(device), weight.to(device), 1e-5)
+        torch.cuda.synchronize()
+        assert dx.dtype == dtype and dw.dtype == wdt
+        for ours, yard, exact in ((dx, dxt, dx64), (dw, dwt, dw64)):
+            exact = exact.to(device)
+            err = float((ours.double() - exact).abs().max())
+            bound = 2 * float((yard.double() - exact).abs().max()) + 1e-6 * float(exact.abs().max())
+            assert err <= bound, (err, bound)
+
+
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float32], ids=['bf16', 'f32'])
 def test_swiglu_matches_torch(device, dtype):
     """silu(x1) * x3 with torch's rounding points: BF16 equal but for
     one-ulp exp differences (checked as at most 1 % of elements, each within
