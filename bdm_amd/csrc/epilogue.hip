@@ -400,18 +400,32 @@ __global__ __launch_bounds__(256) void rms_norm_backward_kernel(const T *__restr
     }
 }
 
-// dw[c] = sum of the partial rows' column c (in partial-row order), rounded
-// once to the weight's dtype.
-__global__ __launch_bounds__(256) void rms_norm_weight_grad_kernel(const float *__restrict__ dw_part, int64_t parts,
-                                                                   int width, void *__restrict__ dw, int dw_dtype) {
-    const int c = int(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (c >= width) return;
+// dw[c] = sum of the partial rows' column c, rounded once to the weight's
+// dtype.  A workgroup of 16 waves owns 64 columns: wave k sums the partial
+// rows k, k + 16, ... (loads unrolled, many in flight), and the 16 wave sums
+// are added in wave order, so the result repeats bit for bit.
+constexpr int kRmsSumWaves = 16;
+
+__global__ __launch_bounds__(kRmsSumWaves * 64) void rms_norm_weight_grad_kernel(const float *__restrict__ dw_part,
+                                                                                 int64_t parts, int width,
+                                                                                 void *__restrict__ dw, int dw_dtype) {
+    __shared__ float slice[kRmsSumWaves][64];
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const int c = int(blockIdx.x) * 64 + lane;
     float total = 0.f;
-    for (int64_t p = 0; p < parts; ++p) total += dw_part[p * width + c];
+    if (c < width) {
+#pragma unroll 8
+        for (int64_t p = wave; p < parts; p += kRmsSumWaves) total += dw_part[p * width + c];
+    }
+    slice[wave][lane] = total;
+    __syncthreads();
+    if (wave != 0 || c >= width) return;
+    float sum = slice[0][lane];
+    for (int k = 1; k < kRmsSumWaves; ++k) sum += slice[k][lane];
     if (dw_dtype == BDM_BF16)
-        static_cast<bf16_t *>(dw)[c] = from_f32<bf16_t>(total);
+        static_cast<bf16_t *>(dw)[c] = from_f32<bf16_t>(sum);
     else
-        static_cast<float *>(dw)[c] = total;
+        static_cast<float *>(dw)[c] = sum;
 }
 
 // SwiGLU of the shell's feed-forward (_shell.py:86-91) over the output of one
@@ -575,12 +589,12 @@ extern "C" int bdm_rms_norm_backward(const void *x, const void *grad_out, const 
         else
             go(0.f);
         if (int rc = check_launch("rms_norm_backward_kernel")) return rc;
-        rms_norm_weight_grad_kernel<<<unsigned((width + 63) / 64), 64, 0, s>>>(partials, parts, width, grad_weight,
-                                                                              weight_dtype);
+        rms_norm_weight_grad_kernel<<<unsigned((width + 63) / 64), kRmsSumWaves * 64, 0, s>>>(
+            partials, parts, width, grad_weight, weight_dtype);
     } else {
         // no rows: the weight gradient is zero
-        rms_norm_weight_grad_kernel<<<unsigned((width + 63) / 64), 64, 0, s>>>(nullptr, 0, width, grad_weight,
-                                                                              weight_dtype);
+        rms_norm_weight_grad_kernel<<<unsigned((width + 63) / 64), kRmsSumWaves * 64, 0, s>>>(
+            nullptr, 0, width, grad_weight, weight_dtype);
     }
     return check_launch("rms_norm_weight_grad_kernel");
 }
