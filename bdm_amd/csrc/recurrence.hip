@@ -347,13 +347,23 @@ struct GatedValues<float, CPL> {
     __device__ __forceinline__ float add_to(float acc, int c) const { return acc + x[c]; }
 };
 
-// Inclusive prefix product over the 16 lanes of a DPP row (lane order).
+// Inclusive prefix product over the 16 lanes of a DPP row (lane order).  Each
+// step is one v_mul_f32 with a row_shr DPP source and bound_ctrl off: a lane
+// whose source lies before the row start does not write, so it keeps x (the
+// product with 1), one instruction where a DPP move of 1.0-filled lanes and a
+// multiply take two.  The s_nop gives the 2 wait states a DPP read of a VGPR
+// needs after a VALU write of it.
 __device__ __forceinline__ float row_prefix_product(float x) {
-    const int one = __float_as_int(1.f);
-    x *= __int_as_float(__builtin_amdgcn_update_dpp(one, __float_as_int(x), 0x111, 0xf, 0xf, false));  // row_shr:1
-    x *= __int_as_float(__builtin_amdgcn_update_dpp(one, __float_as_int(x), 0x112, 0xf, 0xf, false));  // row_shr:2
-    x *= __int_as_float(__builtin_amdgcn_update_dpp(one, __float_as_int(x), 0x114, 0xf, 0xf, false));  // row_shr:4
-    x *= __int_as_float(__builtin_amdgcn_update_dpp(one, __float_as_int(x), 0x118, 0xf, 0xf, false));  // row_shr:8
+    asm volatile(
+        "s_nop 1\n\t"
+        "v_mul_f32_dpp %0, %0, %0 row_shr:1 row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 1\n\t"
+        "v_mul_f32_dpp %0, %0, %0 row_shr:2 row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 1\n\t"
+        "v_mul_f32_dpp %0, %0, %0 row_shr:4 row_mask:0xf bank_mask:0xf\n\t"
+        "s_nop 1\n\t"
+        "v_mul_f32_dpp %0, %0, %0 row_shr:8 row_mask:0xf bank_mask:0xf"
+        : "+v"(x));
     return x;
 }
 
