@@ -356,6 +356,27 @@ __device__ __forceinline__ float row_shift(float x) {
                                                                  __builtin_bit_cast(int, x), CTRL, 0xF, 0xF, false));
 }
 
+// x * (x of the lane CTRL selects within the row), or x where that lane lies
+// outside the row: one v_mul_f32 with a DPP source and bound_ctrl off (the
+// lane without a source does not write).  CTRL: 0x111/0x112/0x114/0x118 are
+// row_shr 1/2/4/8, 0x101/0x102/0x104/0x108 row_shl 1/2/4/8.  The s_nop gives
+// the 2 wait states a DPP read of a VGPR needs after a VALU write of it.
+template <int CTRL>
+__device__ __forceinline__ float row_mul_step(float x) {
+#define BDM_DPP_MUL(SEL) asm volatile("s_nop 1\n\tv_mul_f32_dpp %0, %0, %0 " SEL " row_mask:0xf bank_mask:0xf" : "+v"(x))
+    if constexpr (CTRL == 0x111) BDM_DPP_MUL("row_shr:1");
+    else if constexpr (CTRL == 0x112) BDM_DPP_MUL("row_shr:2");
+    else if constexpr (CTRL == 0x114) BDM_DPP_MUL("row_shr:4");
+    else if constexpr (CTRL == 0x118) BDM_DPP_MUL("row_shr:8");
+    else if constexpr (CTRL == 0x101) BDM_DPP_MUL("row_shl:1");
+    else if constexpr (CTRL == 0x102) BDM_DPP_MUL("row_shl:2");
+    else if constexpr (CTRL == 0x104) BDM_DPP_MUL("row_shl:4");
+    else if constexpr (CTRL == 0x108) BDM_DPP_MUL("row_shl:8");
+    else static_assert(CTRL == 0x111, "row_mul_step: unsupported DPP control");
+#undef BDM_DPP_MUL
+    return x;
+}
+
 // Total of a 16-lane row in every lane of the row.
 __device__ __forceinline__ float row_total(float x) {
     x = dpp_add<0xB1>(x);      // quad_perm [1,0,3,2]
@@ -539,14 +560,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void ch
                 d[i] = wr ? __expf(p.routed_decay ? gv[i] * pw : gv[i]) : 1.f;
                 a[i] = round_to<T>(bv[i] * pw) * x[i];
                 // inclusive prefix and suffix products of the decays over the chunk's events
-                pre[i] = d[i] * row_shift<0x111>(d[i]);
-                pre[i] *= row_shift<0x112>(pre[i]);
-                pre[i] *= row_shift<0x114>(pre[i]);
-                pre[i] *= row_shift<0x118>(pre[i]);
-                suf[i] = d[i] * row_shift<0x101>(d[i]);
-                suf[i] *= row_shift<0x102>(suf[i]);
-                suf[i] *= row_shift<0x104>(suf[i]);
-                suf[i] *= row_shift<0x108>(suf[i]);
+                pre[i] = row_mul_step<0x118>(row_mul_step<0x114>(row_mul_step<0x112>(row_mul_step<0x111>(d[i]))));
+                suf[i] = row_mul_step<0x108>(row_mul_step<0x104>(row_mul_step<0x102>(row_mul_step<0x101>(d[i]))));
                 pre_x[i] = row_shift<0x111>(pre[i]);
                 suf_x[i] = row_shift<0x101>(suf[i]);
                 const float lo = 0x1p-40f, hi = 0x1p40f;
