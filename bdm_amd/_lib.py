@@ -30,6 +30,8 @@ EXPORTED_SYMBOLS = (
     'bdm_adamw_step',
     'bdm_rms_norm_backward_partials',
     'bdm_rms_norm_backward',
+    'bdm_swiglu_pair',
+    'bdm_swiglu_backward',
 )
 
 _i32, _i64, _f32, _vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
@@ -182,6 +184,10 @@ def library() -> ctypes.CDLL:
     lib.bdm_rms_norm_backward_partials.restype = _i64
     lib.bdm_rms_norm_backward.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _f32, _vp]
     lib.bdm_rms_norm_backward.restype = _i32
+    lib.bdm_swiglu_pair.argtypes = [_vp, _vp, _vp, _i64, _i32, _vp]
+    lib.bdm_swiglu_pair.restype = _i32
+    lib.bdm_swiglu_backward.argtypes = [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _vp]
+    lib.bdm_swiglu_backward.restype = _i32
     return lib
 
 

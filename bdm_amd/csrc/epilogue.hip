@@ -450,6 +450,64 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const T *__restrict__ gate_
     store_row<8>(out + row * hidden + c, y);
 }
 
+// The SwiGLU element over two separate tensors (the training path's w1 x and
+// w3 x, _shell.py:86-91), 8 consecutive elements per thread.
+template <typename T, bool VEC>
+__global__ __launch_bounds__(256) void swiglu_pair_kernel(const T *__restrict__ a, const T *__restrict__ b,
+                                                          T *__restrict__ out, int64_t n) {
+    const int64_t i = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
+    if (i >= n) return;
+    if (VEC && i + 8 <= n) {
+        float x[8], y[8], z[8];
+        load8<T, true>(a + i, x);
+        load8<T, true>(b + i, y);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) z[j] = swiglu_value<T>(x[j], y[j]);
+        store_row<8>(out + i, z);
+    } else {
+        for (int64_t e = i; e < min(n, i + 8); ++e) out[e] = from_f32<T>(swiglu_value<T>(to_f32(a[e]), to_f32(b[e])));
+    }
+}
+
+// Gradients of h = round(silu(a)) * b in the order and dtype autograd forms
+// them for F.silu(a) * b: s = round(silu(a)), db = round(dy * s),
+// ds = round(dy * b), da = round(ds * sig * (1 + a * (1 - sig))) with
+// sig = 1 / (1 + exp(-a)) in FP32 (silu's backward).
+__device__ __forceinline__ void swiglu_grad(float a, float b, float dy, float &da, float &db, bool bf16) {
+    const float sig = 1.f / (1.f + expf(-a));
+    const float s = a / (1.f + expf(-a));
+    const float sr = bf16 ? round_bf16(s) : s;
+    const float ds = bf16 ? round_bf16(dy * b) : dy * b;
+    db = dy * sr;
+    da = ds * sig * (1.f + a * (1.f - sig));
+}
+
+template <typename T, bool VEC>
+__global__ __launch_bounds__(256) void swiglu_backward_kernel(const T *__restrict__ a, const T *__restrict__ b,
+                                                              const T *__restrict__ dy, T *__restrict__ da,
+                                                              T *__restrict__ db, int64_t n) {
+    constexpr bool kBf16 = sizeof(T) == 2;
+    const int64_t i = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) * 8;
+    if (i >= n) return;
+    if (VEC && i + 8 <= n) {
+        float x[8], y[8], g[8], ga[8], gb[8];
+        load8<T, true>(a + i, x);
+        load8<T, true>(b + i, y);
+        load8<T, true>(dy + i, g);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) swiglu_grad(x[j], y[j], g[j], ga[j], gb[j], kBf16);
+        store_row<8>(da + i, ga);
+        store_row<8>(db + i, gb);
+    } else {
+        for (int64_t e = i; e < min(n, i + 8); ++e) {
+            float ga, gb;
+            swiglu_grad(to_f32(a[e]), to_f32(b[e]), to_f32(dy[e]), ga, gb, kBf16);
+            da[e] = from_f32<T>(ga);
+            db[e] = from_f32<T>(gb);
+        }
+    }
+}
+
 }  // namespace
 }  // namespace bdm
 
@@ -627,4 +685,58 @@ extern "C" int bdm_swiglu(const void *gate_up, void *out, int64_t rows, int32_t 
             swiglu_kernel<float, false><<<blocks, 256, 0, s>>>(in, o, rows, hidden);
     }
     return check_launch("swiglu_kernel");
+}
+
+extern "C" int bdm_swiglu_pair(const void *a, const void *b, void *out, int64_t n, int32_t dtype, void *stream) {
+    using namespace bdm;
+    if (n < 0) return fail(BDM_ERR_INVALID, "swiglu_pair: bad size");
+    if (dtype != BDM_BF16 && dtype != BDM_F32) return fail(BDM_ERR_INVALID, "swiglu_pair: dtype");
+    if (n == 0) return BDM_OK;
+    if (!a || !b || !out) return fail(BDM_ERR_INVALID, "swiglu_pair: null pointer");
+    const int64_t blocks = (n + 8 * 256 - 1) / (8 * 256);
+    if (blocks > int64_t(INT32_MAX)) return fail(BDM_ERR_UNSUPPORTED, "swiglu_pair: too many elements");
+    const bool vec = aligned(a, 16) && aligned(b, 16) && aligned(out, 16);
+    hipStream_t s = as_stream(stream);
+    auto go = [&](auto tag) {
+        using T = decltype(tag);
+        auto *pa = static_cast<const T *>(a), *pb = static_cast<const T *>(b);
+        auto *po = static_cast<T *>(out);
+        if (vec)
+            swiglu_pair_kernel<T, true><<<unsigned(blocks), 256, 0, s>>>(pa, pb, po, n);
+        else
+            swiglu_pair_kernel<T, false><<<unsigned(blocks), 256, 0, s>>>(pa, pb, po, n);
+    };
+    if (dtype == BDM_BF16)
+        go(bf16_t{});
+    else
+        go(0.f);
+    return check_launch("swiglu_pair_kernel");
+}
+
+extern "C" int bdm_swiglu_backward(const void *a, const void *b, const void *grad_out, void *grad_a, void *grad_b,
+                                   int64_t n, int32_t dtype, void *stream) {
+    using namespace bdm;
+    if (n < 0) return fail(BDM_ERR_INVALID, "swiglu_backward: bad size");
+    if (dtype != BDM_BF16 && dtype != BDM_F32) return fail(BDM_ERR_INVALID, "swiglu_backward: dtype");
+    if (n == 0) return BDM_OK;
+    if (!a || !b || !grad_out || !grad_a || !grad_b) return fail(BDM_ERR_INVALID, "swiglu_backward: null pointer");
+    const int64_t blocks = (n + 8 * 256 - 1) / (8 * 256);
+    if (blocks > int64_t(INT32_MAX)) return fail(BDM_ERR_UNSUPPORTED, "swiglu_backward: too many elements");
+    const bool vec = aligned(a, 16) && aligned(b, 16) && aligned(grad_out, 16) && aligned(grad_a, 16) &&
+                     aligned(grad_b, 16);
+    hipStream_t s = as_stream(stream);
+    auto go = [&](auto tag) {
+        using T = decltype(tag);
+        auto *pa = static_cast<const T *>(a), *pb = static_cast<const T *>(b), *pg = static_cast<const T *>(grad_out);
+        auto *da = static_cast<T *>(grad_a), *db = static_cast<T *>(grad_b);
+        if (vec)
+            swiglu_backward_kernel<T, true><<<unsigned(blocks), 256, 0, s>>>(pa, pb, pg, da, db, n);
+        else
+            swiglu_backward_kernel<T, false><<<unsigned(blocks), 256, 0, s>>>(pa, pb, pg, da, db, n);
+    };
+    if (dtype == BDM_BF16)
+        go(bf16_t{});
+    else
+        go(0.f);
+    return check_launch("swiglu_backward_kernel");
 }

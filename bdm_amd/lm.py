@@ -13,8 +13,9 @@ Under no_grad the shell's elementwise work runs in ``libbdm_hip.so``
 (``bdm_rms_norm``, ``bdm_swiglu``) and the feed-forward's two input
 projections are one GEMM over their concatenated weights.  With autograd on a
 ROCm device RMSNorm runs as ``bdm_rms_norm`` forward and
-``bdm_rms_norm_backward``; the other modules run as the reference writes
-them.
+``bdm_rms_norm_backward`` and the feed-forward's SwiGLU as
+``bdm_swiglu_pair`` and ``bdm_swiglu_backward``; the other modules run as the
+reference writes them.
 """
 
 from __future__ import annotations
@@ -68,6 +69,21 @@ class _RMSNormFunction(torch.autograd.Function):
         x, weight = ctx.saved_tensors
         grad_x, grad_weight = ops.rms_norm_backward(x, grad_out.contiguous(), weight, ctx.eps)
         return grad_x, grad_weight, None
+
+
+class _SwiGLUFunction(torch.autograd.Function):
+    """F.silu(a) * b with HIP forward and backward kernels (one pass each
+    instead of silu, the product and their three backward kernels)."""
+
+    @staticmethod
+    def forward(ctx, a, b):
+        ctx.save_for_backward(a, b)
+        return ops.swiglu_pair(a, b)
+
+    @staticmethod
+    def backward(ctx, grad_out):
+        a, b = ctx.saved_tensors
+        return ops.swiglu_backward(a, b, grad_out)
 
 
 def _rms_norm_trainable(x: Tensor, weight: Tensor) -> bool:
@@ -142,7 +158,10 @@ class FeedForward(nn.Module):
         return self._forward(x)
 
     def _forward(self, x: Tensor) -> Tensor:
-        return self.w2(F.silu(self.w1(x)) * self.w3(x))
+        x1, x3 = self.w1(x), self.w3(x)
+        if x1.is_cuda and x1.dtype in (torch.bfloat16, torch.float32):
+            return self.w2(_SwiGLUFunction.apply(x1, x3))
+        return self.w2(F.silu(x1) * x3)
 
     def reset_parameters(self, init_std=None, factor=1.0):
         in_std = init_std or self.dim ** -0.5

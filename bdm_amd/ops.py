@@ -578,6 +578,33 @@ def rms_norm_backward(x: Tensor, grad_out: Tensor, weight: Tensor, eps: float):
     return grad_x, grad_weight
 
 
+def swiglu_pair(a: Tensor, b: Tensor) -> Tensor:
+    """round(round(silu(a)) * b) elementwise (the shell's SwiGLU with its two
+    inputs from separate GEMMs, _shell.py:86-91)."""
+    _require_gpu(a, b)
+    if a.shape != b.shape or a.dtype != b.dtype or a.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError('swiglu_pair takes two BF16/FP32 tensors of one shape')
+    a, b = a.contiguous(), b.contiguous()
+    out = torch.empty_like(a)
+    _lib.check(_lib.library().bdm_swiglu_pair(_ptr(a), _ptr(b), _ptr(out), a.numel(), _dtype_code(a.dtype),
+                                               _stream(a.device)), 'bdm_swiglu_pair')
+    return out
+
+
+def swiglu_backward(a: Tensor, b: Tensor, grad_out: Tensor):
+    """(grad_a, grad_b) of ``swiglu_pair(a, b)`` as autograd forms them for
+    F.silu(a) * b."""
+    _require_gpu(a, b, grad_out)
+    if not (a.shape == b.shape == grad_out.shape) or not (a.dtype == b.dtype == grad_out.dtype):
+        raise ValueError('swiglu_backward takes three tensors of one shape and dtype')
+    a, b, grad_out = a.contiguous(), b.contiguous(), grad_out.contiguous()
+    grad_a, grad_b = torch.empty_like(a), torch.empty_like(b)
+    _lib.check(_lib.library().bdm_swiglu_backward(_ptr(a), _ptr(b), _ptr(grad_out), _ptr(grad_a), _ptr(grad_b),
+                                                   a.numel(), _dtype_code(a.dtype), _stream(a.device)),
+               'bdm_swiglu_backward')
+    return grad_a, grad_b
+
+
 def swiglu(gate_up: Tensor, hidden: int) -> Tensor:
     """silu(x1) * x3 of the shell's feed-forward (_shell.py:86-91) from the
     output [..., 2*hidden] of one GEMM with the concatenated w1 | w3 weights."""

@@ -322,6 +322,17 @@ int bdm_swiglu(const void *gate_up, void *out, int64_t rows, int32_t hidden, int
  * sum over rows, one rounding).  partials: FP32 scratch of
  * bdm_rms_norm_backward_partials(rows) * width elements, 16-byte aligned.
  * width: a multiple of 8, at most 4096. */
+/* The SwiGLU product of the training path, whose two inputs come from
+ * separate GEMMs (_shell.py:86-91, FeedForward._forward: F.silu(w1 x) * w3 x):
+ * out[i] = round(round(silu(a[i])) * b[i]) over n elements of dtype, the
+ * element of bdm_swiglu.  bdm_swiglu_backward forms autograd's gradients of
+ * that product in the same dtype: s = round(silu(a)), grad_b =
+ * round(grad_out * s), grad_a = round(round(grad_out * b) * silu'(a)), silu'
+ * in FP32. */
+int bdm_swiglu_pair(const void *a, const void *b, void *out, int64_t n, int32_t dtype, void *stream);
+int bdm_swiglu_backward(const void *a, const void *b, const void *grad_out, void *grad_a, void *grad_b, int64_t n,
+                        int32_t dtype, void *stream);
+
 int64_t bdm_rms_norm_backward_partials(int64_t rows);
 int bdm_rms_norm_backward(const void *x, const void *grad_out, const void *weight, void *grad_x, void *grad_weight,
                           float *partials, int64_t rows, int32_t width, int32_t dtype, int32_t weight_dtype,

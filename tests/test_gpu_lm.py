@@ -129,6 +129,33 @@ def _golden_model(device):
     return golden, memory, config, model.to(device)
 
 
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float32], ids=['bf16', 'f32'])
+def test_swiglu_training_pair_matches_autograd(device, dtype):
+    """bdm_swiglu_pair and bdm_swiglu_backward against torch's F.silu(a) * b
+    and its autograd in the same dtype: BF16 within one ulp (at most 2 % of
+    elements differ: exp and rounding order), FP32 within 1e-5.  37 x 1001
+    elements: a ragged tail past the last group of 8."""
+    from bdm_amd import ops
+    gen = torch.Generator().manual_seed(11)
+    a = (torch.randn(37, 1001, generator=gen) * 4).to(dtype).to(device)
+    b = torch.randn(37, 1001, generator=gen).to(dtype).to(device)
+    dy = torch.randn(37, 1001, generator=gen).to(dtype).to(device)
+    announce('swiglu pair', dtype)
+    out = ops.swiglu_pair(a, b)
+    ga, gb = ops.swiglu_backward(a, b, dy)
+    at, bt = a.clone().requires_grad_(True), b.clone().requires_grad_(True)
+    ref = F.silu(at) * bt
+    ra, rb = torch.autograd.grad(ref, (at, bt), dy)
+    torch.cuda.synchronize()
+    for ours, theirs in ((out, ref.detach()), (ga, ra), (gb, rb)):
+        if dtype == torch.float32:
+            assert rel_err(ours, theirs) < 1e-5
+        else:
+            diff = (ours.float() - theirs.float()).abs()
+            assert bool((diff <= theirs.float().abs() * 2 ** -7 + 1e-30).all())
+            assert float((diff > 0).float().mean()) < 0.02
+
+
 def test_lm_matches_reference_fixture(device):
     """FP32 weights; the layer rounds its training state to BF16 every 16
     events as the reference does.  Logits within 1e-4 of the largest, loss
