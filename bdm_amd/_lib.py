@@ -32,6 +32,7 @@ EXPORTED_SYMBOLS = (
     'bdm_rms_norm_backward',
     'bdm_swiglu_pair',
     'bdm_swiglu_backward',
+    'bdm_dispatch_workspace_size_ex',
 )
 
 _i32, _i64, _f32, _vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
@@ -188,6 +189,8 @@ def library() -> ctypes.CDLL:
     lib.bdm_swiglu_pair.restype = _i32
     lib.bdm_swiglu_backward.argtypes = [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _vp]
     lib.bdm_swiglu_backward.restype = _i32
+    lib.bdm_dispatch_workspace_size_ex.argtypes = [_i64, _i64, _i32, _i32, _i32]
+    lib.bdm_dispatch_workspace_size_ex.restype = _size_t
     return lib
 
 

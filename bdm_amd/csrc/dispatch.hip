@@ -19,6 +19,14 @@
 //      popcount(mask[bank] & below(bit)), i.e. the number of earlier
 //      (t, phase) slots of the tile that hit the same bank.  That is the
 //      stable order, computed without any serial step.
+//
+// The masks take one 64-bit LDS word per bank, so that path serves up to
+// 8192 banks.  Above that (the reference's T = N = 2^20 whole-model run has
+// J = 131,072) the keys themselves are radix-sorted (hipCUB, over only the
+// key bits the geometry can set) with the original event index as the value;
+// unique keys make the result the same permutation.
+#include <hipcub/hipcub.hpp>
+
 #include "bdm_common.h"
 
 namespace bdm {
@@ -169,6 +177,89 @@ __global__ __launch_bounds__(512) void dispatch_scatter(const int64_t *__restric
     }
 }
 
+// ---- sort path (bank_count > kMaxBanks)
+
+__device__ __forceinline__ int64_t event_token(int64_t e, const DispatchGeometry &g) {
+    return e < g.nt * g.kw ? e / g.kw : (e - g.nt * g.kw) / g.kr;
+}
+
+// key[e] = ((b*J + bank)*T + t)*2 + is_read and value[e] = e for every event
+// in original order (writes, then reads).
+__global__ __launch_bounds__(256) void dispatch_sort_keys(const int64_t *__restrict__ wi,
+                                                          const int64_t *__restrict__ ri, DispatchGeometry g,
+                                                          uint64_t *__restrict__ keys, int32_t *__restrict__ values,
+                                                          int32_t *status) {
+    const int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t events = g.nt * (g.kw + g.kr);
+    if (e >= events) return;
+    const bool rd = e >= g.nt * g.kw;
+    const int64_t raw = rd ? ri[e - g.nt * g.kw] : wi[e];
+    int64_t bank = raw;
+    if (raw < 0 || raw >= g.banks) {
+        atomicOr(status, int(BDM_ROUTE_OUT_OF_RANGE));
+        bank = raw < 0 ? 0 : g.banks - 1;
+    }
+    const int64_t token = event_token(e, g);
+    const int64_t b = token / g.time, t = token - b * g.time;
+    keys[e] = uint64_t(((b * g.banks + bank) * g.time + t) * 2 + (rd ? 1 : 0));
+    values[e] = int32_t(e);
+}
+
+// Slot i of the sorted keys: order, inverse and tokens, the segment bounds
+// that fall at i, and the duplicate flag (equal neighbouring keys).
+__global__ __launch_bounds__(256) void dispatch_sort_finish(const uint64_t *__restrict__ keys,
+                                                            const int32_t *__restrict__ values, DispatchGeometry g,
+                                                            int64_t *__restrict__ order, int64_t *__restrict__ inverse,
+                                                            int64_t *__restrict__ tokens,
+                                                            int64_t *__restrict__ cu_seqlens, int32_t *status) {
+    const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int64_t events = g.nt * (g.kw + g.kr);
+    const int64_t nseg = g.batch * g.banks;
+    if (i >= events) return;
+    const int64_t o = values[i];
+    order[i] = o;
+    inverse[o] = i;
+    tokens[i] = event_token(o, g);
+    const uint64_t key = keys[i];
+    const int64_t seg = int64_t(key / uint64_t(2 * g.time));
+    int64_t prev = -1;
+    if (i > 0) {
+        const uint64_t pk = keys[i - 1];
+        if (pk == key) atomicOr(status, int(BDM_ROUTE_DUPLICATE));
+        prev = int64_t(pk / uint64_t(2 * g.time));
+    }
+    for (int64_t sg = prev + 1; sg <= seg; ++sg) cu_seqlens[sg] = i;  // segments that start here
+    if (i == events - 1)
+        for (int64_t sg = seg + 1; sg <= nseg; ++sg) cu_seqlens[sg] = events;
+}
+
+struct SortWorkspace {
+    size_t keys = 0, values = 0, temp = 0, total = 0;
+};
+
+int key_bits(int64_t batch, int64_t time, int32_t banks) {
+    const uint64_t max_key = uint64_t(batch) * uint64_t(banks) * uint64_t(time) * 2;  // exclusive bound
+    int bits = 1;
+    while (bits < 64 && (uint64_t(1) << bits) < max_key) ++bits;
+    return bits;
+}
+
+SortWorkspace sort_workspace(int64_t batch, int64_t time, int32_t banks, int64_t events) {
+    auto up = [](size_t x) { return (x + 255) / 256 * 256; };
+    SortWorkspace w;
+    w.keys = up(size_t(events) * sizeof(uint64_t));
+    w.values = up(size_t(events) * sizeof(int32_t));
+    size_t temp = 0;
+    // a failed size query leaves temp 0; the sort itself then reports the error
+    (void)hipcub::DeviceRadixSort::SortPairs(nullptr, temp, static_cast<const uint64_t *>(nullptr),
+                                       static_cast<uint64_t *>(nullptr), static_cast<const int32_t *>(nullptr),
+                                       static_cast<int32_t *>(nullptr), int(events), 0,
+                                       key_bits(batch, time, banks));
+    w.temp = up(temp);
+    w.total = 2 * w.keys + 2 * w.values + w.temp;
+    return w;
+}
+
 }  // namespace
 }  // namespace bdm
 
@@ -178,9 +269,18 @@ using bdm::kTileTokens;
 static int64_t tiles_per_batch(int64_t time) { return (time + kTileTokens - 1) / kTileTokens; }
 
 extern "C" size_t bdm_dispatch_workspace_size(int64_t batch, int64_t time, int32_t bank_count) {
-    if (batch <= 0 || time <= 0 || bank_count <= 0) return 0;
+    if (batch <= 0 || time <= 0 || bank_count <= 0 || bank_count > kMaxBanks) return 0;
     // per-tile bucket counts, then per-segment totals
     return size_t(batch) * (size_t(tiles_per_batch(time)) + 1) * size_t(bank_count) * sizeof(int32_t);
+}
+
+extern "C" size_t bdm_dispatch_workspace_size_ex(int64_t batch, int64_t time, int32_t bank_count,
+                                                 int32_t write_banks, int32_t read_banks) {
+    if (batch <= 0 || time <= 0 || bank_count <= 0 || write_banks < 0 || read_banks < 0) return 0;
+    if (bank_count <= kMaxBanks) return bdm_dispatch_workspace_size(batch, time, bank_count);
+    const int64_t events = batch * time * (int64_t(write_banks) + read_banks);
+    if (events <= 0 || events >= (int64_t(1) << 31)) return 0;
+    return bdm::sort_workspace(batch, time, bank_count, events).total;
 }
 
 extern "C" int bdm_dispatch_build(const int64_t *write_indices, const int64_t *read_indices, int64_t batch,
@@ -192,8 +292,6 @@ extern "C" int bdm_dispatch_build(const int64_t *write_indices, const int64_t *r
         bank_count <= 0)
         return fail(BDM_ERR_INVALID, "dispatch: bad geometry batch=%lld time=%lld KW=%d KR=%d J=%d",
                     (long long)batch, (long long)time, write_banks, read_banks, bank_count);
-    if (bank_count > kMaxBanks)
-        return fail(BDM_ERR_UNSUPPORTED, "dispatch: bank_count=%d above %d", bank_count, kMaxBanks);
     const int64_t nt = batch * time;
     const int64_t events = nt * (write_banks + read_banks);
     if (events >= (int64_t(1) << 31) || batch > 65535)
@@ -201,11 +299,30 @@ extern "C" int bdm_dispatch_build(const int64_t *write_indices, const int64_t *r
     if ((write_banks && !write_indices) || (read_banks && !read_indices) || !order || !inverse || !tokens ||
         !cu_seqlens || !status)
         return fail(BDM_ERR_INVALID, "dispatch: null pointer");
-    const size_t need = bdm_dispatch_workspace_size(batch, time, bank_count);
+    const size_t need = bdm_dispatch_workspace_size_ex(batch, time, bank_count, write_banks, read_banks);
     if (!workspace || workspace_bytes < need)
         return fail(BDM_ERR_WORKSPACE, "dispatch: workspace %zu < %zu bytes", workspace_bytes, need);
     DispatchGeometry g{batch, time, nt, write_banks, read_banks, bank_count, int(tiles_per_batch(time))};
     hipStream_t s = as_stream(stream);
+    if (bank_count > kMaxBanks) {
+        const SortWorkspace w = sort_workspace(batch, time, bank_count, events);
+        char *base = static_cast<char *>(workspace);
+        auto *keys_in = reinterpret_cast<uint64_t *>(base);
+        auto *keys_out = reinterpret_cast<uint64_t *>(base + w.keys);
+        auto *vals_in = reinterpret_cast<int32_t *>(base + 2 * w.keys);
+        auto *vals_out = reinterpret_cast<int32_t *>(base + 2 * w.keys + w.values);
+        void *temp = base + 2 * w.keys + 2 * w.values;
+        const unsigned blocks = unsigned((events + 255) / 256);
+        dispatch_sort_keys<<<blocks, 256, 0, s>>>(write_indices, read_indices, g, keys_in, vals_in, status);
+        if (int rc = check_launch("dispatch_sort_keys")) return rc;
+        size_t temp_bytes = w.temp;
+        if (hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, keys_in, keys_out, vals_in, vals_out, int(events), 0,
+                                               key_bits(batch, time, bank_count), s) != hipSuccess)
+            return fail(BDM_ERR_LAUNCH, "dispatch: radix sort failed");
+        dispatch_sort_finish<<<blocks, 256, 0, s>>>(keys_out, vals_out, g, order, inverse, tokens, cu_seqlens,
+                                                     status);
+        return check_launch("dispatch_sort_finish");
+    }
     auto *tile_counts = static_cast<int32_t *>(workspace);
     const size_t mask_bytes = size_t(bank_count) * sizeof(unsigned long long);
     const dim3 tiles(unsigned(g.tiles), unsigned(batch));

@@ -146,7 +146,7 @@ def dispatch_build(write_indices: Tensor, read_indices: Tensor, bank_count: int)
     tokens = torch.empty(events, device=device, dtype=torch.int64)
     cu = torch.empty(batch * bank_count + 1, device=device, dtype=torch.int64)
     status = torch.zeros(1, device=device, dtype=torch.int32)
-    ws_bytes = lib.bdm_dispatch_workspace_size(batch, time, bank_count)
+    ws_bytes = lib.bdm_dispatch_workspace_size_ex(batch, time, bank_count, kw, kr)
     workspace = torch.empty(max(int(ws_bytes), 1), device=device, dtype=torch.uint8)
     _lib.check(lib.bdm_dispatch_build(
         _ptr(wi), _ptr(ri), batch, time, kw, kr, bank_count, _ptr(order), _ptr(inverse), _ptr(tokens), _ptr(cu),

@@ -76,9 +76,16 @@ int bdm_router_select(const void *scores, int32_t score_dtype, int64_t rows, int
  * tokens     [E] int64  token of each packed slot
  * cu_seqlens [batch*bank_count + 1] int64  segment bounds
  * status     one int32 on device, OR-ed with bdm_route_flags; the caller zeroes it
- * E = NT*(KW+KR).  bank_count <= 8192.
+ * E = NT*(KW+KR) < 2^31.  bank_count <= 8192 runs the LDS-mask counting sort;
+ * larger bank counts radix-sort the keys (same permutation).
  */
 size_t bdm_dispatch_workspace_size(int64_t batch, int64_t time, int32_t bank_count);
+/* Workspace of bdm_dispatch_build for any bank_count: the bucket counts of
+ * the LDS-mask path for bank_count <= 8192 (bdm_dispatch_workspace_size,
+ * which returns 0 above that), else the radix-sort path's keys, values and
+ * sort scratch. */
+size_t bdm_dispatch_workspace_size_ex(int64_t batch, int64_t time, int32_t bank_count, int32_t write_banks,
+                                      int32_t read_banks);
 int bdm_dispatch_build(const int64_t *write_indices, const int64_t *read_indices, int64_t batch,
                        int64_t time, int32_t write_banks, int32_t read_banks, int32_t bank_count,
                        int64_t *order, int64_t *inverse, int64_t *tokens, int64_t *cu_seqlens,

@@ -67,8 +67,9 @@ def test_invalid_arguments_are_rejected_without_a_launch(lib):
     assert rc == -1 and b'bad geometry' in lib.bdm_last_error_string()
     rc = lib.bdm_router_select(None, _lib.BDM_BF16, 4, 32, 16, 16, 20, None, None, None)
     assert rc == -2
+    # more than 8192 banks take the radix-sort path: accepted geometry, then the null operands
     rc = lib.bdm_dispatch_build(None, None, 1, 8, 2, 2, 16384, None, None, None, None, None, None, 0, None)
-    assert rc == -2 and b'bank_count' in lib.bdm_last_error_string()
+    assert rc == -1 and b'null pointer' in lib.bdm_last_error_string()
     rc = lib.bdm_forward(None, None, 0, None)
     assert rc == -1
     args = _lib.ForwardArgs()
@@ -151,6 +152,16 @@ def test_struct_layouts_match_the_header(tmp_path):
         assert got[(struct, 'size')] == ctypes.sizeof(mirror), struct
         for field, _ in mirror._fields_:
             assert got[(struct, field)] == getattr(mirror, field).offset, (struct, field)
+
+
+def test_dispatch_workspace_sizes(lib):
+    """The LDS-mask path's bucket counts up to 8192 banks; above that only the
+    sort path's size (keys, values, sort scratch) is defined."""
+    assert lib.bdm_dispatch_workspace_size(2, 64, 256) == 2 * (2 + 1) * 256 * 4
+    assert lib.bdm_dispatch_workspace_size_ex(2, 64, 256, 8, 8) == lib.bdm_dispatch_workspace_size(2, 64, 256)
+    assert lib.bdm_dispatch_workspace_size(1, 64, 16384) == 0
+    events = 64 * 16
+    assert lib.bdm_dispatch_workspace_size_ex(1, 64, 16384, 8, 8) >= events * (2 * 8 + 2 * 4)
 
 
 def test_adamw_rejects_bad_arguments(lib):

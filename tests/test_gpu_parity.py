@@ -74,7 +74,9 @@ def test_router_module_autograd(device):
 # -------------------------------------------------------------------------- dispatch
 
 @pytest.mark.parametrize('batch,time,bank_count,kw,kr', [
-    (2, 100, 16, 4, 4), (3, 64, 256, 8, 8), (1, 7, 12, 3, 5), (4, 33, 2048, 8, 8), (2, 40, 16, 0, 4)])
+    (2, 100, 16, 4, 4), (3, 64, 256, 8, 8), (1, 7, 12, 3, 5), (4, 33, 2048, 8, 8), (2, 40, 16, 0, 4),
+    # above 8192 banks: the radix-sort path
+    (2, 50, 16384, 8, 8), (3, 20, 9000, 4, 0), (1, 300, 131072, 8, 8)])
 def test_dispatch_bit_exact(device, batch, time, bank_count, kw, kr):
     from bdm_amd import ops
     gen = torch.Generator().manual_seed(batch * 1000 + time)
@@ -91,17 +93,18 @@ def test_dispatch_bit_exact(device, batch, time, bank_count, kw, kr):
     assert torch.equal(meta.tokens.cpu(), ref.tokens)
 
 
-def test_dispatch_flags_bad_routes(device):
+@pytest.mark.parametrize('bank_count', [4, 10000])
+def test_dispatch_flags_bad_routes(device, bank_count):
     from bdm_amd import ops
     wi = torch.tensor([[[0, 1], [2, 2]]])  # duplicate bank in one token's writes
     ri = torch.tensor([[[0, 3], [1, 2]]])
-    announce('dispatch duplicate flag')
-    meta = ops.dispatch_build(wi.to(device), ri.to(device), 4)
+    announce('dispatch duplicate flag', bank_count)
+    meta = ops.dispatch_build(wi.to(device), ri.to(device), bank_count)
     with pytest.raises(ValueError, match='same bank twice'):
         meta.check_routes()
-    wi = torch.tensor([[[0, 9], [2, 1]]])  # out of range
-    announce('dispatch range flag')
-    meta = ops.dispatch_build(wi.to(device), ri.to(device), 4)
+    wi = torch.tensor([[[0, bank_count + 5], [2, 1]]])  # out of range
+    announce('dispatch range flag', bank_count)
+    meta = ops.dispatch_build(wi.to(device), ri.to(device), bank_count)
     with pytest.raises(ValueError, match='outside'):
         meta.check_routes()
 
@@ -121,6 +124,8 @@ FORWARD_CASES = [
     # heads wider than 256 columns run as 128-column virtual heads on the S = 8 path
     (1, 40, 1, 8, 2048, 16, 4, torch.bfloat16, True, torch.bfloat16),
     (2, 36, 2, 8, 384, 16, 4, torch.bfloat16, True, torch.float32),
+    # more than 8192 banks: the radix-sort dispatch
+    (1, 40, 2, 8, 32, 16384, 4, torch.bfloat16, True, torch.bfloat16),
 ]
 
 
