@@ -13,8 +13,10 @@ three flat FP32 buffers.
 
 Differences from the reference wrapper: the gradients are left unscaled
 (the reference leaves them clipped), ``step`` returns the norm as a device
-tensor (the reference returns a Python float, a host synchronisation), and
-every parameter must have a gradient at each step.
+tensor (the reference returns a Python float, a host synchronisation) and
+does not raise on a non-finite norm (the reference's error_if_nonfinite
+check also synchronises the host; test the returned norm instead), and every
+parameter must have a gradient at each step.
 """
 
 from __future__ import annotations
