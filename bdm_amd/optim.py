@@ -107,7 +107,8 @@ class MasterAdamW:
         self.step_count += 1
         if self._desc_copied is not None:
             self._desc_copied.synchronize()  # the previous upload has left the pinned buffer
-        for i, g in enumerate(grads):
+        for i, (p, g) in enumerate(zip(self.params, grads)):
+            self._desc_host[i].param = p.data_ptr()  # current storage, should the parameter have moved
             self._desc_host[i].grad = g.data_ptr()
         ctypes.memmove(self._desc_pinned.data_ptr(), ctypes.addressof(self._desc_host), ctypes.sizeof(self._desc_host))
         self._desc.copy_(self._desc_pinned, non_blocking=True)
