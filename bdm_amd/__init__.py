@@ -12,6 +12,7 @@ graph).  Kernels live in ``libbdm_hip.so``.
 from .config import BDMConfig, BSDMConfig, near_square_factors, replay_interval
 from .graphs import GraphDecoder, LanguageModelGraphDecoder
 from .model import BankedDeltaMemory
+from .ops import route_validation, set_route_validation
 from .occupancy import bank_occupancy, written_banks
 from .routed_update import bank_training, role_bank_training
 from .routing import SharedResidualRouter, product_key_route
@@ -21,4 +22,4 @@ BlockSparseDeltaMemory = BankedDeltaMemory
 __all__ = ['BDMConfig', 'BSDMConfig', 'BankedDeltaMemory', 'BlockSparseDeltaMemory', 'GraphDecoder',
            'LanguageModelGraphDecoder',
            'SharedResidualRouter', 'bank_occupancy', 'bank_training', 'role_bank_training', 'product_key_route',
-           'near_square_factors', 'replay_interval', 'written_banks']
+           'near_square_factors', 'replay_interval', 'route_validation', 'set_route_validation', 'written_banks']

@@ -897,7 +897,10 @@ __global__ __launch_bounds__(256) void read_slot_kernel(const int64_t *__restric
 // y[token, :] = fold over the token's reads in increasing bank id of
 // bf(total + z) (role_bank_dispatch.py:209-215): the token's KR rows of the
 // read buffer are already in that order.  One thread per (token, CPL columns).
-template <typename T, int CPL, int KFIX>
+// EACH = false is the narrow-head rule (head width <= 32,
+// role_bank_dispatch.py:222-226): the reference then sums with index_add_,
+// which accumulates a token's reads in FP32 and rounds once.
+template <typename T, int CPL, int KFIX, bool EACH>
 __global__ __launch_bounds__(256) void ordered_combine_kernel(const T *__restrict__ zbuf, T *__restrict__ y,
                                                               int64_t nt, int kr, int row_width) {
     const int chunks = row_width / CPL;
@@ -922,8 +925,12 @@ __global__ __launch_bounds__(256) void ordered_combine_kernel(const T *__restric
             const uint32_t w[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                total[2 * q] = round_to<T>(total[2 * q] + __uint_as_float(w[q] << 16));
-                total[2 * q + 1] = round_to<T>(total[2 * q + 1] + __uint_as_float(w[q] & 0xffff0000u));
+                total[2 * q] += __uint_as_float(w[q] << 16);
+                total[2 * q + 1] += __uint_as_float(w[q] & 0xffff0000u);
+                if constexpr (EACH) {
+                    total[2 * q] = round_to<T>(total[2 * q]);
+                    total[2 * q + 1] = round_to<T>(total[2 * q + 1]);
+                }
             }
         }
     } else {
@@ -932,7 +939,7 @@ __global__ __launch_bounds__(256) void ordered_combine_kernel(const T *__restric
             float v[CPL];
             load_row<CPL>(z + int64_t(j) * row_width, v);
 #pragma unroll
-            for (int c = 0; c < CPL; ++c) total[c] = round_to<T>(total[c] + v[c]);
+            for (int c = 0; c < CPL; ++c) total[c] = EACH ? round_to<T>(total[c] + v[c]) : total[c] + v[c];
         }
     }
     store_row<CPL>(y + token * row_width + col0, total);
@@ -1065,17 +1072,27 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, int *zslot, const PieceBu
     if (a.read_banks > 0) {
         // 16-byte rows where the layout allows (8 BF16 or 4 FP32 columns)
         constexpr int CC = sizeof(T) == 2 ? 8 : 4;
-        if (row_width % CC == 0) {
-            const int64_t threads = nt * (row_width / CC);
-            if (a.read_banks == 8)
-                ordered_combine_kernel<T, CC, 8><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
+        if (a.head_width <= 32) {
+            // narrow heads: FP32 sum, one rounding (index_add_)
+            const int cc = row_width % CC == 0 ? CC : 1;
+            const int64_t threads = nt * (row_width / cc);
+            if (cc == CC)
+                ordered_combine_kernel<T, CC, 0, false><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
                     zbuf, static_cast<T *>(a.output), nt, a.read_banks, row_width);
             else
-                ordered_combine_kernel<T, CC, 0><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
+                ordered_combine_kernel<T, 1, 0, false><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
+                    zbuf, static_cast<T *>(a.output), nt, a.read_banks, row_width);
+        } else if (row_width % CC == 0) {
+            const int64_t threads = nt * (row_width / CC);
+            if (a.read_banks == 8)
+                ordered_combine_kernel<T, CC, 8, true><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
+                    zbuf, static_cast<T *>(a.output), nt, a.read_banks, row_width);
+            else
+                ordered_combine_kernel<T, CC, 0, true><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
                     zbuf, static_cast<T *>(a.output), nt, a.read_banks, row_width);
         } else {
             const int64_t threads = nt * row_width;
-            ordered_combine_kernel<T, 1, 0><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
+            ordered_combine_kernel<T, 1, 0, true><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
                 zbuf, static_cast<T *>(a.output), nt, a.read_banks, row_width);
         }
     } else {

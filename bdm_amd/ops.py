@@ -9,6 +9,7 @@ current stream without synchronising.
 from __future__ import annotations
 
 import ctypes
+import os
 from dataclasses import dataclass
 
 import torch
@@ -111,6 +112,26 @@ def _row_stride(t: Tensor) -> int:
 # ---------------------------------------------------------------------------
 # dispatch
 
+# Route validation on the product path: off by default, because reading the
+# status word synchronises the host with the device once per dispatch.
+_validate_routes = os.environ.get('BDM_VALIDATE_ROUTES', '0') not in ('', '0')
+
+
+def set_route_validation(enabled: bool) -> None:
+    """When enabled, every ``dispatch_build`` (and so every forward, prefill
+    and training call) reads the route flags the dispatch kernels raise and
+    raises ValueError for a bank index outside [0, bank_count) or a bank
+    selected twice by one token in one role.  Disabled, malformed routes are
+    not reported: out-of-range indices are clamped to a valid bank and the
+    results are undefined.  ``BDM_VALIDATE_ROUTES=1`` enables it at import."""
+    global _validate_routes
+    _validate_routes = bool(enabled)
+
+
+def route_validation() -> bool:
+    return _validate_routes
+
+
 @dataclass
 class Dispatch:
     """Packed-event metadata (role_bank_dispatch.py:135-140)."""
@@ -151,7 +172,10 @@ def dispatch_build(write_indices: Tensor, read_indices: Tensor, bank_count: int)
     _lib.check(lib.bdm_dispatch_build(
         _ptr(wi), _ptr(ri), batch, time, kw, kr, bank_count, _ptr(order), _ptr(inverse), _ptr(tokens), _ptr(cu),
         _ptr(status), _ptr(workspace), ws_bytes, _stream(device)), 'bdm_dispatch_build')
-    return Dispatch(order, inverse, tokens, cu, status)
+    meta = Dispatch(order, inverse, tokens, cu, status)
+    if _validate_routes:
+        meta.check_routes()
+    return meta
 
 
 # ---------------------------------------------------------------------------

@@ -16,7 +16,9 @@ Differences from the reference wrapper: the gradients are left unscaled
 tensor (the reference returns a Python float, a host synchronisation) and
 does not raise on a non-finite norm (the reference's error_if_nonfinite
 check also synchronises the host; test the returned norm instead), and every
-parameter must have a gradient at each step.
+parameter must have a gradient at each step.  ``state_dict`` and
+``load_state_dict`` save and restore the masters, moments and step count;
+``reload_masters`` re-reads the masters from the current weights.
 """
 
 from __future__ import annotations
@@ -127,6 +129,51 @@ class MasterAdamW:
         stream = torch.cuda.current_stream(self.device).cuda_stream
         _lib.check(_lib.library().bdm_adamw_step(ctypes.byref(args), ctypes.c_void_p(stream)), 'bdm_adamw_step')
         return norm
+
+    def state_dict(self) -> dict:
+        """The FP32 masters and both moments per parameter (CPU copies), the
+        step count and the hyperparameters: what resuming needs, as the
+        reference wrapper saves its masters and optimizer state
+        (reproduction/experiments/optim.py:52-54)."""
+        count = len(self.params)
+        return {'masters': [self.master_of(i).detach().cpu().clone() for i in range(count)],
+                'exp_avg': [self.moments_of(i)[0].detach().cpu().clone() for i in range(count)],
+                'exp_avg_sq': [self.moments_of(i)[1].detach().cpu().clone() for i in range(count)],
+                'step': self.step_count, 'lr': self.lr, 'betas': self.betas, 'eps': self.eps,
+                'max_norm': self.max_norm, 'weight_decay': list(self.decay)}
+
+    @torch.no_grad()
+    def load_state_dict(self, state: dict) -> None:
+        """Restore masters, moments and the step count, with the reference's
+        checks (optim.py:57-71): FP32 tensors of the parameters' shapes.  The
+        BF16 weights are left as they are; call ``reload_masters`` first if the
+        weights, not the saved masters, should win."""
+        count = len(self.params)
+        for key in ('masters', 'exp_avg', 'exp_avg_sq'):
+            saved = state[key]
+            if len(saved) != count:
+                raise ValueError('Invalid FP32 master checkpoint: parameter count changed')
+            for p, t in zip(self.params, saved):
+                if t.dtype != torch.float32 or tuple(t.shape) != tuple(p.shape):
+                    raise ValueError('Invalid FP32 master checkpoint' if key == 'masters'
+                                     else 'Optimizer moment precision changed')
+        for i in range(count):
+            self.master_of(i).copy_(state['masters'][i])
+            avg, avg_sq = self.moments_of(i)
+            avg.copy_(state['exp_avg'][i])
+            avg_sq.copy_(state['exp_avg_sq'][i])
+        self.step_count = int(state['step'])
+        self.lr = float(state.get('lr', self.lr))
+        self.betas = tuple(float(b) for b in state.get('betas', self.betas))
+        self.eps = float(state.get('eps', self.eps))
+        self.max_norm = float(state.get('max_norm', self.max_norm))
+
+    @torch.no_grad()
+    def reload_masters(self) -> None:
+        """Copy the current BF16 weights into the FP32 masters (after weights
+        were loaded or edited once the optimizer exists); moments are kept."""
+        for i, p in enumerate(self.params):
+            self.master_of(i).copy_(p.detach())
 
     def master_of(self, i: int) -> Tensor:
         """Parameter i's FP32 master, shaped like the parameter (a view)."""

@@ -17,9 +17,19 @@ from . import ops
 from .config import replay_interval
 
 
-def _round_interval(bank_size: int, state_dtype: torch.dtype) -> int:
+def _round_interval(bank_size: int, state_dtype: torch.dtype, compact_replay, ctrl_dtype: torch.dtype) -> int:
+    """Events between the BF16 roundings of the state (0: never rounded).
+
+    The reference rounds a BF16 training state at every replay checkpoint,
+    ``chunk = min(16, max(4, 128 // next_pow2(S)))`` events apart, and an
+    explicit ``compact_replay=True`` with BF16 controllers shortens the chunk
+    to ``min(8, chunk)`` (role_bank_kernel.py:153-165, 181-193).  With an FP32
+    state the chunk only spaces the checkpoints, which never changes results."""
     if state_dtype == torch.bfloat16:
-        return replay_interval(bank_size)
+        chunk = replay_interval(bank_size)
+        if compact_replay is True and ctrl_dtype == torch.bfloat16:
+            chunk = min(8, chunk)
+        return chunk
     if state_dtype == torch.float32:
         return 0
     raise ValueError('state_dtype must be torch.float32 or torch.bfloat16')
@@ -40,7 +50,7 @@ class RoutedUpdate(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, g, b, w, wi, ww, ri, rw, state, bank_count, scale, compact_replay, state_dtype,
                 routed_decay):
-        interval = _round_interval(q.shape[-1], state_dtype)
+        interval = _round_interval(q.shape[-1], state_dtype, compact_replay, q.dtype)
         meta = ops.dispatch_build(wi, ri, bank_count)
         x = ops.prepare_routed(q, k, v, g, b, w, wi, ww, ri, rw, state, bank_count=bank_count)
         wants_grad = any(ctx.needs_input_grad[i] for i in (0, 1, 2, 3, 4, 5, 7, 9, 10))

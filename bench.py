@@ -10,7 +10,9 @@ Controllers and router scores are computed once before the timed region; a
 timed step is one prefill pass of the hot path over the batch:
 
     router (write and read roles) -> dispatch -> recurrence + ordered read
-    combine, final bank state written (BF16 cache), FP32 recurrence math
+    combine, final bank state written (BF16 cache), FP32 recurrence math on a
+    state rounded to BF16 every 16 packed events (the reference module
+    forward's policy at this geometry)
 
 ``value`` is tokens/s of that step with every input already in HBM.  Extra
 fields report the full-layer prefill (controller GEMMs and output interface
@@ -26,9 +28,10 @@ state once per launch.  ``achieved`` divides them by the launch's average
 duration, measured with events on the stream the kernels run on.
 
 cpu_baseline: the CPU oracle's port of the reference ``backend='reference'``
-path (per-event loop, oracle/bdm_oracle.py) on a bounded sample of the same
-workload: one sequence of the C2 geometry, the first ``--cpu-tokens`` tokens,
-routes and controllers from the same layer.
+forward (per-event loop + index_add_, oracle/bdm_oracle.py) at C1 (BASELINE
+batch 1, T 512, d_model 512, H4, v64, J256, FP32), 1 warmup + 5
+timed runs, median, on the host's cores (at most 16, one GPU's share); the
+HIP module forward at C1 is timed in the same run (``c1_forward``).
 """
 
 from __future__ import annotations
@@ -47,6 +50,11 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0
+# The reference module forward at the C2 geometry (H = 8) runs bank_training
+# per head with training_state_dtype='bfloat16' (heads.py:40-46), which rounds
+# the FP32 state to BF16 every 16 packed events (role_bank_kernel.py:153-165);
+# the FP32-state prefill policy exists in the reference for H = 1 only.
+ROUND_INTERVAL = 16
 TRAFFIC_FILE = os.path.join(ROOT, 'profiles', 'forward_c2_traffic.json')
 
 
@@ -58,8 +66,8 @@ def parse_args():
     ap.add_argument('--batch', type=int, default=8)
     ap.add_argument('--time', type=int, default=4096)
     ap.add_argument('--decode-steps', type=int, default=256)
-    ap.add_argument('--cpu-tokens', type=int, default=512,
-                    help='tokens of sequence 0 the CPU oracle runs (0 skips the CPU baseline)')
+    ap.add_argument('--no-cpu-baseline', dest='cpu_baseline', action='store_false',
+                    help='skip the CPU baseline (the reference CPU path at C1, ~10 s)')
     ap.add_argument('--no-extras', action='store_true', help='skip the full-layer and decode measurements')
     ap.add_argument('--only', choices=('c3', 'c4', 'c5', 'prefill', 'lm', 'lm-prefill', 'lm-train'),
                     help='run one named workload alone (C3 decode, C4 skewed forward, C5 training, C2 full-layer '
@@ -491,37 +499,61 @@ def c5_training(device, steps=3):
     return {'tokens_per_s': round(4 * 2048 / sec, 1), 'ms_per_step': round(sec * 1e3, 3)}
 
 
-def cpu_baseline(layer_gpu, cfg, tokens):
-    """The oracle's per-event loop (port of reference_packed_gdn2 + index_add_
-    readout) on the first `tokens` tokens of one C2 sequence, on the host."""
+def c1_config():
+    """BASELINE configs[0] (the reference's CPU-runnable case): d_model 512, H4 of
+    v = 64, J256 = 16x16, S8, K8, FP32 weights, FP32 training state."""
+    from bdm_amd import BSDMConfig
+    return BSDMConfig(dim=512, bank_count=256, bank_size=8, selected_banks=8, value_width=256, num_heads=4,
+                      training_state_dtype='float32')
+
+
+def c1_input():
+    import torch
+    return torch.randn(1, 512, 512, generator=torch.Generator().manual_seed(512))
+
+
+def c1_gpu(device, steps=20):
+    """The HIP module forward at C1 (FP32): controllers, routing, dispatch,
+    recurrence, combine and output interface; tokens/s of one forward."""
+    import torch
+    from bdm_amd import BankedDeltaMemory
+    layer = BankedDeltaMemory(c1_config(), layer_id=0, seed=0).to(device)
+    x = c1_input().to(device)
+    with torch.no_grad():
+        sec, _ = timed(lambda: layer(x), steps, 3)
+    return {'tokens_per_s': round(512 / sec, 1), 'ms_per_forward': round(sec * 1e3, 4),
+            'config': 'C1: batch 1, T 512, d_model 512, H4, v64, J256 (16x16), S8, K8, FP32, FP32 state'}
+
+
+def cpu_threads():
+    """Host threads for the CPU baseline: the cores this process may run on,
+    at most 16 (one GPU's share of the box, whatever os.cpu_count() reports)."""
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count() or 1
+    return max(1, min(usable, 16)), usable
+
+
+def cpu_baseline():
+    """BASELINE.md's CPU plan: the reference backend='reference' forward at C1
+    (oracle/bdm_oracle.py OracleBankedDeltaMemory.forward, the per-event loop
+    of reference_packed_gdn2 and index_add_), under no_grad, 1 warmup and 5
+    timed runs, the median; tokens/s = 512 / median."""
     import torch
     from oracle import bdm_oracle as O
-    threads = min(os.cpu_count() or 1, 16)
+    threads, usable = cpu_threads()
     torch.set_num_threads(threads)
-    gen = torch.Generator().manual_seed(7)
-    x = torch.randn(1, tokens, cfg.dim, generator=gen).to(torch.bfloat16)
-    with torch.no_grad():
-        xd = x.to(next(layer_gpu.parameters()).device)
-        q, k, v, g, b, w = (t.cpu() for t in layer_gpu._controllers(xd))
-        rr, wr = (t.cpu() for t in layer_gpu._route_projections(xd))
-        initial = layer_gpu._state_heads(layer_gpu.materialize_initial_state()).cpu()
+    oracle = O.OracleBankedDeltaMemory(c1_config(), layer_id=0, seed=0)
+    x = c1_input()
 
     def run():
         with torch.no_grad():
-            ww, wi = O.product_key_route(wr, bank_count=cfg.bank_count, selected_banks=cfg.selected_banks)
-            rw, ri = O.product_key_route(rr, bank_count=cfg.bank_count, selected_banks=cfg.selected_banks)
-            outs = []
-            for h in range(cfg.num_heads):
-                sl = lambda t: t[:, :, h].contiguous()  # noqa: E731
-                outs.append(O.bank_forward(sl(q), sl(k), sl(v), sl(g), sl(b), sl(w), wi, ww, ri, rw,
-                                           initial[:, h], cfg.bank_count, cfg.bank_size ** -0.5,
-                                           routed_decay=True, state_dtype=torch.float32,
-                                           combine='index_add', lockstep=False))
-            return torch.cat(outs, -1)
+            return oracle(x, combine='index_add', lockstep=False)
 
     run()  # warmup
     times = []
-    for _ in range(3):
+    for _ in range(5):
         t0 = time.perf_counter()
         run()
         times.append(time.perf_counter() - t0)
@@ -535,10 +567,11 @@ def cpu_baseline(layer_gpu, cfg, tokens):
                     break
     except OSError:
         pass
-    return {'value': round(tokens / med, 2), 'unit': 'tokens/s', 'cores': threads, 'kind': 'port',
-            'sample': (f'batch 1 x T={tokens} of the C2 geometry (H8 S8 v128 J256 KW=KR=8), FP32 state, '
-                       f'per-event loop of oracle/bdm_oracle.py packed_recurrence, median of 3 '
-                       f'({med:.2f} s each); host CPU: {model}')}
+    return {'value': round(512 / med, 2), 'unit': 'tokens/s', 'cores': threads, 'kind': 'port',
+            'sample': (f'C1 whole: batch 1 x T=512, d_model 512, H4 v64 J256 (16x16) S8 K8, FP32 weights and '
+                       f'state; OracleBankedDeltaMemory.forward (per-event loop + index_add_), 1 warmup + 5 runs, '
+                       f'median {med:.3f} s; {threads} threads ({usable} usable cores, os.cpu_count() = '
+                       f'{os.cpu_count()}); host CPU: {model}')}
 
 
 def load_traffic():
@@ -596,7 +629,7 @@ def main():
         if record['on']:
             ev_start[record['i']].record(stream)
         y = ops.routed_forward(q, k, v, g, b, w, wi, ww, ri, rw, initial, meta, bank_count=j, scale=scale,
-                               routed_decay=True, round_interval=0, final_state=final)
+                               routed_decay=True, round_interval=ROUND_INTERVAL, final_state=final)
         if record['on']:
             ev_stop[record['i']].record(stream)
             record['i'] += 1
@@ -626,10 +659,11 @@ def main():
         'metric': 'BDM-layer prefill tokens/sec (routed-memory hot path, N=2048,S=8,B=8)',
         'value': round(tokens / sec, 1), 'unit': 'tokens/s', 'n_gpus': 1, 'steps': args.steps,
         'warmup': args.warmup, 'ms_per_step': round(sec * 1e3, 4), 'higher_is_better': True,
-        'scaling': 'weak', 'vs_baseline': None, 'dtype': 'bf16 storage, fp32 recurrence',
+        'scaling': 'weak', 'vs_baseline': None,
+        'dtype': 'bf16 controllers and state storage (state rounded every 16 events), fp32 recurrence math',
         'data': 'synthetic: x ~ N(0,1), seeded random-init BSDM layer weights',
         'config': {'workload': 'C2 prefill hot path: router x2 + dispatch + recurrence + ordered combine '
-                               '+ final BF16 state', 'batch': batch, 'seq_len': time_, 'd_model': cfg.dim,
+                               '+ final BF16 state', 'state_rounding_interval': ROUND_INTERVAL, 'batch': batch, 'seq_len': time_, 'd_model': cfg.dim,
                    'heads': cfg.num_heads, 'bank_count': j, 'bank_size': cfg.bank_size,
                    'selected_banks': kk, 'head_value_width': cfg.head_value_width},
         'roofline': {'bound': 'hbm', 'kernel': 'bdm_forward (read_slot_kernel + lazy_forward_kernel + ordered_combine_kernel)',
@@ -655,9 +689,13 @@ def main():
         result['whole_model_training'] = whole_model_training(device, args.lm_context)
     progress('copy probe')
     result['hbm_copy_GBps'] = round(copy_probe(device), 1)
-    if args.cpu_tokens > 0:
-        progress('cpu baseline', args.cpu_tokens, 'tokens')
-        result['cpu_baseline'] = cpu_baseline(layer, cfg, args.cpu_tokens)
+    progress('C1 forward on the GPU')
+    result['c1_forward'] = c1_gpu(device)
+    if args.cpu_baseline:
+        progress('cpu baseline at C1')
+        result['cpu_baseline'] = cpu_baseline()
+        result['c1_forward']['gpu_over_cpu'] = round(result['c1_forward']['tokens_per_s']
+                                                     / result['cpu_baseline']['value'], 1)
     else:
         result['cpu_baseline'] = None
     print(json.dumps(result), flush=True)

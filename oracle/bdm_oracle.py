@@ -365,8 +365,11 @@ def bank_forward(q, k, v, g, b, w, wi, ww, ri, rw, state, bank_count: int, scale
 
     q,k,g,b [B,T,S]; v,w [B,T,V]; wi,ri int64 [B,T,K]; ww,rw [B,T,K];
     ``state`` [J,S,V] shared by the batch or [B,J,S,V] per sequence.
-    ``combine='ordered'`` is the production readout, ``'index_add'`` the CPU
-    reference backend's.  Differentiable through torch autograd."""
+    ``combine='ordered'`` is the per-add rounded fold of the production
+    readout, ``'index_add'`` the CPU reference backend's FP32 sum, and
+    ``'role'`` the production rule by head width: ordered above 32 columns,
+    index_add_ at or below (role_bank_dispatch.py:222-226).  Differentiable
+    through torch autograd."""
     batch, time, s = q.shape
     nt = batch * time
     meta = dispatch_metadata(wi, ri, bank_count)
@@ -380,6 +383,8 @@ def bank_forward(q, k, v, g, b, w, wi, ww, ri, rw, state, bank_count: int, scale
     run = lockstep_recurrence if lockstep else packed_recurrence
     out, final = run(ev, initial, meta.cu_seqlens, scale, state_dtype=state_dtype, interval=interval,
                      return_final=True)
+    if combine == 'role':
+        combine = 'ordered' if v.shape[-1] > 32 else 'index_add'
     if combine == 'ordered':
         raw = ordered_readout(out, meta.inverse, nt, wi.shape[-1], ri.shape[-1])
     else:
@@ -559,7 +564,7 @@ class OracleBankedDeltaMemory(nn.Module):
         normalized = normalized * self.output_norm_weight.to(raw.dtype)
         return self.o_proj(normalized * torch.sigmoid(self.output_gate(hidden)).to(raw.dtype))
 
-    def bank_reads(self, hidden: Tensor, *, combine: str = 'ordered', lockstep: bool = True,
+    def bank_reads(self, hidden: Tensor, *, combine: str = 'role', lockstep: bool = True,
                    state=None, state_dtype=None, return_final: bool = False):
         """Concatenated per-head reads [B,T,V] (heads.py:25-66)."""
         q, k, v, g, b, w = self.controllers(hidden)

@@ -64,3 +64,46 @@ def test_fused_adamw_matches_the_reference_recipe():
             assert torch.equal(eas, state['exp_avg_sq']), (step, i, 'exp_avg_sq')
             assert torch.equal(p.detach(), q.detach()), (step, i, 'weight')
         fused.zero_grad()
+
+
+def test_state_dict_round_trip_resumes_bit_exact():
+    """Save after two steps, restore into a fresh optimizer on copies of the
+    weights, and take a third step on both: weights, masters and moments stay
+    bit-identical.  Invalid checkpoints raise as the reference's do."""
+    from bdm_amd.optim import MasterAdamW
+    device = torch.device('cuda', 0)
+    params = make_params(device, 3)
+    opt = MasterAdamW(params, lr=1e-3)
+    gen = torch.Generator().manual_seed(4)
+    grads = [[(torch.randn(p.shape, generator=gen) * s).to(torch.bfloat16).to(device) for p in params]
+             for s in (1.0, 0.01, 0.5)]
+    for step in range(2):
+        for p, g in zip(params, grads[step]):
+            p.grad = g.clone()
+        opt.step()
+    saved = opt.state_dict()
+    copies = [torch.nn.Parameter(p.detach().clone()) for p in params]
+    for p, c in zip(params, copies):
+        if hasattr(p, '_no_weight_decay'):
+            c._no_weight_decay = True
+    resumed = MasterAdamW(copies, lr=5.0)  # hyperparameters come from the checkpoint
+    resumed.load_state_dict(saved)
+    assert resumed.step_count == 2 and resumed.lr == opt.lr
+    for ps in (params, copies):
+        for p, g in zip(ps, grads[2]):
+            p.grad = g.clone()
+    opt.step()
+    resumed.step()
+    torch.cuda.synchronize()
+    for i, (p, c) in enumerate(zip(params, copies)):
+        assert torch.equal(p.detach(), c.detach()), i
+        assert torch.equal(opt.master_of(i), resumed.master_of(i)), i
+        assert all(torch.equal(a, b) for a, b in zip(opt.moments_of(i), resumed.moments_of(i))), i
+    bad = dict(saved, masters=[t.to(torch.bfloat16) for t in saved['masters']])
+    with pytest.raises(ValueError, match='master'):
+        resumed.load_state_dict(bad)
+    # weights edited after construction: reload_masters makes them the masters
+    with torch.no_grad():
+        copies[0].add_(1.0)
+    resumed.reload_masters()
+    assert torch.equal(resumed.master_of(0), copies[0].detach().float())

@@ -1,7 +1,8 @@
 """Inference epilogues against the torch ops they replace, on identical inputs.
 
 The controller epilogue and the output epilogue are compared with the layer's
-own torch formulas (heads.controllers, heads.py:11-22; _normalize_qk and
+own torch formulas, and the controller epilogue also with the CPU oracle's
+controllers on the same weights (heads.controllers, heads.py:11-22; _normalize_qk and
 _project_bank_output, _parameters.py:214-232) applied to the same projection
 matrix.  BF16 results may differ by one BF16 ulp (exp/log1p/rsqrt of the
 device libm against torch's), FP32 g by 1e-5 relative.  End to end, prefill
@@ -83,6 +84,34 @@ def test_controller_epilogue_matches_torch_ops(device, qk, bank_size):
         assert rel_err(rr.reshape(ref_rr.shape), ref_rr) < 1e-2 and rel_err(wr.reshape(ref_wr.shape), ref_wr) < 1e-2
 
 
+@pytest.mark.parametrize('qk', ['nvidia', 'original'])
+def test_controller_epilogue_matches_oracle_controllers(device, qk):
+    """The fused projection + controller epilogue against the CPU oracle's own
+    controllers and router scores (heads.py:11-22, _parameters.py:189-220,
+    routing.py:23-35) on the same weights: GPU and CPU GEMMs round
+    differently, so BF16 outputs agree to a few BF16 ulps of each row."""
+    from oracle import bdm_oracle as O
+    layer = _layer(device, torch.bfloat16, qk, 'layer')
+    oracle = O.OracleBankedDeltaMemory(layer.config, layer_id=2, seed=7).to(torch.bfloat16)
+    oracle.load_state_dict({k_: t.cpu() for k_, t in layer.state_dict().items()})
+    gen = torch.Generator().manual_seed(55)
+    x = torch.randn(2, 41, layer.hidden_size, generator=gen).to(torch.bfloat16)
+    announce('controller epilogue vs oracle', qk)
+    with torch.no_grad():
+        (q, k, v, g, b, w), (rr, wr), _ = layer._fused_controllers(x.to(device))
+        torch.cuda.synchronize()
+        ref = oracle.controllers(x)
+        ref_rr, ref_wr = oracle.shared_router.read(x), oracle.shared_router.write(x)
+    for name, ours, theirs in zip('qkvgbw', (q, k, v, g, b, w), ref):
+        width = theirs.shape[-1]
+        err = rel_err(ours.reshape(-1, width), theirs.reshape(-1, width))
+        assert ours.dtype == theirs.dtype, name
+        assert err < 2e-2, (name, err)
+    width = ref_rr.shape[-1]
+    assert rel_err(rr.reshape(-1, width), ref_rr.reshape(-1, width)) < 2e-2
+    assert rel_err(wr.reshape(-1, width), ref_wr.reshape(-1, width)) < 2e-2
+
+
 @pytest.mark.parametrize('norm', ['layer', 'rms'])
 @pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float32], ids=['bf16', 'f32'])
 def test_output_epilogue_matches_torch_ops(device, norm, dtype):
@@ -133,6 +162,17 @@ def test_fused_prefill_matches_unfused_path(device):
         layer._fused_supported = lambda hidden: False  # the torch path for the same call
         ref_out, ref_state = layer.prefill(x, state_dtype=torch.float32)
         torch.cuda.synchronize()
-    if not same_routes:
-        pytest.skip('a route score near-tie selects other banks under the two GEMMs')
-    assert rel_err(out, ref_out) < 1e-2 and rel_err(state, ref_state) < 1e-2
+    # A route-score near-tie can select other banks under the two GEMMs.  A
+    # token's output depends on the writes up to it, so the outputs are
+    # compared before each sequence's first token whose routes differ, and the
+    # final cache only where no route differs.
+    differ = torch.zeros(x.shape[:2], dtype=torch.bool, device=device)
+    for a, b_ in ((rr, ref_rr), (wr, ref_wr)):
+        differ |= (layer._route(a, 4)[1] != layer._route(b_, 4)[1]).any(-1)
+    first = torch.where(differ.any(-1), differ.float().argmax(-1), torch.full_like(differ[:, 0], x.shape[1],
+                                                                                   dtype=torch.long))
+    keep = torch.arange(x.shape[1], device=device)[None, :] < first[:, None]
+    assert float(keep.float().mean()) >= 0.75, 'too many near-ties for this seed'
+    assert rel_err(out[keep], ref_out[keep]) < 1e-2
+    if same_routes:
+        assert rel_err(state, ref_state) < 1e-2

@@ -18,7 +18,7 @@ import sys
 import pytest
 import torch
 
-from _inputs import controllers, initial_state, oracle_reads, rel_err, routes
+from _inputs import controllers, initial_state, oracle_reads, rel_err, routes, tie_dependent_rows
 from oracle import bdm_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -69,6 +69,28 @@ def test_c3_decode_full_size(device):
     assert torch.equal(dstate.cpu()[~touched], state[~touched])
 
 
+def test_c2_router_full_size_with_ties(device):
+    """C2 score geometry (B8 T4096, 16 + 16 BF16 factor scores, B = 8) for both
+    roles: indices and weights bit-exact against the oracle on every row,
+    including the ~11% whose selected set depends on a tie."""
+    from bdm_amd import ops
+    gen = torch.Generator().manual_seed(2222)
+    for role in ('write', 'read'):
+        scores = torch.randn(8, 4096, 32, generator=gen).to(torch.bfloat16)
+        announce('C2 router full size', role)
+        w_, i_ = ops.router_select(scores.to(device), bank_count=256, selected_banks=8)
+        torch.cuda.synchronize()
+        wr, ir = O.product_key_route(scores, bank_count=256, selected_banks=8)
+        ties = tie_dependent_rows(scores, 256, 8)
+        print(f'C2 {role} tie-dependent router rows: {float(ties.float().mean()):.4f}', flush=True)
+        assert float(ties.float().mean()) > 0.01  # the check covers tied rows
+        assert torch.equal(i_.cpu(), ir)
+        # weights within one BF16 ulp (the softmax exp's last FP32 bits differ
+        # between torch's CPU kernel and the device libm)
+        diff = (w_.cpu().float() - wr.float()).abs()
+        assert bool((diff <= wr.float().abs() * 2 ** -7 + 1e-12).all()), float(diff.max())
+
+
 @pytest.fixture(scope='module')
 def c4(device):
     gen = torch.Generator().manual_seed(44)
@@ -88,6 +110,12 @@ def test_c4_router_and_dispatch_bit_exact(device, c4):
         w_, i_ = ops.router_select(scores.to(device), bank_count=c4['j'], selected_banks=c4['kk'])
         assert torch.equal(i_.cpu(), wi)
         assert torch.equal(w_.cpu(), ww)
+        # rows whose selected set depends on the tie order (equal BF16 scores
+        # or pair sums at a top-s or top-B boundary) match too: both sides keep
+        # the lower index first
+        ties = tie_dependent_rows(scores, c4['j'], c4['kk'])
+        print(f'C4 tie-dependent router rows: {float(ties.float().mean()):.4f}', flush=True)
+        assert torch.equal(i_.cpu()[ties], wi[ties])
     announce('C4 dispatch')
     meta = ops.dispatch_build(c4['wi'].to(device), c4['ri'].to(device), c4['j'])
     ref = O.dispatch_metadata(c4['wi'], c4['ri'], c4['j'])
@@ -158,7 +186,7 @@ def test_c5_backward_full_size_truncated_gradient(device):
         hs = lambda x: x[:, :, h]  # noqa: E731
         outs.append(O.bank_forward(hs(cut[0]), hs(cut[1]), hs(cut[2]), hs(cut[3]), hs(cut[4]), hs(cut[5]),
                                    wi[:1, :t0], cut[6], ri[:1, :t0], cut[7], st[:, h], j, s ** -0.5,
-                                   routed_decay=True, state_dtype=torch.bfloat16, combine='ordered'))
+                                   routed_decay=True, state_dtype=torch.bfloat16, combine='role'))
     (torch.cat(outs, -1).float() * dy[:1, :t0].float()).sum().backward()
     names = ('q', 'k', 'v', 'g', 'b', 'w', 'ww', 'rw')
     for name, leaf, ref in zip(names, leaves[:8], cut):

@@ -109,6 +109,30 @@ def test_dispatch_flags_bad_routes(device, bank_count):
         meta.check_routes()
 
 
+def test_route_validation_on_the_product_path(device):
+    """With route validation on, the routed operator itself raises on
+    malformed routes; off (the default), it runs without a host sync."""
+    import bdm_amd
+    gen = torch.Generator().manual_seed(9)
+    q, k, v, g, b, w = controllers(1, 4, 1, 8, 32, gen)
+    wi = torch.tensor([[[0, 1], [2, 2], [0, 1], [3, 1]]])  # token 1 writes bank 2 twice
+    ri = torch.tensor([[[0, 3], [1, 2], [2, 3], [0, 1]]])
+    ww = torch.full((1, 4, 2), 0.5, dtype=torch.bfloat16)
+    state = initial_state(4, 1, 8, 32, gen)[:, 0]
+    args = [t.to(device) for t in (q[:, :, 0], k[:, :, 0], v[:, :, 0], g[:, :, 0], b[:, :, 0], w[:, :, 0], wi, ww,
+                                   ri, ww, state)]
+    assert not bdm_amd.route_validation()
+    announce('route validation')
+    bdm_amd.bank_training(*args, 4, 8 ** -0.5)  # unchecked by default
+    bdm_amd.set_route_validation(True)
+    try:
+        with pytest.raises(ValueError, match='same bank twice'):
+            bdm_amd.bank_training(*args, 4, 8 ** -0.5)
+    finally:
+        bdm_amd.set_route_validation(False)
+    torch.cuda.synchronize()
+
+
 # --------------------------------------------------------------------------- forward
 
 FORWARD_CASES = [
@@ -438,10 +462,15 @@ def test_decode_kernel_matches_oracle(device, heads, v):
 
 # ---------------------------------------------------------------- full benchmark size
 
-def test_full_size_prefill_c2(device):
+@pytest.mark.parametrize('policy', ['module', 'prefill'])
+def test_full_size_prefill_c2(device, policy):
     """C2 geometry (B8 T4096 H8 S8 v128 J256 K8): dispatch bit-exact against the
-    CPU oracle over all 524,288 events; read outputs and final states of
-    sequence 0 against the oracle recurrence (sequences are independent)."""
+    CPU oracle over all 524,288 events; read outputs and final states of the
+    first and the last sequence against the oracle recurrence (sequences are
+    independent).  ``module`` is the reference module forward's policy at this
+    geometry (BF16 state rounded every 16 events, heads.py:40-46 with
+    training_state_dtype='bfloat16'), ``prefill`` the stateful prefill's (FP32
+    state, rounded at the handoff, inference.py:1-7)."""
     from bdm_amd import ops
     gen = torch.Generator().manual_seed(2026)
     batch, time, heads, s, v, j, kk = 8, 4096, 8, 8, 128, 256, 8
@@ -456,13 +485,18 @@ def test_full_size_prefill_c2(device):
     assert torch.equal(meta.order.cpu(), ref.order)
     assert torch.equal(meta.cu_seqlens.cpu(), ref.cu_seqlens)
     assert torch.equal(meta.inverse.cpu(), ref.inverse)
-    announce('full size C2 forward')
+    announce('full size C2 forward', policy)
+    interval = 16 if policy == 'module' else 0
+    state_dtype = torch.bfloat16 if policy == 'module' else torch.float32
     final = torch.empty(batch, j, heads, s, v, device=device, dtype=torch.bfloat16)
     y = ops.routed_forward(*dev[:10], dev[10], meta, bank_count=j, scale=s ** -0.5, routed_decay=True,
-                           round_interval=16, final_state=final)
+                           round_interval=interval, final_state=final)
     torch.cuda.synchronize()
-    one = lambda t: t[:1]  # noqa: E731
-    ref_y, ref_final = oracle_reads(*(one(t) for t in (q, k, v_, g, b, w, wi, ww, ri, rw)), state, j,
-                                    routed_decay=True, state_dtype=torch.bfloat16, return_final=True)
-    assert rel_err(y[:1], ref_y) < TOL, rel_err(y[:1], ref_y)
-    assert rel_err(final[:1], ref_final) < TOL, rel_err(final[:1], ref_final)
+    for seq in (0, batch - 1):
+        one = lambda t: t[seq:seq + 1]  # noqa: E731
+        ref_y, ref_final = oracle_reads(*(one(t) for t in (q, k, v_, g, b, w, wi, ww, ri, rw)), state, j,
+                                        routed_decay=True, state_dtype=state_dtype, interval=16,
+                                        return_final=True)
+        err_y = rel_err(one(y), ref_y)  # per token (its H*v outputs)
+        err_s = rel_err(one(final), ref_final)
+        assert err_y < TOL and err_s < TOL, (seq, err_y, err_s)

@@ -307,3 +307,26 @@ def test_written_bank_curve_boundaries():
     for i, t in enumerate(prefixes):
         assert torch.all(curve[:, i] <= min(banks, 6 * t))
     assert torch.equal(curve[:, -1].float() / banks, hard)
+
+
+def test_index_add_combine_is_one_fp32_sum():
+    """The CPU reference's readout, index_add_ on BF16 rows
+    (gdn2_banks.py:280-283), adds a token's reads in FP32 and rounds once;
+    the 'ordered' fold rounds after every add.  The HIP combine takes the
+    former for heads of <= 32 columns, so the fact is pinned here."""
+    gen = torch.Generator().manual_seed(17)
+    nt, kr, width = 64, 8, 32
+    rows = (torch.randn(nt * kr, width, generator=gen) * 3).to(torch.bfloat16)
+    tokens = torch.arange(nt).repeat_interleave(kr)
+    got = O.scatter_bank_outputs(rows, tokens, nt)
+    want = rows.float().reshape(nt, kr, width).sum(1).to(torch.bfloat16)
+    assert torch.equal(got, want)
+    # the per-add fold differs on these rows, so the two rules are distinct
+    inverse = torch.cat([torch.zeros(0, dtype=torch.long), torch.arange(nt * kr)])
+    folded = O.ordered_readout(rows, inverse, nt, 0, kr)
+    assert not torch.equal(folded, got)
+    # and 'role' picks index_add at <= 32 columns, the fold above
+    total = torch.zeros(nt, width)
+    for j in range(kr):
+        total = (total + rows.reshape(nt, kr, width)[:, j].float()).to(torch.bfloat16).float()
+    assert torch.equal(folded, total.to(torch.bfloat16))
