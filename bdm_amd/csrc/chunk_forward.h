@@ -25,6 +25,7 @@ struct ChunkForwardParams {
     int s_heads;      // real heads
     int64_t row_stride;  // columns of a real head
     int banks, kw, kr;
+    int kw_shift, kr_shift;  // log2 of kw, kr when powers of two, else -1
     int routed_decay;
     int init_dtype, final_dtype;
     int xcd_remap;

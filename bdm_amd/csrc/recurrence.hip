@@ -24,10 +24,13 @@
 // reads by bank id (read_slot_kernel); the combine kernel then streams each
 // token's KR consecutive rows and adds them in that order, rounding after
 // every add (the production readout order).
+#include <cstdlib>
+#include <cstring>
 #include <type_traits>
 
 #include "bdm_common.h"
 #include "recurrence_ops.h"
+#include "chunk_forward.h"
 
 namespace bdm {
 namespace {
@@ -971,6 +974,45 @@ struct PieceBuffers {
     int64_t max_pieces = 0;  // 0: the path is off
 };
 
+// The read combine of bdm_forward: y from the read buffer (or zeros when the
+// routes have no reads).
+template <typename T>
+int launch_combine(const bdm_forward_args &a, const T *zbuf, hipStream_t stream) {
+    const int row_width = a.heads * a.head_width;
+    const int64_t nt = a.batch * a.time;
+    if (a.read_banks > 0) {
+        // 16-byte rows where the layout allows (8 BF16 or 4 FP32 columns)
+        constexpr int CC = sizeof(T) == 2 ? 8 : 4;
+        if (a.head_width <= 32) {
+            // narrow heads: FP32 sum, one rounding (index_add_)
+            const int cc = row_width % CC == 0 ? CC : 1;
+            const int64_t threads = nt * (row_width / cc);
+            if (cc == CC)
+                ordered_combine_kernel<T, CC, 0, false><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
+                    zbuf, static_cast<T *>(a.output), nt, a.read_banks, row_width);
+            else
+                ordered_combine_kernel<T, 1, 0, false><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
+                    zbuf, static_cast<T *>(a.output), nt, a.read_banks, row_width);
+        } else if (row_width % CC == 0) {
+            const int64_t threads = nt * (row_width / CC);
+            if (a.read_banks == 8)
+                ordered_combine_kernel<T, CC, 8, true><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
+                    zbuf, static_cast<T *>(a.output), nt, a.read_banks, row_width);
+            else
+                ordered_combine_kernel<T, CC, 0, true><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
+                    zbuf, static_cast<T *>(a.output), nt, a.read_banks, row_width);
+        } else {
+            const int64_t threads = nt * row_width;
+            ordered_combine_kernel<T, 1, 0, true><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
+                zbuf, static_cast<T *>(a.output), nt, a.read_banks, row_width);
+        }
+    } else {
+        const int64_t count = nt * row_width;
+        zero_fill_kernel<T><<<unsigned((count + 255) / 256), 256, 0, stream>>>(static_cast<T *>(a.output), count);
+    }
+    return check_launch("ordered_combine_kernel");
+}
+
 template <typename T, int S, int CPL, bool kLazy = false>
 int launch_forward(const bdm_forward_args &a, T *zbuf, int *zslot, const PieceBuffers &pb, hipStream_t stream) {
     const int split = kLazy ? lazy_split(a) : 1;
@@ -1067,39 +1109,7 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, int *zslot, const PieceBu
         if (int rc = check_launch("routed_forward_kernel")) return rc;
     }
 
-    const int row_width = a.heads * a.head_width;
-    const int64_t nt = a.batch * a.time;
-    if (a.read_banks > 0) {
-        // 16-byte rows where the layout allows (8 BF16 or 4 FP32 columns)
-        constexpr int CC = sizeof(T) == 2 ? 8 : 4;
-        if (a.head_width <= 32) {
-            // narrow heads: FP32 sum, one rounding (index_add_)
-            const int cc = row_width % CC == 0 ? CC : 1;
-            const int64_t threads = nt * (row_width / cc);
-            if (cc == CC)
-                ordered_combine_kernel<T, CC, 0, false><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
-                    zbuf, static_cast<T *>(a.output), nt, a.read_banks, row_width);
-            else
-                ordered_combine_kernel<T, 1, 0, false><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
-                    zbuf, static_cast<T *>(a.output), nt, a.read_banks, row_width);
-        } else if (row_width % CC == 0) {
-            const int64_t threads = nt * (row_width / CC);
-            if (a.read_banks == 8)
-                ordered_combine_kernel<T, CC, 8, true><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
-                    zbuf, static_cast<T *>(a.output), nt, a.read_banks, row_width);
-            else
-                ordered_combine_kernel<T, CC, 0, true><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
-                    zbuf, static_cast<T *>(a.output), nt, a.read_banks, row_width);
-        } else {
-            const int64_t threads = nt * row_width;
-            ordered_combine_kernel<T, 1, 0, true><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
-                zbuf, static_cast<T *>(a.output), nt, a.read_banks, row_width);
-        }
-    } else {
-        const int64_t count = nt * row_width;
-        zero_fill_kernel<T><<<unsigned((count + 255) / 256), 256, 0, stream>>>(static_cast<T *>(a.output), count);
-    }
-    return check_launch("ordered_combine_kernel");
+    return launch_combine<T>(a, zbuf, stream);
 }
 
 // The S = 8 lazy kernel takes: 16-byte aligned state rows, 4-column lane
@@ -1124,11 +1134,74 @@ int64_t max_pieces(const bdm_forward_args &a) {
     return 2 * (events / kPieceEvents) + 1;
 }
 
+// BDM_FORWARD_KERNEL=mfma selects the matrix-core recurrence where it
+// applies; the vector-ALU kernel is the default (both are complete
+// implementations of the same forward; the variable is read at every call).
+// On MI355X at the C2 geometry the matrix-core form is the slower one: its
+// coefficient scan and exact gated-value split cost more vector instructions
+// than the state update they move to the matrix cores.
+bool chunk_enabled() {
+    const char *e = getenv("BDM_FORWARD_KERNEL");
+    return e && strcmp(e, "mfma") == 0;
+}
+
+// The matrix-core recurrence (chunk_forward.hip) between the read-slot map
+// and the combine.
+int launch_chunked(const bdm_forward_args &a, bf16_t *zbuf, int *zslot, hipStream_t stream) {
+    const int64_t nt = a.batch * a.time;
+    if (a.read_banks > 0) {
+        const int64_t routes = nt * a.read_banks;
+        read_slot_kernel<<<unsigned((routes + 255) / 256), 256, 0, stream>>>(a.read_indices, routes, a.read_banks,
+                                                                              zslot);
+        if (int rc = check_launch("read_slot_kernel")) return rc;
+    }
+    const int split = a.head_width > 256 ? a.head_width / 128 : 1;
+    ChunkForwardParams p{};
+    p.q = static_cast<const bf16_t *>(a.q);
+    p.k = static_cast<const bf16_t *>(a.k);
+    p.b = static_cast<const bf16_t *>(a.b);
+    p.g = a.g;
+    p.v = static_cast<const bf16_t *>(a.v);
+    p.w = static_cast<const bf16_t *>(a.w);
+    p.ww = static_cast<const bf16_t *>(a.write_weights);
+    p.rw = static_cast<const bf16_t *>(a.read_weights);
+    p.order = a.order;
+    p.cu = a.cu_seqlens;
+    p.initial = a.initial;
+    p.final_state = a.final_state;
+    p.snap = static_cast<bf16_t *>(a.snapshots);
+    p.zbuf = zbuf;
+    p.zslot = zslot;
+    p.init_bstride = a.initial_batch_stride;
+    p.nt = nt;
+    p.split = split;
+    p.s_heads = a.heads;
+    p.heads = a.heads * split;
+    p.width = a.head_width / split;
+    p.row_stride = a.head_width;
+    p.banks = a.bank_count;
+    p.kw = a.write_banks;
+    p.kr = a.read_banks;
+    p.kw_shift = (a.write_banks > 0 && (a.write_banks & (a.write_banks - 1)) == 0) ? __builtin_ctz(a.write_banks) : -1;
+    p.kr_shift = (a.read_banks > 0 && (a.read_banks & (a.read_banks - 1)) == 0) ? __builtin_ctz(a.read_banks) : -1;
+    p.routed_decay = a.routed_decay;
+    p.init_dtype = a.initial_dtype;
+    p.final_dtype = a.final_dtype;
+    p.nseg = int(a.batch * a.bank_count);
+    p.xcd_remap = p.nseg % 8 == 0 ? 1 : 0;
+    p.scale = a.scale;
+    if (int rc = launch_chunk_forward(p, p.width / 32, stream)) return rc;
+    return launch_combine<bf16_t>(a, zbuf, stream);
+}
+
 template <typename T>
 int dispatch_forward(const bdm_forward_args &a, T *zbuf, int *zslot, const PieceBuffers &pb, hipStream_t stream) {
     // Vector row loads need 16-byte aligned rows: aligned bases, and a state
     // batch stride that keeps them aligned.
     const bool vec = a.initial_batch_stride % 8 == 0;
+    if constexpr (std::is_same<T, bf16_t>::value) {
+        if (chunk_path(a) && chunk_enabled()) return launch_chunked(a, zbuf, zslot, stream);
+    }
     if (a.bank_size <= 8) {
         if (lazy_path(a)) return launch_forward<T, 8, 4, true>(a, zbuf, zslot, pb, stream);
         if (vec && a.head_width % 8 == 0) return launch_forward<T, 8, 8>(a, zbuf, zslot, pb, stream);

@@ -69,7 +69,7 @@ def parse_args():
     ap.add_argument('--no-cpu-baseline', dest='cpu_baseline', action='store_false',
                     help='skip the CPU baseline (the reference CPU path at C1, ~10 s)')
     ap.add_argument('--no-extras', action='store_true', help='skip the full-layer and decode measurements')
-    ap.add_argument('--only', choices=('c3', 'c4', 'c5', 'prefill', 'lm', 'lm-prefill', 'lm-train'),
+    ap.add_argument('--only', choices=('c2-forward', 'c3', 'c4', 'c5', 'prefill', 'lm', 'lm-prefill', 'lm-train'),
                     help='run one named workload alone (C3 decode, C4 skewed forward, C5 training, C2 full-layer '
                          'prefill, whole-model prefill and decode) and print its figures as one JSON line; used to '
                          'profile a workload on its own')
@@ -499,6 +499,29 @@ def c5_training(device, steps=3):
     return {'tokens_per_s': round(4 * 2048 / sec, 1), 'ms_per_step': round(sec * 1e3, 3)}
 
 
+def c2_forward_only(layer, device, batch, time_, launches):
+    """``launches`` bdm_forward launches of the C2 hot path (routes and dispatch
+    built once), for profilers; BDM_FORWARD_KERNEL picks the recurrence."""
+    import torch
+    from bdm_amd import ops
+    _, (q, k, v, g, b, w), (read_scores, write_scores), initial = make_inputs(layer, batch, time_, device)
+    cfg = layer.config
+    final = torch.empty(batch, cfg.bank_count, cfg.num_heads, cfg.bank_size, cfg.head_value_width,
+                        device=device, dtype=torch.bfloat16)
+    with torch.no_grad():
+        ww, wi = ops.router_select(write_scores, bank_count=cfg.bank_count, selected_banks=cfg.selected_banks)
+        rw, ri = ops.router_select(read_scores, bank_count=cfg.bank_count, selected_banks=cfg.selected_banks)
+        meta = ops.dispatch_build(wi, ri, cfg.bank_count)
+        t0 = time.perf_counter()
+        for _ in range(launches):
+            ops.routed_forward(q, k, v, g, b, w, wi, ww, ri, rw, initial, meta, bank_count=cfg.bank_count,
+                               scale=cfg.bank_size ** -0.5, routed_decay=True, round_interval=ROUND_INTERVAL,
+                               final_state=final)
+        torch.cuda.synchronize()
+    return {'launches': launches, 'ms_per_launch': round((time.perf_counter() - t0) / launches * 1e3, 4),
+            'recurrence': os.environ.get('BDM_FORWARD_KERNEL', 'vector')}
+
+
 def c1_config():
     """BASELINE configs[0] (the reference's CPU-runnable case): d_model 512, H4 of
     v = 64, J256 = 16x16, S8, K8, FP32 weights, FP32 training state."""
@@ -603,7 +626,8 @@ def main():
     batch, time_ = args.batch, args.time
     layer = BankedDeltaMemory(cfg, layer_id=0, seed=0).to(device=device, dtype=torch.bfloat16)
     if args.only:
-        run = {'c3': lambda: decode_bench(layer, device, args.decode_steps), 'c4': lambda: c4_forward(device),
+        run = {'c2-forward': lambda: c2_forward_only(layer, device, batch, time_, args.steps),
+               'c3': lambda: decode_bench(layer, device, args.decode_steps), 'c4': lambda: c4_forward(device),
                'c5': lambda: c5_training(device),
                'prefill': lambda: full_layer_prefill(layer, device, batch, time_, max(3, args.steps // 4)),
                'lm': lambda: whole_model(device, args.lm_context, tune=args.lm_gemm_tuning == 'on'),
