@@ -86,10 +86,14 @@ __global__ __launch_bounds__(512) void dispatch_tile_count(const int64_t *__rest
 // tiles are split over the four waves of the workgroup; a wave first sums its
 // range (loads in flight together), the waves' sums are scanned through LDS,
 // then each wave rewrites its range as running offsets.
+// It also clears the route flags: the counting pass before it raised them
+// and the scatter pass after it raises every one of them again (both build
+// the same tile masks), so the caller need not clear the word.
 __global__ __launch_bounds__(256) void dispatch_tile_scan(DispatchGeometry g, int32_t *__restrict__ tile_counts,
-                                                          int32_t *__restrict__ totals) {
+                                                          int32_t *__restrict__ totals, int32_t *status) {
     __shared__ int32_t part[4][kWave];
     const int b = blockIdx.x;
+    if (b == 0 && blockIdx.y == 0 && threadIdx.x == 0) *status = 0;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const int bank = blockIdx.y * kWave + lane;
     const bool live = bank < g.banks;
@@ -115,52 +119,55 @@ __global__ __launch_bounds__(256) void dispatch_tile_scan(DispatchGeometry g, in
     }
 }
 
-// One workgroup per batch: exclusive scan of the segment lengths over banks
-// gives the segment starts.  Batch b's segments start at b*T*(KW+KR): every
+// One workgroup per (tile, batch): the batch's segment starts (an exclusive
+// scan of the segment lengths over banks, in LDS; every tile of the batch
+// computes the same scan, and tile 0 stores it as cu_seqlens), then each of
+// the tile's events goes to start + its tile's offset in the segment + its
+// rank in the tile's mask.  Batch b's segments start at b*T*(KW+KR): every
 // token adds exactly KW+KR events to its own batch.
-__global__ __launch_bounds__(1024) void dispatch_bank_scan(DispatchGeometry g, const int32_t *__restrict__ totals,
-                                                           int64_t *__restrict__ cu_seqlens) {
-    __shared__ int32_t wave_sums[1024 / kWave];
-    const int b = blockIdx.x;
-    const int32_t *tot = totals + int64_t(b) * g.banks;
-    // each thread owns a contiguous chunk of banks
-    const int per = (g.banks + blockDim.x - 1) / blockDim.x;
-    const int lo = min(g.banks, int(threadIdx.x) * per), hi = min(g.banks, lo + per);
-    int32_t local = 0;
-    for (int x = lo; x < hi; ++x) local += tot[x];
-    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-    int32_t incl = local;
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-        const int32_t up = __shfl_up(incl, d, kWave);
-        if (lane >= d) incl += up;
-    }
-    if (lane == kWave - 1) wave_sums[wave] = incl;
-    __syncthreads();
-    int32_t running = incl - local;
-    for (int w = 0; w < wave; ++w) running += wave_sums[w];
-    const int64_t batch_base = int64_t(b) * g.time * (g.kw + g.kr);
-    for (int x = lo; x < hi; ++x) {
-        cu_seqlens[int64_t(b) * g.banks + x] = batch_base + running;
-        running += tot[x];
-    }
-    if (b == g.batch - 1 && threadIdx.x == 0) cu_seqlens[g.batch * g.banks] = g.nt * (g.kw + g.kr);
-}
-
 __global__ __launch_bounds__(512) void dispatch_scatter(const int64_t *__restrict__ wi,
                                                         const int64_t *__restrict__ ri, DispatchGeometry g,
                                                         const int32_t *__restrict__ tile_base,
-                                                        const int64_t *__restrict__ cu_seqlens,
+                                                        const int32_t *__restrict__ totals,
+                                                        int64_t *__restrict__ cu_seqlens,
                                                         int64_t *__restrict__ order, int64_t *__restrict__ inverse,
                                                         int64_t *__restrict__ tokens, int32_t *status) {
     extern __shared__ unsigned long long masks[];
+    int32_t *starts = reinterpret_cast<int32_t *>(masks + g.banks);
+    __shared__ int32_t wave_sums[512 / kWave];
     const int tile = blockIdx.x, b = blockIdx.y;
-    build_masks(masks, wi, ri, g, b, tile, status);
+    {
+        const int32_t *tot = totals + int64_t(b) * g.banks;
+        const int per = (g.banks + int(blockDim.x) - 1) / int(blockDim.x);
+        const int lo = min(g.banks, int(threadIdx.x) * per), hi = min(g.banks, lo + per);
+        int32_t local = 0;
+        for (int x = lo; x < hi; ++x) local += tot[x];
+        const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+        int32_t incl = local;
+#pragma unroll
+        for (int d = 1; d < kWave; d <<= 1) {
+            const int32_t up = __shfl_up(incl, d, kWave);
+            if (lane >= d) incl += up;
+        }
+        if (lane == kWave - 1) wave_sums[wave] = incl;
+        __syncthreads();
+        int32_t running = incl - local;
+        for (int w = 0; w < wave; ++w) running += wave_sums[w];
+        const int64_t batch_base = int64_t(b) * g.time * (g.kw + g.kr);
+        for (int x = lo; x < hi; ++x) {
+            starts[x] = running;
+            if (tile == 0) cu_seqlens[int64_t(b) * g.banks + x] = batch_base + running;
+            running += tot[x];
+        }
+        if (tile == 0 && b == g.batch - 1 && threadIdx.x == 0) cu_seqlens[g.batch * g.banks] = g.nt * (g.kw + g.kr);
+    }
+    build_masks(masks, wi, ri, g, b, tile, status);  // ends with a barrier, which also publishes starts
     const int per_token = g.kw + g.kr;
     const int t0 = tile * kTileTokens;
     const int ntok = min(kTileTokens, int(g.time - t0));
     const int32_t *tb = tile_base + (int64_t(b) * g.tiles + tile) * g.banks;
     const int64_t events = g.nt * per_token;
+    const int64_t batch_base = int64_t(b) * g.time * per_token;
     for (int i = threadIdx.x; i < ntok * per_token; i += blockDim.x) {
         const int tl = i / per_token, j = i - tl * per_token;
         const int64_t token = int64_t(b) * g.time + t0 + tl;
@@ -168,7 +175,7 @@ __global__ __launch_bounds__(512) void dispatch_scatter(const int64_t *__restric
         const int bank = raw < 0 ? 0 : (raw >= g.banks ? g.banks - 1 : int(raw));
         const int bit = 2 * tl + (j >= g.kw);
         const int rank = __popcll(masks[bank] & ((1ull << bit) - 1ull));
-        int64_t pos = cu_seqlens[int64_t(b) * g.banks + bank] + tb[bank] + rank;
+        int64_t pos = batch_base + starts[bank] + tb[bank] + rank;
         pos = pos < 0 ? 0 : (pos >= events ? events - 1 : pos);
         const int64_t original = j < g.kw ? token * g.kw + j : g.nt * g.kw + token * g.kr + (j - g.kw);
         order[pos] = original;
@@ -231,6 +238,36 @@ __global__ __launch_bounds__(256) void dispatch_sort_finish(const uint64_t *__re
     for (int64_t sg = prev + 1; sg <= seg; ++sg) cu_seqlens[sg] = i;  // segments that start here
     if (i == events - 1)
         for (int64_t sg = seg + 1; sg <= nseg; ++sg) cu_seqlens[sg] = events;
+}
+
+__global__ void dispatch_clear_status(int32_t *status) {
+    if (threadIdx.x == 0) *status = 0;
+}
+
+// The LDS-mask path (bank_count <= kMaxBanks): per-tile counts, per-bank tile
+// offsets and segment lengths (clearing the route flags), then the scatter
+// with the segment starts.  Scratch: batch * (tiles + 1) * banks int32, every
+// element written before it is read.
+int launch_mask_dispatch(const int64_t *wi, const int64_t *ri, const DispatchGeometry &g, int64_t *order,
+                         int64_t *inverse, int64_t *tokens, int64_t *cu_seqlens, int32_t *status, void *scratch,
+                         hipStream_t s) {
+    auto *tile_counts = static_cast<int32_t *>(scratch);
+    const size_t mask_bytes = size_t(g.banks) * sizeof(unsigned long long);
+    const dim3 tiles(unsigned(g.tiles), unsigned(g.batch));
+    dispatch_tile_count<<<tiles, 512, mask_bytes, s>>>(wi, ri, g, tile_counts, status);
+    if (int rc = check_launch("dispatch_tile_count")) return rc;
+    int32_t *totals = tile_counts + int64_t(g.batch) * g.tiles * g.banks;
+    dispatch_tile_scan<<<dim3(unsigned(g.batch), unsigned((g.banks + kWave - 1) / kWave)), 256, 0, s>>>(
+        g, tile_counts, totals, status);
+    if (int rc = check_launch("dispatch_tile_scan")) return rc;
+    const size_t scatter_lds = mask_bytes + size_t(g.banks) * sizeof(int32_t);
+    if (scatter_lds > 64 * 1024 &&
+        hipFuncSetAttribute(reinterpret_cast<const void *>(dispatch_scatter),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, int(scatter_lds)) != hipSuccess)
+        return fail(BDM_ERR_LAUNCH, "dispatch: %zu bytes of LDS for %d banks", scatter_lds, g.banks);
+    dispatch_scatter<<<tiles, 512, scatter_lds, s>>>(wi, ri, g, tile_counts, totals, cu_seqlens, order, inverse,
+                                                    tokens, status);
+    return check_launch("dispatch_scatter");
 }
 
 struct SortWorkspace {
@@ -313,6 +350,8 @@ extern "C" int bdm_dispatch_build(const int64_t *write_indices, const int64_t *r
         auto *vals_out = reinterpret_cast<int32_t *>(base + 2 * w.keys + w.values);
         void *temp = base + 2 * w.keys + 2 * w.values;
         const unsigned blocks = unsigned((events + 255) / 256);
+        dispatch_clear_status<<<1, 64, 0, s>>>(status);
+        if (int rc = check_launch("dispatch_clear_status")) return rc;
         dispatch_sort_keys<<<blocks, 256, 0, s>>>(write_indices, read_indices, g, keys_in, vals_in, status);
         if (int rc = check_launch("dispatch_sort_keys")) return rc;
         size_t temp_bytes = w.temp;
@@ -323,18 +362,7 @@ extern "C" int bdm_dispatch_build(const int64_t *write_indices, const int64_t *r
                                                      status);
         return check_launch("dispatch_sort_finish");
     }
-    auto *tile_counts = static_cast<int32_t *>(workspace);
-    const size_t mask_bytes = size_t(bank_count) * sizeof(unsigned long long);
-    const dim3 tiles(unsigned(g.tiles), unsigned(batch));
-    dispatch_tile_count<<<tiles, 512, mask_bytes, s>>>(write_indices, read_indices, g, tile_counts, status);
-    if (int rc = check_launch("dispatch_tile_count")) return rc;
-    int32_t *totals = tile_counts + int64_t(batch) * g.tiles * bank_count;
-    dispatch_tile_scan<<<dim3(unsigned(batch), unsigned((bank_count + kWave - 1) / kWave)), 256, 0, s>>>(
-        g, tile_counts, totals);
-    if (int rc = check_launch("dispatch_tile_scan")) return rc;
-    dispatch_bank_scan<<<unsigned(batch), 1024, 0, s>>>(g, totals, cu_seqlens);
-    if (int rc = check_launch("dispatch_bank_scan")) return rc;
-    dispatch_scatter<<<tiles, 512, mask_bytes, s>>>(write_indices, read_indices, g, tile_counts, cu_seqlens,
-                                                    order, inverse, tokens, status);
-    return check_launch("dispatch_scatter");
+    return bdm::launch_mask_dispatch(write_indices, read_indices, g, order, inverse, tokens, cu_seqlens, status,
+                                     workspace, s);
 }
+

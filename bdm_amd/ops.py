@@ -166,7 +166,7 @@ def dispatch_build(write_indices: Tensor, read_indices: Tensor, bank_count: int)
     inverse = torch.empty(events, device=device, dtype=torch.int64)
     tokens = torch.empty(events, device=device, dtype=torch.int64)
     cu = torch.empty(batch * bank_count + 1, device=device, dtype=torch.int64)
-    status = torch.zeros(1, device=device, dtype=torch.int32)
+    status = torch.empty(1, device=device, dtype=torch.int32)  # cleared and set by the dispatch itself
     ws_bytes = lib.bdm_dispatch_workspace_size_ex(batch, time, bank_count, kw, kr)
     workspace = torch.empty(max(int(ws_bytes), 1), device=device, dtype=torch.uint8)
     _lib.check(lib.bdm_dispatch_build(

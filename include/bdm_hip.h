@@ -75,7 +75,8 @@ int bdm_router_select(const void *scores, int32_t score_dtype, int64_t rows, int
  * inverse    [E] int64  packed slot of each original event
  * tokens     [E] int64  token of each packed slot
  * cu_seqlens [batch*bank_count + 1] int64  segment bounds
- * status     one int32 on device, OR-ed with bdm_route_flags; the caller zeroes it
+ * status     one int32 on device: cleared by the call, then OR-ed with
+ *            bdm_route_flags (the caller need not clear it)
  * E = NT*(KW+KR) < 2^31.  bank_count <= 8192 runs the LDS-mask counting sort;
  * larger bank counts radix-sort the keys (same permutation).
  */

@@ -75,6 +75,8 @@ def test_router_module_autograd(device):
 
 @pytest.mark.parametrize('batch,time,bank_count,kw,kr', [
     (2, 100, 16, 4, 4), (3, 64, 256, 8, 8), (1, 7, 12, 3, 5), (4, 33, 2048, 8, 8), (2, 40, 16, 0, 4),
+    # the largest bank count of the LDS-mask path (masks and segment starts: 96 KiB of LDS)
+    (2, 70, 8192, 8, 8), (1, 5, 4096, 2, 3),
     # above 8192 banks: the radix-sort path
     (2, 50, 16384, 8, 8), (3, 20, 9000, 4, 0), (1, 300, 131072, 8, 8)])
 def test_dispatch_bit_exact(device, batch, time, bank_count, kw, kr):
