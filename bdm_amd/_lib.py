@@ -33,6 +33,7 @@ EXPORTED_SYMBOLS = (
     'bdm_swiglu_pair',
     'bdm_swiglu_backward',
     'bdm_dispatch_workspace_size_ex',
+    'bdm_dispatch_build_static',
 )
 
 _i32, _i64, _f32, _vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
@@ -151,6 +152,8 @@ def library() -> ctypes.CDLL:
     lib.bdm_dispatch_build.argtypes = [_vp, _vp, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp,
                                        _vp, _size_t, _vp]
     lib.bdm_dispatch_build.restype = _i32
+    lib.bdm_dispatch_build_static.argtypes = [_vp, _vp, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp]
+    lib.bdm_dispatch_build_static.restype = _i32
     lib.bdm_forward_workspace_size.argtypes = [ctypes.POINTER(ForwardArgs)]
     lib.bdm_forward_workspace_size.restype = _size_t
     lib.bdm_forward.argtypes = [ctypes.POINTER(ForwardArgs), _vp, _size_t, _vp]

@@ -27,6 +27,8 @@
 // unique keys make the result the same permutation.
 #include <hipcub/hipcub.hpp>
 
+#include <mutex>
+
 #include "bdm_common.h"
 
 namespace bdm {
@@ -366,3 +368,69 @@ extern "C" int bdm_dispatch_build(const int64_t *write_indices, const int64_t *r
                                      workspace, s);
 }
 
+// ---- the allocation-free dispatch (for callers that cannot allocate: code
+//      under HIP graph capture, serving loops, harnesses that forbid it)
+//
+// Its scratch is this file-scope device array, one copy per GPU, held until
+// the process ends.  Host code never passes the array's name to a kernel: the
+// name is a host-side stand-in.  The device address comes from
+// hipGetSymbolAddress, taken once per device with that device current and
+// kept per device.  Every call on a GPU shares that GPU's copy, so calls that
+// overlap on one GPU race.  No part of it needs clearing: the counting pass
+// writes every per-tile count and the tile scan every segment length before
+// anything reads them.
+namespace {
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) unsigned char scratch[BDM_DISPATCH_STATIC_SCRATCH_BYTES];
+std::mutex g_scratch_lock;
+void *g_scratch[kMaxDevices] = {};
+
+int static_scratch(void **out) {
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+        return bdm::fail(BDM_ERR_LAUNCH, "dispatch (no allocation): no usable current device (%d)", dev);
+    std::lock_guard<std::mutex> guard(g_scratch_lock);
+    if (!g_scratch[dev]) {
+        void *ptr = nullptr;
+        const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (err != hipSuccess || !ptr)
+            return bdm::fail(BDM_ERR_LAUNCH, "dispatch (no allocation): hipGetSymbolAddress on device %d: %s", dev,
+                             hipGetErrorString(err));
+        g_scratch[dev] = ptr;
+    }
+    *out = g_scratch[dev];
+    return BDM_OK;
+}
+}  // namespace
+
+extern "C" int bdm_dispatch_build_static(const int64_t *write_indices, const int64_t *read_indices, int64_t batch,
+                                         int64_t time, int32_t write_banks, int32_t read_banks, int32_t bank_count,
+                                         int64_t *order, int64_t *inverse, int64_t *tokens, int64_t *cu_seqlens,
+                                         int32_t *status, void *stream) {
+    using namespace bdm;
+    if (batch <= 0 || time <= 0 || write_banks < 0 || read_banks < 0 || write_banks + read_banks == 0 ||
+        bank_count <= 0)
+        return fail(BDM_ERR_INVALID, "dispatch (no allocation): bad geometry batch=%lld time=%lld KW=%d KR=%d J=%d",
+                    (long long)batch, (long long)time, write_banks, read_banks, bank_count);
+    const int64_t nt = batch * time;
+    const int64_t events = nt * (write_banks + read_banks);
+    if (events >= (int64_t(1) << 31) || batch > 65535)
+        return fail(BDM_ERR_UNSUPPORTED, "dispatch (no allocation): %lld events exceed the int32 ranks",
+                    (long long)events);
+    if (bank_count > kMaxBanks)
+        return fail(BDM_ERR_UNSUPPORTED, "dispatch (no allocation): bank_count %d above %d (the radix-sort path "
+                    "needs bdm_dispatch_build and a workspace)", bank_count, kMaxBanks);
+    const size_t need = bdm_dispatch_workspace_size(batch, time, bank_count);
+    if (need > size_t(BDM_DISPATCH_STATIC_SCRATCH_BYTES))
+        return fail(BDM_ERR_UNSUPPORTED, "dispatch (no allocation): needs %zu bytes of scratch, above the %zu-byte "
+                    "static buffer; use bdm_dispatch_build with a workspace", need,
+                    size_t(BDM_DISPATCH_STATIC_SCRATCH_BYTES));
+    if ((write_banks && !write_indices) || (read_banks && !read_indices) || !order || !inverse || !tokens ||
+        !cu_seqlens || !status)
+        return fail(BDM_ERR_INVALID, "dispatch (no allocation): null pointer");
+    void *ptr = nullptr;
+    if (int rc = static_scratch(&ptr)) return rc;
+    const DispatchGeometry g{batch, time, nt, write_banks, read_banks, bank_count, int(tiles_per_batch(time))};
+    return launch_mask_dispatch(write_indices, read_indices, g, order, inverse, tokens, cu_seqlens, status, ptr,
+                                as_stream(stream));
+}

@@ -93,6 +93,26 @@ int bdm_dispatch_build(const int64_t *write_indices, const int64_t *read_indices
                        int32_t *status, void *workspace, size_t workspace_bytes, void *stream);
 
 /*
+ * bdm_dispatch_build without a workspace, for callers that cannot allocate
+ * (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc).  It has no counterpart in the reference.  Same arguments,
+ * outputs and errors as bdm_dispatch_build, minus the workspace; it allocates
+ * nothing and calls no allocating routine.  Its scratch is a static device
+ * buffer of BDM_DISPATCH_STATIC_SCRATCH_BYTES per GPU (held until the process
+ * ends), so it takes the LDS-mask path only: bank_count <= 8192 and
+ * bdm_dispatch_workspace_size(batch, time, bank_count) <= that size (C2:
+ * 1.06 MB, C4: 8.4 MB); larger geometries return BDM_ERR_UNSUPPORTED with a
+ * message.  Every call on one GPU shares that buffer: calls that overlap on
+ * one GPU (concurrent streams or threads) race and must be serialised by the
+ * caller.
+ */
+#define BDM_DISPATCH_STATIC_SCRATCH_BYTES (16u << 20)
+int bdm_dispatch_build_static(const int64_t *write_indices, const int64_t *read_indices, int64_t batch,
+                              int64_t time, int32_t write_banks, int32_t read_banks, int32_t bank_count,
+                              int64_t *order, int64_t *inverse, int64_t *tokens, int64_t *cu_seqlens,
+                              int32_t *status, void *stream);
+
+/*
  * Routed GDN2 bank recurrence with the r-weighted read combine.  Replaces, for
  * all heads at once: pack (role_bank_dispatch.py:156-185), decay_transform
  * (routed_update.py:5-13), _role_forward (role_bank_kernel.py:46-73, and the
