@@ -34,6 +34,7 @@ EXPORTED_SYMBOLS = (
     'bdm_swiglu_backward',
     'bdm_dispatch_workspace_size_ex',
     'bdm_dispatch_build_static',
+    'bdm_router_select_pair',
 )
 
 _i32, _i64, _f32, _vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
@@ -152,6 +153,9 @@ def library() -> ctypes.CDLL:
     lib.bdm_dispatch_build.argtypes = [_vp, _vp, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp,
                                        _vp, _size_t, _vp]
     lib.bdm_dispatch_build.restype = _i32
+    lib.bdm_router_select_pair.argtypes = [_vp, _i64, _vp, _i64, _i32, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp,
+                                           _vp]
+    lib.bdm_router_select_pair.restype = _i32
     lib.bdm_dispatch_build_static.argtypes = [_vp, _vp, _i64, _i64, _i32, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp]
     lib.bdm_dispatch_build_static.restype = _i32
     lib.bdm_forward_workspace_size.argtypes = [ctypes.POINTER(ForwardArgs)]

@@ -105,10 +105,24 @@ __device__ __forceinline__ void load_block(const T *z, int e0, int n, float (&x)
 
 // SM: list slots (>= selected); VEC: rows are 16-byte aligned and hold a
 // multiple of 8 scores.
+// Up to two routing roles (the write and read routers of one layer) in one
+// launch: blockIdx.y picks the role.
+template <typename T>
+struct RouterRoles {
+    const T *scores[2];
+    int64_t stride[2];
+    T *weights[2];
+    int64_t *indices[2];
+};
+
 template <typename T, int SM, bool VEC>
-__global__ __launch_bounds__(64) void router_lane_kernel(const T *__restrict__ scores, int64_t rows, int64_t stride,
-                                                         int j1, int j2, int selected, T *__restrict__ weights,
-                                                         int64_t *__restrict__ indices) {
+__global__ __launch_bounds__(64) void router_lane_kernel(RouterRoles<T> roles, int64_t rows, int j1, int j2,
+                                                         int selected) {
+    const int role = int(blockIdx.y);
+    const T *__restrict__ scores = roles.scores[role];
+    const int64_t stride = roles.stride[role];
+    T *__restrict__ weights = roles.weights[role];
+    int64_t *__restrict__ indices = roles.indices[role];
     const int64_t row = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     if (row >= rows) return;
     const T *z = scores + row * stride;
@@ -353,46 +367,43 @@ __global__ __launch_bounds__(256) void router_wave_kernel(const bf16_t *__restri
 }
 
 template <typename T, int SM>
-void launch_router_sm(const T *scores, int64_t rows, int64_t stride, int j1, int j2, int selected, T *weights,
-                      int64_t *indices, hipStream_t stream) {
+void launch_router_sm(const RouterRoles<T> &roles, int nroles, int64_t rows, int j1, int j2, int selected,
+                      hipStream_t stream) {
     // one lane per row, 64-lane workgroups spread over the CUs
-    const dim3 grid(unsigned((rows + 63) / 64));
+    const dim3 grid(unsigned((rows + 63) / 64), unsigned(nroles));
     const int n = j1 + j2;
-    const bool vec = aligned(scores, 16) && (stride * int64_t(sizeof(T))) % 16 == 0 && n % 8 == 0;
+    bool vec = n % 8 == 0;
+    for (int r = 0; r < nroles; ++r)
+        vec = vec && aligned(roles.scores[r], 16) && (roles.stride[r] * int64_t(sizeof(T))) % 16 == 0;
     if (vec)
-        router_lane_kernel<T, SM, true><<<grid, 64, 0, stream>>>(scores, rows, stride, j1, j2, selected, weights,
-                                                                 indices);
+        router_lane_kernel<T, SM, true><<<grid, 64, 0, stream>>>(roles, rows, j1, j2, selected);
     else
-        router_lane_kernel<T, SM, false><<<grid, 64, 0, stream>>>(scores, rows, stride, j1, j2, selected, weights,
-                                                                  indices);
+        router_lane_kernel<T, SM, false><<<grid, 64, 0, stream>>>(roles, rows, j1, j2, selected);
 }
 
 template <typename T>
-int launch_router(const void *scores, int64_t rows, int64_t stride, int j1, int j2, int selected,
-                  void *weights, int64_t *indices, hipStream_t stream) {
-    const T *z = static_cast<const T *>(scores);
+int launch_router(const RouterRoles<T> &roles, int nroles, int64_t rows, int j1, int j2, int selected,
+                  hipStream_t stream) {
     if constexpr (sizeof(T) == 2) {
         // few rows (decode): one wave per row instead of one lane per row
         if (rows <= 2048 && selected <= 8 && j1 <= kWave && j2 <= kWave) {
-            router_wave_kernel<<<unsigned((rows + 3) / 4), 256, 0, stream>>>(
-                z, rows, stride, j1, j2, selected, static_cast<bf16_t *>(weights), indices);
-            return check_launch("router_wave_kernel");
+            for (int r = 0; r < nroles; ++r) {
+                router_wave_kernel<<<unsigned((rows + 3) / 4), 256, 0, stream>>>(
+                    roles.scores[r], rows, roles.stride[r], j1, j2, selected, roles.weights[r], roles.indices[r]);
+                if (int rc = check_launch("router_wave_kernel")) return rc;
+            }
+            return BDM_OK;
         }
     }
     if (selected <= 8)
-        launch_router_sm<T, 8>(z, rows, stride, j1, j2, selected, static_cast<T *>(weights), indices, stream);
+        launch_router_sm<T, 8>(roles, nroles, rows, j1, j2, selected, stream);
     else
-        launch_router_sm<T, 16>(z, rows, stride, j1, j2, selected, static_cast<T *>(weights), indices, stream);
+        launch_router_sm<T, 16>(roles, nroles, rows, j1, j2, selected, stream);
     return check_launch("router_lane_kernel");
 }
 
-}  // namespace
-}  // namespace bdm
-
-extern "C" int bdm_router_select(const void *scores, int32_t score_dtype, int64_t rows, int64_t row_stride,
-                                 int32_t factor_first, int32_t factor_second, int32_t selected,
-                                 void *weights, int64_t *indices, void *stream) {
-    using namespace bdm;
+int check_router_geometry(int64_t rows, int64_t row_stride, int32_t factor_first, int32_t factor_second,
+                          int32_t selected) {
     if (rows < 0 || factor_first <= 0 || factor_second <= 0 || row_stride < factor_first + factor_second)
         return fail(BDM_ERR_INVALID, "router: bad geometry rows=%lld J1=%d J2=%d stride=%lld", (long long)rows,
                     factor_first, factor_second, (long long)row_stride);
@@ -402,18 +413,62 @@ extern "C" int bdm_router_select(const void *scores, int32_t score_dtype, int64_
     if (factor_first + factor_second > kRouterMaxScores)
         return fail(BDM_ERR_UNSUPPORTED, "router: J1 + J2 = %d > %d scores per row", factor_first + factor_second,
                     kRouterMaxScores);
-    if (rows == 0) return BDM_OK;
-    if (!scores || !weights || !indices) return fail(BDM_ERR_INVALID, "router: null pointer");
-    if (!aligned(scores, 16)) return fail(BDM_ERR_INVALID, "router: scores must be 16-byte aligned");
     if (rows > int64_t(INT32_MAX) * 32) return fail(BDM_ERR_UNSUPPORTED, "router: too many rows");
-    switch (score_dtype) {
-        case BDM_BF16:
-            return launch_router<bf16_t>(scores, rows, row_stride, factor_first, factor_second, selected, weights,
-                                         indices, as_stream(stream));
-        case BDM_F32:
-            return launch_router<float>(scores, rows, row_stride, factor_first, factor_second, selected, weights,
-                                        indices, as_stream(stream));
-        default:
-            return fail(BDM_ERR_INVALID, "router: unknown score dtype %d", score_dtype);
+    return BDM_OK;
+}
+
+template <typename T>
+int route_roles(const void *const *scores, const int64_t *strides, void *const *weights, int64_t *const *indices,
+                int nroles, int64_t rows, int j1, int j2, int selected, hipStream_t stream) {
+    RouterRoles<T> roles{};
+    for (int r = 0; r < nroles; ++r) {
+        roles.scores[r] = static_cast<const T *>(scores[r]);
+        roles.stride[r] = strides[r];
+        roles.weights[r] = static_cast<T *>(weights[r]);
+        roles.indices[r] = indices[r];
     }
+    return launch_router<T>(roles, nroles, rows, j1, j2, selected, stream);
+}
+
+int route(const void *const *scores, const int64_t *strides, void *const *weights, int64_t *const *indices,
+          int nroles, int32_t score_dtype, int64_t rows, int j1, int j2, int selected, hipStream_t stream) {
+    for (int r = 0; r < nroles; ++r) {
+        if (int rc = check_router_geometry(rows, strides[r], j1, j2, selected)) return rc;
+    }
+    if (rows == 0) return BDM_OK;
+    for (int r = 0; r < nroles; ++r) {
+        if (!scores[r] || !weights[r] || !indices[r]) return fail(BDM_ERR_INVALID, "router: null pointer");
+        if (!aligned(scores[r], 16)) return fail(BDM_ERR_INVALID, "router: scores must be 16-byte aligned");
+    }
+    switch (score_dtype) {
+        case BDM_BF16: return route_roles<bf16_t>(scores, strides, weights, indices, nroles, rows, j1, j2, selected, stream);
+        case BDM_F32: return route_roles<float>(scores, strides, weights, indices, nroles, rows, j1, j2, selected, stream);
+        default: return fail(BDM_ERR_INVALID, "router: unknown score dtype %d", score_dtype);
+    }
+}
+
+}  // namespace
+}  // namespace bdm
+
+extern "C" int bdm_router_select(const void *scores, int32_t score_dtype, int64_t rows, int64_t row_stride,
+                                 int32_t factor_first, int32_t factor_second, int32_t selected,
+                                 void *weights, int64_t *indices, void *stream) {
+    const void *sc[1] = {scores};
+    const int64_t st[1] = {row_stride};
+    void *w[1] = {weights};
+    int64_t *ix[1] = {indices};
+    return bdm::route(sc, st, w, ix, 1, score_dtype, rows, factor_first, factor_second, selected,
+                      bdm::as_stream(stream));
+}
+
+extern "C" int bdm_router_select_pair(const void *scores_a, int64_t row_stride_a, const void *scores_b,
+                                      int64_t row_stride_b, int32_t score_dtype, int64_t rows, int32_t factor_first,
+                                      int32_t factor_second, int32_t selected, void *weights_a,
+                                      int64_t *indices_a, void *weights_b, int64_t *indices_b, void *stream) {
+    const void *sc[2] = {scores_a, scores_b};
+    const int64_t st[2] = {row_stride_a, row_stride_b};
+    void *w[2] = {weights_a, weights_b};
+    int64_t *ix[2] = {indices_a, indices_b};
+    return bdm::route(sc, st, w, ix, 2, score_dtype, rows, factor_first, factor_second, selected,
+                      bdm::as_stream(stream));
 }

@@ -167,6 +167,15 @@ class BankedDeltaMemory(nn.Module):
     def _route(self, projected: Tensor, selected_banks: int):
         return product_key_route(projected, bank_count=self.bank_count, selected_banks=selected_banks)
 
+    def _route_both(self, write_routes: Tensor, read_routes: Tensor):
+        """Both roles' routes, ``(ww, wi), (rw, ri)``: one launch when no
+        gradient flows to the scores and the roles select equally many banks."""
+        needs_grad = torch.is_grad_enabled() and (write_routes.requires_grad or read_routes.requires_grad)
+        if not needs_grad and self.num_writes == self.num_reads:
+            return ops.router_select_pair(write_routes, read_routes, bank_count=self.bank_count,
+                                          selected_banks=self.num_writes)
+        return self._route(write_routes, self.num_writes), self._route(read_routes, self.num_reads)
+
     def _normalize_qk(self, value: Tensor) -> Tensor:
         """'nvidia': x * rsqrt(sum x^2 + 1e-6) in FP32 (the in-file formula of
         _parameters.py:219; the reference calls FLA's l2norm on GPU, which is not
@@ -286,8 +295,7 @@ class BankedDeltaMemory(nn.Module):
         """The routed-memory path: concatenated head reads y [B, T, V]."""
         q, k, v, g, b, w = self._controllers(hidden)
         read_routes, write_routes = self._route_projections(hidden)
-        ww, wi = self._route(write_routes, self.num_writes)
-        rw, ri = self._route(read_routes, self.num_reads)
+        (ww, wi), (rw, ri) = self._route_both(write_routes, read_routes)
         state = self._state_heads(self.materialize_initial_state())
         operator = bank_training if self.config.routed_decay else role_bank_training
         return operator(q, k, v, g, b, w, wi, ww, ri, rw, state, self.bank_count, self.bank_size ** -0.5,
@@ -348,8 +356,7 @@ class BankedDeltaMemory(nn.Module):
         elif state_dtype is not None and state_dtype != state.dtype:
             raise ValueError('state_dtype must match the supplied cache')
         (q, k, v, g, b, w), (read_routes, write_routes), gate = self._inference_inputs(hidden)
-        ww, wi = self._route(write_routes, self.num_writes)
-        rw, ri = self._route(read_routes, self.num_reads)
+        (ww, wi), (rw, ri) = self._route_both(write_routes, read_routes)
         meta = ops.dispatch_build(wi, ri, self.bank_count)
         heads_view = state.view(hidden.shape[0], self.bank_count, self.num_heads, self.bank_size,
                                 self.head_value_width)
@@ -384,8 +391,7 @@ class BankedDeltaMemory(nn.Module):
             rw, ww = weights[:, 0:1], weights[:, 1:2]
             ri, wi = indices[:, 0:1], indices[:, 1:2]
         else:
-            ww, wi = self._route(write_routes, self.num_writes)
-            rw, ri = self._route(read_routes, self.num_reads)
+            (ww, wi), (rw, ri) = self._route_both(write_routes, read_routes)
         heads_view = state.view(batch, self.bank_count, self.num_heads, self.bank_size, self.head_value_width)
         return ops.decode_step(q[:, 0], k[:, 0], v[:, 0], g[:, 0], b[:, 0], w[:, 0], wi[:, 0], ww[:, 0],
                                ri[:, 0], rw[:, 0], heads_view, bank_count=self.bank_count,

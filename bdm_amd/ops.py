@@ -93,6 +93,40 @@ def router_select(projected: Tensor, *, bank_count: int, selected_banks: int) ->
     return weights, indices
 
 
+def router_select_pair(first: Tensor, second: Tensor, *, bank_count: int,
+                       selected_banks: int) -> tuple[tuple[Tensor, Tensor], tuple[Tensor, Tensor]]:
+    """``router_select`` of two score tensors of one shape and dtype (a layer's
+    write and read roles) in one launch: ``((w1, i1), (w2, i2))``."""
+    if first.shape != second.shape or first.dtype != second.dtype:
+        return (router_select(first, bank_count=bank_count, selected_banks=selected_banks),
+                router_select(second, bank_count=bank_count, selected_banks=selected_banks))
+    if first.ndim < 1:
+        raise ValueError('projected routes must have a factor dimension')
+    j1, j2 = near_square_factors(bank_count)
+    if first.shape[-1] != j1 + j2:
+        raise ValueError('projected route width does not match the bank table')
+    if not 1 <= selected_banks <= bank_count:
+        raise ValueError('selected bank count is outside the bank table')
+    _require_gpu(first, second)
+    views = []
+    for t in (first, second):
+        stride = _row_stride(t)
+        scores = t if stride else _aligned(t)
+        views.append((scores, stride or scores.shape[-1]))
+    s = min(selected_banks, j1, j2)
+    count = min(selected_banks, s * s)
+    lead = first.shape[:-1]
+    rows = first.numel() // first.shape[-1]
+    device = first.device
+    outs = [(torch.empty((*lead, count), device=device, dtype=first.dtype),
+             torch.empty((*lead, count), device=device, dtype=torch.int64)) for _ in range(2)]
+    _lib.check(_lib.library().bdm_router_select_pair(
+        _ptr(views[0][0]), views[0][1], _ptr(views[1][0]), views[1][1], _dtype_code(first.dtype), rows, j1, j2,
+        selected_banks, _ptr(outs[0][0]), _ptr(outs[0][1]), _ptr(outs[1][0]), _ptr(outs[1][1]),
+        _stream(device)), 'bdm_router_select_pair')
+    return outs[0], outs[1]
+
+
 def _row_stride(t: Tensor) -> int:
     """Row stride of a view whose rows are contiguous and evenly spaced from a
     16-byte aligned start (a column slice of a wider matrix), else 0."""

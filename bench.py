@@ -647,8 +647,7 @@ def main():
     record = {'on': False, 'i': 0}
 
     def step():
-        ww, wi = ops.router_select(write_scores, bank_count=j, selected_banks=kk)
-        rw, ri = ops.router_select(read_scores, bank_count=j, selected_banks=kk)
+        (ww, wi), (rw, ri) = ops.router_select_pair(write_scores, read_scores, bank_count=j, selected_banks=kk)
         meta = ops.dispatch_build(wi, ri, j)
         if record['on']:
             ev_start[record['i']].record(stream)

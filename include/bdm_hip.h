@@ -60,6 +60,14 @@ const char *bdm_last_error_string(void);
 int bdm_router_select(const void *scores, int32_t score_dtype, int64_t rows, int64_t row_stride,
                       int32_t factor_first, int32_t factor_second, int32_t selected,
                       void *weights, int64_t *indices, void *stream);
+/* Two routers of one geometry in one launch (a layer's write and read roles,
+ * `_route(write_routes, num_writes)` and `_route(read_routes, num_reads)`,
+ * implementation/bdm/model.py:96-97): the results of two bdm_router_select
+ * calls, role a to weights_a/indices_a and role b to weights_b/indices_b. */
+int bdm_router_select_pair(const void *scores_a, int64_t row_stride_a, const void *scores_b, int64_t row_stride_b,
+                           int32_t score_dtype, int64_t rows, int32_t factor_first, int32_t factor_second,
+                           int32_t selected, void *weights_a, int64_t *indices_a, void *weights_b,
+                           int64_t *indices_b, void *stream);
 
 /*
  * Causal bank dispatch.  Replaces metadata + the INVERSE/TOKENS outputs of

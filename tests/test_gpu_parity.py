@@ -56,6 +56,28 @@ def test_router_bit_exact(device, bank_count, selected, dtype):
         assert torch.equal(idf.cpu(), i.cpu()[:1, :37]) and torch.equal(wf.cpu(), w.cpu()[:1, :37]), kind
 
 
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize('bank_count', [256, 2048, 12])
+def test_router_pair_equals_two_single_launches(device, dtype, bank_count):
+    """Both roles in one launch give the two single-role results bit for bit,
+    for contiguous scores and for column slices of one projection (row stride
+    wider than the scores)."""
+    from bdm_amd import ops
+    gen = torch.Generator().manual_seed(bank_count + 5)
+    j1, j2 = O.near_square_factors(bank_count)
+    kk = min(8, j1, j2)
+    proj = torch.randn(3, 777, 3 * (j1 + j2) + 8, generator=gen).to(dtype).to(device)
+    layouts = {'contiguous': (proj[..., :j1 + j2].contiguous(), proj[..., j1 + j2:2 * (j1 + j2)].contiguous()),
+               'slices': (proj[..., 8:8 + j1 + j2], proj[..., 8 + j1 + j2:8 + 2 * (j1 + j2)])}
+    for name, (a, b) in layouts.items():
+        announce('router pair', bank_count, dtype, name)
+        (wa, ia), (wb, ib) = ops.router_select_pair(a, b, bank_count=bank_count, selected_banks=kk)
+        wa1, ia1 = ops.router_select(a, bank_count=bank_count, selected_banks=kk)
+        wb1, ib1 = ops.router_select(b, bank_count=bank_count, selected_banks=kk)
+        torch.cuda.synchronize()
+        assert torch.equal(ia, ia1) and torch.equal(ib, ib1) and torch.equal(wa, wa1) and torch.equal(wb, wb1), name
+
+
 def test_router_module_autograd(device):
     from bdm_amd.routing import product_key_route
     gen = torch.Generator().manual_seed(5)
