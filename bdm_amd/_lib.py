@@ -53,6 +53,7 @@ class ForwardArgs(ctypes.Structure):
         ('ctrl_dtype', _i32), ('initial_dtype', _i32), ('final_dtype', _i32),
         ('routed_decay', _i32), ('round_interval', _i32), ('scale', _f32),
         ('snapshots', _vp), ('snapshot_interval', _i32), ('snapshot_dtype', _i32),
+        ('phase_events', _vp * 3),
     ]
 
 

@@ -974,10 +974,19 @@ struct PieceBuffers {
     int64_t max_pieces = 0;  // 0: the path is off
 };
 
+// Profiling events of bdm_forward (phase_events): 0 before the recurrence,
+// 1 before the combine, 2 after it.
+int record_phase(const bdm_forward_args &a, int which, hipStream_t stream) {
+    if (!a.phase_events[0] || !a.phase_events[which]) return BDM_OK;
+    if (hipEventRecord(static_cast<hipEvent_t>(a.phase_events[which]), stream) != hipSuccess)
+        return fail(BDM_ERR_LAUNCH, "forward: recording profiling event %d", which);
+    return BDM_OK;
+}
+
 // The read combine of bdm_forward: y from the read buffer (or zeros when the
 // routes have no reads).
 template <typename T>
-int launch_combine(const bdm_forward_args &a, const T *zbuf, hipStream_t stream) {
+int launch_combine_kernels(const bdm_forward_args &a, const T *zbuf, hipStream_t stream) {
     const int row_width = a.heads * a.head_width;
     const int64_t nt = a.batch * a.time;
     if (a.read_banks > 0) {
@@ -1011,6 +1020,13 @@ int launch_combine(const bdm_forward_args &a, const T *zbuf, hipStream_t stream)
         zero_fill_kernel<T><<<unsigned((count + 255) / 256), 256, 0, stream>>>(static_cast<T *>(a.output), count);
     }
     return check_launch("ordered_combine_kernel");
+}
+
+template <typename T>
+int launch_combine(const bdm_forward_args &a, const T *zbuf, hipStream_t stream) {
+    if (int rc = record_phase(a, 1, stream)) return rc;
+    if (int rc = launch_combine_kernels(a, zbuf, stream)) return rc;
+    return record_phase(a, 2, stream);
 }
 
 template <typename T, int S, int CPL, bool kLazy = false>
@@ -1071,6 +1087,7 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, int *zslot, const PieceBu
         if (int rc = check_launch("read_slot_kernel")) return rc;
     }
     p.nseg = int(nseg);
+    if (int rc = record_phase(a, 0, stream)) return rc;
     if constexpr (kLazy) {
         // the prep role needs one lane per (event, head, half): 32 per head
         const int lthreads = lazy_hb == 2 ? 64 : 256;
@@ -1155,6 +1172,7 @@ int launch_chunked(const bdm_forward_args &a, bf16_t *zbuf, int *zslot, hipStrea
                                                                               zslot);
         if (int rc = check_launch("read_slot_kernel")) return rc;
     }
+    if (int rc = record_phase(a, 0, stream)) return rc;
     const int split = a.head_width > 256 ? a.head_width / 128 : 1;
     ChunkForwardParams p{};
     p.q = static_cast<const bf16_t *>(a.q);

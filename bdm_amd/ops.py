@@ -302,14 +302,17 @@ def snapshot_buffer(x: RoutedInputs, interval: int, dtype: torch.dtype) -> Tenso
 def routed_forward(q, k, v, g, b, w, wi, ww, ri, rw, initial: Tensor, meta: Dispatch, *, bank_count: int,
                    scale: float, routed_decay: bool, round_interval: int = 0,
                    final_state: Tensor | None = None, snapshots: Tensor | None = None,
-                   snapshot_interval: int = 0, prepared: RoutedInputs | None = None) -> Tensor:
+                   snapshot_interval: int = 0, prepared: RoutedInputs | None = None,
+                   phase_events=None) -> Tensor:
     """Bank recurrence and ordered read combine for every head.
 
     q,k,g,b: [B,T,S] or [B,T,H,S];  v,w: [B,T,v] or [B,T,H,v];
     initial: [J,S,v] / [J,H,S,v] shared by the batch, or [B,J,S,v] /
     [B,J,H,S,v] per sequence (4-D is read as per-head when q is 4-D);
     final_state: optional [B,J,H,S,v] (or [B,J,S,v]) output, may alias initial;
-    snapshots: optional buffer from ``snapshot_buffer`` for the backward.
+    snapshots: optional buffer from ``snapshot_buffer`` for the backward;
+    phase_events: optional three torch.cuda.Event (timing enabled) recorded on
+    the current stream before the recurrence, before the combine and after it.
     Returns y [B, T, H*v] in the controller dtype."""
     x = prepared or prepare_routed(q, k, v, g, b, w, wi, ww, ri, rw, initial, bank_count=bank_count)
     _require_gpu(meta.order, final_state, snapshots)
@@ -341,6 +344,11 @@ def routed_forward(q, k, v, g, b, w, wi, ww, ri, rw, initial: Tensor, meta: Disp
         args.snapshots = snapshots.data_ptr()
         args.snapshot_interval = int(snapshot_interval)
         args.snapshot_dtype = _dtype_code(snapshots.dtype)
+    if phase_events is not None:
+        for i, ev in enumerate(phase_events):
+            if ev.cuda_event == 0:  # torch creates the HIP event on first use
+                ev.record()
+            args.phase_events[i] = ev.cuda_event
     lib = _lib.library()
     ws_bytes = lib.bdm_forward_workspace_size(ctypes.byref(args))
     workspace = torch.empty(max(int(ws_bytes), 1), device=x.device, dtype=torch.uint8)

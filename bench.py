@@ -117,6 +117,44 @@ def hot_path_algorithmic_bytes(cfg, batch, time_):
     return per_token * batch * time_ + batch * cfg.bank_count * h * s * (v_total // h) * 2
 
 
+VALU_FP32_TFLOPS = 78.6   # MI355X FP32 vector peak without packed-FP32 instructions (disabled in this build)
+MFMA_FP32_TFLOPS = 157.3  # MI355X FP32 matrix peak
+MFMA_BF16_TFLOPS = 2500.0  # MI355X BF16 matrix peak, dense
+
+
+def recurrence_flop(cfg, batch, time_):
+    """Algorithmic FLOPs of the sequential recurrence: 5*S*v per write and
+    2*S*v per read, per head (458,752 per token at C2)."""
+    s, v, h, k = cfg.bank_size, cfg.head_value_width, cfg.num_heads, cfg.selected_banks
+    return batch * time_ * h * k * (5 * s * v + 2 * s * v)
+
+
+def recurrence_roofline(cfg, batch, time_, ms):
+    """The recurrence kernels, timed with events bdm_forward records around
+    them: algorithmic FLOPs against the compute peaks.  The default kernel runs
+    on the vector ALUs (no MFMA: BDM_FORWARD_KERNEL=mfma selects the
+    matrix-core variant)."""
+    flop = recurrence_flop(cfg, batch, time_)
+    tflops = flop / (ms * 1e-3) / 1e12
+    kernel = os.environ.get('BDM_FORWARD_KERNEL', 'vector')
+    return {'kernel': 'chunk_forward_kernel (MFMA)' if kernel == 'mfma' else 'lazy_forward_kernel (vector ALU)',
+            'ms': round(ms, 4), 'flop': flop, 'achieved_tflops': round(tflops, 2),
+            'bound': 'mfma' if kernel == 'mfma' else 'valu',
+            'valu_fp32_peak_tflops': VALU_FP32_TFLOPS, 'frac_valu_fp32': round(tflops / VALU_FP32_TFLOPS, 4),
+            'mfma_fp32_peak_tflops': MFMA_FP32_TFLOPS, 'frac_mfma_fp32': round(tflops / MFMA_FP32_TFLOPS, 4),
+            'mfma_utilisation': None if kernel == 'mfma' else 0.0,
+            'note': 'FLOPs of the sequential form (5Sv per write, 2Sv per read, per head); the vector kernel '
+                    'issues 2 FMAs per state element per write, 1 per read (lazy decay)'}
+
+
+def combine_roofline(cfg, batch, time_, ms):
+    """The ordered read combine: KR rows of V BF16 values in, V out, per token."""
+    nbytes = batch * time_ * (cfg.selected_banks + 1) * cfg.value_width * 2
+    gbps = nbytes / (ms * 1e-3) / 1e9
+    return {'kernel': 'ordered_combine_kernel', 'ms': round(ms, 4), 'bytes': nbytes, 'achieved_GBps': round(gbps, 1),
+            'peak_GBps': HBM_PEAK_GBPS, 'frac': round(gbps / HBM_PEAK_GBPS, 4)}
+
+
 def timed(fn, steps, warmup):
     """Run fn warmup times, then time exactly `steps` calls between two
     device synchronisations.  Returns (seconds per step, last result)."""
@@ -459,8 +497,7 @@ def c4_forward(device, steps=3):
                         dtype=torch.bfloat16)
 
     def step():
-        ww, wi = ops.router_select(wr, bank_count=cfg.bank_count, selected_banks=8)
-        rw, ri = ops.router_select(rr, bank_count=cfg.bank_count, selected_banks=8)
+        (ww, wi), (rw, ri) = ops.router_select_pair(wr, rr, bank_count=cfg.bank_count, selected_banks=8)
         meta = ops.dispatch_build(wi, ri, cfg.bank_count)
         ops.routed_forward(q, k, v, g, b, w, wi, ww, ri, rw, initial, meta, bank_count=cfg.bank_count,
                            scale=cfg.bank_size ** -0.5, routed_decay=True, round_interval=0, final_state=final)
@@ -469,7 +506,11 @@ def c4_forward(device, steps=3):
     with torch.no_grad():
         sec, meta = timed(step, steps, 1)
     lengths = (meta.cu_seqlens[1:] - meta.cu_seqlens[:-1]).float()
+    hot_bytes = hot_path_algorithmic_bytes(cfg, 4, 8192)
     return {'tokens_per_s': round(4 * 8192 / sec, 1), 'ms_per_step': round(sec * 1e3, 3),
+            'policy': 'FP32 state (prefill), long segments cut into pieces',
+            'hot_path_bytes_per_token': hot_bytes // (4 * 8192),
+            'hot_path_roofline_frac': round(hot_bytes / sec / 1e9 / HBM_PEAK_GBPS, 4),
             'max_segment_events': int(lengths.max()), 'mean_segment_events': round(float(lengths.mean()), 1)}
 
 
@@ -518,8 +559,15 @@ def c2_forward_only(layer, device, batch, time_, launches):
                                scale=cfg.bank_size ** -0.5, routed_decay=True, round_interval=ROUND_INTERVAL,
                                final_state=final)
         torch.cuda.synchronize()
-    return {'launches': launches, 'ms_per_launch': round((time.perf_counter() - t0) / launches * 1e3, 4),
-            'recurrence': os.environ.get('BDM_FORWARD_KERNEL', 'vector')}
+        ms = (time.perf_counter() - t0) / launches * 1e3
+        # one copy of known size, the reference for calibrating FETCH_SIZE and
+        # WRITE_SIZE counters: 512 MiB read and 512 MiB written by torch.neg
+        src = torch.empty(256 * 1024 * 1024, device=device, dtype=torch.bfloat16).fill_(1.0)
+        dst = torch.empty_like(src)
+        torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+    return {'launches': launches, 'ms_per_launch': round(ms, 4),
+            'recurrence': os.environ.get('BDM_FORWARD_KERNEL', 'vector'), 'copy_probe_bytes': 2 * src.numel() * 2}
 
 
 def c1_config():
@@ -644,6 +692,8 @@ def main():
     stream = torch.cuda.current_stream(device)
     ev_start = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
     ev_stop = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    # recorded by bdm_forward itself: before the recurrence, before the combine, after it
+    ev_phase = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
     record = {'on': False, 'i': 0}
 
     def step():
@@ -651,8 +701,10 @@ def main():
         meta = ops.dispatch_build(wi, ri, j)
         if record['on']:
             ev_start[record['i']].record(stream)
+        phases = ev_phase[record['i']] if record['on'] else None
         y = ops.routed_forward(q, k, v, g, b, w, wi, ww, ri, rw, initial, meta, bank_count=j, scale=scale,
-                               routed_decay=True, round_interval=ROUND_INTERVAL, final_state=final)
+                               routed_decay=True, round_interval=ROUND_INTERVAL, final_state=final,
+                               phase_events=phases)
         if record['on']:
             ev_stop[record['i']].record(stream)
             record['i'] += 1
@@ -673,6 +725,8 @@ def main():
     sec = elapsed / args.steps
     tokens = batch * time_
     fwd_ms = statistics.mean(a.elapsed_time(bb) for a, bb in zip(ev_start, ev_stop))
+    rec_ms = statistics.mean(e[0].elapsed_time(e[1]) for e in ev_phase)
+    comb_ms = statistics.mean(e[1].elapsed_time(e[2]) for e in ev_phase)
     fwd_bytes = forward_algorithmic_bytes(cfg, batch, time_, initial.numel() * initial.element_size())
     achieved = fwd_bytes / (fwd_ms * 1e-3) / 1e9
     hot_bytes = hot_path_algorithmic_bytes(cfg, batch, time_)
@@ -693,8 +747,14 @@ def main():
                      'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBPS, 'unit': 'GB/s',
                      'frac': round(achieved / HBM_PEAK_GBPS, 4),
                      'traffic': traffic.get('bytes_per_launch') if traffic else None,
+                     'traffic_source': ('FETCH_SIZE x2 + WRITE_SIZE x1 per launch from rocprofv3 --pmc runs of '
+                                        'bench.py --only c2-forward, calibrated on a 512 MiB copy in the same '
+                                        'process (profiles/forward_c2_traffic.json)') if traffic else None,
                      'launch_ms': round(fwd_ms, 4), 'algorithmic_bytes': fwd_bytes},
         'hot_path_roofline_frac': round(hot_bytes / sec / 1e9 / HBM_PEAK_GBPS, 4),
+        'recurrence': recurrence_roofline(cfg, batch, time_, rec_ms),
+        'combine': combine_roofline(cfg, batch, time_, comb_ms),
+        'front_end_ms': round(sec * 1e3 - fwd_ms, 4),
     }
     if not args.no_extras:
         progress('full layer prefill')

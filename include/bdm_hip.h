@@ -170,6 +170,10 @@ typedef struct bdm_forward_args {
     void *snapshots;           /* NULL or [rows, H, S, v] of snapshot_dtype (see above) */
     int32_t snapshot_interval;
     int32_t snapshot_dtype;    /* BDM_BF16 only with round_interval == snapshot_interval */
+    /* Profiling: NULL, or three hipEvent_t the call records on its stream
+     * before the recurrence kernels, between them and the read combine, and
+     * after the combine, so a caller can time the two phases apart. */
+    void *phase_events[3];
 } bdm_forward_args;
 
 /* Rows of the snapshot buffer for E packed events: E / interval. */
