@@ -496,10 +496,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     const bool rounding = MODE == 0 && p.round_interval > 0;
     const int nstages = int((end - start + NE - 1) / NE);
 
+    // Pointers used once per stage or less live in LDS rather than in SGPRs:
+    // the event loop keeps most scalar registers busy, and each SGPR the
+    // compiler spills to a VGPR lane costs a v_readlane at every use.  Only
+    // v, w and zbuf (addressed at every event) stay scalar.
+    enum { P_ORDER, P_ZSLOT, P_Q, P_K, P_B, P_G, P_WW, P_RW, P_SNAP, P_FINAL, P_COUNT };
+    __shared__ uint64_t s_ptr[P_COUNT];
+    if (tid == 0) {
+        s_ptr[P_ORDER] = reinterpret_cast<uint64_t>(p.order);
+        s_ptr[P_ZSLOT] = reinterpret_cast<uint64_t>(p.zslot);
+        s_ptr[P_Q] = reinterpret_cast<uint64_t>(p.q);
+        s_ptr[P_K] = reinterpret_cast<uint64_t>(p.k);
+        s_ptr[P_B] = reinterpret_cast<uint64_t>(p.b);
+        s_ptr[P_G] = reinterpret_cast<uint64_t>(p.g);
+        s_ptr[P_WW] = reinterpret_cast<uint64_t>(p.ww);
+        s_ptr[P_RW] = reinterpret_cast<uint64_t>(p.rw);
+        s_ptr[P_SNAP] = reinterpret_cast<uint64_t>(p.snap);
+        s_ptr[P_FINAL] = reinterpret_cast<uint64_t>(p.final_state);
+    }
+    __syncthreads();
+    // (a pointer read back from LDS is generic; casting it through the global
+    // address space keeps its accesses global, not flat, which would also
+    // count against the LDS wait counter)
+    auto lds_ptr = [&](int which) -> void * {
+        return (void *)(__attribute__((address_space(1))) char *)(s_ptr[which]);
+    };
+
     // ---- metadata of a stage from its packed order entries (lanes 0..15)
     auto load_order = [&](int stage) -> int {
         const int64_t pos = start + int64_t(stage) * NE + tid;
-        if (tid < NE && stage < nstages && pos < end) return int(p.order[pos]);
+        if (tid < NE && stage < nstages && pos < end) return int(static_cast<const int64_t *>(lds_ptr(P_ORDER))[pos]);
         return -1;
     };
     auto decode_order = [&](int stage, int o) {
@@ -535,20 +561,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         const int64_t row = (int64_t(s_tok[slot][pe]) * p.s_heads + (head0 + ph) / p.split) * S + 4 * half;
         const int route = s_route[slot][pe];
         if (rd) {
-            if (tid < NE) pl.zrow = p.zslot[route];
-            load_vec4(p.q + row, pl.key);
+            if (tid < NE) pl.zrow = static_cast<const int *>(lds_ptr(P_ZSLOT))[route];
+            load_vec4(static_cast<const T *>(lds_ptr(P_Q)) + row, pl.key);
+            const T *rw = static_cast<const T *>(lds_ptr(P_RW));
             if constexpr (std::is_same<T, bf16_t>::value)
-                pl.weight = p.rw[route].bits;
+                pl.weight = rw[route].bits;
             else
-                pl.weight_raw = p.rw[route];
+                pl.weight_raw = rw[route];
         } else {
-            load_vec4(p.k + row, pl.key);
-            load_vec4(p.b + row, pl.erase);
-            pl.gate = *reinterpret_cast<const float4 *>(p.g + row);
+            load_vec4(static_cast<const T *>(lds_ptr(P_K)) + row, pl.key);
+            load_vec4(static_cast<const T *>(lds_ptr(P_B)) + row, pl.erase);
+            pl.gate = *reinterpret_cast<const float4 *>(static_cast<const float *>(lds_ptr(P_G)) + row);
+            const T *ww = static_cast<const T *>(lds_ptr(P_WW));
             if constexpr (std::is_same<T, bf16_t>::value)
-                pl.weight = p.ww[route].bits;
+                pl.weight = ww[route].bits;
             else
-                pl.weight_raw = p.ww[route];
+                pl.weight_raw = ww[route];
         }
     };
     // compute the row operands of `stage` into buffer stage & 1 (two barriers)
@@ -676,10 +704,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
                     for (int c = 0; c < CPL; ++c) h[r][c] = round_bf16(h[r][c]);
             }
             // snapshot of the state before event `base` (see routed_forward_kernel)
-            if (p.snap) {
+            if (void *snap = lds_ptr(P_SNAP)) {
                 // stage starts are the multiples of snap_interval = kLazyStage
                 const int64_t sslot = (start / NE) + st - 1;
-                store_state<S, CPL>(p.snap, p.snap_dtype, sslot * p.s_heads * S * p.row_stride + head_cols,
+                store_state<S, CPL>(snap, p.snap_dtype, sslot * p.s_heads * S * p.row_stride + head_cols,
                                     p.row_stride, S, h);
             }
         }
@@ -791,9 +819,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 #pragma unroll
             for (int r = 0; r < S; ++r) pt[r * S + pcol] = pc[r];
         }
-    } else if (p.final_state && piece == pieces - 1) {
+    } else if (lds_ptr(P_FINAL) && piece == pieces - 1) {
         const int64_t final_offset = bidx * (int64_t(p.banks) * p.s_heads * S * p.row_stride) + state_offset;
-        store_state<S, CPL>(p.final_state, p.final_dtype, final_offset, p.row_stride, S, h);
+        store_state<S, CPL>(lds_ptr(P_FINAL), p.final_dtype, final_offset, p.row_stride, S, h);
     }
 }
 

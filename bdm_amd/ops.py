@@ -303,7 +303,7 @@ def routed_forward(q, k, v, g, b, w, wi, ww, ri, rw, initial: Tensor, meta: Disp
                    scale: float, routed_decay: bool, round_interval: int = 0,
                    final_state: Tensor | None = None, snapshots: Tensor | None = None,
                    snapshot_interval: int = 0, prepared: RoutedInputs | None = None,
-                   phase_events=None) -> Tensor:
+                   phase_events=None, workspace: Tensor | None = None) -> Tensor:
     """Bank recurrence and ordered read combine for every head.
 
     q,k,g,b: [B,T,S] or [B,T,H,S];  v,w: [B,T,v] or [B,T,H,v];
@@ -312,7 +312,10 @@ def routed_forward(q, k, v, g, b, w, wi, ww, ri, rw, initial: Tensor, meta: Disp
     final_state: optional [B,J,H,S,v] (or [B,J,S,v]) output, may alias initial;
     snapshots: optional buffer from ``snapshot_buffer`` for the backward;
     phase_events: optional three torch.cuda.Event (timing enabled) recorded on
-    the current stream before the recurrence, before the combine and after it.
+    the current stream before the recurrence, before the combine and after it;
+    workspace: optional uint8 device tensor of at least
+    bdm_forward_workspace_size bytes (allocated per call otherwise); its
+    contents on entry do not matter.
     Returns y [B, T, H*v] in the controller dtype."""
     x = prepared or prepare_routed(q, k, v, g, b, w, wi, ww, ri, rw, initial, bank_count=bank_count)
     _require_gpu(meta.order, final_state, snapshots)
@@ -351,7 +354,11 @@ def routed_forward(q, k, v, g, b, w, wi, ww, ri, rw, initial: Tensor, meta: Disp
             args.phase_events[i] = ev.cuda_event
     lib = _lib.library()
     ws_bytes = lib.bdm_forward_workspace_size(ctypes.byref(args))
-    workspace = torch.empty(max(int(ws_bytes), 1), device=x.device, dtype=torch.uint8)
+    if workspace is None:
+        workspace = torch.empty(max(int(ws_bytes), 1), device=x.device, dtype=torch.uint8)
+    elif workspace.dtype != torch.uint8 or workspace.device != x.device or workspace.numel() < ws_bytes \
+            or not workspace.is_contiguous():
+        raise ValueError(f'workspace must be a contiguous uint8 tensor of at least {ws_bytes} bytes on {x.device}')
     _lib.check(lib.bdm_forward(ctypes.byref(args), _ptr(workspace), ws_bytes, _stream(x.device)), 'bdm_forward')
     return output
 
