@@ -280,7 +280,9 @@ __global__ __launch_bounds__(256) void routed_forward_kernel(ForwardParams<T> p)
 // x = bf(w*p) * v: w*p is an exact FP32 product of two BF16 values, rounded
 // to nearest even by v_cvt_pk_bf16_f32; the product bf(w*p) * v is added to
 // the erase sum by v_dot2c_f32_bf16 against an operand whose other half is
-// zero, which adds the exact FP32 product of the two BF16 values.
+// zero, which adds the exact FP32 product of the two BF16 values (the zero
+// half multiplies a finite neighbour column).  w*p itself is formed the same
+// way, against (p, 0) or (0, p).
 
 // CPL consecutive columns of T kept as raw 32-bit words (BF16 pairs unpacked
 // on use), so a prefetched row costs CPL/2 (BF16) or CPL (FP32) registers.
@@ -316,6 +318,19 @@ __device__ __forceinline__ float dot_half_acc(float acc, uint32_t a, uint32_t b_
                                            acc, false);
 }
 
+// A read row of CPL columns stored with nontemporal stores (4-byte words).
+template <int CPL>
+__device__ __forceinline__ void store_row_nt(bf16_t *p, const float (&z)[CPL]) {
+    uint32_t *dst = reinterpret_cast<uint32_t *>(p);
+#pragma unroll
+    for (int i = 0; i < CPL / 2; ++i) __builtin_nontemporal_store(pack_bf16x2(z[2 * i], z[2 * i + 1]), dst + i);
+}
+template <int CPL>
+__device__ __forceinline__ void store_row_nt(float *p, const float (&z)[CPL]) {
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) __builtin_nontemporal_store(z[i], p + i);
+}
+
 // The gated value of a write, x[c] = bf(w[c] * pw) * v[c], kept in a form
 // whose product is added to an accumulator as the last step of the erase sum.
 template <typename T, int CPL>
@@ -323,20 +338,27 @@ struct GatedValues;
 
 template <int CPL>
 struct GatedValues<bf16_t, CPL> {
-    uint32_t ew[CPL / 2];  // bf(w * pw), packed pairs
+    // bf(w * pw) of each column, packed with a zero in the other half:
+    // lo[i] = (bf(w[2i] pw), 0), hi[i] = (0, bf(w[2i+1] pw))
+    uint32_t lo[CPL / 2], hi[CPL / 2];
     uint32_t v[CPL / 2];
+    // pw is a BF16 value (the route weight): w * pw is an exact FP32 product,
+    // formed by v_dot2c_f32_bf16 from the packed w pair and (pw, 0) or (0, pw)
     __device__ __forceinline__ void make(const RawCols<bf16_t, CPL> &w, const RawCols<bf16_t, CPL> &vv, float pw) {
+        const uint32_t pb = __float_as_uint(pw) >> 16;
+        const uint32_t p_lo = pb, p_hi = pb << 16;
 #pragma unroll
         for (int i = 0; i < CPL / 2; ++i) {
-            const float e0 = __uint_as_float(w.u[i] << 16) * pw;        // exact: BF16 * BF16
-            const float e1 = __uint_as_float(w.u[i] & 0xffff0000u) * pw;
-            ew[i] = pack_bf16x2(e0, e1);
+            const float e0 = dot_half_acc(0.f, w.u[i], p_lo);
+            const float e1 = dot_half_acc(0.f, w.u[i], p_hi);
+            lo[i] = pack_bf16x2(e0, 0.f);
+            hi[i] = pack_bf16x2(0.f, e1);
             v[i] = vv.u[i];
         }
     }
     // acc + x[c]
     __device__ __forceinline__ float add_to(float acc, int c) const {
-        return dot_half_acc(acc, ew[c / 2], (c & 1) ? (v[c / 2] & 0xffff0000u) : (v[c / 2] & 0x0000ffffu));
+        return dot_half_acc(acc, (c & 1) ? hi[c / 2] : lo[c / 2], v[c / 2]);
     }
 };
 
@@ -679,14 +701,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     issue_prep(0);
     finish_prep(0);
 
-    // v, w of the next write in stream order (across stages)
-    RawCols<T, CPL> nv, nw_;
+    // v, w of the writes in stream order (across stages), in two register
+    // sets used alternately: write k's rows are loaded while write k-1 runs,
+    // into the set write k-1 does not use, so no registers are copied.  At a
+    // stage start the stage's first write is in set A.
+    RawCols<T, CPL> va, wa, vb, wb;
     auto fetch = [&](int slot, int e, RawCols<T, CPL> &vv, RawCols<T, CPL> &ww) {
         const int64_t row = int64_t(__builtin_amdgcn_readfirstlane(s_tok[slot][e])) * hw;
         vv.load(reinterpret_cast<const T *>(reinterpret_cast<const char *>(p.v + row) + lane_bytes));
         ww.load(reinterpret_cast<const T *>(reinterpret_cast<const char *>(p.w + row) + lane_bytes));
     };
-    bool prefetched = false;  // nv, nw_ hold the current stage's first write
+    bool prefetched = false;  // the current stage's first write was fetched by the previous stage
+    bool in_b = false;        // ... into set B (an odd number of writes ran since)
 
     for (int st = 0; st < nstages; ++st) {
         const int slot = st % 3;
@@ -720,7 +746,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 
         auto read_event = [&](int i) {
             if constexpr (MODE == 1) return;  // a read does not change the state
-            const int64_t zrow = int64_t(__builtin_amdgcn_readfirstlane(s_route[slot][i])) * hw;
+            const int zrow = __builtin_amdgcn_readfirstlane(s_route[slot][i]);
             const float *row = &s_rows[i][lh][0][0];
             float gamma[S];
 #pragma unroll
@@ -733,67 +759,109 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
                 for (int r = 0; r < S; ++r) acc = fmaf(gamma[r], h[r][c], acc);
                 z[c] = acc;
             }
-            store_row<CPL>(reinterpret_cast<T *>(reinterpret_cast<char *>(p.zbuf + zrow) + lane_bytes), z);
+            // nontemporal: the rows are read once, by the combine after the
+            // recurrence, and should not displace the v, w rows that the
+            // token's other write banks are about to read from L2
+            store_row_nt<CPL>(reinterpret_cast<T *>(reinterpret_cast<char *>(p.zbuf + int64_t(zrow) * hw) + lane_bytes),
+                              z);
+        };
+        // write `wi_` of the stage with its v, w rows in (vc, wc)
+        auto write_event = [&](int wi_, const RawCols<T, CPL> &vc, const RawCols<T, CPL> &wc) {
+            const float *row = &s_rows[wi_][lh][0][0];
+            const float pw = s_pw[wi_];
+            if (eager) {
+                // hd = diag(d) M first; the update below then uses a and k
+                // (a wave-uniform branch: the stage's form is uniform)
+#pragma unroll
+                for (int r = 0; r < S; ++r) {
+                    const float d = row[2 * S + r];
+#pragma unroll
+                    for (int c = 0; c < CPL; ++c) h[r][c] *= d;
+                    if constexpr (MODE == 1) pc[r] *= d;
+                }
+            }
+            float nalpha[S], beta[S];
+#pragma unroll
+            for (int r = 0; r < S; ++r) {
+                nalpha[r] = row[r];
+                beta[r] = row[S + r];
+            }
+            // lazy: u = x - sum (a s') Mh, Mh += (k / s') u;  eager: u = x - sum a hd, M = hd + k u.
+            // The sums over rows come first: they need no v, w, whose loads
+            // are waited for only when the gated value x is formed.
+            float u[CPL];
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+                u[c] = nalpha[0] * h[0][c];
+#pragma unroll
+                for (int r = 1; r < S; ++r) u[c] = fmaf(nalpha[r], h[r][c], u[c]);
+            }
+            GatedValues<T, CPL> x;
+            x.make(wc, vc, pw);
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+                u[c] = x.add_to(u[c], c);
+#pragma unroll
+                for (int r = 0; r < S; ++r) h[r][c] = fmaf(beta[r], u[c], h[r][c]);
+            }
+            if constexpr (MODE == 1) {
+                // the transition column: the same update with x = 0
+                float uc = nalpha[0] * pc[0];
+#pragma unroll
+                for (int r = 1; r < S; ++r) uc = fmaf(nalpha[r], pc[r], uc);
+#pragma unroll
+                for (int r = 0; r < S; ++r) pc[r] = fmaf(beta[r], uc, pc[r]);
+            }
         };
         // Events in packed order, as runs: the reads before each write, then
         // the write, so the state is updated exactly once per iteration and
-        // never merged from branches.
+        // never merged from branches.  Writes alternate between the register
+        // sets A and B (two writes per loop iteration).
         {
-            if (nw > 0 && !prefetched) fetch(slot, __builtin_amdgcn_readfirstlane(s_wpos[slot][0]), nv, nw_);
+            if (nw > 0) {
+                if (!prefetched) {
+                    fetch(slot, __builtin_amdgcn_readfirstlane(s_wpos[slot][0]), va, wa);
+                } else if (in_b) {
+                    va = vb;
+                    wa = wb;
+                }
+            }
             prefetched = false;
-            int i = 0;
-#pragma unroll 1
-            for (int wk = 0; wk < nw; ++wk) {
-                const int wi_ = __builtin_amdgcn_readfirstlane(s_wpos[slot][wk]);
-                const RawCols<T, CPL> vc = nv, wc = nw_;
+            in_b = false;
+            // the rows of write wk + 1 (of this stage, or the next stage's
+            // first).  Always two loads, so that the compiler can wait for
+            // the previous set with vmcnt(2) instead of draining these; with
+            // no next write, write wk's rows are loaded again (harmless).
+            auto fetch_next = [&](int wk, RawCols<T, CPL> &vv, RawCols<T, CPL> &ww) {
+                int fs = slot, fe = wk;
                 if (wk + 1 < nw) {
-                    fetch(slot, __builtin_amdgcn_readfirstlane(s_wpos[slot][wk + 1]), nv, nw_);
+                    fe = wk + 1;
                 } else if (next_has_write) {
-                    fetch(next_slot, __builtin_amdgcn_readfirstlane(s_wpos[next_slot][0]), nv, nw_);
+                    fs = next_slot;
+                    fe = 0;
                     prefetched = true;
                 }
+                fetch(fs, __builtin_amdgcn_readfirstlane(s_wpos[fs][fe]), vv, ww);
+            };
+            int i = 0;
+#pragma unroll 1
+            for (int wk = 0; wk < nw; wk += 2) {
+                int wi_ = __builtin_amdgcn_readfirstlane(s_wpos[slot][wk]);
+                fetch_next(wk, vb, wb);
 #pragma unroll 1
                 for (; i < wi_; ++i) read_event(i);
                 i = wi_ + 1;
-                const float *row = &s_rows[wi_][lh][0][0];
-                const float pw = s_pw[wi_];
-                if (eager) {
-                    // hd = diag(d) M first; the update below then uses a and k
-                    // (a wave-uniform branch: the stage's form is uniform)
-#pragma unroll
-                    for (int r = 0; r < S; ++r) {
-                        const float d = row[2 * S + r];
-#pragma unroll
-                        for (int c = 0; c < CPL; ++c) h[r][c] *= d;
-                        if constexpr (MODE == 1) pc[r] *= d;
-                    }
+                write_event(wi_, va, wa);
+                if (wk + 1 >= nw) {
+                    in_b = prefetched;
+                    break;
                 }
-                float nalpha[S], beta[S];
-#pragma unroll
-                for (int r = 0; r < S; ++r) {
-                    nalpha[r] = row[r];
-                    beta[r] = row[S + r];
-                }
-                GatedValues<T, CPL> x;
-                x.make(wc, vc, pw);
-                // lazy: u = x - sum (a s') Mh, Mh += (k / s') u;  eager: u = x - sum a hd, M = hd + k u
-#pragma unroll
-                for (int c = 0; c < CPL; ++c) {
-                    float u = nalpha[0] * h[0][c];
-#pragma unroll
-                    for (int r = 1; r < S; ++r) u = fmaf(nalpha[r], h[r][c], u);
-                    u = x.add_to(u, c);
-#pragma unroll
-                    for (int r = 0; r < S; ++r) h[r][c] = fmaf(beta[r], u, h[r][c]);
-                }
-                if constexpr (MODE == 1) {
-                    // the transition column: the same update with x = 0
-                    float u = nalpha[0] * pc[0];
-#pragma unroll
-                    for (int r = 1; r < S; ++r) u = fmaf(nalpha[r], pc[r], u);
-#pragma unroll
-                    for (int r = 0; r < S; ++r) pc[r] = fmaf(beta[r], u, pc[r]);
-                }
+                wi_ = __builtin_amdgcn_readfirstlane(s_wpos[slot][wk + 1]);
+                fetch_next(wk + 1, va, wa);
+#pragma unroll 1
+                for (; i < wi_; ++i) read_event(i);
+                i = wi_ + 1;
+                write_event(wi_, vb, wb);
             }
 #pragma unroll 1
             for (; i < n; ++i) read_event(i);
