@@ -20,7 +20,8 @@ BDM_ROUTE_DUPLICATE = 2
 EXPORTED_SYMBOLS = (
     'bdm_version', 'bdm_last_error_string', 'bdm_router_select', 'bdm_dispatch_workspace_size',
     'bdm_dispatch_build', 'bdm_forward_workspace_size', 'bdm_forward', 'bdm_snapshot_rows',
-    'bdm_backward_workspace_size', 'bdm_backward', 'bdm_decode', 'bdm_controller_epilogue', 'bdm_output_epilogue',
+    'bdm_backward_workspace_size', 'bdm_backward', 'bdm_decode', 'bdm_decode_fused', 'bdm_decode_fused_supported',
+    'bdm_controller_epilogue', 'bdm_output_epilogue',
     'bdm_bank_occupancy',
     'bdm_written_bank_curve',
     'bdm_rms_norm',
@@ -82,6 +83,20 @@ class DecodeArgs(ctypes.Structure):
         ('heads', _i32), ('bank_size', _i32), ('head_width', _i32), ('bank_count', _i32),
         ('write_banks', _i32), ('read_banks', _i32),
         ('ctrl_dtype', _i32), ('state_dtype', _i32), ('routed_decay', _i32), ('scale', _f32),
+    ]
+
+
+class DecodeFusedArgs(ctypes.Structure):
+    """Mirror of ``bdm_decode_fused_args``."""
+    _fields_ = [
+        ('proj', _vp), ('f', _vp), ('a_log', _vp), ('dt_bias', _vp), ('state', _vp), ('output', _vp),
+        ('batch', _i64), ('proj_stride', _i64), ('f_stride', _i64),
+        ('q_col', _i32), ('k_col', _i32), ('v_col', _i32), ('b_col', _i32), ('w_col', _i32),
+        ('read_col', _i32), ('write_col', _i32),
+        ('heads', _i32), ('bank_size', _i32), ('head_width', _i32), ('factor_first', _i32),
+        ('factor_second', _i32), ('selected_banks', _i32),
+        ('ctrl_dtype', _i32), ('param_dtype', _i32), ('state_dtype', _i32), ('qk_norm', _i32),
+        ('routed_decay', _i32), ('scale', _f32),
     ]
 
 
@@ -171,6 +186,10 @@ def library() -> ctypes.CDLL:
     lib.bdm_backward.restype = _i32
     lib.bdm_decode.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
     lib.bdm_decode.restype = _i32
+    lib.bdm_decode_fused.argtypes = [ctypes.POINTER(DecodeFusedArgs), _vp]
+    lib.bdm_decode_fused.restype = _i32
+    lib.bdm_decode_fused_supported.argtypes = [ctypes.POINTER(DecodeFusedArgs)]
+    lib.bdm_decode_fused_supported.restype = _i32
     lib.bdm_controller_epilogue.argtypes = [ctypes.POINTER(ControllerArgs), _vp]
     lib.bdm_controller_epilogue.restype = _i32
     lib.bdm_output_epilogue.argtypes = [ctypes.POINTER(OutputArgs), _vp]

@@ -19,7 +19,9 @@
 #include <type_traits>
 
 #include "bdm_common.h"
+#include "epilogue_ops.h"
 #include "recurrence_ops.h"
+#include "router_ops.h"
 
 namespace bdm {
 namespace {
@@ -53,11 +55,24 @@ struct DecodeParams {
     int vec_rows;  // q, k, b, g rows of S elements can be read as 16-byte vectors
     int state_dtype, routed_decay;
     float scale;
+    // fused step (bdm_decode_fused): the controllers and routes come from the
+    // projection row proj[seq] (column offsets below) and the f_proj output
+    const T *proj, *f;
+    const void *a_log, *dt_bias;
+    int64_t proj_stride, f_stride;
+    int q_col, k_col, v_col, b_col, w_col, read_col, write_col;
+    int j1, j2, param_dtype, qk_norm;
 };
 
 // SE: the state element type (bf16_t or float, the state_dtype argument);
 // KMAX >= the selected banks per role, KFIX: exactly KMAX banks in both roles.
-template <typename T, typename SE, int S, int CPL, bool VEC, int KMAX, bool KFIX>
+// FUSED: the step starts from the projection outputs (bdm_decode_fused):
+// waves 0 and 1 route the write and read scores of the sequence (the wave
+// router of router_ops.h), lanes 0..3 of wave 2 form the head's q, k, b, g
+// rows and every lane its own v, w columns (the controller epilogue's
+// helpers of epilogue_ops.h), so the inputs equal those the separate kernels
+// would have stored, bit for bit.
+template <typename T, typename SE, int S, int CPL, bool VEC, int KMAX, bool KFIX, bool FUSED = false>
 __global__ __launch_bounds__(512) void decode_kernel(DecodeParams<T> p) {
     extern __shared__ float smem[];
     // smem layout: written states [kw][S][span], read values [kr][span]
@@ -76,48 +91,104 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeParams<T> p) {
     const bool has_read = slot < p.kr;
     auto clamp_bank = [&](int64_t bank) { return bank < 0 ? int64_t(0) : (bank >= p.banks ? int64_t(p.banks - 1) : bank); };
 
-    // ---- round trip 1: everything that does not depend on a bank index,
-    // issued together with no barrier behind it.  The token's bank indices,
-    // route weights and controller rows have workgroup-uniform addresses and
-    // are read by scalar loads (entry j >= K re-reads entry K-1, so every
-    // address is in bounds and the loads are unconditional); each lane group
-    // selects its own slot's entries.  The lane's value columns are vector loads.
-    const int64_t *wi = p.wi + seq * p.kw;
-    const int64_t *ri = p.ri + seq * p.kr;
-    const T *wwp = p.ww + seq * p.kw;
-    const T *rwp = p.rw + seq * p.kr;
     int64_t wbank[KMAX], rbank[KMAX];
     float wwt[KMAX], rwt[KMAX];
-    if constexpr (KFIX) {
-        // exactly KMAX banks per role: straight-line loads of whole rows
-#pragma unroll
-        for (int j = 0; j < KMAX; ++j) {
-            wbank[j] = clamp_bank(wi[j]);
-            rbank[j] = clamp_bank(ri[j]);
-        }
-        load_row<KMAX>(wwp, wwt);
-        load_row<KMAX>(rwp, rwt);
-    } else {
-#pragma unroll
-        for (int j = 0; j < KMAX; ++j) {
-            const int jw = min(j, max(p.kw - 1, 0)), jr = min(j, max(p.kr - 1, 0));
-            wbank[j] = p.kw > 0 ? clamp_bank(wi[jw]) : 0;
-            wwt[j] = p.kw > 0 ? to_f32(wwp[jw]) : 0.f;
-            rbank[j] = p.kr > 0 ? clamp_bank(ri[jr]) : 0;
-            rwt[j] = p.kr > 0 ? to_f32(rwp[jr]) : 0.f;
-        }
-    }
     float kk[S], gg[S], bb[S], qq[S];
-    {
-        const int64_t at = row * p.s_real;
-        load_ctrl_row<S, VEC>(p.k + at, p.s_real, kk);
-        load_ctrl_row<S, VEC>(p.g + at, p.s_real, gg);
-        load_ctrl_row<S, VEC>(p.b + at, p.s_real, bb);
-        load_ctrl_row<S, VEC>(p.q + at, p.s_real, qq);
-    }
     float vv[CPL], wv[CPL];
-    load_row<CPL>(p.v + row * p.width + col0, vv);
-    load_row<CPL>(p.w + row * p.width + col0, wv);
+    if constexpr (FUSED) {
+        static_assert(KFIX && VEC && KMAX == 8 && S == 8 && std::is_same<T, bf16_t>::value, "fused geometry");
+        __shared__ int64_t s_bank[2][KMAX];
+        __shared__ float s_wt[2][KMAX];
+        __shared__ float s_ctrl[4][S];
+        const T *prow = p.proj + seq * p.proj_stride;
+        const int wave = int(threadIdx.x) / kWave, lane = int(threadIdx.x) % kWave;
+        if (wave < 2) {
+            // routes of both roles (gdn2_banks.py:74-114): wave 0 writes, wave 1 reads
+            float wt;
+            int64_t bk;
+            route_row_wave(prow + (wave == 0 ? p.write_col : p.read_col), p.j1, p.j2, KMAX, lane, wt, bk);
+            if (lane < KMAX) {
+                s_bank[wave][lane] = bk;
+                s_wt[wave][lane] = wt;
+            }
+        } else if (wave == 2 && lane < 4) {
+            // the head's controller rows (heads.py:11-22): q, k, b rounded to T, g FP32
+            float y[S];
+            if (lane < 2)
+                qk_row<T, S, true>(prow + (lane == 0 ? p.q_col : p.k_col) + head * S, p.qk_norm, y);
+            else if (lane == 2)
+                sigmoid_row<T, S, true>(prow + p.b_col + head * S, y);
+            else
+                decay_row<T, S, true>(p.f + seq * p.f_stride + head * S, p.a_log, p.dt_bias, p.param_dtype, head, y);
+#pragma unroll
+            for (int r = 0; r < S; ++r) s_ctrl[lane][r] = lane == 3 ? y[r] : round_to<T>(y[r]);
+        }
+        {
+            // this lane's value columns: v = silu, w = sigmoid, rounded to T
+            float tv[CPL], tw[CPL];
+            load_row<CPL>(prow + p.v_col + int64_t(head) * p.width + col0, tv);
+            load_row<CPL>(prow + p.w_col + int64_t(head) * p.width + col0, tw);
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+                vv[c] = round_to<T>(silu_f(tv[c]));
+                wv[c] = round_to<T>(sigmoid_f(tw[c]));
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < KMAX; ++j) {
+            wbank[j] = clamp_bank(s_bank[0][j]);
+            rbank[j] = clamp_bank(s_bank[1][j]);
+            wwt[j] = s_wt[0][j];
+            rwt[j] = s_wt[1][j];
+        }
+#pragma unroll
+        for (int r = 0; r < S; ++r) {
+            qq[r] = s_ctrl[0][r];
+            kk[r] = s_ctrl[1][r];
+            bb[r] = s_ctrl[2][r];
+            gg[r] = s_ctrl[3][r];
+        }
+    } else {
+        // ---- round trip 1: everything that does not depend on a bank index,
+        // issued together with no barrier behind it.  The token's bank indices,
+        // route weights and controller rows have workgroup-uniform addresses and
+        // are read by scalar loads (entry j >= K re-reads entry K-1, so every
+        // address is in bounds and the loads are unconditional); each lane group
+        // selects its own slot's entries.  The lane's value columns are vector loads.
+        const int64_t *wi = p.wi + seq * p.kw;
+        const int64_t *ri = p.ri + seq * p.kr;
+        const T *wwp = p.ww + seq * p.kw;
+        const T *rwp = p.rw + seq * p.kr;
+        if constexpr (KFIX) {
+            // exactly KMAX banks per role: straight-line loads of whole rows
+#pragma unroll
+            for (int j = 0; j < KMAX; ++j) {
+                wbank[j] = clamp_bank(wi[j]);
+                rbank[j] = clamp_bank(ri[j]);
+            }
+            load_row<KMAX>(wwp, wwt);
+            load_row<KMAX>(rwp, rwt);
+        } else {
+#pragma unroll
+            for (int j = 0; j < KMAX; ++j) {
+                const int jw = min(j, max(p.kw - 1, 0)), jr = min(j, max(p.kr - 1, 0));
+                wbank[j] = p.kw > 0 ? clamp_bank(wi[jw]) : 0;
+                wwt[j] = p.kw > 0 ? to_f32(wwp[jw]) : 0.f;
+                rbank[j] = p.kr > 0 ? clamp_bank(ri[jr]) : 0;
+                rwt[j] = p.kr > 0 ? to_f32(rwp[jr]) : 0.f;
+            }
+        }
+        {
+            const int64_t at = row * p.s_real;
+            load_ctrl_row<S, VEC>(p.k + at, p.s_real, kk);
+            load_ctrl_row<S, VEC>(p.g + at, p.s_real, gg);
+            load_ctrl_row<S, VEC>(p.b + at, p.s_real, bb);
+            load_ctrl_row<S, VEC>(p.q + at, p.s_real, qq);
+        }
+        load_row<CPL>(p.v + row * p.width + col0, vv);
+        load_row<CPL>(p.w + row * p.width + col0, wv);
+    }
     int64_t my_w = 0, my_r = 0;
     float pw = 0.f, pr = 0.f;
 #pragma unroll
@@ -301,6 +372,49 @@ int launch_decode(const bdm_decode_args &a, hipStream_t stream) {
     return check_launch("decode_kernel");
 }
 
+// The fused step (bdm_decode_fused): BF16 controllers, S = 8, 8 banks per
+// role, two columns per lane, spans of 128 columns at most; at least three
+// waves per workgroup (two routers and the controller rows).
+int launch_decode_fused(const bdm_decode_fused_args &a, hipStream_t stream) {
+    constexpr int S = 8, CPL = 2, K = 8;
+    DecodeParams<bf16_t> p{};
+    p.proj = static_cast<const bf16_t *>(a.proj);
+    p.f = static_cast<const bf16_t *>(a.f);
+    p.a_log = a.a_log;
+    p.dt_bias = a.dt_bias;
+    p.proj_stride = a.proj_stride;
+    p.f_stride = a.f_stride;
+    p.q_col = a.q_col, p.k_col = a.k_col, p.v_col = a.v_col, p.b_col = a.b_col, p.w_col = a.w_col;
+    p.read_col = a.read_col, p.write_col = a.write_col;
+    p.j1 = a.factor_first, p.j2 = a.factor_second;
+    p.param_dtype = a.param_dtype;
+    p.qk_norm = a.qk_norm;
+    p.state = a.state;
+    p.out = static_cast<bf16_t *>(a.output);
+    p.heads = a.heads;
+    p.s_real = S;
+    p.width = a.head_width;
+    p.banks = a.factor_first * a.factor_second;
+    p.kw = p.kr = K;
+    int span = a.head_width;
+    while (span > 128 && span % 2 == 0) span /= 2;
+    p.span = span;
+    p.spans = a.head_width / span;
+    p.lanes_per_slot = span / CPL;
+    p.vec_rows = 1;
+    p.state_dtype = a.state_dtype;
+    p.routed_decay = a.routed_decay;
+    p.scale = a.scale;
+    const int threads = K * p.lanes_per_slot;
+    const size_t lds = (size_t(K) * S * span + size_t(K) * span) * sizeof(float);
+    const unsigned grid = unsigned(a.batch * a.heads * p.spans);
+    if (a.state_dtype == BDM_BF16)
+        decode_kernel<bf16_t, bf16_t, S, CPL, true, K, true, true><<<grid, threads, lds, stream>>>(p);
+    else
+        decode_kernel<bf16_t, float, S, CPL, true, K, true, true><<<grid, threads, lds, stream>>>(p);
+    return check_launch("decode_kernel (fused step)");
+}
+
 template <typename T>
 int dispatch_decode(const bdm_decode_args &a, hipStream_t stream) {
     if (a.bank_size <= 8) {
@@ -345,4 +459,37 @@ extern "C" int bdm_decode(const bdm_decode_args *a, void *stream) {
     hipStream_t s = as_stream(stream);
     if (a->ctrl_dtype == BDM_BF16) return dispatch_decode<bf16_t>(*a, s);
     return dispatch_decode<float>(*a, s);
+}
+
+extern "C" int bdm_decode_fused_supported(const bdm_decode_fused_args *a) {
+    if (!a) return 0;
+    const int j1 = a->factor_first, j2 = a->factor_second;
+    const int s = a->selected_banks < j1 ? (a->selected_banks < j2 ? a->selected_banks : j2) : (j1 < j2 ? j1 : j2);
+    const int count = a->selected_banks < s * s ? a->selected_banks : s * s;
+    int span = a->head_width;
+    while (span > 128 && span % 2 == 0) span /= 2;
+    const bool cols8 = a->q_col % 8 == 0 && a->k_col % 8 == 0 && a->v_col % 8 == 0 && a->b_col % 8 == 0 &&
+                       a->w_col % 8 == 0 && a->read_col % 8 == 0 && a->write_col % 8 == 0;
+    return a->batch > 0 && a->heads > 0 && a->ctrl_dtype == BDM_BF16 && a->bank_size == 8 &&
+           a->selected_banks == 8 && count == 8 && j1 >= 1 && j2 >= 1 && j1 <= 64 && j2 <= 64 &&
+           a->head_width % 2 == 0 && span <= 128 && span >= 48 && a->head_width % span == 0 &&
+           (a->state_dtype == BDM_BF16 || a->state_dtype == BDM_F32) &&
+           (a->param_dtype == BDM_BF16 || a->param_dtype == BDM_F32) && a->proj_stride % 8 == 0 &&
+           a->f_stride % 8 == 0 && cols8 && a->q_col >= 0 && a->k_col >= 0 && a->v_col >= 0 && a->b_col >= 0 &&
+           a->w_col >= 0 && a->read_col >= 0 && a->write_col >= 0;
+}
+
+extern "C" int bdm_decode_fused(const bdm_decode_fused_args *a, void *stream) {
+    using namespace bdm;
+    if (!a) return fail(BDM_ERR_INVALID, "decode_fused: null args");
+    if (!bdm_decode_fused_supported(a))
+        return fail(BDM_ERR_UNSUPPORTED, "decode_fused: geometry outside the fused step (BF16, S = 8, 8 banks per "
+                                         "role, J1, J2 <= 64, aligned column offsets, head spans of 48..128)");
+    if (a->batch * a->heads > int64_t(INT32_MAX) / 16) return fail(BDM_ERR_UNSUPPORTED, "decode_fused: grid too large");
+    if (!a->proj || !a->f || !a->a_log || !a->dt_bias || !a->state || !a->output)
+        return fail(BDM_ERR_INVALID, "decode_fused: null pointer");
+    const void *ptrs[] = {a->proj, a->f, a->a_log, a->dt_bias, a->state, a->output};
+    for (const void *ptr : ptrs)
+        if (!aligned(ptr, 16)) return fail(BDM_ERR_INVALID, "decode_fused: tensors must be 16-byte aligned");
+    return launch_decode_fused(*a, as_stream(stream));
 }

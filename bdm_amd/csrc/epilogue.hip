@@ -13,6 +13,8 @@
 // fused with RMSNorm (_shell.py:10-35) and the SwiGLU product
 // silu(w1 x) * (w3 x) (_shell.py:86-91) over one GEMM of the concatenated
 // w1 | w3 weights.
+#include <type_traits>
+
 #include "epilogue_ops.h"
 
 namespace bdm {
@@ -42,70 +44,37 @@ __global__ __launch_bounds__(64) void controller_epilogue_kernel(ControllerParam
     if (it >= items) return;
     const T *row = p.proj + token * p.proj_stride;
     const int64_t hs = int64_t(p.heads) * S;
+    // the row helpers are shared with the fused decode step (decode.hip)
+    auto store = [&](auto *dst, const float (&y)[S]) {
+#pragma unroll
+        for (int r0 = 0; r0 < S; r0 += 8) {
+            float t[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) t[j] = y[r0 + j];
+            if constexpr (VEC)
+                store_row<8>(dst + r0, t);
+            else
+#pragma unroll
+                for (int j = 0; j < 8; ++j) dst[r0 + j] = from_f32<std::remove_pointer_t<decltype(dst)>>(t[j]);
+        }
+    };
     if (it < 2 * p.heads) {
         // q or k: silu, rounded, then the l2 normalization over the head's S values
         const int h = it % p.heads;
-        const T *src = row + (it < p.heads ? p.q_col : p.k_col) + h * S;
-        float x[S], ss = 0.f;
-#pragma unroll
-        for (int r0 = 0; r0 < S; r0 += 8) {
-            float t[8];
-            load8<T, VEC>(src + r0, t);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                x[r0 + j] = round_to<T>(silu_f(t[j]));
-                ss = fmaf(x[r0 + j], x[r0 + j], ss);
-            }
-        }
-        T *dst = (it < p.heads ? p.q : p.k) + token * hs + h * S;
-        const float inv = p.qk_norm == 1 ? rsqrtf(ss + 1e-6f) : 0.f;
-        const float norm = fmaxf(sqrtf(ss), 1e-12f);
-#pragma unroll
-        for (int r0 = 0; r0 < S; r0 += 8) {
-            float y[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) y[j] = p.qk_norm == 1 ? x[r0 + j] * inv : x[r0 + j] / norm;
-            if constexpr (VEC)
-                store_row<8>(dst + r0, y);
-            else
-#pragma unroll
-                for (int j = 0; j < 8; ++j) dst[r0 + j] = from_f32<T>(y[j]);
-        }
+        float y[S];
+        qk_row<T, S, VEC>(row + (it < p.heads ? p.q_col : p.k_col) + h * S, p.qk_norm, y);
+        store((it < p.heads ? p.q : p.k) + token * hs + h * S, y);
     } else if (it < 3 * p.heads) {
         const int h = it - 2 * p.heads;
-        const T *src = row + p.b_col + h * S;
-        T *dst = p.b + token * hs + h * S;
-#pragma unroll
-        for (int r0 = 0; r0 < S; r0 += 8) {
-            float t[8];
-            load8<T, VEC>(src + r0, t);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) t[j] = sigmoid_f(t[j]);
-            if constexpr (VEC)
-                store_row<8>(dst + r0, t);
-            else
-#pragma unroll
-                for (int j = 0; j < 8; ++j) dst[r0 + j] = from_f32<T>(t[j]);
-        }
+        float y[S];
+        sigmoid_row<T, S, VEC>(row + p.b_col + h * S, y);
+        store(p.b + token * hs + h * S, y);
     } else if (it < 4 * p.heads) {
         // g = -exp(A_log[h]) * softplus(f + dt_bias), FP32
         const int h = it - 3 * p.heads;
-        const T *src = p.f + token * p.f_stride + h * S;
-        const float a = -expf(param_at(p.a_log, p.param_dtype, h));
-        float *dst = p.g + token * hs + h * S;
-#pragma unroll
-        for (int r0 = 0; r0 < S; r0 += 8) {
-            float t[8], bias[8];
-            load8<T, VEC>(src + r0, t);
-            param8<VEC>(p.dt_bias, p.param_dtype, int64_t(h) * S + r0, bias);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) t[j] = a * softplus_f(t[j] + bias[j]);
-            if constexpr (VEC)
-                store_row<8>(dst + r0, t);
-            else
-#pragma unroll
-                for (int j = 0; j < 8; ++j) dst[r0 + j] = t[j];
-        }
+        float y[S];
+        decay_row<T, S, VEC>(p.f + token * p.f_stride + h * S, p.a_log, p.dt_bias, p.param_dtype, h, y);
+        store(p.g + token * hs + h * S, y);
     } else {
         const int c = it - 4 * p.heads;
         const bool is_v = c < chunks;

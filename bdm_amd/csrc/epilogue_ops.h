@@ -55,6 +55,57 @@ __device__ __forceinline__ void param8(const void *p, int dtype, int64_t at, flo
         load8<float, VEC>(static_cast<const float *>(p) + at, x);
 }
 
+// One head's controller rows (heads.py:11-22), from the projection outputs;
+// every value here is what the controller epilogue stores (the caller rounds
+// q, k and b to the controller dtype as the store does; g stays FP32).
+// q or k: silu rounded to T, then the l2 normalization over the S values
+// (qk_norm 1: x * rsqrt(sum x^2 + 1e-6); 0: x / max(|x|_2, 1e-12)).
+template <typename T, int S, bool VEC>
+__device__ __forceinline__ void qk_row(const T *src, int qk_norm, float (&y)[S]) {
+    float x[S], ss = 0.f;
+#pragma unroll
+    for (int r0 = 0; r0 < S; r0 += 8) {
+        float t[8];
+        load8<T, VEC>(src + r0, t);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            x[r0 + j] = round_to<T>(silu_f(t[j]));
+            ss = fmaf(x[r0 + j], x[r0 + j], ss);
+        }
+    }
+    const float inv = qk_norm == 1 ? rsqrtf(ss + 1e-6f) : 0.f;
+    const float norm = fmaxf(sqrtf(ss), 1e-12f);
+#pragma unroll
+    for (int r = 0; r < S; ++r) y[r] = qk_norm == 1 ? x[r] * inv : x[r] / norm;
+}
+
+// b: sigmoid of the projection
+template <typename T, int S, bool VEC>
+__device__ __forceinline__ void sigmoid_row(const T *src, float (&y)[S]) {
+#pragma unroll
+    for (int r0 = 0; r0 < S; r0 += 8) {
+        float t[8];
+        load8<T, VEC>(src + r0, t);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) y[r0 + j] = sigmoid_f(t[j]);
+    }
+}
+
+// g = -exp(A_log[h]) * softplus(f + dt_bias) in FP32 for head h
+template <typename T, int S, bool VEC>
+__device__ __forceinline__ void decay_row(const T *f, const void *a_log, const void *dt_bias, int param_dtype, int h,
+                                          float (&y)[S]) {
+    const float a = -expf(param_at(a_log, param_dtype, h));
+#pragma unroll
+    for (int r0 = 0; r0 < S; r0 += 8) {
+        float t[8], bias[8];
+        load8<T, VEC>(f + r0, t);
+        param8<VEC>(dt_bias, param_dtype, int64_t(h) * S + r0, bias);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) y[r0 + j] = a * softplus_f(t[j] + bias[j]);
+    }
+}
+
 // Butterfly sum over N lanes, the result in every lane.
 template <int N>
 __device__ __forceinline__ float wave_total(float x) {

@@ -31,6 +31,11 @@ Tensor = torch.Tensor
 class BankedDeltaMemory(nn.Module):
     """Shared-residual product routing around dense GDN2 memory banks."""
 
+    # Inference steps run the controller epilogue, both routes and the decode
+    # kernel as one launch (``ops.decode_fused``) where the geometry allows;
+    # False keeps the three separate kernels (same results).
+    fused_decode = True
+
     def __init__(self, config: BDMConfig, *, layer_id=0, seed=0, backend='hip', compact_replay=None):
         super().__init__()
         if backend not in ('hip', 'role'):
@@ -373,9 +378,36 @@ class BankedDeltaMemory(nn.Module):
         self._validate_stateful(hidden, state)
         if torch.is_grad_enabled() or hidden.shape[1] != 1:
             raise ValueError('step requires one token under no_grad/inference_mode')
+        if self._fused_supported(hidden):
+            weight, bias, cols = self._fused_weights()
+            proj = ops.linear(hidden.reshape(-1, self.hidden_size), weight, bias)
+            gate = proj[:, cols['gate']:cols['gate'] + self.value_width]
+            raw = self._decode_fused(proj, state)
+            if raw is None:
+                controllers, scores, gate = self._fused_controllers(hidden, proj=proj)
+                raw = self._decode_banks(controllers, scores, hidden.shape[0], state)
+            return self._fused_output(gate, raw.unsqueeze(1)), state
         (q, k, v, g, b, w), (read_routes, write_routes), gate = self._inference_inputs(hidden)
         raw = self._decode_banks((q, k, v, g, b, w), (read_routes, write_routes), hidden.shape[0], state)
         return self._inference_output(hidden, gate, raw.unsqueeze(1)), state
+
+    def _decode_fused(self, proj: Tensor, state: Tensor) -> Tensor | None:
+        """The step's controller epilogue, routes and decode kernel in one
+        launch from the fused projection ``proj`` [B, P]: the bank reads [B, V],
+        or None where ``ops.decode_fused`` does not take the geometry."""
+        if not self.fused_decode or self.num_reads != self.num_writes:
+            return None
+        _, _, cols = self._fused_weights()
+        rows, hv = proj.shape[0], self.head_value_width
+        heads_view = state.view(rows, self.bank_count, self.num_heads, self.bank_size, hv)
+        f = ops.linear(proj[:, cols['f']:cols['f'] + hv], self.f_proj[1].weight)
+        geometry = dict(heads=self.num_heads, bank_size=self.bank_size, head_width=hv, bank_count=self.bank_count,
+                        selected_banks=self.num_writes)
+        if not ops.decode_fused_supported(proj, f, cols, self.A_log, self.dt_bias, heads_view, **geometry):
+            return None
+        return ops.decode_fused(proj, f, cols, self.A_log, self.dt_bias, heads_view, **geometry,
+                                qk_norm=self.config.qk_normalization, routed_decay=self.config.routed_decay,
+                                scale=self.bank_size ** -0.5)
 
     def _decode_banks(self, controllers, scores, batch: int, state: Tensor) -> Tensor:
         """Both routes and the decode kernel of one step: the bank reads [B, V]."""
@@ -414,8 +446,12 @@ class BankedDeltaMemory(nn.Module):
             proj, total = ops.gemv_fused(delta.reshape(rows, self.hidden_size), weight, bias, prologue='rms',
                                          residual=flat, norm_weight=norm_weight, eps=norm_eps)
             new_hidden = total.view_as(hidden)
-        controllers, scores, gate = self._fused_controllers(new_hidden, proj=proj)
-        raw = self._decode_banks(controllers, scores, rows, state)
+        _, _, cols = self._fused_weights()
+        gate = proj[:, cols['gate']:cols['gate'] + self.value_width]
+        raw = self._decode_fused(proj, state)
+        if raw is None:
+            controllers, scores, gate = self._fused_controllers(new_hidden, proj=proj)
+            raw = self._decode_banks(controllers, scores, rows, state)
         layer = self.config.output_normalization == 'layer'
         out = ops.gemv_fused(raw, self.o_proj.weight, self.o_proj.bias,
                              prologue='out_layer' if layer else 'out_rms', norm_weight=self.output_norm_weight,

@@ -454,6 +454,65 @@ def decode_step(q, k, v, g, b, w, wi, ww, ri, rw, state: Tensor, *, bank_count: 
     return output
 
 
+def _decode_fused_args(proj, f, columns, a_log, dt_bias, state, heads, bank_size, head_width, bank_count,
+                       selected_banks, qk_norm, routed_decay, scale):
+    j1, j2 = near_square_factors(bank_count)
+    args = _lib.DecodeFusedArgs()
+    args.batch, args.proj_stride, args.f_stride = proj.shape[0], proj.stride(0), f.stride(0)
+    args.q_col, args.k_col, args.v_col = columns['q'], columns['k'], columns['v']
+    args.b_col, args.w_col, args.read_col, args.write_col = columns['b'], columns['w'], columns['read'], columns['write']
+    args.heads, args.bank_size, args.head_width = heads, bank_size, head_width
+    args.factor_first, args.factor_second, args.selected_banks = j1, j2, selected_banks
+    args.ctrl_dtype, args.param_dtype = _dtype_code(proj.dtype), _dtype_code(a_log.dtype)
+    args.state_dtype = _dtype_code(state.dtype)
+    args.qk_norm = 1 if qk_norm == 'nvidia' else 0
+    args.routed_decay = int(bool(routed_decay))
+    args.scale = float(scale)
+    return args
+
+
+def decode_fused_supported(proj: Tensor, f: Tensor, columns: dict, a_log: Tensor, dt_bias: Tensor, state: Tensor, *,
+                           heads: int, bank_size: int, head_width: int, bank_count: int, selected_banks: int) -> bool:
+    """Whether ``decode_fused`` takes this geometry (BF16 controllers, S = 8,
+    8 banks per role from J1, J2 <= 64, aligned slices, spans of 48..128)."""
+    if not (proj.is_cuda and proj.ndim == 2 and f.ndim == 2 and proj.stride(-1) == 1 and f.stride(-1) == 1):
+        return False
+    if proj.dtype != torch.bfloat16 or f.dtype != proj.dtype or a_log.dtype != dt_bias.dtype:
+        return False
+    if a_log.dtype not in (torch.bfloat16, torch.float32) or state.dtype not in (torch.bfloat16, torch.float32):
+        return False
+    if any(t.data_ptr() % 16 for t in (proj, f, state)) or not state.is_contiguous():
+        return False
+    args = _decode_fused_args(proj, f, columns, a_log, dt_bias, state, heads, bank_size, head_width, bank_count,
+                              selected_banks, 'nvidia', True, 1.0)
+    return bool(_lib.library().bdm_decode_fused_supported(ctypes.byref(args)))
+
+
+def decode_fused(proj: Tensor, f: Tensor, columns: dict, a_log: Tensor, dt_bias: Tensor, state: Tensor, *,
+                 heads: int, bank_size: int, head_width: int, bank_count: int, selected_banks: int, qk_norm: str,
+                 routed_decay: bool, scale: float) -> Tensor:
+    """One decode step from the projection outputs in one launch: the
+    controller epilogue (``controller_epilogue``), both routes
+    (``router_select_pair``) and ``decode_step``, with identical results.
+
+    proj: [B, P] the fused projection row of each sequence's token (q, k, v,
+    b, w and the read/write route scores at ``columns``); f: [B, H*S] the
+    f_proj output; state: [B, J, H, S, v], updated in place.  Returns y
+    [B, H*v]."""
+    _require_gpu(proj, f, a_log, dt_bias, state)
+    batch = proj.shape[0]
+    if state.shape != (batch, bank_count, heads, bank_size, head_width) or not state.is_contiguous():
+        raise ValueError('state must be a contiguous [batch, banks, heads, bank_size, head_width] tensor')
+    a_log, dt_bias = _aligned(a_log.contiguous()), _aligned(dt_bias.contiguous())
+    output = torch.empty((batch, heads * head_width), device=proj.device, dtype=proj.dtype)
+    args = _decode_fused_args(proj, f, columns, a_log, dt_bias, state, heads, bank_size, head_width, bank_count,
+                              selected_banks, qk_norm, routed_decay, scale)
+    args.proj, args.f, args.a_log, args.dt_bias = (t.data_ptr() for t in (proj, f, a_log, dt_bias))
+    args.state, args.output = state.data_ptr(), output.data_ptr()
+    _lib.check(_lib.library().bdm_decode_fused(ctypes.byref(args), _stream(proj.device)), 'bdm_decode_fused')
+    return output
+
+
 # ---------------------------------------------------------------------------
 # inference epilogues (the controller activations and the output interface)
 

@@ -260,6 +260,39 @@ typedef struct bdm_decode_args {
 int bdm_decode(const bdm_decode_args *args, void *stream);
 
 /*
+ * The decode step of the inference path from the projection outputs, in one
+ * launch: the controller epilogue (bdm_controller_epilogue, heads.py:11-22),
+ * both routers (bdm_router_select_pair, gdn2_banks.py:74-114) and bdm_decode
+ * (inference.py:161-194).  Replaces the three calls of a step; every input the
+ * decode sees equals, bit for bit, what those kernels would have stored.
+ * proj is [batch, proj_stride] ctrl_dtype with the q, k, v, b, w slices and
+ * the read and write route scores (J1 + J2 each) at the given column offsets;
+ * f is the f_proj output [batch, f_stride]; a_log [H] and dt_bias [H*S] in
+ * param_dtype.  The state [batch, J1*J2, H, S, v] is updated in place and y
+ * [batch, H*v] written.  Geometry: BF16 controllers, S = 8, 8 banks per role
+ * from J1, J2 <= 64, column offsets and strides multiples of 8 elements,
+ * head_width even with spans of 48..128 columns
+ * (bdm_decode_fused_supported); anything else returns BDM_ERR_UNSUPPORTED.
+ */
+typedef struct bdm_decode_fused_args {
+    const void *proj;
+    const void *f;
+    const void *a_log;         /* [H], param_dtype */
+    const void *dt_bias;       /* [H*S], param_dtype */
+    void *state;
+    void *output;              /* [batch, H*v] ctrl_dtype */
+    int64_t batch, proj_stride, f_stride;
+    int32_t q_col, k_col, v_col, b_col, w_col, read_col, write_col;
+    int32_t heads, bank_size, head_width, factor_first, factor_second, selected_banks;
+    int32_t ctrl_dtype, param_dtype, state_dtype, qk_norm, routed_decay;
+    float scale;
+} bdm_decode_fused_args;
+
+int bdm_decode_fused(const bdm_decode_fused_args *args, void *stream);
+/* 1 when bdm_decode_fused takes this geometry, else 0 (no launch). */
+int bdm_decode_fused_supported(const bdm_decode_fused_args *args);
+
+/*
  * Controller epilogue of the inference path.  Replaces the activations of
  * heads.controllers (implementation/bdm/heads.py:11-22) applied to the
  * outputs of one concatenated projection GEMM:
