@@ -97,6 +97,7 @@ class DecodeFusedArgs(ctypes.Structure):
         ('factor_second', _i32), ('selected_banks', _i32),
         ('ctrl_dtype', _i32), ('param_dtype', _i32), ('state_dtype', _i32), ('qk_norm', _i32),
         ('routed_decay', _i32), ('scale', _f32),
+        ('f_weight', _vp), ('f_out', _vp), ('f_col', _i32), ('f_width', _i32),
     ]
 
 

@@ -62,6 +62,10 @@ struct DecodeParams {
     int64_t proj_stride, f_stride;
     int q_col, k_col, v_col, b_col, w_col, read_col, write_col;
     int j1, j2, param_dtype, qk_norm;
+    // f formed in the launch (f_weight set): f_proj's second factor [H*S, f_width]
+    const T *f_weight;
+    T *f_out;
+    int f_col, f_width;
 };
 
 // SE: the state element type (bf16_t or float, the state_dtype argument);
@@ -111,7 +115,7 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeParams<T> p) {
                 s_bank[wave][lane] = bk;
                 s_wt[wave][lane] = wt;
             }
-        } else if (wave == 2 && lane < 4) {
+        } else if (wave == 2 && (lane < 3 || (lane == 3 && !p.f_weight))) {
             // the head's controller rows (heads.py:11-22): q, k, b rounded to T, g FP32
             float y[S];
             if (lane < 2)
@@ -122,6 +126,32 @@ __global__ __launch_bounds__(512) void decode_kernel(DecodeParams<T> p) {
                 decay_row<T, S, true>(p.f + seq * p.f_stride + head * S, p.a_log, p.dt_bias, p.param_dtype, head, y);
 #pragma unroll
             for (int r = 0; r < S; ++r) s_ctrl[lane][r] = lane == 3 ? y[r] : round_to<T>(y[r]);
+        } else if (wave == 3 && p.f_weight) {
+            // f = f_proj[1](f_proj[0] slice) for this head's S rows: lane
+            // (r, part) sums elements part*8 + 64*i .. +7 of row r in FP32, in
+            // increasing order, then the 8 parts add in a fixed butterfly and
+            // the sum is rounded to T (the GEMM's output dtype)
+            const int r = lane / 8, part = lane % 8;
+            const T *x = prow + p.f_col;
+            const T *wrow = p.f_weight + int64_t(head * S + r) * p.f_width;
+            float acc = 0.f;
+            for (int i0 = part * 8; i0 < p.f_width; i0 += 64) {
+                float xa[8], wb[8];
+                load_row<8>(x + i0, xa);
+                load_row<8>(wrow + i0, wb);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) acc = fmaf(xa[j], wb[j], acc);
+            }
+            acc += __shfl_xor(acc, 1, 8);
+            acc += __shfl_xor(acc, 2, 8);
+            acc += __shfl_xor(acc, 4, 8);
+            const float f = round_to<T>(acc);
+            if (part == 0) {
+                // decay_row's element: g = -exp(A_log[h]) * softplus(f + dt_bias)
+                const float a = -expf(param_at(p.a_log, p.param_dtype, head));
+                s_ctrl[3][r] = a * softplus_f(f + param_at(p.dt_bias, p.param_dtype, int64_t(head) * S + r));
+                if (p.f_out) p.f_out[seq * int64_t(p.heads) * S + head * S + r] = from_f32<T>(f);
+            }
         }
         {
             // this lane's value columns: v = silu, w = sigmoid, rounded to T
@@ -387,6 +417,10 @@ int launch_decode_fused(const bdm_decode_fused_args &a, hipStream_t stream) {
     p.q_col = a.q_col, p.k_col = a.k_col, p.v_col = a.v_col, p.b_col = a.b_col, p.w_col = a.w_col;
     p.read_col = a.read_col, p.write_col = a.write_col;
     p.j1 = a.factor_first, p.j2 = a.factor_second;
+    p.f_weight = static_cast<const bf16_t *>(a.f_weight);
+    p.f_out = static_cast<bf16_t *>(a.f_out);
+    p.f_col = a.f_col;
+    p.f_width = a.f_width;
     p.param_dtype = a.param_dtype;
     p.qk_norm = a.qk_norm;
     p.state = a.state;
@@ -470,7 +504,10 @@ extern "C" int bdm_decode_fused_supported(const bdm_decode_fused_args *a) {
     while (span > 128 && span % 2 == 0) span /= 2;
     const bool cols8 = a->q_col % 8 == 0 && a->k_col % 8 == 0 && a->v_col % 8 == 0 && a->b_col % 8 == 0 &&
                        a->w_col % 8 == 0 && a->read_col % 8 == 0 && a->write_col % 8 == 0;
-    return a->batch > 0 && a->heads > 0 && a->ctrl_dtype == BDM_BF16 && a->bank_size == 8 &&
+    // f formed in the launch: a fourth wave (64-column spans at least) and 16-byte aligned rows
+    const bool f_ok = !a->f_weight || (span >= 64 && a->f_width > 0 && a->f_width % 8 == 0 && a->f_col % 8 == 0 &&
+                                       a->f_col >= 0);
+    return f_ok && a->batch > 0 && a->heads > 0 && a->ctrl_dtype == BDM_BF16 && a->bank_size == 8 &&
            a->selected_banks == 8 && count == 8 && j1 >= 1 && j2 >= 1 && j1 <= 64 && j2 <= 64 &&
            a->head_width % 2 == 0 && span <= 128 && span >= 48 && a->head_width % span == 0 &&
            (a->state_dtype == BDM_BF16 || a->state_dtype == BDM_F32) &&
@@ -486,10 +523,10 @@ extern "C" int bdm_decode_fused(const bdm_decode_fused_args *a, void *stream) {
         return fail(BDM_ERR_UNSUPPORTED, "decode_fused: geometry outside the fused step (BF16, S = 8, 8 banks per "
                                          "role, J1, J2 <= 64, aligned column offsets, head spans of 48..128)");
     if (a->batch * a->heads > int64_t(INT32_MAX) / 16) return fail(BDM_ERR_UNSUPPORTED, "decode_fused: grid too large");
-    if (!a->proj || !a->f || !a->a_log || !a->dt_bias || !a->state || !a->output)
+    if (!a->proj || (!a->f && !a->f_weight) || !a->a_log || !a->dt_bias || !a->state || !a->output)
         return fail(BDM_ERR_INVALID, "decode_fused: null pointer");
-    const void *ptrs[] = {a->proj, a->f, a->a_log, a->dt_bias, a->state, a->output};
+    const void *ptrs[] = {a->proj, a->f, a->a_log, a->dt_bias, a->state, a->output, a->f_weight, a->f_out};
     for (const void *ptr : ptrs)
-        if (!aligned(ptr, 16)) return fail(BDM_ERR_INVALID, "decode_fused: tensors must be 16-byte aligned");
+        if (ptr && !aligned(ptr, 16)) return fail(BDM_ERR_INVALID, "decode_fused: tensors must be 16-byte aligned");
     return launch_decode_fused(*a, as_stream(stream));
 }

@@ -400,14 +400,20 @@ class BankedDeltaMemory(nn.Module):
         _, _, cols = self._fused_weights()
         rows, hv = proj.shape[0], self.head_value_width
         heads_view = state.view(rows, self.bank_count, self.num_heads, self.bank_size, hv)
-        f = ops.linear(proj[:, cols['f']:cols['f'] + hv], self.f_proj[1].weight)
         geometry = dict(heads=self.num_heads, bank_size=self.bank_size, head_width=hv, bank_count=self.bank_count,
                         selected_banks=self.num_writes)
+        options = dict(qk_norm=self.config.qk_normalization, routed_decay=self.config.routed_decay,
+                       scale=self.bank_size ** -0.5)
+        f_weight = self.f_proj[1].weight
+        # f_proj's second factor inside the launch where it takes it (one GEMM node fewer)
+        if ops.decode_fused_supported(proj, None, cols, self.A_log, self.dt_bias, heads_view, **geometry,
+                                      f_weight=f_weight):
+            return ops.decode_fused(proj, None, cols, self.A_log, self.dt_bias, heads_view, **geometry, **options,
+                                    f_weight=f_weight)
+        f = ops.linear(proj[:, cols['f']:cols['f'] + hv], f_weight)
         if not ops.decode_fused_supported(proj, f, cols, self.A_log, self.dt_bias, heads_view, **geometry):
             return None
-        return ops.decode_fused(proj, f, cols, self.A_log, self.dt_bias, heads_view, **geometry,
-                                qk_norm=self.config.qk_normalization, routed_decay=self.config.routed_decay,
-                                scale=self.bank_size ** -0.5)
+        return ops.decode_fused(proj, f, cols, self.A_log, self.dt_bias, heads_view, **geometry, **options)
 
     def _decode_banks(self, controllers, scores, batch: int, state: Tensor) -> Tensor:
         """Both routes and the decode kernel of one step: the bank reads [B, V]."""

@@ -455,10 +455,13 @@ def decode_step(q, k, v, g, b, w, wi, ww, ri, rw, state: Tensor, *, bank_count: 
 
 
 def _decode_fused_args(proj, f, columns, a_log, dt_bias, state, heads, bank_size, head_width, bank_count,
-                       selected_banks, qk_norm, routed_decay, scale):
+                       selected_banks, qk_norm, routed_decay, scale, f_weight=None):
     j1, j2 = near_square_factors(bank_count)
     args = _lib.DecodeFusedArgs()
-    args.batch, args.proj_stride, args.f_stride = proj.shape[0], proj.stride(0), f.stride(0)
+    args.batch, args.proj_stride = proj.shape[0], proj.stride(0)
+    args.f_stride = f.stride(0) if f is not None else 0
+    if f_weight is not None:
+        args.f_col, args.f_width = columns['f'], f_weight.shape[1]
     args.q_col, args.k_col, args.v_col = columns['q'], columns['k'], columns['v']
     args.b_col, args.w_col, args.read_col, args.write_col = columns['b'], columns['w'], columns['read'], columns['write']
     args.heads, args.bank_size, args.head_width = heads, bank_size, head_width
@@ -471,26 +474,40 @@ def _decode_fused_args(proj, f, columns, a_log, dt_bias, state, heads, bank_size
     return args
 
 
-def decode_fused_supported(proj: Tensor, f: Tensor, columns: dict, a_log: Tensor, dt_bias: Tensor, state: Tensor, *,
-                           heads: int, bank_size: int, head_width: int, bank_count: int, selected_banks: int) -> bool:
+def _f_weight_ok(proj, f_weight, heads, bank_size):
+    return (f_weight.dtype == proj.dtype and f_weight.ndim == 2 and f_weight.is_contiguous()
+            and f_weight.shape[0] == heads * bank_size and f_weight.data_ptr() % 16 == 0)
+
+
+def decode_fused_supported(proj: Tensor, f: Tensor | None, columns: dict, a_log: Tensor, dt_bias: Tensor,
+                           state: Tensor, *, heads: int, bank_size: int, head_width: int, bank_count: int,
+                           selected_banks: int, f_weight: Tensor | None = None) -> bool:
     """Whether ``decode_fused`` takes this geometry (BF16 controllers, S = 8,
-    8 banks per role from J1, J2 <= 64, aligned slices, spans of 48..128)."""
-    if not (proj.is_cuda and proj.ndim == 2 and f.ndim == 2 and proj.stride(-1) == 1 and f.stride(-1) == 1):
+    8 banks per role from J1, J2 <= 64, aligned slices, spans of 48..128, of
+    64..128 when f is formed in the launch from ``f_weight``)."""
+    if not (proj.is_cuda and proj.ndim == 2 and proj.stride(-1) == 1 and proj.dtype == torch.bfloat16):
         return False
-    if proj.dtype != torch.bfloat16 or f.dtype != proj.dtype or a_log.dtype != dt_bias.dtype:
+    if f_weight is None:
+        if f is None or f.ndim != 2 or f.stride(-1) != 1 or f.dtype != proj.dtype or f.data_ptr() % 16:
+            return False
+    elif not _f_weight_ok(proj, f_weight, heads, bank_size):
         return False
-    if a_log.dtype not in (torch.bfloat16, torch.float32) or state.dtype not in (torch.bfloat16, torch.float32):
+    if a_log.dtype != dt_bias.dtype or a_log.dtype not in (torch.bfloat16, torch.float32):
         return False
-    if any(t.data_ptr() % 16 for t in (proj, f, state)) or not state.is_contiguous():
+    if state.dtype not in (torch.bfloat16, torch.float32):
         return False
-    args = _decode_fused_args(proj, f, columns, a_log, dt_bias, state, heads, bank_size, head_width, bank_count,
-                              selected_banks, 'nvidia', True, 1.0)
+    if any(t.data_ptr() % 16 for t in (proj, state)) or not state.is_contiguous():
+        return False
+    args = _decode_fused_args(proj, f if f_weight is None else None, columns, a_log, dt_bias, state, heads, bank_size,
+                              head_width, bank_count, selected_banks, 'nvidia', True, 1.0, f_weight)
+    args.f_weight = f_weight.data_ptr() if f_weight is not None else None
     return bool(_lib.library().bdm_decode_fused_supported(ctypes.byref(args)))
 
 
-def decode_fused(proj: Tensor, f: Tensor, columns: dict, a_log: Tensor, dt_bias: Tensor, state: Tensor, *,
+def decode_fused(proj: Tensor, f: Tensor | None, columns: dict, a_log: Tensor, dt_bias: Tensor, state: Tensor, *,
                  heads: int, bank_size: int, head_width: int, bank_count: int, selected_banks: int, qk_norm: str,
-                 routed_decay: bool, scale: float) -> Tensor:
+                 routed_decay: bool, scale: float, f_weight: Tensor | None = None,
+                 f_out: Tensor | None = None) -> Tensor:
     """One decode step from the projection outputs in one launch: the
     controller epilogue (``controller_epilogue``), both routes
     (``router_select_pair``) and ``decode_step``, with identical results.
@@ -498,16 +515,37 @@ def decode_fused(proj: Tensor, f: Tensor, columns: dict, a_log: Tensor, dt_bias:
     proj: [B, P] the fused projection row of each sequence's token (q, k, v,
     b, w and the read/write route scores at ``columns``); f: [B, H*S] the
     f_proj output; state: [B, J, H, S, v], updated in place.  Returns y
-    [B, H*v]."""
-    _require_gpu(proj, f, a_log, dt_bias, state)
+    [B, H*v].
+
+    With ``f_weight`` (f_proj's second factor, [H*S, F]) f is formed in the
+    launch from proj's f_proj first-factor slice at ``columns['f']`` (F
+    columns) and ``f`` is ignored: FP32 dot products in a fixed order, rounded
+    to the projection dtype.  ``f_out`` [B, H*S], when given, receives it."""
+    _require_gpu(proj, a_log, dt_bias, state)
     batch = proj.shape[0]
     if state.shape != (batch, bank_count, heads, bank_size, head_width) or not state.is_contiguous():
         raise ValueError('state must be a contiguous [batch, banks, heads, bank_size, head_width] tensor')
+    if f_weight is not None:
+        _require_gpu(f_weight)
+        if not _f_weight_ok(proj, f_weight, heads, bank_size):
+            raise ValueError('f_weight must be a contiguous, 16-byte aligned [heads*bank_size, F] matrix of '
+                             'the projection dtype')
+        f = None
+        if f_out is not None and (f_out.shape != (batch, heads * bank_size) or f_out.dtype != proj.dtype
+                                  or not f_out.is_contiguous()):
+            raise ValueError('f_out must be a contiguous [batch, heads*bank_size] tensor of the projection dtype')
+    elif f is None:
+        raise ValueError('decode_fused needs f or f_weight')
+    else:
+        _require_gpu(f)
     a_log, dt_bias = _aligned(a_log.contiguous()), _aligned(dt_bias.contiguous())
     output = torch.empty((batch, heads * head_width), device=proj.device, dtype=proj.dtype)
     args = _decode_fused_args(proj, f, columns, a_log, dt_bias, state, heads, bank_size, head_width, bank_count,
-                              selected_banks, qk_norm, routed_decay, scale)
-    args.proj, args.f, args.a_log, args.dt_bias = (t.data_ptr() for t in (proj, f, a_log, dt_bias))
+                              selected_banks, qk_norm, routed_decay, scale, f_weight)
+    args.proj, args.a_log, args.dt_bias = (t.data_ptr() for t in (proj, a_log, dt_bias))
+    args.f = f.data_ptr() if f is not None else None
+    args.f_weight = f_weight.data_ptr() if f_weight is not None else None
+    args.f_out = f_out.data_ptr() if (f_weight is not None and f_out is not None) else None
     args.state, args.output = state.data_ptr(), output.data_ptr()
     _lib.check(_lib.library().bdm_decode_fused(ctypes.byref(args), _stream(proj.device)), 'bdm_decode_fused')
     return output

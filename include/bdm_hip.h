@@ -273,6 +273,11 @@ int bdm_decode(const bdm_decode_args *args, void *stream);
  * from J1, J2 <= 64, column offsets and strides multiples of 8 elements,
  * head_width even with spans of 48..128 columns
  * (bdm_decode_fused_supported); anything else returns BDM_ERR_UNSUPPORTED.
+ * With f_weight set (f_proj's second factor [H*S, f_width] ctrl_dtype, rows
+ * contiguous), f is formed in the launch from the f_proj first-factor slice
+ * of proj at f_col instead of read from f: FP32 dot products in a fixed order,
+ * rounded to ctrl_dtype as the GEMM output is (spans of 64..128 columns);
+ * f_out, when set, receives that f [batch, H*S].
  */
 typedef struct bdm_decode_fused_args {
     const void *proj;
@@ -286,6 +291,9 @@ typedef struct bdm_decode_fused_args {
     int32_t heads, bank_size, head_width, factor_first, factor_second, selected_banks;
     int32_t ctrl_dtype, param_dtype, state_dtype, qk_norm, routed_decay;
     float scale;
+    const void *f_weight;      /* optional: f_proj's second factor [H*S, f_width] */
+    void *f_out;               /* optional: [batch, H*S] ctrl_dtype */
+    int32_t f_col, f_width;
 } bdm_decode_fused_args;
 
 int bdm_decode_fused(const bdm_decode_fused_args *args, void *stream);
