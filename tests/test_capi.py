@@ -133,7 +133,8 @@ def test_struct_layouts_match_the_header(tmp_path):
     if gcc is None:
         pytest.skip('no host C compiler')
     mirrors = {'bdm_forward_args': _lib.ForwardArgs, 'bdm_backward_args': _lib.BackwardArgs,
-               'bdm_decode_args': _lib.DecodeArgs, 'bdm_controller_args': _lib.ControllerArgs,
+               'bdm_decode_args': _lib.DecodeArgs, 'bdm_decode_fused_args': _lib.DecodeFusedArgs,
+               'bdm_controller_args': _lib.ControllerArgs,
                'bdm_output_args': _lib.OutputArgs, 'bdm_gemv_args': _lib.GemvArgs,
                'bdm_adamw_tensor': _lib.AdamwTensor, 'bdm_adamw_args': _lib.AdamwArgs}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', 'int main(void) {']
