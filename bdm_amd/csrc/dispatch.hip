@@ -85,40 +85,54 @@ __global__ __launch_bounds__(512) void dispatch_tile_count(const int64_t *__rest
 
 // Per (batch, 64-bank chunk): tile_counts[b][t][bank] becomes each tile's
 // offset inside its segment, and totals[b][bank] the segment length.  The
-// tiles are split over the four waves of the workgroup; a wave first sums its
-// range (loads in flight together), the waves' sums are scanned through LDS,
-// then each wave rewrites its range as running offsets.
+// tiles are split over the kScanWaves waves of the workgroup; a wave loads its
+// range kScanBatch counts at a time (all in flight together) and sums it, the
+// waves' sums are scanned through LDS, then each wave rewrites its range as
+// running offsets, from the counts it still holds when the range is one batch
+// (sequences of up to 8,192 tokens), else reloading them a batch at a time.
 // It also clears the route flags: the counting pass before it raised them
 // and the scatter pass after it raises every one of them again (both build
 // the same tile masks), so the caller need not clear the word.
-__global__ __launch_bounds__(256) void dispatch_tile_scan(DispatchGeometry g, int32_t *__restrict__ tile_counts,
-                                                          int32_t *__restrict__ totals, int32_t *status) {
-    __shared__ int32_t part[4][kWave];
+constexpr int kScanWaves = 16, kScanBatch = 16;
+
+__global__ __launch_bounds__(kScanWaves * kWave) void dispatch_tile_scan(DispatchGeometry g,
+                                                                         int32_t *__restrict__ tile_counts,
+                                                                         int32_t *__restrict__ totals,
+                                                                         int32_t *status) {
+    __shared__ int32_t part[kScanWaves][kWave];
     const int b = blockIdx.x;
     if (b == 0 && blockIdx.y == 0 && threadIdx.x == 0) *status = 0;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
     const int bank = blockIdx.y * kWave + lane;
     const bool live = bank < g.banks;
-    const int per = (g.tiles + 3) / 4;
+    const int per = (g.tiles + kScanWaves - 1) / kScanWaves;
     const int t0 = min(g.tiles, wave * per), t1 = min(g.tiles, t0 + per);
     int32_t *base = tile_counts + int64_t(b) * g.tiles * g.banks + bank;
+    auto load_batch = [&](int t, int32_t (&c)[kScanBatch]) {
+#pragma unroll
+        for (int k = 0; k < kScanBatch; ++k) c[k] = (live && t + k < t1) ? base[int64_t(t + k) * g.banks] : 0;
+    };
+    int32_t c[kScanBatch];
     int32_t sum = 0;
-    if (live) {
-#pragma unroll 8
-        for (int t = t0; t < t1; ++t) sum += base[int64_t(t) * g.banks];
+    for (int t = t0; t < t1; t += kScanBatch) {
+        load_batch(t, c);
+#pragma unroll
+        for (int k = 0; k < kScanBatch; ++k) sum += c[k];
     }
     part[wave][lane] = sum;
     __syncthreads();
     int32_t running = 0;
     for (int w = 0; w < wave; ++w) running += part[w][lane];
-    if (live) {
-        for (int t = t0; t < t1; ++t) {
-            const int32_t c = base[int64_t(t) * g.banks];
-            base[int64_t(t) * g.banks] = running;
-            running += c;
+    const bool held = t1 - t0 <= kScanBatch;  // c still holds the wave's whole range
+    for (int t = t0; t < t1; t += kScanBatch) {
+        if (!held) load_batch(t, c);
+#pragma unroll
+        for (int k = 0; k < kScanBatch; ++k) {
+            if (live && t + k < t1) base[int64_t(t + k) * g.banks] = running;
+            running += c[k];
         }
-        if (wave == 3) totals[int64_t(b) * g.banks + bank] = running;
     }
+    if (live && wave == kScanWaves - 1) totals[int64_t(b) * g.banks + bank] = running;
 }
 
 // One workgroup per (tile, batch): the batch's segment starts (an exclusive
@@ -259,8 +273,8 @@ int launch_mask_dispatch(const int64_t *wi, const int64_t *ri, const DispatchGeo
     dispatch_tile_count<<<tiles, 512, mask_bytes, s>>>(wi, ri, g, tile_counts, status);
     if (int rc = check_launch("dispatch_tile_count")) return rc;
     int32_t *totals = tile_counts + int64_t(g.batch) * g.tiles * g.banks;
-    dispatch_tile_scan<<<dim3(unsigned(g.batch), unsigned((g.banks + kWave - 1) / kWave)), 256, 0, s>>>(
-        g, tile_counts, totals, status);
+    dispatch_tile_scan<<<dim3(unsigned(g.batch), unsigned((g.banks + kWave - 1) / kWave)), kScanWaves * kWave, 0,
+                         s>>>(g, tile_counts, totals, status);
     if (int rc = check_launch("dispatch_tile_scan")) return rc;
     const size_t scatter_lds = mask_bytes + size_t(g.banks) * sizeof(int32_t);
     if (scatter_lds > 64 * 1024 &&

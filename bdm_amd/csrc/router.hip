@@ -239,6 +239,296 @@ __global__ __launch_bounds__(64) void router_lane_kernel(RouterRoles<T> roles, i
     }
 }
 
+// Four lanes per row (a DPP quad), BF16 scores, selected = 8 from J1, J2 in
+// [8, 64]: the lane kernel's selection and softmax with a quarter of its
+// serial chain (one lane per row runs ~1,500 dependent instructions, which
+// sets that kernel's time at any row count).  Lanes q = 0, 1 take factor 0
+// and q = 2, 3 factor 1; lane q sorts its blocks of 8 entries (blocks
+// q%2, q%2 + 2, ... of its factor) with a 19-comparator network and merges
+// them into a top 8; the quad then merges across lanes with DPP quad
+// permutes.  The 20 candidate pairs (i+1)(l+1) <= 8 are formed 5 per lane,
+// sorted and merged the same way, and lane q keeps selection slots 2q, 2q+1.
+// Entries are the packed (value desc, index asc) keys of router_ops.h, a
+// strict order, so any exact top-8 selection gives the lane kernel's list;
+// the softmax sums the 8 exponentials in selection order as it does.
+__device__ __forceinline__ void cex(uint32_t &a, uint32_t &b) {
+    const uint32_t hi = max(a, b), lo = min(a, b);
+    a = hi;
+    b = lo;
+}
+
+// Sort 8 entries descending (Knuth's 19-comparator network).
+__device__ __forceinline__ void sort8(uint32_t (&x)[8]) {
+    cex(x[0], x[2]), cex(x[1], x[3]), cex(x[4], x[6]), cex(x[5], x[7]);
+    cex(x[0], x[4]), cex(x[1], x[5]), cex(x[2], x[6]), cex(x[3], x[7]);
+    cex(x[0], x[1]), cex(x[2], x[3]), cex(x[4], x[5]), cex(x[6], x[7]);
+    cex(x[2], x[4]), cex(x[3], x[5]);
+    cex(x[1], x[4]), cex(x[3], x[6]);
+    cex(x[1], x[2]), cex(x[3], x[4]), cex(x[5], x[6]);
+}
+
+// a := the 8 largest of a and b (each sorted descending), sorted descending:
+// max(a[p], b[7-p]) holds them as a bitonic sequence, which a bitonic merge sorts.
+__device__ __forceinline__ void merge_top8(uint32_t (&a)[8], const uint32_t (&b)[8]) {
+#pragma unroll
+    for (int p = 0; p < 8; ++p) a[p] = max(a[p], b[7 - p]);
+    cex(a[0], a[4]), cex(a[1], a[5]), cex(a[2], a[6]), cex(a[3], a[7]);
+    cex(a[0], a[2]), cex(a[1], a[3]), cex(a[4], a[6]), cex(a[5], a[7]);
+    cex(a[0], a[1]), cex(a[2], a[3]), cex(a[4], a[5]), cex(a[6], a[7]);
+}
+
+// Lane (lane & ~3) + perm[lane & 3] of the quad, perm packed 2 bits per lane.
+template <int PERM>
+__device__ __forceinline__ uint32_t quad_get(uint32_t x) {
+    return uint32_t(__builtin_amdgcn_update_dpp(0, int(x), PERM, 0xF, 0xF, false));
+}
+
+template <int PERM>
+__device__ __forceinline__ void quad_merge(uint32_t (&a)[8]) {
+    uint32_t b[8];
+#pragma unroll
+    for (int p = 0; p < 8; ++p) b[p] = quad_get<PERM>(a[p]);
+    merge_top8(a, b);
+}
+
+__device__ __forceinline__ uint32_t pick4(int q, uint32_t a0, uint32_t a1, uint32_t a2, uint32_t a3) {
+    const uint32_t lo = (q & 1) ? a1 : a0, hi = (q & 1) ? a3 : a2;
+    return (q & 2) ? hi : lo;
+}
+
+constexpr int kQuadXor1 = 0xB1;  // quad_perm [1, 0, 3, 2]
+constexpr int kQuadXor2 = 0x4E;  // quad_perm [2, 3, 0, 1]
+
+template <int NB>
+__global__ __launch_bounds__(256) void router_quad_kernel(RouterRoles<bf16_t> roles, int64_t rows, int j1, int j2) {
+    const int role = int(blockIdx.y);
+    const int q = int(threadIdx.x) & 3;
+    const int64_t row_raw = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) >> 2;
+    const bool live = row_raw < rows;  // uniform over a quad
+    const int64_t row = live ? row_raw : rows - 1;
+    const int factor = q >> 1, half = q & 1;
+    const int jf = factor ? j2 : j1;
+    const bf16_t *zf = roles.scores[role] + row * roles.stride[role] + (factor ? j1 : 0);
+
+    // (1) top 8 of each factor
+    uint4 raw[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int e0 = (half + 2 * b) * 8;
+        raw[b] = *reinterpret_cast<const uint4 *>(zf + (e0 < jf ? e0 : 0));
+    }
+    uint32_t top[8];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int e0 = (half + 2 * b) * 8;
+        const uint32_t w[4] = {raw[b].x, raw[b].y, raw[b].z, raw[b].w};
+        // packed unconditionally, then cleared past the factor (a select, not a branch per entry)
+        const uint32_t keep = e0 < jf ? 0xffffffffu : 0u;
+        uint32_t en[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float x = __uint_as_float(k & 1 ? (w[k / 2] & 0xffff0000u) : (w[k / 2] << 16));
+            en[k] = pack_entry(x, e0 + k) & keep;
+        }
+        sort8(en);
+        if (b == 0) {
+#pragma unroll
+            for (int p = 0; p < 8; ++p) top[p] = en[p];
+        } else {
+            merge_top8(top, en);
+        }
+    }
+    quad_merge<kQuadXor1>(top);  // the factor's top 8 in both of its lanes
+    uint32_t f0[8], f1[8];
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+        const uint32_t other = quad_get<kQuadXor2>(top[p]);
+        f0[p] = factor ? other : top[p];
+        f1[p] = factor ? top[p] : other;
+    }
+    // factor ids of the two lists, one byte each, for the bank lookup at the end
+    __shared__ uint32_t s_ids[256][4];
+    uint32_t packed[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const uint32_t(&f)[8] = w < 2 ? f0 : f1;
+        const int p0 = (w & 1) * 4;
+        packed[w] = uint32_t(entry_id(f[p0])) | uint32_t(entry_id(f[p0 + 1])) << 8 |
+                    uint32_t(entry_id(f[p0 + 2])) << 16 | uint32_t(entry_id(f[p0 + 3])) << 24;
+    }
+    *reinterpret_cast<uint4 *>(s_ids[threadIdx.x]) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+
+    // (2) candidates (0, q), (0, 4+q), (1, q), (2 + q/2, q%2), (4+q, 0) with
+    // ids i*8 + l, pair sums in BF16 (gdn2_banks.py:106)
+    const float a0 = entry_value(f0[0]), a1 = entry_value(f0[1]), b0 = entry_value(f1[0]);
+    const float bq = entry_value(pick4(q, f1[0], f1[1], f1[2], f1[3]));
+    const float bq4 = entry_value(pick4(q, f1[4], f1[5], f1[6], f1[7]));
+    const float aq4 = entry_value(pick4(q, f0[4], f0[5], f0[6], f0[7]));
+    const float a3 = entry_value((q & 2) ? f0[3] : f0[2]);
+    const float b3 = entry_value((q & 1) ? f1[1] : f1[0]);
+    uint32_t c[8];
+    c[0] = pack_entry(round_to<bf16_t>(a0 + bq), q);
+    c[1] = pack_entry(round_to<bf16_t>(a0 + bq4), 4 + q);
+    c[2] = pack_entry(round_to<bf16_t>(a1 + bq), 8 + q);
+    c[3] = pack_entry(round_to<bf16_t>(a3 + b3), 16 + 8 * (q >> 1) + (q & 1));
+    c[4] = pack_entry(round_to<bf16_t>(aq4 + b0), 32 + 8 * q);
+    c[5] = c[6] = c[7] = 0u;
+    sort8(c);
+    quad_merge<kQuadXor1>(c);
+    quad_merge<kQuadXor2>(c);
+
+    // (3) softmax over the selected sums in FP32, the exponentials summed in
+    // selection order (gdn2_banks.py:114); lane q keeps slots 2q and 2q+1
+    const float top_value = entry_value(c[0]);
+    const uint32_t ea = pick4(q, c[0], c[2], c[4], c[6]), eb = pick4(q, c[1], c[3], c[5], c[7]);
+    const float xa = expf(entry_value(ea) - top_value), xb = expf(entry_value(eb) - top_value);
+    const uint32_t ua = __float_as_uint(xa), ub = __float_as_uint(xb);
+    const float ex[8] = {__uint_as_float(quad_get<0x00>(ua)), __uint_as_float(quad_get<0x00>(ub)),
+                         __uint_as_float(quad_get<0x55>(ua)), __uint_as_float(quad_get<0x55>(ub)),
+                         __uint_as_float(quad_get<0xAA>(ua)), __uint_as_float(quad_get<0xAA>(ub)),
+                         __uint_as_float(quad_get<0xFF>(ua)), __uint_as_float(quad_get<0xFF>(ub))};
+    float total = 0.f;
+#pragma unroll
+    for (int p = 0; p < 8; ++p) total += ex[p];
+    const uint8_t *ids = reinterpret_cast<const uint8_t *>(s_ids[threadIdx.x]);
+    auto bank_of = [&](uint32_t e) {
+        const int cid = entry_id(e) & 63;
+        return int64_t(ids[cid >> 3]) * j2 + int64_t(ids[8 + (cid & 7)]);
+    };
+    const int64_t bank_a = bank_of(ea), bank_b = bank_of(eb);
+    if (live) {
+        const uint32_t wa = __float_as_uint(round_to<bf16_t>(xa / total)) >> 16;
+        const uint32_t wb = __float_as_uint(round_to<bf16_t>(xb / total)) & 0xffff0000u;
+        *reinterpret_cast<uint32_t *>(roles.weights[role] + row * 8 + 2 * q) = wa | wb;
+        int64_t *iout = roles.indices[role] + row * 8 + 2 * q;
+        *reinterpret_cast<longlong2 *>(iout) = make_longlong2(bank_a, bank_b);
+    }
+}
+
+// Two lanes per row, BF16 scores, selected = 8 from J1, J2 in [8, 32]: half
+// the quad kernel's instructions per row (no work is repeated in four lanes)
+// at half its lanes.  Lane h sorts factor h's blocks of 8 and merges them;
+// the pair swaps lists (DPP quad_perm [1, 0, 3, 2]), lane 0 forms the
+// candidate pairs of flattened index 0..9 and lane 1 the other 10, each
+// sorts its 10 into a top 8, and one swap and merge leaves the selection in
+// both lanes; lane h keeps slots 4h..4h+3.
+template <int NB>
+__global__ __launch_bounds__(256) void router_pair_kernel(RouterRoles<bf16_t> roles, int64_t rows, int j1, int j2) {
+    const int role = int(blockIdx.y);
+    const int h = int(threadIdx.x) & 1;
+    const int64_t row_raw = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) >> 1;
+    const bool live = row_raw < rows;  // uniform over a pair
+    const int64_t row = live ? row_raw : rows - 1;
+    const int jf = h ? j2 : j1;
+    const bf16_t *zf = roles.scores[role] + row * roles.stride[role] + (h ? j1 : 0);
+
+    // (1) top 8 of factor h
+    uint4 raw[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) raw[b] = *reinterpret_cast<const uint4 *>(zf + (b * 8 < jf ? b * 8 : 0));
+    uint32_t top[8];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const uint32_t w[4] = {raw[b].x, raw[b].y, raw[b].z, raw[b].w};
+        const uint32_t keep = b * 8 < jf ? 0xffffffffu : 0u;
+        uint32_t en[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float x = __uint_as_float(k & 1 ? (w[k / 2] & 0xffff0000u) : (w[k / 2] << 16));
+            en[k] = pack_entry(x, b * 8 + k) & keep;
+        }
+        sort8(en);
+        if (b == 0) {
+#pragma unroll
+            for (int p = 0; p < 8; ++p) top[p] = en[p];
+        } else {
+            merge_top8(top, en);
+        }
+    }
+    uint32_t f0[8], f1[8];
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+        const uint32_t other = quad_get<kQuadXor1>(top[p]);
+        f0[p] = h ? other : top[p];
+        f1[p] = h ? top[p] : other;
+    }
+    __shared__ uint32_t s_ids[256][4];
+    uint32_t packed[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const uint32_t(&f)[8] = w < 2 ? f0 : f1;
+        const int p0 = (w & 1) * 4;
+        packed[w] = uint32_t(entry_id(f[p0])) | uint32_t(entry_id(f[p0 + 1])) << 8 |
+                    uint32_t(entry_id(f[p0 + 2])) << 16 | uint32_t(entry_id(f[p0 + 3])) << 24;
+    }
+    *reinterpret_cast<uint4 *>(s_ids[threadIdx.x]) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+
+    // (2) candidates: lane 0 (0,0..7), (1,0), (1,1); lane 1 (1,2), (1,3),
+    // (2,0), (2,1), (3,0), (3,1), (4..7,0); ids i*8 + l, sums in BF16
+    float a[8], b[8];
+#pragma unroll
+    for (int p = 0; p < 8; ++p) a[p] = entry_value(f0[p]), b[p] = entry_value(f1[p]);
+    // (operands passed as values: an index chosen per lane would become a
+    // select over all eight registers)
+    auto cand = [&](float x0, float y0, int id0, float x1, float y1, int id1) {
+        return pack_entry(round_to<bf16_t>(h ? x1 + y1 : x0 + y0), h ? id1 : id0);
+    };
+    uint32_t c[8];
+    c[0] = cand(a[0], b[0], 0, a[1], b[2], 10);
+    c[1] = cand(a[0], b[1], 1, a[1], b[3], 11);
+    c[2] = cand(a[0], b[2], 2, a[2], b[0], 16);
+    c[3] = cand(a[0], b[3], 3, a[2], b[1], 17);
+    c[4] = cand(a[0], b[4], 4, a[3], b[0], 24);
+    c[5] = cand(a[0], b[5], 5, a[3], b[1], 25);
+    c[6] = cand(a[0], b[6], 6, a[4], b[0], 32);
+    c[7] = cand(a[0], b[7], 7, a[5], b[0], 40);
+    const uint32_t extra0 = cand(a[1], b[0], 8, a[6], b[0], 48);
+    const uint32_t extra1 = cand(a[1], b[1], 9, a[7], b[0], 56);
+    sort8(c);
+    insert_entry<8>(c, extra0);
+    insert_entry<8>(c, extra1);
+    quad_merge<kQuadXor1>(c);
+
+    // (3) softmax over the selected sums in FP32, the exponentials summed in
+    // selection order (gdn2_banks.py:114)
+    const float top_value = entry_value(c[0]);
+    // slot 4h + k by a bit mask: a select between c[k] and c[4 + k] is
+    // turned into an index chosen per lane, which moves c to LDS
+    const uint32_t upper = 0u - uint32_t(h);
+    uint32_t e[4];
+    float xs[4], ex[8];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        e[k] = c[k] ^ ((c[k] ^ c[4 + k]) & upper);
+        xs[k] = expf(entry_value(e[k]) - top_value);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float other = __uint_as_float(quad_get<kQuadXor1>(__float_as_uint(xs[k])));
+        ex[k] = h ? other : xs[k];
+        ex[4 + k] = h ? xs[k] : other;
+    }
+    float total = 0.f;
+#pragma unroll
+    for (int p = 0; p < 8; ++p) total += ex[p];
+    const uint8_t *ids = reinterpret_cast<const uint8_t *>(s_ids[threadIdx.x]);
+    int64_t bank[4];
+    uint32_t wbits[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int cid = entry_id(e[k]) & 63;
+        bank[k] = int64_t(ids[cid >> 3]) * j2 + int64_t(ids[8 + (cid & 7)]);
+        wbits[k] = __float_as_uint(round_to<bf16_t>(xs[k] / total)) >> 16;
+    }
+    if (live) {
+        *reinterpret_cast<uint2 *>(roles.weights[role] + row * 8 + 4 * h) =
+            make_uint2(wbits[0] | wbits[1] << 16, wbits[2] | wbits[3] << 16);
+        longlong2 *iout = reinterpret_cast<longlong2 *>(roles.indices[role] + row * 8 + 4 * h);
+        iout[0] = make_longlong2(bank[0], bank[1]);
+        iout[1] = make_longlong2(bank[2], bank[3]);
+    }
+}
+
 __global__ __launch_bounds__(256) void router_wave_kernel(const bf16_t *__restrict__ scores, int64_t rows,
                                                           int64_t stride, int j1, int j2, int selected,
                                                           bf16_t *__restrict__ weights,
@@ -282,6 +572,40 @@ int launch_router(const RouterRoles<T> &roles, int nroles, int64_t rows, int j1,
                 if (int rc = check_launch("router_wave_kernel")) return rc;
             }
             return BDM_OK;
+        }
+    }
+    if constexpr (sizeof(T) == 2) {
+        // selected = 8 from J1, J2 in [8, 64] (multiples of 8), aligned rows: four lanes per row
+        bool quad = selected == 8 && j1 >= 8 && j2 >= 8 && j1 <= 64 && j2 <= 64 && j1 % 8 == 0 && j2 % 8 == 0;
+        for (int r = 0; r < nroles; ++r)
+            quad = quad && aligned(roles.scores[r], 16) && roles.stride[r] % 8 == 0 && aligned(roles.weights[r], 4) &&
+                   aligned(roles.indices[r], 16);
+        const int jmax = j1 > j2 ? j1 : j2;
+        if (quad && jmax <= 32 && rows * 2 <= int64_t(UINT32_MAX)) {
+            // two lanes per row up to 4 blocks of 8 per factor
+            for (int r = 0; r < nroles; ++r) quad = quad && aligned(roles.weights[r], 8);
+            if (quad) {
+                const dim3 grid(unsigned((rows * 2 + 255) / 256), unsigned(nroles));
+                switch ((jmax + 7) / 8) {
+                    case 1: router_pair_kernel<1><<<grid, 256, 0, stream>>>(roles, rows, j1, j2); break;
+                    case 2: router_pair_kernel<2><<<grid, 256, 0, stream>>>(roles, rows, j1, j2); break;
+                    case 3: router_pair_kernel<3><<<grid, 256, 0, stream>>>(roles, rows, j1, j2); break;
+                    default: router_pair_kernel<4><<<grid, 256, 0, stream>>>(roles, rows, j1, j2); break;
+                }
+                return check_launch("router_pair_kernel");
+            }
+            quad = true;  // weights only 4-byte aligned: the quad kernel takes them
+        }
+        if (quad && rows * 4 <= int64_t(UINT32_MAX)) {
+            const dim3 grid(unsigned((rows * 4 + 255) / 256), unsigned(nroles));
+            const int nb = (jmax + 15) / 16;
+            switch (nb) {
+                case 1: router_quad_kernel<1><<<grid, 256, 0, stream>>>(roles, rows, j1, j2); break;
+                case 2: router_quad_kernel<2><<<grid, 256, 0, stream>>>(roles, rows, j1, j2); break;
+                case 3: router_quad_kernel<3><<<grid, 256, 0, stream>>>(roles, rows, j1, j2); break;
+                default: router_quad_kernel<4><<<grid, 256, 0, stream>>>(roles, rows, j1, j2); break;
+            }
+            return check_launch("router_quad_kernel");
         }
     }
     if (selected <= 8)

@@ -25,7 +25,7 @@ def announce(*what):
 # ---------------------------------------------------------------------------- router
 
 @pytest.mark.parametrize('bank_count,selected', [(16, 4), (256, 8), (2048, 8), (12, 3), (6, 2), (256, 16),
-                                                  (131072, 8)])
+                                                  (131072, 8), (512, 8), (576, 8), (768, 8), (4096, 8)])
 @pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float32])
 def test_router_bit_exact(device, bank_count, selected, dtype):
     from bdm_amd import ops
@@ -49,7 +49,8 @@ def test_router_bit_exact(device, bank_count, selected, dtype):
         ulp = wr.float().abs() * (2 ** -7 if dtype == torch.bfloat16 else 1e-6)
         assert bool((diff <= ulp + 1e-12).all()), float(diff.max())
         # few rows (a decode step) take the one-wave-per-row kernel for BF16
-        # scores: identical weights and indices to the one-lane-per-row kernel
+        # scores: identical weights and indices to the many-row kernels (one
+        # lane per row, or four for B = 8 from factors of 8..64)
         few = scores[:1, :37]
         wf, idf = ops.router_select(few.to(device), bank_count=bank_count, selected_banks=selected)
         torch.cuda.synchronize()
