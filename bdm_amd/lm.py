@@ -35,7 +35,9 @@ Tensor = torch.Tensor
 
 @dataclass(frozen=True)
 class LanguageModelConfig:
-    """model.py:143-161."""
+    """Shape of the whole language model around the memory layers: the field
+    names, defaults and record format of model.py:143-161, so a reference
+    record loads unchanged."""
     memory: BDMConfig = field(default_factory=BDMConfig)
     vocab_size: int = 192
     layers: int = 8
@@ -45,13 +47,18 @@ class LanguageModelConfig:
     compact_replay: bool | None = None
 
     def __post_init__(self):
-        if min(self.vocab_size, self.layers, self.ffn_multiple_of) <= 0 or self.seed < 0:
-            raise ValueError('invalid language-model geometry or seed')
-        if self.compact_replay is not None and type(self.compact_replay) is not bool:
-            raise ValueError('compact_replay must be None, True, or False')
+        sizes = {'vocab_size': self.vocab_size, 'layers': self.layers, 'ffn_multiple_of': self.ffn_multiple_of}
+        bad = [name for name, value in sizes.items() if value <= 0]
+        if bad or self.seed < 0:
+            raise ValueError(f'language model needs positive {", ".join(bad) or "sizes"} and a seed >= 0')
+        if not (self.compact_replay is None or isinstance(self.compact_replay, bool)):
+            raise ValueError(f'compact_replay takes None or a bool, not {self.compact_replay!r}')
 
     def record(self):
-        return dict(asdict(self), memory=self.memory.record())
+        """Plain-dict form, the memory config nested as its own record."""
+        out = asdict(self)
+        out['memory'] = self.memory.record()
+        return out
 
 
 class _RMSNormFunction(torch.autograd.Function):
@@ -190,8 +197,10 @@ class BDMBlock(nn.Module):
 
 
 class BDMLanguageModel(nn.Module):
-    """Checkpoint-compatible all-bank shell with independent width and depth
-    (model.py:179-216)."""
+    """Token embedding, a stack of BDMBlocks, a final RMSNorm and an untied
+    vocabulary head (model.py:179-216).  Module names and the seeded
+    initialisation follow the reference, so state dicts interchange bit for
+    bit; the memory layers run on the HIP path."""
 
     def __init__(self, config: LanguageModelConfig, *, backend='hip'):
         super().__init__()
@@ -201,16 +210,29 @@ class BDMLanguageModel(nn.Module):
         self.tok_embeddings = nn.Embedding(config.vocab_size, self.dim)
         self.norm = RMSNorm(self.dim, eps=config.memory.norm_eps)
         self.output = nn.Linear(self.dim, config.vocab_size, bias=False)
-        base, std = config.seed * 100_000, self.dim ** -.5
-        with torch.random.fork_rng(devices=[]):
-            torch.manual_seed(base + 100)
-            for parameter in (self.tok_embeddings.weight, self.output.weight):
-                nn.init.trunc_normal_(parameter, mean=0, std=std, a=-3 * std, b=3 * std)
-        for i, block in enumerate(self.layers):
-            block.attention.init_weights(initialization_seed=base + 6000 + i)
+        self._seeded_init()
+
+    def _seeded_init(self) -> None:
+        """Every parameter from a seed derived from config.seed (offsets 100
+        for the embedding and the head, 6000 + i for memory layer i, 1000 + i
+        for feed-forward i), each draw under its own forked RNG so the
+        caller's generator state is untouched."""
+        root = self.config.seed * 100_000
+        bound = self.dim ** -.5
+
+        def seeded(offset, fill):
             with torch.random.fork_rng(devices=[]):
-                torch.manual_seed(base + 1000 + i)
-                block.feed_forward.reset_parameters()
+                torch.manual_seed(root + offset)
+                fill()
+
+        def fill_ends():
+            for weight in (self.tok_embeddings.weight, self.output.weight):
+                nn.init.trunc_normal_(weight, mean=0, std=bound, a=-3 * bound, b=3 * bound)
+
+        seeded(100, fill_ends)
+        for index, block in enumerate(self.layers):
+            block.attention.init_weights(initialization_seed=root + 6000 + index)
+            seeded(1000 + index, block.feed_forward.reset_parameters)
 
     def _hidden(self, tokens: Tensor) -> Tensor:
         hidden = self.tok_embeddings(tokens)

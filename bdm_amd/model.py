@@ -40,10 +40,10 @@ class BankedDeltaMemory(nn.Module):
         super().__init__()
         if backend not in ('hip', 'role'):
             raise ValueError("backend must be hip (or its alias role); the CPU equation oracle lives in oracle/")
-        if seed < 0 or layer_id < 0:
-            raise ValueError('seed and layer_id must be nonnegative')
-        if compact_replay is not None and type(compact_replay) is not bool:
-            raise ValueError('compact_replay must be None, True, or False')
+        if min(seed, layer_id) < 0:
+            raise ValueError(f'seed and layer_id must be >= 0, got seed={seed}, layer_id={layer_id}')
+        if not (compact_replay is None or isinstance(compact_replay, bool)):
+            raise ValueError(f'compact_replay takes None or a bool, not {compact_replay!r}')
         self.compact_replay = compact_replay
         self.config, self.backend = config, 'hip'
         self.hidden_size, self.bank_count, self.bank_size = config.dim, config.bank_count, config.bank_size

@@ -94,7 +94,7 @@ def bank_training(q, k, v, g, b, w, wi, ww, ri, rw, state, bank_count, scale, *,
                   state_dtype=torch.float32):
     """Routed-decay bank operator (routed_update.py:52-53)."""
     if compact_replay is not None and type(compact_replay) is not bool:
-        raise ValueError('compact_replay must be None, True, or False')
+        raise ValueError(f'compact_replay takes None or a bool, not {compact_replay!r}')
     return RoutedUpdate.apply(q, k, v, g, b, w, wi, ww, ri, rw, state, bank_count, scale, compact_replay,
                               state_dtype, True)
 
@@ -103,6 +103,6 @@ def role_bank_training(q, k, v, g, b, w, wi, ww, ri, rw, state, bank_count, scal
                        state_dtype=torch.float32):
     """Bank operator without routed decay (role_bank_kernel.py:258-259)."""
     if compact_replay is not None and type(compact_replay) is not bool:
-        raise ValueError('compact_replay must be None, True, or False')
+        raise ValueError(f'compact_replay takes None or a bool, not {compact_replay!r}')
     return RoutedUpdate.apply(q, k, v, g, b, w, wi, ww, ri, rw, state, bank_count, scale, compact_replay,
                               state_dtype, False)

@@ -18,12 +18,14 @@ from .config import near_square_factors
 
 
 class SharedResidualRouter(nn.Module):
-    """One routing base plus independent learned read and write residuals."""
+    """Read and write score projections that share a base map: each role's
+    weight and bias are the base's plus that role's own residual, so the two
+    roles start equal and learn apart (parameter names of routing.py:11-35)."""
 
     def __init__(self, input_width: int, output_width: int) -> None:
         super().__init__()
-        if input_width <= 0 or output_width <= 0:
-            raise ValueError('router widths must be positive')
+        if min(input_width, output_width) <= 0:
+            raise ValueError(f'SharedResidualRouter needs positive widths, got {input_width} -> {output_width}')
         self.base = nn.Linear(input_width, output_width)
         self.read_residual = nn.Linear(input_width, output_width)
         self.write_residual = nn.Linear(input_width, output_width)
@@ -40,8 +42,8 @@ class SharedResidualRouter(nn.Module):
     def initialize_from_independent(self, *, std: float, read_generator=None, write_generator=None) -> None:
         """Base = mean of two truncated-normal draws; residuals and biases zero
         (routing.py:37-68)."""
-        if std <= 0:
-            raise ValueError('router initialization scale must be positive')
+        if not std > 0:
+            raise ValueError(f'router init std must be > 0, got {std}')
         draws = []
         for generator in (read_generator, write_generator):
             draw = torch.empty_like(self.base.weight)
