@@ -52,6 +52,7 @@ struct ForwardParams {
     int64_t init_bstride;
     int64_t nt, time;
     int heads, s_real, width, banks, kw, kr;
+    int k_shift;  // log2 of KW and KR when both are that power of two, else -1 (route -> token by shift)
     int lanes_per_head, heads_per_block;
     // Column split of wide heads (lazy kernel): `heads` and `width` above are
     // then virtual heads of `width` columns, `split` of them per real head;
@@ -68,6 +69,7 @@ struct ForwardParams {
     const int4 *items;     // pieces of cut segments: (segment, piece q, pieces of the segment, state slot)
     const int *n_items;    // [0]: number of pieces
     int nseg;              // segments (batch * J)
+    int piece_blocks;      // MODE 2: blocks of pieces ahead of the segments (a multiple of 8)
     float *pstate;         // [slots, H, S, v] FP32: zero-start end state R_q, then start state M_(q+1)
     float *ptrans;         // [slots, H, S, S] FP32: transition P_q of piece q
 };
@@ -438,16 +440,18 @@ __device__ __forceinline__ void load_vec4(const float *p, float4 &out) { out = *
 // (no rounding inside the recurrence, no snapshots) a segment is an affine
 // map of its start state, M_end = P M_start + R, so segments longer than
 // kPieceEvents are cut into pieces to balance skewed routing:
-//   MODE 1 runs each piece q of a cut segment from a zero state, without
-//          reads, and stores its end state R_q and its transition P_q (the
-//          lanes 0..7 of a head also carry the 8 columns of P, started at
-//          the identity, through the same write updates with x = 0);
+//   MODE 1 runs each piece q of a cut segment but the last from a zero
+//          state, without reads, and stores its end state R_q and its
+//          transition P_q (the lanes 0..7 of a head also carry the 8 columns
+//          of P, started at the identity, through the same write updates
+//          with x = 0); the scan never uses a last piece's R and P;
 //   piece_scan_kernel composes M_(q+1) = P_q M_q + R_q from the segment's
 //          initial state;
-//   MODE 2 runs, in one launch, the uncut segments whole (blocks below
-//          nseg, mapped as in MODE 0) and every piece from its start state
-//          M_q (blocks from nseg on), with reads; the last piece of a
-//          segment stores the final state.
+//   MODE 2 runs, in one launch, every piece from its start state M_q
+//          (blocks below piece_blocks, so the long pieces start first) and
+//          the uncut segments whole (blocks from piece_blocks on, mapped as
+//          in MODE 0), with reads; the last piece of a segment stores the
+//          final state.
 template <typename T, int CPL, int HB, int MODE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void lazy_forward_kernel(
     ForwardParams<T> p) {
@@ -471,20 +475,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 
     int seg, piece = 0, pieces = 1, pslot = -1;
     const int block = int(blockIdx.x);
-    if (MODE == 0 || (MODE == 2 && block < p.nseg)) {
-        seg = p.xcd_remap ? int((block % 8) * (p.nseg / 8) + block / 8) : block;
-        // a cut segment's pieces run in the blocks from nseg on (the whole
-        // workgroup leaves together)
+    if (MODE == 0 || (MODE == 2 && block >= p.piece_blocks)) {
+        // (piece_blocks is a multiple of 8, so a segment keeps its XCD)
+        const int sb = MODE == 2 ? block - p.piece_blocks : block;
+        seg = p.xcd_remap ? int((sb % 8) * (p.nseg / 8) + sb / 8) : sb;
+        // a cut segment runs as its pieces (the whole workgroup leaves together)
         if (MODE == 2 && p.cu[seg + 1] - p.cu[seg] > kPieceEvents) return;
     } else {
-        // the grid is an upper bound on the pieces
-        const int idx = MODE == 2 ? block - p.nseg : block;
-        if (idx >= p.n_items[0]) return;
-        const int4 it = p.items[idx];
+        // pieces take the first blocks; the grid is an upper bound on them
+        if (block >= p.n_items[0]) return;
+        const int4 it = p.items[block];
         seg = it.x;
         piece = it.y;
         pieces = it.z;
         pslot = it.w;
+        if (MODE == 1 && piece == pieces - 1) return;
     }
     const int bank = seg % p.banks;
     const int64_t bidx = seg / p.banks;
@@ -561,7 +566,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         const uint64_t read_mask = __ballot(live && rd && tid < NE);
         const uint64_t write_mask = live_mask & ~read_mask;
         if (tid < NE) {
-            s_tok[slot][tid] = int(uint32_t(route) / uint32_t(rd ? p.kr : p.kw));
+            // (a wave-uniform choice: the shift when KW = KR = 2^k, else a division)
+            s_tok[slot][tid] = p.k_shift >= 0 ? int(uint32_t(route) >> p.k_shift)
+                                              : int(uint32_t(route) / uint32_t(rd ? p.kr : p.kw));
             s_route[slot][tid] = route;
             if (live && !rd) s_wpos[slot][__popcll(write_mask & ((uint64_t(1) << tid) - 1))] = tid;
         }
@@ -1157,6 +1164,9 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, int *zslot, const PieceBu
     p.banks = a.bank_count;
     p.kw = a.write_banks;
     p.kr = a.read_banks;
+    p.k_shift = -1;
+    for (int sh = 0; sh < 8; ++sh)
+        if (a.write_banks == (1 << sh) && a.read_banks == (1 << sh)) p.k_shift = sh;
     p.lanes_per_head = p.width / CPL;
     p.heads_per_block = 256 / p.lanes_per_head;
     // lazy kernel: 2 heads per one-wave workgroup when a head has 32 lanes, else 8 per 256 threads
@@ -1205,7 +1215,8 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, int *zslot, const PieceBu
                 pb.items, pb.count, a.initial, a.initial_dtype, a.initial_batch_stride, a.bank_count, p.heads,
                 p.width, p.split, p.row_stride, pb.pstate, pb.ptrans);
             if (int rc = check_launch("piece_scan_kernel")) return rc;
-            const dim3 g2(unsigned(nseg + pb.max_pieces), grid.y);
+            p.piece_blocks = int((pb.max_pieces + 7) / 8 * 8);
+            const dim3 g2(unsigned(nseg + p.piece_blocks), grid.y);
             if (lazy_hb == 2)
                 lazy_forward_kernel<T, CPL, 2, 2><<<g2, lthreads, 0, stream>>>(p);
             else
