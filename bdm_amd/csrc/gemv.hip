@@ -358,6 +358,112 @@ int launch_gemv_pro(const GemvParams<T> &p, int64_t m, hipStream_t s) {
     return fail(BDM_ERR_UNSUPPORTED, "gemv: %lld rows (at most 4)", (long long)m);
 }
 
+// ---- 5 to 64 rows (a decode batch): matrix-core tiles
+//
+// y = x W^T + bias for BF16 x [M, K] and W [N, K] with M <= 64.  A workgroup
+// owns 16 output columns for every row; its four waves each take a quarter of
+// K and accumulate all M rows in v_mfma_f32_16x16x32_bf16 tiles (16 rows by
+// 16 columns by 32 k), so the workgroup streams its 16 weight rows once and
+// the rows of x, shared by every workgroup, come from L2.  The quarters'
+// FP32 partials are added through LDS in wave order, the bias added in FP32
+// and the sum rounded once, as F.linear does (the summation order differs
+// from the library GEMM's, so results agree to FP32 rounding before the BF16
+// one).  Against the library GEMM at the decode shapes (M = 64,
+// graph-replayed): about equal with the weights in cache, ~1 µs faster with
+// them coming from HBM, ~1 µs faster at M = 16; 64-column workgroups (x read
+// from L2 a quarter as often) were twice as slow.
+// Operand fragments: lane l supplies row (or column) l % 16 and the 8
+// consecutive k at 8 * (l / 16) of the 32; A and B use the same lane-to-k
+// assignment, so every product pairs equal k.  The 16 x 16 FP32 result holds
+// rows 4 * (l / 16) .. + 3 of column l % 16 in lane l.
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+constexpr int kSkinnyWaves = 4;
+constexpr int kSkinnyMaxRows = 64;  // above 64 rows the library GEMM is faster (8.3 against 12 us at 128)
+
+template <int MT>
+__global__ __launch_bounds__(kSkinnyWaves * kWave) void skinny_gemm_kernel(const bf16_t *__restrict__ x,
+                                                                           const bf16_t *__restrict__ w,
+                                                                           const bf16_t *__restrict__ bias,
+                                                                           bf16_t *__restrict__ y, int m, int n,
+                                                                           int k) {
+    __shared__ float part[kSkinnyWaves][MT * 256];  // each wave's partial tile
+    __shared__ float bcol[16];                       // the workgroup's 16 biases
+    const int wave = int(threadIdx.x) / kWave, lane = int(threadIdx.x) % kWave;
+    const int col = lane % 16, kg = lane / 16;
+    const int c = int(blockIdx.x) * 16 + col;  // this lane's output column
+    // rows and columns past the matrix read the last one; their results are not stored
+    const bf16_t *wrow = w + int64_t(min(c, n - 1)) * k + kg * 8;
+    const bf16_t *xrow[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) xrow[t] = x + int64_t(min(t * 16 + col, m - 1)) * k + kg * 8;
+    const float bc = bias ? to_f32(bias[min(c, n - 1)]) : 0.f;  // loaded before the products
+    f32x4_t acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const int steps = k / 32;
+    const int per = (steps + kSkinnyWaves - 1) / kSkinnyWaves;
+    const int s0 = min(steps, wave * per), s1 = min(steps, s0 + per);
+    // CH steps of 32 k at a time, every load of a chunk issued before its
+    // products (K = 1024: the wave's whole quarter in one chunk)
+    constexpr int CH = 8;
+    for (int base = s0; base < s1; base += CH) {
+        u32x4_t b[CH], a[CH][MT];
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+            const int kk = min(base + j, s1 - 1) * 32;
+            b[j] = *reinterpret_cast<const u32x4_t *>(wrow + kk);
+#pragma unroll
+            for (int t = 0; t < MT; ++t) a[j][t] = *reinterpret_cast<const u32x4_t *>(xrow[t] + kk);
+        }
+        // (the scheduler would interleave loads and products to save
+        // registers, leaving 2 or 3 loads in flight; the latency is the cost)
+        __builtin_amdgcn_sched_barrier(0);
+        // steps past the range multiply a zero weight fragment: the products
+        // stay unconditional, so no load is sunk behind a branch
+#pragma unroll
+        for (int j = 0; j < CH; ++j) {
+            if (base + j >= s1) b[j] = u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a[j][t]),
+                                                                __builtin_bit_cast(bf16x8_t, b[j]), acc[t], 0, 0, 0);
+        }
+    }
+    // partial tiles to LDS as [tile][row][column]; then every thread adds the
+    // four quarters of its outputs in wave order
+#pragma unroll
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) part[wave][t * 256 + (4 * kg + i) * 16 + col] = acc[t][i];
+    bcol[lane % 16] = bc;  // (every wave writes the same 16 values)
+    __syncthreads();
+    for (int o = int(threadIdx.x); o < MT * 256; o += kSkinnyWaves * kWave) {
+        float sum = 0.f;
+#pragma unroll
+        for (int q = 0; q < kSkinnyWaves; ++q) sum += part[q][o];
+        const int row = (o / 256) * 16 + (o % 256) / 16, cn = int(blockIdx.x) * 16 + o % 16;
+        if (row < m && cn < n) y[int64_t(row) * n + cn] = from_f32<bf16_t>(sum + bcol[o % 16]);
+    }
+}
+
+int launch_skinny(const bdm_gemv_args &a, hipStream_t s) {
+    const auto *x = static_cast<const bf16_t *>(a.x);
+    const auto *w = static_cast<const bf16_t *>(a.weight);
+    const auto *bias = static_cast<const bf16_t *>(a.bias);
+    auto *y = static_cast<bf16_t *>(a.y);
+    const int m = int(a.rows), n = int(a.n), k = int(a.k);
+    const unsigned grid = unsigned((a.n + 15) / 16);
+    const int threads = kSkinnyWaves * kWave;
+    if (m <= 16)
+        skinny_gemm_kernel<1><<<grid, threads, 0, s>>>(x, w, bias, y, m, n, k);
+    else if (m <= 32)
+        skinny_gemm_kernel<2><<<grid, threads, 0, s>>>(x, w, bias, y, m, n, k);
+    else
+        skinny_gemm_kernel<4><<<grid, threads, 0, s>>>(x, w, bias, y, m, n, k);
+    return check_launch("skinny_gemm_kernel");
+}
+
 template <typename T>
 int launch_gemv(const bdm_gemv_args &a, hipStream_t s) {
     GemvParams<T> p{};
@@ -411,6 +517,14 @@ extern "C" int bdm_gemv_ex(const bdm_gemv_args *a, void *stream) {
         if (ptr && !aligned(ptr, 16)) return fail(BDM_ERR_INVALID, "gemv: operands must be 16-byte aligned");
     if ((a->n + 3) / 4 > int64_t(UINT32_MAX)) return fail(BDM_ERR_UNSUPPORTED, "gemv: too many rows");
     hipStream_t s = as_stream(stream);
+    if (a->rows > 4) {
+        // a decode batch: matrix-core tiles (BF16, no prologue, K a multiple of 32)
+        if (a->dtype != BDM_BF16 || a->prologue != BDM_GEMV_PLAIN || a->rows > kSkinnyMaxRows || a->k % 32 != 0 ||
+            a->n > INT32_MAX || (a->bias && !aligned(a->bias, 2)))
+            return fail(BDM_ERR_UNSUPPORTED, "gemv: %lld rows take BF16 operands without a prologue, K %% 32 == 0 and "
+                                             "at most %d rows", (long long)a->rows, kSkinnyMaxRows);
+        return launch_skinny(*a, s);
+    }
     if (a->dtype == BDM_BF16) return launch_gemv<bf16_t>(*a, s);
     return launch_gemv<float>(*a, s);
 }

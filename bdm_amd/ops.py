@@ -611,24 +611,31 @@ def output_epilogue(raw: Tensor, gate: Tensor, weight: Tensor, bias: Tensor | No
 # ---------------------------------------------------------------------------
 # skinny linear maps (decode)
 
-GEMV_MAX_ROWS = 4
+GEMV_MAX_ROWS = 4            # the streaming GEMV and its prologues
+SKINNY_MAX_ROWS = 64         # the matrix-core tiles (BF16, no prologue)
 GEMV_PROLOGUE_MAX_K = 6144
 
 
 def gemv_supported(x: Tensor, weight: Tensor, bias: Tensor | None) -> bool:
     rows = x.numel() // max(x.shape[-1], 1)
-    return (x.is_cuda and 1 <= rows <= GEMV_MAX_ROWS and x.dtype in (torch.bfloat16, torch.float32)
-            and weight.dtype == x.dtype and weight.ndim == 2 and weight.is_contiguous()
-            and x.shape[-1] == weight.shape[1] and x.shape[-1] % 8 == 0 and weight.data_ptr() % 16 == 0
-            and (bias is None or (bias.dtype == x.dtype and bias.shape == (weight.shape[0],))))
+    k = x.shape[-1]
+    common = (x.is_cuda and weight.dtype == x.dtype and weight.ndim == 2 and weight.is_contiguous()
+              and k == weight.shape[1] and weight.data_ptr() % 16 == 0
+              and (bias is None or (bias.dtype == x.dtype and bias.shape == (weight.shape[0],))))
+    if 1 <= rows <= GEMV_MAX_ROWS:
+        return common and x.dtype in (torch.bfloat16, torch.float32) and k % 8 == 0
+    return (common and rows <= SKINNY_MAX_ROWS and x.dtype == torch.bfloat16 and k % 32 == 0
+            and weight.shape[0] < 2 ** 31)
 
 
 def gemv(x: Tensor, weight: Tensor, bias: Tensor | None = None) -> Tensor:
-    """F.linear(x, weight, bias) for 1 to 4 rows of x, streaming the weight
-    once at HBM bandwidth (FP32 accumulation, one rounding)."""
+    """F.linear(x, weight, bias) for the rows of a decode step: 1 to 4 rows
+    stream the weight once at HBM bandwidth, 5 to 64 BF16 rows run as
+    matrix-core tiles (K % 32 == 0); FP32 accumulation, one rounding."""
     _require_gpu(x, weight, bias)
     if not gemv_supported(x, weight, bias):
-        raise ValueError('gemv takes 1-4 BF16/FP32 rows, a contiguous aligned [N, K] weight and K % 8 == 0')
+        raise ValueError('gemv takes 1-4 BF16/FP32 rows (K % 8 == 0) or 5-64 BF16 rows (K % 32 == 0) and a '
+                         'contiguous aligned [N, K] weight')
     lead, k = x.shape[:-1], x.shape[-1]
     rows, n = x.numel() // k, weight.shape[0]
     x2 = _aligned(x.reshape(rows, k))
@@ -689,8 +696,9 @@ def gemv_fused(x: Tensor, weight: Tensor, bias: Tensor | None = None, *, prologu
 
 
 def linear(x: Tensor, weight: Tensor, bias: Tensor | None = None) -> Tensor:
-    """Inference F.linear: the HBM-streaming GEMV for the few rows of a
-    decode step, the library GEMM otherwise (and under autograd)."""
+    """Inference F.linear: the HBM-streaming GEMV (1-4 rows) or the
+    matrix-core tiles (5-64 BF16 rows) for a decode step, the library GEMM
+    otherwise (and under autograd)."""
     if not torch.is_grad_enabled() and gemv_supported(x, weight, bias):
         return gemv(x, weight, bias)
     return F.linear(x, weight, bias)

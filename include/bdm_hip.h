@@ -419,12 +419,14 @@ int bdm_rms_norm_backward(const void *x, const void *grad_out, const void *weigh
                           float *partials, int64_t rows, int32_t width, int32_t dtype, int32_t weight_dtype,
                           float eps, void *stream);
 
-/* y[m] = W x[m] + bias for the few rows of a decode step: torch's F.linear
+/* y[m] = W x[m] + bias for the rows of a decode step: torch's F.linear
  * (nn.Linear.forward, used by every projection of implementation/bdm/
- * _parameters.py:189-232 and _shell.py:86-91) when the batch of rows is 1 to
- * 4.  x [rows, k], W [n, k] row-major, bias [n] or null, y [rows, n], all of
- * dtype (BDM_BF16 or BDM_F32); FP32 accumulation, bias added in FP32, one
- * rounding.  k: a multiple of 8; x and W 16-byte aligned. */
+ * _parameters.py:189-232 and _shell.py:86-91).  x [rows, k], W [n, k]
+ * row-major, bias [n] or null, y [rows, n], all of dtype; FP32 accumulation,
+ * bias added in FP32, one rounding; x and W 16-byte aligned.  1 to 4 rows:
+ * BDM_BF16 or BDM_F32, k a multiple of 8 (a stream over W).  5 to 64 rows:
+ * BDM_BF16, k a multiple of 32 (matrix-core tiles); other shapes return
+ * BDM_ERR_UNSUPPORTED. */
 int bdm_gemv(const void *x, const void *weight, const void *bias, void *y, int64_t rows, int64_t n, int64_t k,
              int32_t dtype, void *stream);
 

@@ -41,13 +41,41 @@ def test_gemv_matches_fp32_linear(device, dtype, n, k, rows):
         assert bool((diff <= ref.abs() * 2 ** -7 + 1e-6).all())
 
 
+@pytest.mark.parametrize('n,k', [(3456, 1024), (1024, 1024), (1000, 96), (17, 2048), (64, 4128)])
+@pytest.mark.parametrize('rows', [5, 16, 17, 33, 48, 64])
+def test_skinny_matches_fp32_linear(device, n, k, rows):
+    """5 to 64 BF16 rows (a decode batch) take the matrix-core tiles: within
+    one BF16 rounding of the FP32 product plus the FP32 sum-order error, for
+    ragged row counts, ragged column counts and K past one load chunk."""
+    from bdm_amd import ops
+    gen = torch.Generator().manual_seed(n * 3 + k + rows)
+    x = torch.randn(rows, k, generator=gen).to(torch.bfloat16).to(device)
+    w = (torch.randn(n, k, generator=gen) * k ** -0.5).to(torch.bfloat16).to(device)
+    bias = torch.randn(n, generator=gen).to(torch.bfloat16).to(device) if n % 2 == 0 else None
+    announce('skinny', rows, n, k)
+    y = ops.gemv(x, w, bias)
+    x64, w64 = x.double(), w.double()
+    ref = x64 @ w64.t()
+    if bias is not None:
+        ref = ref + bias.double()
+    magnitude = x64.abs() @ w64.abs().t() + (bias.double().abs() if bias is not None else 0)
+    torch.cuda.synchronize()
+    assert y.shape == (rows, n) and y.dtype == torch.bfloat16
+    diff = (y.double() - ref).abs()
+    assert bool((diff <= ref.abs() * 2.0 ** -8 + magnitude * k * 2.0 ** -23 + 1e-30).all())
+    # and the library GEMM agrees to a BF16 rounding or two
+    lib = torch.nn.functional.linear(x, w, bias)
+    assert bool(((y.float() - lib.float()).abs() <= lib.float().abs() * 2 ** -6 + 1e-3).all())
+
+
 def test_linear_dispatch(device):
-    """ops.linear takes the GEMV for 1-4 rows without autograd, the library
-    GEMM otherwise; both agree with F.linear to rounding."""
+    """ops.linear takes the GEMV for 1-4 rows and the matrix-core tiles for
+    5-64 BF16 rows without autograd, the library GEMM otherwise; all agree
+    with F.linear to rounding."""
     from bdm_amd import ops
     gen = torch.Generator().manual_seed(3)
     w = torch.randn(96, 64, generator=gen).to(torch.bfloat16).to(device)
-    for rows in (1, 4, 5, 64):
+    for rows in (1, 4, 5, 64, 65):
         x = torch.randn(rows, 64, generator=gen).to(torch.bfloat16).to(device)
         with torch.no_grad():
             y = ops.linear(x, w)
