@@ -312,7 +312,24 @@ class BankedDeltaMemory(nn.Module):
             raise ValueError('hidden must be [batch, positive time, dim]')
         if not hidden.is_cuda:
             raise ValueError('the hip backend requires ROCm tensors; the CPU oracle lives in oracle/')
+        if not torch.is_grad_enabled() and self._fused_supported(hidden):
+            return self._forward_inference(hidden)
         return self._project_bank_output(hidden, self.bank_reads(hidden))
+
+    def _forward_inference(self, hidden: Tensor) -> Tensor:
+        """forward without autograd: the projections through one GEMM and the
+        controller epilogue, both routes in one launch, the routed operator's
+        forward (the training state and rounding policy of bank_reads, no
+        snapshots) and the output interface in one epilogue before o_proj --
+        about a third of the launches of the autograd path."""
+        controllers, (read_routes, write_routes), gate = self._fused_controllers(hidden)
+        (ww, wi), (rw, ri) = self._route_both(write_routes, read_routes)
+        q, k, v, g, b, w = controllers
+        state = self._state_heads(self.materialize_initial_state())
+        operator = bank_training if self.config.routed_decay else role_bank_training
+        raw = operator(q, k, v, g, b, w, wi, ww, ri, rw, state, self.bank_count, self.bank_size ** -0.5,
+                       compact_replay=self.compact_replay, state_dtype=getattr(torch, self.config.training_state_dtype))
+        return self._fused_output(gate, raw)
 
     # -- stateful inference (inference.py:88-194) -----------------------------------
     def _cache_shape(self, batch: int) -> tuple[int, ...]:
