@@ -440,18 +440,19 @@ __device__ __forceinline__ void load_vec4(const float *p, float4 &out) { out = *
 // (no rounding inside the recurrence, no snapshots) a segment is an affine
 // map of its start state, M_end = P M_start + R, so segments longer than
 // kPieceEvents are cut into pieces to balance skewed routing:
-//   MODE 1 runs each piece q of a cut segment but the last from a zero
-//          state, without reads, and stores its end state R_q and its
-//          transition P_q (the lanes 0..7 of a head also carry the 8 columns
-//          of P, started at the identity, through the same write updates
-//          with x = 0); the scan never uses a last piece's R and P;
+//   MODE 1 runs, in one launch, the pieces of every cut segment but the
+//          last (in the first blocks, so the long ones start first): a
+//          middle piece q from a zero state, without reads, storing its end
+//          state R_q and transition P_q (the lanes 0..7 of a head also carry
+//          the 8 columns of P, started at the identity, through the same
+//          write updates with x = 0); a first piece from the segment's
+//          initial state with its reads, storing its end state as R_0 and
+//          P_0 = 0; then the uncut segments whole, with reads and the final
+//          state, in the slots the pieces leave free;
 //   piece_scan_kernel composes M_(q+1) = P_q M_q + R_q from the segment's
 //          initial state;
-//   MODE 2 runs, in one launch, every piece from its start state M_q
-//          (blocks below piece_blocks, so the long pieces start first) and
-//          the uncut segments whole (blocks from piece_blocks on, mapped as
-//          in MODE 0), with reads; the last piece of a segment stores the
-//          final state.
+//   MODE 2 runs pieces 1.. of each cut segment from their start states M_q,
+//          with reads; the last piece stores the final state.
 template <typename T, int CPL, int HB, int MODE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void lazy_forward_kernel(
     ForwardParams<T> p) {
@@ -475,12 +476,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 
     int seg, piece = 0, pieces = 1, pslot = -1;
     const int block = int(blockIdx.x);
-    if (MODE == 0 || (MODE == 2 && block >= p.piece_blocks)) {
+    if (MODE == 0 || (MODE == 1 && block >= p.piece_blocks)) {
         // (piece_blocks is a multiple of 8, so a segment keeps its XCD)
-        const int sb = MODE == 2 ? block - p.piece_blocks : block;
+        const int sb = MODE == 1 ? block - p.piece_blocks : block;
         seg = p.xcd_remap ? int((sb % 8) * (p.nseg / 8) + sb / 8) : sb;
         // a cut segment runs as its pieces (the whole workgroup leaves together)
-        if (MODE == 2 && p.cu[seg + 1] - p.cu[seg] > kPieceEvents) return;
+        if (MODE == 1 && p.cu[seg + 1] - p.cu[seg] > kPieceEvents) return;
     } else {
         // pieces take the first blocks; the grid is an upper bound on them
         if (block >= p.n_items[0]) return;
@@ -489,8 +490,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         piece = it.y;
         pieces = it.z;
         pslot = it.w;
-        if (MODE == 1 && piece == pieces - 1) return;
+        if (MODE == 1 && piece == pieces - 1) return;  // the scan never uses a last piece's R and P
+        if (MODE == 2 && piece == 0) return;           // MODE 1 ran it from the true start
     }
+    // MODE 1 roles: a middle piece runs from zero with its transition and no
+    // reads; a first piece from the segment's initial state with its reads,
+    // storing its end state as R and a zero P; an uncut segment whole
+    const bool from_zero = MODE == 1 && pslot >= 0 && piece > 0;
+    const bool reads_on = MODE != 1 || !from_zero;
     const int bank = seg % p.banks;
     const int64_t bidx = seg / p.banks;
     const int head0 = blockIdx.y * p.heads_per_block;
@@ -674,7 +681,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     const int64_t state_offset = int64_t(bank) * p.s_heads * S * p.row_stride + head_cols;
     // piece-state rows of this (piece, head): [S, v] FP32
     const int64_t pstate_offset = ((int64_t(pslot) * p.heads + head) * S) * p.width + col0;
-    if (MODE == 1) {
+    if (from_zero) {
 #pragma unroll
         for (int r = 0; r < S; ++r)
 #pragma unroll
@@ -689,7 +696,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     const int pcol = tid % p.lanes_per_head;
     float pc[S];
 #pragma unroll
-    for (int r = 0; r < S; ++r) pc[r] = (MODE == 1 && r == pcol) ? 1.f : 0.f;
+    for (int r = 0; r < S; ++r) pc[r] = (from_zero && r == pcol) ? 1.f : 0.f;
     if (rounding) {
 #pragma unroll
         for (int r = 0; r < S; ++r)
@@ -752,7 +759,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         const bool next_has_write = st + 1 < nstages && s_nw[next_slot] > 0;
 
         auto read_event = [&](int i) {
-            if constexpr (MODE == 1) return;  // a read does not change the state
+            if (MODE == 1 && !reads_on) return;  // a read does not change the state (wave-uniform)
             const int zrow = __builtin_amdgcn_readfirstlane(s_route[slot][i]);
             const float *row = &s_rows[i][lh][0][0];
             float gamma[S];
@@ -811,7 +818,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 #pragma unroll
                 for (int r = 0; r < S; ++r) h[r][c] = fmaf(beta[r], u[c], h[r][c]);
             }
-            if constexpr (MODE == 1) {
+            if (MODE == 1 && from_zero) {
                 // the transition column: the same update with x = 0
                 float uc = nalpha[0] * pc[0];
 #pragma unroll
@@ -886,13 +893,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         if (tid < 64) decode_order(st + 2, o2);
         if (st + 1 < nstages) finish_prep(st + 1);
     }
-    if constexpr (MODE == 1) {
-        // R_q and P_q of this piece
+    if (MODE == 1 && pslot >= 0) {
+        // R_q and P_q of this piece (a first piece: its end state and P = 0,
+        // so the scan's M_1 = P_0 M_0 + R_0 is that end state)
         store_state<S, CPL>(p.pstate, BDM_F32, pstate_offset, p.width, S, h);
         if (pcol < S && tid < nheads * p.lanes_per_head) {
             float *pt = p.ptrans + ((int64_t(pslot) * p.heads + head) * S) * S;
 #pragma unroll
-            for (int r = 0; r < S; ++r) pt[r * S + pcol] = pc[r];
+            for (int r = 0; r < S; ++r) pt[r * S + pcol] = from_zero ? pc[r] : 0.f;
         }
     } else if (lds_ptr(P_FINAL) && piece == pieces - 1) {
         const int64_t final_offset = bidx * (int64_t(p.banks) * p.s_heads * S * p.row_stride) + state_offset;
@@ -1205,7 +1213,10 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, int *zslot, const PieceBu
             p.ptrans = pb.ptrans;
             piece_table_kernel<<<1, 1024, 0, stream>>>(a.cu_seqlens, int(nseg), pb.items, pb.count);
             if (int rc = check_launch("piece_table_kernel")) return rc;
-            const dim3 pgrid(unsigned(pb.max_pieces), grid.y);
+            // MODE 1: the pieces (in the first blocks, so the long ones start
+            // first), then the uncut segments in the slots they leave free
+            p.piece_blocks = int((pb.max_pieces + 7) / 8 * 8);
+            const dim3 pgrid(unsigned(p.piece_blocks + nseg), grid.y);
             if (lazy_hb == 2)
                 lazy_forward_kernel<T, CPL, 2, 1><<<pgrid, lthreads, 0, stream>>>(p);
             else
@@ -1215,8 +1226,7 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, int *zslot, const PieceBu
                 pb.items, pb.count, a.initial, a.initial_dtype, a.initial_batch_stride, a.bank_count, p.heads,
                 p.width, p.split, p.row_stride, pb.pstate, pb.ptrans);
             if (int rc = check_launch("piece_scan_kernel")) return rc;
-            p.piece_blocks = int((pb.max_pieces + 7) / 8 * 8);
-            const dim3 g2(unsigned(nseg + p.piece_blocks), grid.y);
+            const dim3 g2(unsigned(p.piece_blocks), grid.y);  // MODE 2: pieces 1.. of each cut segment
             if (lazy_hb == 2)
                 lazy_forward_kernel<T, CPL, 2, 2><<<g2, lthreads, 0, stream>>>(p);
             else
