@@ -16,7 +16,6 @@ struct ChunkForwardParams {
     void *final_state;            // NULL or [batch, J, s_heads, 8, row_stride]
     bf16_t *snap;                 // NULL or [rows, s_heads, 8, row_stride] BF16
     bf16_t *zbuf;                 // [NT*KR, heads * width] read rows
-    const int *zslot;             // read route -> its row of zbuf
     int64_t init_bstride;
     int64_t nt;
     int heads;        // virtual heads: s_heads * split

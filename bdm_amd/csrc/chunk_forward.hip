@@ -172,7 +172,7 @@ __global__ __launch_bounds__(64) void chunk_forward_kernel(ChunkForwardParams p)
             const uint32_t below = (1u << lane) - 1u;
             if (rd) {
                 const int route = o - write_events;
-                s_zrow[__popc(rmask & below)] = p.zslot[route];
+                s_zrow[__popc(rmask & below)] = route;  // a read's row of zbuf: its route
             } else {
                 const int j = __popc(wmask & below);
                 s_wrow[j] = route_token(o, p.kw, p.kw_shift) * vrow + vhead;

@@ -20,10 +20,10 @@
 // one L2 instead of eight.
 //
 // Read results (one S-row contraction per read event and head) go to a BF16
-// (ctrl dtype) buffer at row token*KR + rank, where rank orders the token's
-// reads by bank id (read_slot_kernel); the combine kernel then streams each
-// token's KR consecutive rows and adds them in that order, rounding after
-// every add (the production readout order).
+// (ctrl dtype) buffer at row token*KR + j, j the read's route slot; the
+// combine kernel then streams each token's KR consecutive rows and adds them
+// in increasing bank id, rounding after every add (the production readout
+// order), ordering the token's KR bank ids itself.
 #include <cstdlib>
 #include <cstring>
 #include <type_traits>
@@ -48,7 +48,6 @@ struct ForwardParams {
     void *final_state;
     void *snap;
     T *zbuf;
-    const int *zslot;  // read route -> its row of zbuf (token*KR + rank of the bank)
     int64_t init_bstride;
     int64_t nt, time;
     int heads, s_real, width, banks, kw, kr;
@@ -184,7 +183,7 @@ __global__ __launch_bounds__(256) void routed_forward_kernel(ForwardParams<T> p)
             const bool rd = o >= write_events;
             const int64_t route = rd ? o - write_events : o;
             s_token[threadIdx.x] = rd ? route / p.kr : route / p.kw;
-            s_slot[threadIdx.x] = rd ? p.zslot[route] : -1;
+            s_slot[threadIdx.x] = rd ? route : -1;  // a read's row of zbuf: its route
             s_weight[threadIdx.x] = rd ? to_f32(p.rw[route]) : to_f32(p.ww[route]);
         }
         __syncthreads();
@@ -534,11 +533,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     // the event loop keeps most scalar registers busy, and each SGPR the
     // compiler spills to a VGPR lane costs a v_readlane at every use.  Only
     // v, w and zbuf (addressed at every event) stay scalar.
-    enum { P_ORDER, P_ZSLOT, P_Q, P_K, P_B, P_G, P_WW, P_RW, P_SNAP, P_FINAL, P_COUNT };
+    enum { P_ORDER, P_Q, P_K, P_B, P_G, P_WW, P_RW, P_SNAP, P_FINAL, P_COUNT };
     __shared__ uint64_t s_ptr[P_COUNT];
     if (tid == 0) {
         s_ptr[P_ORDER] = reinterpret_cast<uint64_t>(p.order);
-        s_ptr[P_ZSLOT] = reinterpret_cast<uint64_t>(p.zslot);
         s_ptr[P_Q] = reinterpret_cast<uint64_t>(p.q);
         s_ptr[P_K] = reinterpret_cast<uint64_t>(p.k);
         s_ptr[P_B] = reinterpret_cast<uint64_t>(p.b);
@@ -597,7 +595,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         const int64_t row = (int64_t(s_tok[slot][pe]) * p.s_heads + (head0 + ph) / p.split) * S + 4 * half;
         const int route = s_route[slot][pe];
         if (rd) {
-            if (tid < NE) pl.zrow = static_cast<const int *>(lds_ptr(P_ZSLOT))[route];
+            if (tid < NE) pl.zrow = route;  // a read's row of zbuf: its route
             load_vec4(static_cast<const T *>(lds_ptr(P_Q)) + row, pl.key);
             const T *rw = static_cast<const T *>(lds_ptr(P_RW));
             if constexpr (std::is_same<T, bf16_t>::value)
@@ -988,72 +986,104 @@ __global__ __launch_bounds__(256) void piece_scan_kernel(const int4 *__restrict_
     }
 }
 
-// zslot[token*KR + j] = token*KR + (rank of read j among the token's reads
-// in increasing bank id, ties by j): the row of the read buffer that read
-// goes to, so the combine folds a token's rows in their stored order.
-__global__ __launch_bounds__(256) void read_slot_kernel(const int64_t *__restrict__ read_indices, int64_t routes,
-                                                        int kr, int *__restrict__ zslot) {
-    // one thread per read route; the token's KR indices are independent loads
-    const int64_t route = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (route >= routes) return;
-    const int64_t first = route - route % kr;
-    const int j = int(route - first);
-    const int64_t mine = read_indices[route];
-    int rank = 0;
-#pragma unroll 8
-    for (int jj = 0; jj < kr; ++jj) {
-        const int64_t other = read_indices[first + jj];
-        rank += (other < mine) || (other == mine && jj < j);
-    }
-    zslot[route] = int(first + rank);
-}
-
 // y[token, :] = fold over the token's reads in increasing bank id of
-// bf(total + z) (role_bank_dispatch.py:209-215): the token's KR rows of the
-// read buffer are already in that order.  One thread per (token, CPL columns).
-// EACH = false is the narrow-head rule (head width <= 32,
+// bf(total + z) (role_bank_dispatch.py:209-215).  A token's KR rows of the
+// read buffer are in route order (row token*KR + j), so each thread orders the
+// token's KR bank ids itself: keys (bank << bits | j) sort by bank, ties by
+// route slot, and the low bits give each fold position its row.  The token's
+// indices are 64 bytes that every thread of the token reads (from L1); the
+// rows themselves are loaded in fold order, so no row moves twice.  Banks are
+// clamped to [0, banks) as the dispatch clamps them.  One thread per (token,
+// CPL columns).  EACH = false is the narrow-head rule (head width <= 32,
 // role_bank_dispatch.py:222-226): the reference then sums with index_add_,
 // which accumulates a token's reads in FP32 and rounds once.
+__device__ __forceinline__ void sort8_ascending(uint32_t (&x)[8]) {
+    auto cex = [](uint32_t &a, uint32_t &b) {
+        const uint32_t lo = min(a, b), hi = max(a, b);
+        a = lo;
+        b = hi;
+    };
+    cex(x[0], x[2]), cex(x[1], x[3]), cex(x[4], x[6]), cex(x[5], x[7]);
+    cex(x[0], x[4]), cex(x[1], x[5]), cex(x[2], x[6]), cex(x[3], x[7]);
+    cex(x[0], x[1]), cex(x[2], x[3]), cex(x[4], x[5]), cex(x[6], x[7]);
+    cex(x[2], x[4]), cex(x[3], x[5]);
+    cex(x[1], x[4]), cex(x[3], x[6]);
+    cex(x[1], x[2]), cex(x[3], x[4]), cex(x[5], x[6]);
+}
+
 template <typename T, int CPL, int KFIX, bool EACH>
-__global__ __launch_bounds__(256) void ordered_combine_kernel(const T *__restrict__ zbuf, T *__restrict__ y,
-                                                              int64_t nt, int kr, int row_width) {
+__global__ __launch_bounds__(256) void ordered_combine_kernel(const T *__restrict__ zbuf,
+                                                              const int64_t *__restrict__ read_indices,
+                                                              T *__restrict__ y, int64_t nt, int kr, int row_width,
+                                                              int banks) {
     const int chunks = row_width / CPL;
     const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     const int64_t token = idx / chunks;
     if (token >= nt) return;
     const int col0 = int(idx - token * chunks) * CPL;
     const T *z = zbuf + token * kr * row_width + col0;
+    const int64_t *ri = read_indices + token * kr;
+    auto bank_of = [&](int j) -> uint32_t {
+        const int64_t b = ri[j];
+        return uint32_t(b < 0 ? 0 : (b >= banks ? banks - 1 : b));
+    };
     float total[CPL];
 #pragma unroll
     for (int c = 0; c < CPL; ++c) total[c] = 0.f;
-    if constexpr (KFIX > 0 && sizeof(T) == 2 && CPL == 8) {
-        // exactly KFIX rows: 16-byte nontemporal loads (the rows are used
-        // once), all in flight before the fold
-        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-        u32x4 raw[KFIX];
+    auto add = [&](const float (&v)[CPL]) {
 #pragma unroll
-        for (int j = 0; j < KFIX; ++j)
-            raw[j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(z + int64_t(j) * row_width));
+        for (int c = 0; c < CPL; ++c) total[c] = EACH ? round_to<T>(total[c] + v[c]) : total[c] + v[c];
+    };
+    if constexpr (KFIX == 8) {
+        // eight reads: a 19-comparator sort of (bank << 3 | slot), banks < 2^29
+        uint32_t key[8];
 #pragma unroll
-        for (int j = 0; j < KFIX; ++j) {
-            const uint32_t w[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+        for (int j = 0; j < 8; ++j) key[j] = (bank_of(j) << 3) | uint32_t(j);
+        sort8_ascending(key);
+        if constexpr (sizeof(T) == 2 && CPL == 8) {
+            // 16-byte nontemporal loads (the rows are used once), all in flight before the fold
+            typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+            u32x4 raw[8];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                total[2 * q] += __uint_as_float(w[q] << 16);
-                total[2 * q + 1] += __uint_as_float(w[q] & 0xffff0000u);
-                if constexpr (EACH) {
-                    total[2 * q] = round_to<T>(total[2 * q]);
-                    total[2 * q + 1] = round_to<T>(total[2 * q + 1]);
+            for (int i = 0; i < 8; ++i)
+                raw[i] = __builtin_nontemporal_load(
+                    reinterpret_cast<const u32x4 *>(z + int64_t(key[i] & 7u) * row_width));
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const uint32_t w[4] = {raw[i].x, raw[i].y, raw[i].z, raw[i].w};
+                float v[CPL];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    v[2 * q] = __uint_as_float(w[q] << 16);
+                    v[2 * q + 1] = __uint_as_float(w[q] & 0xffff0000u);
                 }
+                add(v);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                float v[CPL];
+                load_row<CPL>(z + int64_t(key[i] & 7u) * row_width, v);
+                add(v);
             }
         }
     } else {
-#pragma unroll 8
-        for (int j = 0; j < kr; ++j) {
-            float v[CPL];
-            load_row<CPL>(z + int64_t(j) * row_width, v);
+        // up to 32 reads: the next row is the one with the smallest key above
+        // the last row's, keys (bank << 5 | slot) in 64 bits
+        constexpr int KMAX = 32;
+        uint64_t key[KMAX];
 #pragma unroll
-            for (int c = 0; c < CPL; ++c) total[c] = EACH ? round_to<T>(total[c] + v[c]) : total[c] + v[c];
+        for (int j = 0; j < KMAX; ++j) key[j] = j < kr ? (uint64_t(bank_of(j)) << 5) | uint64_t(j) : ~uint64_t(0);
+        uint64_t last = 0;
+        for (int i = 0; i < kr; ++i) {
+            uint64_t next = ~uint64_t(0);
+#pragma unroll
+            for (int j = 0; j < KMAX; ++j)
+                if ((i == 0 || key[j] > last) && key[j] < next) next = key[j];
+            last = next;
+            float v[CPL];
+            load_row<CPL>(z + int64_t(next & 31u) * row_width, v);
+            add(v);
         }
     }
     store_row<CPL>(y + token * row_width + col0, total);
@@ -1109,22 +1139,22 @@ int launch_combine_kernels(const bdm_forward_args &a, const T *zbuf, hipStream_t
             const int64_t threads = nt * (row_width / cc);
             if (cc == CC)
                 ordered_combine_kernel<T, CC, 0, false><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
-                    zbuf, static_cast<T *>(a.output), nt, a.read_banks, row_width);
+                    zbuf, a.read_indices, static_cast<T *>(a.output), nt, a.read_banks, row_width, a.bank_count);
             else
                 ordered_combine_kernel<T, 1, 0, false><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
-                    zbuf, static_cast<T *>(a.output), nt, a.read_banks, row_width);
+                    zbuf, a.read_indices, static_cast<T *>(a.output), nt, a.read_banks, row_width, a.bank_count);
         } else if (row_width % CC == 0) {
             const int64_t threads = nt * (row_width / CC);
-            if (a.read_banks == 8)
+            if (a.read_banks == 8 && a.bank_count < (1 << 29))
                 ordered_combine_kernel<T, CC, 8, true><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
-                    zbuf, static_cast<T *>(a.output), nt, a.read_banks, row_width);
+                    zbuf, a.read_indices, static_cast<T *>(a.output), nt, a.read_banks, row_width, a.bank_count);
             else
                 ordered_combine_kernel<T, CC, 0, true><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
-                    zbuf, static_cast<T *>(a.output), nt, a.read_banks, row_width);
+                    zbuf, a.read_indices, static_cast<T *>(a.output), nt, a.read_banks, row_width, a.bank_count);
         } else {
             const int64_t threads = nt * row_width;
             ordered_combine_kernel<T, 1, 0, true><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
-                zbuf, static_cast<T *>(a.output), nt, a.read_banks, row_width);
+                zbuf, a.read_indices, static_cast<T *>(a.output), nt, a.read_banks, row_width, a.bank_count);
         }
     } else {
         const int64_t count = nt * row_width;
@@ -1141,7 +1171,7 @@ int launch_combine(const bdm_forward_args &a, const T *zbuf, hipStream_t stream)
 }
 
 template <typename T, int S, int CPL, bool kLazy = false>
-int launch_forward(const bdm_forward_args &a, T *zbuf, int *zslot, const PieceBuffers &pb, hipStream_t stream) {
+int launch_forward(const bdm_forward_args &a, T *zbuf, const PieceBuffers &pb, hipStream_t stream) {
     const int split = kLazy ? lazy_split(a) : 1;
     if (a.head_width / split / CPL > 256)
         return fail(BDM_ERR_UNSUPPORTED, "forward: head_width %d needs more than 256 lanes", a.head_width);
@@ -1159,7 +1189,6 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, int *zslot, const PieceBu
     p.initial = a.initial;
     p.final_state = a.final_state;
     p.zbuf = zbuf;
-    p.zslot = zslot;
     p.init_bstride = a.initial_batch_stride;
     p.nt = a.batch * a.time;
     p.time = a.time;
@@ -1193,13 +1222,6 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, int *zslot, const PieceBu
     p.xcd_remap = (nseg % 8 == 0) ? 1 : 0;
     const int threads = ((p.heads_per_block * p.lanes_per_head + kWave - 1) / kWave) * kWave;
     const dim3 grid(unsigned(nseg), unsigned((p.heads + p.heads_per_block - 1) / p.heads_per_block));
-    if (a.read_banks > 0) {
-        const int64_t nt = a.batch * a.time;
-        const int64_t routes = nt * a.read_banks;
-        read_slot_kernel<<<unsigned((routes + 255) / 256), 256, 0, stream>>>(a.read_indices, routes, a.read_banks,
-                                                                              zslot);
-        if (int rc = check_launch("read_slot_kernel")) return rc;
-    }
     p.nseg = int(nseg);
     if (int rc = record_phase(a, 0, stream)) return rc;
     if constexpr (kLazy) {
@@ -1279,16 +1301,9 @@ bool chunk_enabled() {
     return e && strcmp(e, "mfma") == 0;
 }
 
-// The matrix-core recurrence (chunk_forward.hip) between the read-slot map
-// and the combine.
-int launch_chunked(const bdm_forward_args &a, bf16_t *zbuf, int *zslot, hipStream_t stream) {
+// The matrix-core recurrence (chunk_forward.hip), then the combine.
+int launch_chunked(const bdm_forward_args &a, bf16_t *zbuf, hipStream_t stream) {
     const int64_t nt = a.batch * a.time;
-    if (a.read_banks > 0) {
-        const int64_t routes = nt * a.read_banks;
-        read_slot_kernel<<<unsigned((routes + 255) / 256), 256, 0, stream>>>(a.read_indices, routes, a.read_banks,
-                                                                              zslot);
-        if (int rc = check_launch("read_slot_kernel")) return rc;
-    }
     if (int rc = record_phase(a, 0, stream)) return rc;
     const int split = a.head_width > 256 ? a.head_width / 128 : 1;
     ChunkForwardParams p{};
@@ -1306,7 +1321,6 @@ int launch_chunked(const bdm_forward_args &a, bf16_t *zbuf, int *zslot, hipStrea
     p.final_state = a.final_state;
     p.snap = static_cast<bf16_t *>(a.snapshots);
     p.zbuf = zbuf;
-    p.zslot = zslot;
     p.init_bstride = a.initial_batch_stride;
     p.nt = nt;
     p.split = split;
@@ -1330,24 +1344,24 @@ int launch_chunked(const bdm_forward_args &a, bf16_t *zbuf, int *zslot, hipStrea
 }
 
 template <typename T>
-int dispatch_forward(const bdm_forward_args &a, T *zbuf, int *zslot, const PieceBuffers &pb, hipStream_t stream) {
+int dispatch_forward(const bdm_forward_args &a, T *zbuf, const PieceBuffers &pb, hipStream_t stream) {
     // Vector row loads need 16-byte aligned rows: aligned bases, and a state
     // batch stride that keeps them aligned.
     const bool vec = a.initial_batch_stride % 8 == 0;
     if constexpr (std::is_same<T, bf16_t>::value) {
-        if (chunk_path(a) && chunk_enabled()) return launch_chunked(a, zbuf, zslot, stream);
+        if (chunk_path(a) && chunk_enabled()) return launch_chunked(a, zbuf, stream);
     }
     if (a.bank_size <= 8) {
-        if (lazy_path(a)) return launch_forward<T, 8, 4, true>(a, zbuf, zslot, pb, stream);
-        if (vec && a.head_width % 8 == 0) return launch_forward<T, 8, 8>(a, zbuf, zslot, pb, stream);
-        return launch_forward<T, 8, 1>(a, zbuf, zslot, pb, stream);
+        if (lazy_path(a)) return launch_forward<T, 8, 4, true>(a, zbuf, pb, stream);
+        if (vec && a.head_width % 8 == 0) return launch_forward<T, 8, 8>(a, zbuf, pb, stream);
+        return launch_forward<T, 8, 1>(a, zbuf, pb, stream);
     }
     if (a.bank_size <= 16) {
-        if (vec && a.head_width % 4 == 0) return launch_forward<T, 16, 4>(a, zbuf, zslot, pb, stream);
-        return launch_forward<T, 16, 1>(a, zbuf, zslot, pb, stream);
+        if (vec && a.head_width % 4 == 0) return launch_forward<T, 16, 4>(a, zbuf, pb, stream);
+        return launch_forward<T, 16, 1>(a, zbuf, pb, stream);
     }
-    if (vec && a.head_width % 2 == 0) return launch_forward<T, 32, 2>(a, zbuf, zslot, pb, stream);
-    return launch_forward<T, 32, 1>(a, zbuf, zslot, pb, stream);
+    if (vec && a.head_width % 2 == 0) return launch_forward<T, 32, 2>(a, zbuf, pb, stream);
+    return launch_forward<T, 32, 1>(a, zbuf, pb, stream);
 }
 
 size_t elem_size(int dtype) { return dtype == BDM_BF16 ? 2 : 4; }
@@ -1366,10 +1380,6 @@ static size_t forward_zbuf_bytes(const bdm_forward_args *a) {
                     size_t(a->head_width) * bdm::elem_size(a->ctrl_dtype));
 }
 
-static size_t forward_zslot_bytes(const bdm_forward_args *a) {
-    return round256(size_t(a->batch) * size_t(a->time) * size_t(a->read_banks) * sizeof(int));
-}
-
 static size_t forward_piece_bytes(const bdm_forward_args *a) {
     const size_t n = size_t(bdm::max_pieces(*a));
     if (!n) return 0;
@@ -1382,7 +1392,7 @@ extern "C" size_t bdm_forward_workspace_size(const bdm_forward_args *a) {
     if (!a || a->batch <= 0 || a->time <= 0 || a->heads <= 0 || a->head_width <= 0 || a->read_banks < 0 ||
         a->write_banks < 0 || a->bank_size <= 0)
         return 0;
-    return forward_zbuf_bytes(a) + forward_zslot_bytes(a) + forward_piece_bytes(a);
+    return forward_zbuf_bytes(a) + forward_piece_bytes(a);
 }
 
 extern "C" int bdm_forward(const bdm_forward_args *a, void *workspace, size_t workspace_bytes, void *stream) {
@@ -1423,12 +1433,11 @@ extern "C" int bdm_forward(const bdm_forward_args *a, void *workspace, size_t wo
         return fail(BDM_ERR_UNSUPPORTED, "forward: more than 2^31 read events");
     hipStream_t s = as_stream(stream);
     char *ws = static_cast<char *>(workspace);
-    int *zslot = reinterpret_cast<int *>(ws + forward_zbuf_bytes(a));
     PieceBuffers pb;
     pb.max_pieces = max_pieces(*a);
     if (pb.max_pieces > INT32_MAX / 2) return fail(BDM_ERR_UNSUPPORTED, "forward: too many pieces");
     if (pb.max_pieces) {
-        char *at = ws + forward_zbuf_bytes(a) + forward_zslot_bytes(a);
+        char *at = ws + forward_zbuf_bytes(a);
         const size_t n = size_t(pb.max_pieces);
         pb.items = reinterpret_cast<int4 *>(at);
         at += round256(n * sizeof(int4));
@@ -1439,6 +1448,6 @@ extern "C" int bdm_forward(const bdm_forward_args *a, void *workspace, size_t wo
         pb.ptrans = reinterpret_cast<float *>(at);
     }
     if (a->ctrl_dtype == BDM_BF16)
-        return dispatch_forward<bf16_t>(*a, static_cast<bf16_t *>(workspace), zslot, pb, s);
-    return dispatch_forward<float>(*a, static_cast<float *>(workspace), zslot, pb, s);
+        return dispatch_forward<bf16_t>(*a, static_cast<bf16_t *>(workspace), pb, s);
+    return dispatch_forward<float>(*a, static_cast<float *>(workspace), pb, s);
 }

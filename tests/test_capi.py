@@ -45,10 +45,9 @@ def test_workspace_sizes(lib):
     args.bank_size, args.write_banks = 4, 4
     args.ctrl_dtype = _lib.BDM_BF16
     r256 = lambda x: (x + 255) // 256 * 256  # noqa: E731
-    # read rows (BF16, H*v per read event) then their row map (int32 per read event)
+    # read rows: BF16, H*v per read event, row token*KR + j
     rows = r256(2 * 10 * 4 * 3 * 16 * 2)
-    slots = r256(2 * 10 * 4 * 4)
-    assert lib.bdm_forward_workspace_size(ctypes.byref(args)) == rows + slots
+    assert lib.bdm_forward_workspace_size(ctypes.byref(args)) == rows
     # S = 8 under the prefill policy (no rounding, no snapshots) adds the
     # piece list of cut segments: at most 2 * (E // 512) + 1 pieces, with
     # their FP32 start states [H, 8, v] and transitions [H, 8, 8]
@@ -56,9 +55,9 @@ def test_workspace_sizes(lib):
     rows = r256(2 * 10 * 4 * 3 * 128 * 2)
     pieces = 2 * ((2 * 10 * 8) // 512) + 1
     extra = r256(pieces * 16) + 256 + r256(pieces * 3 * 8 * 128 * 4) + r256(pieces * 3 * 64 * 4)
-    assert lib.bdm_forward_workspace_size(ctypes.byref(args)) == rows + slots + extra
+    assert lib.bdm_forward_workspace_size(ctypes.byref(args)) == rows + extra
     args.round_interval = 16  # the training policy rounds inside the recurrence: no pieces
-    assert lib.bdm_forward_workspace_size(ctypes.byref(args)) == rows + slots
+    assert lib.bdm_forward_workspace_size(ctypes.byref(args)) == rows
 
 
 def test_invalid_arguments_are_rejected_without_a_launch(lib):
