@@ -404,7 +404,6 @@ struct PrepLoads<bf16_t> {
     uint2 key, erase;  // k (or q for a read), b: 4 BF16 each
     float4 gate;       // g
     uint32_t weight;   // route weight, BF16 in the low half
-    int zrow;          // a read's row of the read buffer
     __device__ __forceinline__ float key_at(int r) const {
         const uint32_t w = r < 2 ? key.x : key.y;
         return __uint_as_float((r & 1) ? (w & 0xffff0000u) : (w << 16));
@@ -419,7 +418,6 @@ template <>
 struct PrepLoads<float> {
     float4 key, erase, gate;
     float weight_raw;
-    int zrow;
     __device__ __forceinline__ float key_at(int r) const { return (&key.x)[r]; }
     __device__ __forceinline__ float erase_at(int r) const { return (&erase.x)[r]; }
     __device__ __forceinline__ float weight_f() const { return weight_raw; }
@@ -595,7 +593,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         const int64_t row = (int64_t(s_tok[slot][pe]) * p.s_heads + (head0 + ph) / p.split) * S + 4 * half;
         const int route = s_route[slot][pe];
         if (rd) {
-            if (tid < NE) pl.zrow = route;  // a read's row of zbuf: its route
             load_vec4(static_cast<const T *>(lds_ptr(P_Q)) + row, pl.key);
             const T *rw = static_cast<const T *>(lds_ptr(P_RW));
             if constexpr (std::is_same<T, bf16_t>::value)
@@ -657,10 +654,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
                     row[2][rr] = d[r];
                 }
             }
-            if (tid < NE) {
-                s_pw[pe] = pw;
-                if (rd) s_route[slot][pe] = pl.zrow;  // from here on: the read's row of zbuf
-            }
+            if (tid < NE) s_pw[pe] = pw;
             if (pe == n - 1) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) s_fold[ph][4 * half + r] = eager ? 1.f : sc[r];
@@ -1370,9 +1364,9 @@ size_t elem_size(int dtype) { return dtype == BDM_BF16 ? 2 : 4; }
 }  // namespace bdm
 
 // Workspace of bdm_forward: the read buffer (one ctrl_dtype row of H*v per
-// read event), its row map (one int32 per read event), then, under the
-// prefill policy, the piece list, its count and the FP32 piece states and
-// transitions ([pieces, H, 8, v] and [pieces, H, 8, 8]).
+// read event, row token*KR + j), then, under the prefill policy, the piece
+// list, its count and the FP32 piece states and transitions ([pieces, H, 8,
+// v] and [pieces, H, 8, 8]).
 static size_t round256(size_t x) { return (x + 255) / 256 * 256; }
 
 static size_t forward_zbuf_bytes(const bdm_forward_args *a) {
