@@ -71,6 +71,9 @@ struct ForwardParams {
     int piece_blocks;      // MODE 2: blocks of pieces ahead of the segments (a multiple of 8)
     float *pstate;         // [slots, H, S, v] FP32: zero-start end state R_q, then start state M_(q+1)
     float *ptrans;         // [slots, H, S, S] FP32: transition P_q of piece q
+    // MODE 0 with xcd_remap: the segments of each XCD's range, longest first
+    // (segment_order_kernel); null keeps the range in bank order
+    const int *seg_order;
 };
 
 // Events per piece when long segments are cut (a multiple of the stage size).
@@ -472,8 +475,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     __shared__ int s_flag[2];  // by stage parity: reset two barriers before its next use
 
     int seg, piece = 0, pieces = 1, pslot = -1;
+    int group = int(blockIdx.y);  // head group of the block
     const int block = int(blockIdx.x);
-    if (MODE == 0 || (MODE == 1 && block >= p.piece_blocks)) {
+    if (MODE == 0 && p.seg_order) {
+        // Longest segments first: workgroups reach the XCDs round-robin in
+        // dispatch order (x fastest), so the k-th block of XCD x takes item k
+        // of that XCD's range, every head group of a segment in a row, the
+        // segments in decreasing length.  Slots that run a long segment in
+        // the first round take a short one in the last, and the rounds end
+        // together instead of in a long tail.
+        const int64_t linear = int64_t(blockIdx.y) * gridDim.x + blockIdx.x;
+        const int64_t k = linear / 8;
+        const int range = p.nseg / 8;
+        seg = p.seg_order[int(linear % 8) * range + int(k / gridDim.y)];
+        group = int(k % gridDim.y);
+    } else if (MODE == 0 || (MODE == 1 && block >= p.piece_blocks)) {
         // (piece_blocks is a multiple of 8, so a segment keeps its XCD)
         const int sb = MODE == 1 ? block - p.piece_blocks : block;
         seg = p.xcd_remap ? int((sb % 8) * (p.nseg / 8) + sb / 8) : sb;
@@ -497,7 +513,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     const bool reads_on = MODE != 1 || !from_zero;
     const int bank = seg % p.banks;
     const int64_t bidx = seg / p.banks;
-    const int head0 = blockIdx.y * p.heads_per_block;
+    const int head0 = group * p.heads_per_block;
     const int nheads = min(p.heads_per_block, p.heads - head0);
     const int tid = threadIdx.x;
     // value-column role.  Lanes past the block's heads shadow lanes of the
@@ -900,6 +916,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     }
 }
 
+// Segments of each of the 8 XCD ranges (range = nseg / 8 consecutive
+// segments) in decreasing length, ties by index: order[x * range + rank] =
+// the segment of rank `rank` in range x.  One workgroup per range; a
+// segment's rank counts the longer segments and the equal ones before it.
+constexpr int kOrderMaxRange = 1024;
+__global__ __launch_bounds__(256) void segment_order_kernel(const int64_t *__restrict__ cu, int range,
+                                                            int *__restrict__ order) {
+    __shared__ int s_len[kOrderMaxRange];
+    const int base = int(blockIdx.x) * range;
+    for (int i = threadIdx.x; i < range; i += blockDim.x) s_len[i] = int(cu[base + i + 1] - cu[base + i]);
+    __syncthreads();
+    for (int i = threadIdx.x; i < range; i += blockDim.x) {
+        const int li = s_len[i];
+        int rank = 0;
+        for (int j = 0; j < range; ++j) {
+            const int lj = s_len[j];
+            rank += (lj > li || (lj == li && j < i)) ? 1 : 0;
+        }
+        order[base + rank] = base + i;
+    }
+}
+
 // The piece list: a segment longer than kPieceEvents becomes
 // ceil(len / kPieceEvents) pieces with consecutive piece-state slots.  One
 // workgroup of 1024 threads; thread t handles a contiguous run of segments.
@@ -1101,12 +1139,14 @@ int lazy_split(const bdm_forward_args &a) {
     return a.head_width % 128 == 0 ? a.head_width / 128 : 0;
 }
 
-// Scratch of the cut-segment path, carved from the bdm_forward workspace.
+// Scratch carved from the bdm_forward workspace: the cut-segment path's and
+// the longest-first segment order's.
 struct PieceBuffers {
     int4 *items = nullptr;
     int *count = nullptr;
     float *pstate = nullptr, *ptrans = nullptr;
     int64_t max_pieces = 0;  // 0: the path is off
+    int *seg_order = nullptr;  // null: segments in bank order
 };
 
 // Profiling events of bdm_forward (phase_events): 0 before the recurrence,
@@ -1248,6 +1288,11 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, const PieceBuffers &pb, h
             else
                 lazy_forward_kernel<T, CPL, 8, 2><<<g2, lthreads, 0, stream>>>(p);
         } else {
+            if (pb.seg_order) {
+                segment_order_kernel<<<8, 256, 0, stream>>>(a.cu_seqlens, int(nseg / 8), pb.seg_order);
+                if (int rc = check_launch("segment_order_kernel")) return rc;
+                p.seg_order = pb.seg_order;
+            }
             if (lazy_hb == 2)
                 lazy_forward_kernel<T, CPL, 2, 0><<<grid, lthreads, 0, stream>>>(p);
             else
@@ -1282,6 +1327,19 @@ int64_t max_pieces(const bdm_forward_args &a) {
     if (!lazy_path(a) || a.round_interval > 0 || a.snapshots) return 0;
     const int64_t events = a.batch * a.time * (int64_t(a.write_banks) + a.read_banks);
     return 2 * (events / kPieceEvents) + 1;
+}
+
+// Whether the lazy kernel's MODE 0 takes each XCD range's segments longest
+// first (segment_order_kernel): whole segments (no pieces), ranges that the
+// XCD remap forms, at most kOrderMaxRange segments each.  BDM_SEGMENT_ORDER=0
+// keeps bank order (results are identical either way).
+bool order_path(const bdm_forward_args &a) {
+    const int64_t nseg = a.batch * a.bank_count;
+    return lazy_path(a) && max_pieces(a) == 0 && nseg % 8 == 0 && nseg / 8 <= kOrderMaxRange;
+}
+bool order_enabled() {
+    const char *e = getenv("BDM_SEGMENT_ORDER");
+    return !(e && strcmp(e, "0") == 0);
 }
 
 // BDM_FORWARD_KERNEL=mfma selects the matrix-core recurrence where it
@@ -1366,7 +1424,8 @@ size_t elem_size(int dtype) { return dtype == BDM_BF16 ? 2 : 4; }
 // Workspace of bdm_forward: the read buffer (one ctrl_dtype row of H*v per
 // read event, row token*KR + j), then, under the prefill policy, the piece
 // list, its count and the FP32 piece states and transitions ([pieces, H, 8,
-// v] and [pieces, H, 8, 8]).
+// v] and [pieces, H, 8, 8]), or else, where segments run longest first, the
+// segment order (int32 per segment).
 static size_t round256(size_t x) { return (x + 255) / 256 * 256; }
 
 static size_t forward_zbuf_bytes(const bdm_forward_args *a) {
@@ -1382,11 +1441,15 @@ static size_t forward_piece_bytes(const bdm_forward_args *a) {
            round256(n * a->heads * size_t(bdm::lazy_split(*a)) * 64 * 4);
 }
 
+static size_t forward_order_bytes(const bdm_forward_args *a) {
+    return bdm::order_path(*a) ? round256(size_t(a->batch) * size_t(a->bank_count) * 4) : 0;
+}
+
 extern "C" size_t bdm_forward_workspace_size(const bdm_forward_args *a) {
     if (!a || a->batch <= 0 || a->time <= 0 || a->heads <= 0 || a->head_width <= 0 || a->read_banks < 0 ||
         a->write_banks < 0 || a->bank_size <= 0)
         return 0;
-    return forward_zbuf_bytes(a) + forward_piece_bytes(a);
+    return forward_zbuf_bytes(a) + forward_piece_bytes(a) + forward_order_bytes(a);
 }
 
 extern "C" int bdm_forward(const bdm_forward_args *a, void *workspace, size_t workspace_bytes, void *stream) {
@@ -1441,6 +1504,8 @@ extern "C" int bdm_forward(const bdm_forward_args *a, void *workspace, size_t wo
         at += round256(n * a->heads * 8 * size_t(a->head_width) * 4);
         pb.ptrans = reinterpret_cast<float *>(at);
     }
+    if (order_path(*a) && order_enabled())
+        pb.seg_order = reinterpret_cast<int *>(ws + forward_zbuf_bytes(a) + forward_piece_bytes(a));
     if (a->ctrl_dtype == BDM_BF16)
         return dispatch_forward<bf16_t>(*a, static_cast<bf16_t *>(workspace), pb, s);
     return dispatch_forward<float>(*a, static_cast<float *>(workspace), pb, s);

@@ -487,6 +487,46 @@ def test_decode_kernel_matches_oracle(device, heads, v):
 
 # ---------------------------------------------------------------- full benchmark size
 
+@pytest.mark.gpu
+def test_segment_order_bit_identical(device, monkeypatch):
+    """At C2 size under the module policy the recurrence runs each XCD's
+    segments longest first; y and the final state must equal those of the
+    bank-order launch (BDM_SEGMENT_ORDER=0) bit for bit, from workspaces
+    filled with 0xff."""
+    from bdm_amd import ops
+    gen = torch.Generator().manual_seed(77)
+    batch, time, heads, s, v, j, kk = 8, 4096, 8, 8, 128, 256, 8
+    _, ww, wi = routes(batch, time, j, kk, gen)
+    _, rw, ri = routes(batch, time, j, kk, gen)
+    q, k, v_, g, b, w = controllers(batch, time, heads, s, v, gen)
+    state = initial_state(j, heads, s, v, gen, scale=0.05)
+    dev = [t.to(device) for t in (q, k, v_, g, b, w, wi, ww, ri, rw, state)]
+    meta = ops.dispatch_build(dev[6], dev[8], j)
+    ws_bytes = batch * time * kk * heads * v * 2 + batch * j * 4
+
+    def run():
+        ws = torch.full((ws_bytes,), 0xff, device=device, dtype=torch.uint8)
+        final = torch.empty(batch, j, heads, s, v, device=device, dtype=torch.bfloat16)
+        y = ops.routed_forward(*dev[:10], dev[10], meta, bank_count=j, scale=s ** -0.5, routed_decay=True,
+                               round_interval=16, final_state=final, workspace=ws)
+        torch.cuda.synchronize()
+        return y, final, ws
+
+    announce('segment order at C2 size')
+    y_lpt, f_lpt, ws = run()
+    # the order: every segment once, each XCD range in decreasing length
+    order = ws[-batch * j * 4:].view(torch.int32).cpu().long()
+    lengths = (meta.cu_seqlens[1:] - meta.cu_seqlens[:-1]).cpu()
+    rng = batch * j // 8
+    for x in range(8):
+        part = order[x * rng:(x + 1) * rng]
+        assert sorted(part.tolist()) == list(range(x * rng, (x + 1) * rng))
+        assert bool((lengths[part][1:] <= lengths[part][:-1]).all())
+    monkeypatch.setenv('BDM_SEGMENT_ORDER', '0')
+    y_ref, f_ref, _ = run()
+    assert torch.equal(y_lpt, y_ref)
+    assert torch.equal(f_lpt, f_ref)
+
 @pytest.mark.parametrize('policy', ['module', 'prefill'])
 def test_full_size_prefill_c2(device, policy):
     """C2 geometry (B8 T4096 H8 S8 v128 J256 K8): dispatch bit-exact against the
