@@ -36,6 +36,7 @@
 // token_vjp_kernel: the same for shapes outside that kernel's limits.
 #include "bdm_common.h"
 #include "recurrence_ops.h"
+#include "segment_order.h"
 
 namespace bdm {
 namespace {
@@ -62,7 +63,33 @@ struct BackwardParams {
     int init_dtype, snap_dtype, routed_decay, rounding;
     int xcd_remap;
     float scale;
+    // chunk kernel: each XCD range's segments longest first
+    // (segment_order_kernel); null keeps bank order
+    const int *seg_order;
 };
+
+// The (segment, head, column tile) of this block.  In order: segments
+// remapped so each XCD takes a contiguous range, head = y, tile = z.  With
+// p.seg_order: blocks reach the XCDs round-robin in dispatch order (x
+// fastest), and the k-th block of XCD x runs item k of its range, the (head,
+// tile) items of a segment in a row, segments in decreasing length.
+template <typename T>
+__device__ __forceinline__ void block_item(const BackwardParams<T> &p, int &seg, int &head, int &tile) {
+    const int nseg = gridDim.x;
+    if (p.seg_order) {
+        const int64_t linear = (int64_t(blockIdx.z) * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+        const int64_t k = linear / 8;
+        const int per = int(gridDim.y * gridDim.z);
+        seg = p.seg_order[int(linear % 8) * (nseg / 8) + int(k / per)];
+        const int item = int(k % per);
+        head = item / int(gridDim.z);
+        tile = item % int(gridDim.z);
+    } else {
+        seg = p.xcd_remap ? int((blockIdx.x % 8) * (nseg / 8) + blockIdx.x / 8) : int(blockIdx.x);
+        head = blockIdx.y;
+        tile = blockIdx.z;
+    }
+}
 
 __device__ __forceinline__ int64_t uniform64(int64_t x) {
     const int lo = __builtin_amdgcn_readfirstlane(int(uint32_t(uint64_t(x))));
@@ -138,12 +165,10 @@ __global__ __launch_bounds__(64) void routed_backward_kernel(BackwardParams<T> p
     __shared__ float s_weight[C];
     __shared__ int s_read[C];
 
-    const int nseg = gridDim.x;
-    const int seg = p.xcd_remap ? int((blockIdx.x % 8) * (nseg / 8) + blockIdx.x / 8) : int(blockIdx.x);
+    int seg, head, tile;
+    block_item(p, seg, head, tile);
     const int bank = seg % p.banks;
     const int64_t bidx = seg / p.banks;
-    const int head = blockIdx.y;
-    const int tile = blockIdx.z;
     const int lane = threadIdx.x;
     const int col0 = (tile * kLanes + lane) * CPL;
     const int64_t start = p.cu[seg], end = p.cu[seg + 1];
@@ -473,12 +498,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void ch
     __shared__ float s_fold[S];         // product of the chunk's decays per row (lazy chunks) or 1
     __shared__ int s_eager;
 
-    const int nseg = gridDim.x;
-    const int seg = p.xcd_remap ? int((blockIdx.x % 8) * (nseg / 8) + blockIdx.x / 8) : int(blockIdx.x);
+    int seg, head, tile;
+    block_item(p, seg, head, tile);
     const int bank = seg % p.banks;
     const int64_t bidx = seg / p.banks;
-    const int head = blockIdx.y;
-    const int tile = blockIdx.z;
     const int lane = threadIdx.x;
     const int col0 = (tile * kLanes + lane) * CPL;
     const bool live = col0 < p.width;
@@ -1148,6 +1171,7 @@ __global__ __launch_bounds__(256) void token_vjp_kernel(VjpParams<T> p) {
 struct Workspace {
     float *du, *wpart, *rpart;
     int4 *meta;  // per-event meta of the S = 8 chunk kernel (null otherwise)
+    int *seg_order;  // the chunk kernel's segment order (null: bank order)
     size_t bytes;
 };
 
@@ -1189,13 +1213,16 @@ Workspace carve(const bdm_backward_args &a, void *base) {
     const size_t wp = align256(tiles * 3 * nt * a.write_banks * hs * sizeof(float));
     const size_t rp = align256(tiles * nt * a.read_banks * hs * sizeof(float));
     const size_t mt = chunk_path(a) ? align256(nt * size_t(a.write_banks + a.read_banks) * sizeof(int4)) : 0;
+    const int64_t nseg = int64_t(a.batch) * a.bank_count;
+    const size_t so = chunk_path(a) && order_geometry(nseg) ? align256(size_t(nseg) * sizeof(int)) : 0;
     char *c = static_cast<char *>(base);
     Workspace w{};
     w.du = reinterpret_cast<float *>(c);
     w.wpart = reinterpret_cast<float *>(c ? c + du : nullptr);
     w.rpart = reinterpret_cast<float *>(c ? c + du + wp : nullptr);
     w.meta = reinterpret_cast<int4 *>(c && mt ? c + du + wp + rp : nullptr);
-    w.bytes = du + wp + rp + mt;
+    w.seg_order = reinterpret_cast<int *>(c && so && order_enabled() ? c + du + wp + rp + mt : nullptr);
+    w.bytes = du + wp + rp + mt + so;
     return w;
 }
 
@@ -1244,6 +1271,11 @@ int launch_backward(const bdm_backward_args &a, const Workspace &ws, hipStream_t
                                                             ws.meta);
             if (int rc = check_launch("event_meta_kernel")) return rc;
             p.meta = ws.meta;
+            if (ws.seg_order) {
+                launch_segment_order(p.cu, nseg, ws.seg_order, stream);
+                if (int rc = check_launch("segment_order_kernel")) return rc;
+                p.seg_order = ws.seg_order;
+            }
             if (a.snapshot_dtype == BDM_BF16)
                 chunk_backward_kernel<T, bf16_t><<<grid, kLanes, 0, stream>>>(p);
             else

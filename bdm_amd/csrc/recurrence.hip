@@ -31,6 +31,7 @@
 #include "bdm_common.h"
 #include "recurrence_ops.h"
 #include "chunk_forward.h"
+#include "segment_order.h"
 
 namespace bdm {
 namespace {
@@ -916,28 +917,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     }
 }
 
-// Segments of each of the 8 XCD ranges (range = nseg / 8 consecutive
-// segments) in decreasing length, ties by index: order[x * range + rank] =
-// the segment of rank `rank` in range x.  One workgroup per range; a
-// segment's rank counts the longer segments and the equal ones before it.
-constexpr int kOrderMaxRange = 1024;
-__global__ __launch_bounds__(256) void segment_order_kernel(const int64_t *__restrict__ cu, int range,
-                                                            int *__restrict__ order) {
-    __shared__ int s_len[kOrderMaxRange];
-    const int base = int(blockIdx.x) * range;
-    for (int i = threadIdx.x; i < range; i += blockDim.x) s_len[i] = int(cu[base + i + 1] - cu[base + i]);
-    __syncthreads();
-    for (int i = threadIdx.x; i < range; i += blockDim.x) {
-        const int li = s_len[i];
-        int rank = 0;
-        for (int j = 0; j < range; ++j) {
-            const int lj = s_len[j];
-            rank += (lj > li || (lj == li && j < i)) ? 1 : 0;
-        }
-        order[base + rank] = base + i;
-    }
-}
-
 // The piece list: a segment longer than kPieceEvents becomes
 // ceil(len / kPieceEvents) pieces with consecutive piece-state slots.  One
 // workgroup of 1024 threads; thread t handles a contiguous run of segments.
@@ -1289,7 +1268,7 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, const PieceBuffers &pb, h
                 lazy_forward_kernel<T, CPL, 8, 2><<<g2, lthreads, 0, stream>>>(p);
         } else {
             if (pb.seg_order) {
-                segment_order_kernel<<<8, 256, 0, stream>>>(a.cu_seqlens, int(nseg / 8), pb.seg_order);
+                launch_segment_order(a.cu_seqlens, nseg, pb.seg_order, stream);
                 if (int rc = check_launch("segment_order_kernel")) return rc;
                 p.seg_order = pb.seg_order;
             }
@@ -1331,15 +1310,9 @@ int64_t max_pieces(const bdm_forward_args &a) {
 
 // Whether the lazy kernel's MODE 0 takes each XCD range's segments longest
 // first (segment_order_kernel): whole segments (no pieces), ranges that the
-// XCD remap forms, at most kOrderMaxRange segments each.  BDM_SEGMENT_ORDER=0
-// keeps bank order (results are identical either way).
+// XCD remap forms, at most kOrderMaxRange segments each.
 bool order_path(const bdm_forward_args &a) {
-    const int64_t nseg = a.batch * a.bank_count;
-    return lazy_path(a) && max_pieces(a) == 0 && nseg % 8 == 0 && nseg / 8 <= kOrderMaxRange;
-}
-bool order_enabled() {
-    const char *e = getenv("BDM_SEGMENT_ORDER");
-    return !(e && strcmp(e, "0") == 0);
+    return lazy_path(a) && max_pieces(a) == 0 && order_geometry(a.batch * a.bank_count);
 }
 
 // BDM_FORWARD_KERNEL=mfma selects the matrix-core recurrence where it

@@ -1,0 +1,77 @@
+// Longest-first segment order for the recurrence kernels: one workgroup
+// per segment (and head group), blocks reach the 8 XCDs round-robin in
+// dispatch order (x fastest), and a block starts when a slot frees.  Ranking
+// each XCD range's segments by length lets the k-th block of XCD x run item
+// k of its range, long segments in the first rounds and short ones in the
+// last, so the rounds end together instead of in a long tail.
+#pragma once
+
+#include <cstdlib>
+
+#include "bdm_common.h"
+
+namespace bdm {
+namespace {
+
+// Ranges of at most this many segments are ranked (a range's lengths sit in LDS).
+constexpr int kOrderMaxRange = 1024;
+
+// order[x * range + rank] = the segment of rank `rank` in XCD range x (the
+// `range` consecutive segments from x * range), by decreasing length, ties by
+// index: a segment's rank counts the longer segments and the equal ones
+// before it.  Grid (8, ceil(range / 64)) of 256 threads: a workgroup ranks 64
+// segments of its range, each wave against a quarter of the range, the four
+// counts summed in LDS.
+constexpr int kOrderRows = 64;
+__global__ __launch_bounds__(256) void segment_order_kernel(const int64_t *__restrict__ cu, int range,
+                                                            int *__restrict__ order) {
+    // lengths padded to a multiple of 16 with -1 (never longer than or equal
+    // to a real length), read four at a time
+    __shared__ __align__(16) int s_len[kOrderMaxRange];
+    __shared__ int s_rank[kOrderRows];
+    const int base = int(blockIdx.x) * range;
+    const int padded = (range + 15) & ~15;
+    const int t = int(threadIdx.x);
+    for (int i = t; i < padded; i += blockDim.x) s_len[i] = i < range ? int(cu[base + i + 1] - cu[base + i]) : -1;
+    if (t < kOrderRows) s_rank[t] = 0;
+    __syncthreads();
+    const int i = int(blockIdx.y) * kOrderRows + (t % kOrderRows);
+    const int quarter = t / kOrderRows;
+    if (i < range) {
+        const int li = s_len[i];
+        const int j0 = quarter * (padded / 4);
+        const int4 *lens = reinterpret_cast<const int4 *>(s_len + j0);
+        int rank = 0;
+#pragma unroll 4
+        for (int m = 0; m < padded / 16; ++m) {
+            const int4 l = lens[m];
+            const int j = j0 + 4 * m;
+            rank += (l.x > li || (l.x == li && j < i)) ? 1 : 0;
+            rank += (l.y > li || (l.y == li && j + 1 < i)) ? 1 : 0;
+            rank += (l.z > li || (l.z == li && j + 2 < i)) ? 1 : 0;
+            rank += (l.w > li || (l.w == li && j + 3 < i)) ? 1 : 0;
+        }
+        atomicAdd(&s_rank[t % kOrderRows], rank);
+    }
+    __syncthreads();
+    if (quarter == 0 && i < range) order[base + s_rank[t]] = base + i;
+}
+
+// Launch of segment_order_kernel over `nseg` segments (8 ranges).
+inline void launch_segment_order(const int64_t *cu, int64_t nseg, int *order, hipStream_t stream) {
+    const int range = int(nseg / 8);
+    segment_order_kernel<<<dim3(8, unsigned((range + kOrderRows - 1) / kOrderRows)), 256, 0, stream>>>(cu, range,
+                                                                                                       order);
+}
+
+// Whether a launch over `nseg` segments can take the order.
+inline bool order_geometry(int64_t nseg) { return nseg > 0 && nseg % 8 == 0 && nseg / 8 <= kOrderMaxRange; }
+
+// BDM_SEGMENT_ORDER=0 keeps bank order (results are identical either way).
+inline bool order_enabled() {
+    const char *e = getenv("BDM_SEGMENT_ORDER");
+    return !(e && e[0] == '0' && e[1] == 0);
+}
+
+}  // namespace
+}  // namespace bdm

@@ -195,3 +195,33 @@ def test_c5_backward_full_size_truncated_gradient(device):
         rest = torch.cat([grad[:1, t0:].flatten(), grad[1:].flatten()])
         assert float(rest.abs().max()) == 0.0, name
     assert rel_err(leaves[8].grad, st.grad) < 2e-2
+
+
+def test_c5_segment_order_bit_identical(device, monkeypatch):
+    """C5 geometry: the forward and the backward chunk kernel run each XCD's
+    segments longest first; every gradient and the output must equal those of
+    the bank-order launches (BDM_SEGMENT_ORDER=0) bit for bit."""
+    from bdm_amd import bank_training
+    gen = torch.Generator().manual_seed(56)
+    batch, time, heads, s, v, j, kk = 4, 2048, 8, 8, 128, 256, 8
+    _, ww, wi = routes(batch, time, j, kk, gen)
+    _, rw, ri = routes(batch, time, j, kk, gen)
+    q, k, v_, g, b, w = controllers(batch, time, heads, s, v, gen)
+    state = initial_state(j, heads, s, v, gen, scale=0.05)
+    dy = torch.randn(batch, time, heads * v, generator=gen).to(torch.bfloat16).to(device)
+
+    def run():
+        leaves = [t.to(device).requires_grad_(True) for t in (q, k, v_, g, b, w, ww, rw, state)]
+        y = bank_training(*leaves[:6], wi.to(device), leaves[6], ri.to(device), leaves[7], leaves[8], j,
+                          s ** -0.5, state_dtype=torch.bfloat16)
+        (y.float() * dy.float()).sum().backward()
+        torch.cuda.synchronize()
+        return [y.detach()] + [leaf.grad for leaf in leaves]
+
+    announce('C5 segment order')
+    ordered = run()
+    monkeypatch.setenv('BDM_SEGMENT_ORDER', '0')
+    banked = run()
+    names = ('y', 'q', 'k', 'v', 'g', 'b', 'w', 'ww', 'rw', 'state')
+    for name, a, b_ in zip(names, ordered, banked):
+        assert torch.equal(a, b_), name
