@@ -64,26 +64,28 @@ struct BackwardParams {
     int xcd_remap;
     float scale;
     // chunk kernel: each XCD range's segments longest first
-    // (segment_order_kernel); null keeps bank order
+    // (segment_order_kernel), in rounds of order_gpr (head, tile) items;
+    // null keeps bank order
     const int *seg_order;
+    int order_gpr;
 };
 
 // The (segment, head, column tile) of this block.  In order: segments
 // remapped so each XCD takes a contiguous range, head = y, tile = z.  With
 // p.seg_order: blocks reach the XCDs round-robin in dispatch order (x
-// fastest), and the k-th block of XCD x runs item k of its range, the (head,
-// tile) items of a segment in a row, segments in decreasing length.
+// fastest), and the k-th block of XCD x runs item k of its range
+// (order_item): rounds of (head, tile) groups, segments longest first.
 template <typename T>
 __device__ __forceinline__ void block_item(const BackwardParams<T> &p, int &seg, int &head, int &tile) {
     const int nseg = gridDim.x;
     if (p.seg_order) {
         const int64_t linear = (int64_t(blockIdx.z) * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
-        const int64_t k = linear / 8;
-        const int per = int(gridDim.y * gridDim.z);
-        seg = p.seg_order[int(linear % 8) * (nseg / 8) + int(k / per)];
-        const int item = int(k % per);
-        head = item / int(gridDim.z);
-        tile = item % int(gridDim.z);
+        const int range = nseg / 8;
+        int rank, group;
+        order_item(linear / 8, range, int(gridDim.y * gridDim.z), p.order_gpr, rank, group);
+        seg = p.seg_order[int(linear % 8) * range + rank];
+        head = group / int(gridDim.z);
+        tile = group % int(gridDim.z);
     } else {
         seg = p.xcd_remap ? int((blockIdx.x % 8) * (nseg / 8) + blockIdx.x / 8) : int(blockIdx.x);
         head = blockIdx.y;
@@ -1275,6 +1277,10 @@ int launch_backward(const bdm_backward_args &a, const Workspace &ws, hipStream_t
                 launch_segment_order(p.cu, nseg, ws.seg_order, stream);
                 if (int rc = check_launch("segment_order_kernel")) return rc;
                 p.seg_order = ws.seg_order;
+                const void *kernel = a.snapshot_dtype == BDM_BF16
+                                         ? reinterpret_cast<const void *>(&chunk_backward_kernel<T, bf16_t>)
+                                         : reinterpret_cast<const void *>(&chunk_backward_kernel<T, float>);
+                p.order_gpr = order_groups_per_round(kernel, kLanes, nseg, int(grid.y * grid.z));
             }
             if (a.snapshot_dtype == BDM_BF16)
                 chunk_backward_kernel<T, bf16_t><<<grid, kLanes, 0, stream>>>(p);

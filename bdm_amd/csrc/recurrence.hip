@@ -73,8 +73,10 @@ struct ForwardParams {
     float *pstate;         // [slots, H, S, v] FP32: zero-start end state R_q, then start state M_(q+1)
     float *ptrans;         // [slots, H, S, S] FP32: transition P_q of piece q
     // MODE 0 with xcd_remap: the segments of each XCD's range, longest first
-    // (segment_order_kernel); null keeps the range in bank order
+    // (segment_order_kernel), run in rounds of order_gpr head groups; null
+    // keeps the range in bank order
     const int *seg_order;
+    int order_gpr;
 };
 
 // Events per piece when long segments are cut (a multiple of the stage size).
@@ -479,17 +481,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     int group = int(blockIdx.y);  // head group of the block
     const int block = int(blockIdx.x);
     if (MODE == 0 && p.seg_order) {
-        // Longest segments first: workgroups reach the XCDs round-robin in
-        // dispatch order (x fastest), so the k-th block of XCD x takes item k
-        // of that XCD's range, every head group of a segment in a row, the
-        // segments in decreasing length.  Slots that run a long segment in
-        // the first round take a short one in the last, and the rounds end
-        // together instead of in a long tail.
+        // Workgroups reach the XCDs round-robin in dispatch order (x
+        // fastest), so the k-th block of XCD x takes item k of that XCD's
+        // range (order_item): rounds of head groups, segments longest first.
         const int64_t linear = int64_t(blockIdx.y) * gridDim.x + blockIdx.x;
-        const int64_t k = linear / 8;
         const int range = p.nseg / 8;
-        seg = p.seg_order[int(linear % 8) * range + int(k / gridDim.y)];
-        group = int(k % gridDim.y);
+        int rank;
+        order_item(linear / 8, range, int(gridDim.y), p.order_gpr, rank, group);
+        seg = p.seg_order[int(linear % 8) * range + rank];
     } else if (MODE == 0 || (MODE == 1 && block >= p.piece_blocks)) {
         // (piece_blocks is a multiple of 8, so a segment keeps its XCD)
         const int sb = MODE == 1 ? block - p.piece_blocks : block;
@@ -1271,6 +1270,9 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, const PieceBuffers &pb, h
                 launch_segment_order(a.cu_seqlens, nseg, pb.seg_order, stream);
                 if (int rc = check_launch("segment_order_kernel")) return rc;
                 p.seg_order = pb.seg_order;
+                const void *kernel = lazy_hb == 2 ? reinterpret_cast<const void *>(&lazy_forward_kernel<T, CPL, 2, 0>)
+                                                  : reinterpret_cast<const void *>(&lazy_forward_kernel<T, CPL, 8, 0>);
+                p.order_gpr = order_groups_per_round(kernel, lthreads, nseg, int(grid.y));
             }
             if (lazy_hb == 2)
                 lazy_forward_kernel<T, CPL, 2, 0><<<grid, lthreads, 0, stream>>>(p);

@@ -64,6 +64,33 @@ inline void launch_segment_order(const int64_t *cu, int64_t nseg, int *order, hi
                                                                                                        order);
 }
 
+// The item of the k-th block on an XCD: rounds of `gpr` head groups (the
+// groups whose blocks for every segment of the range the XCD's slots hold at
+// once, so a token's write segments share that XCD's L2), each round
+// segment-major over the range in decreasing length.  The slot that the
+// shortest segment of a round frees first takes the longest of the next.
+__device__ __forceinline__ void order_item(int64_t k, int range, int groups, int gpr, int &rank, int &group) {
+    const int64_t per_round = int64_t(range) * gpr;
+    const int round = int(k / per_round);
+    const int in_round = min(gpr, groups - round * gpr);
+    const int w = int(k - round * per_round);
+    rank = w / in_round;
+    group = round * gpr + w % in_round;
+}
+
+// Head groups per round: slots of one XCD (its CUs times the kernel's
+// resident blocks per CU) over the range's segments, in [1, groups].
+inline int order_groups_per_round(const void *kernel, int block_threads, int64_t nseg, int groups) {
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block_threads, 0) != hipSuccess)
+        return 1;
+    const int64_t slots = int64_t(cus / 8) * per_cu;
+    const int64_t gpr = slots / (nseg / 8);
+    return int(gpr < 1 ? 1 : (gpr > groups ? groups : gpr));
+}
+
 // Whether a launch over `nseg` segments can take the order.
 inline bool order_geometry(int64_t nseg) { return nseg > 0 && nseg % 8 == 0 && nseg / 8 <= kOrderMaxRange; }
 
