@@ -743,7 +743,7 @@ def main():
                                '+ final BF16 state', 'state_rounding_interval': ROUND_INTERVAL, 'batch': batch, 'seq_len': time_, 'd_model': cfg.dim,
                    'heads': cfg.num_heads, 'bank_count': j, 'bank_size': cfg.bank_size,
                    'selected_banks': kk, 'head_value_width': cfg.head_value_width},
-        'roofline': {'bound': 'hbm', 'kernel': 'bdm_forward (lazy_forward_kernel + ordered_combine_kernel)',
+        'roofline': {'bound': 'hbm', 'kernel': 'bdm_forward (segment_order_kernel + lazy_forward_kernel + ordered_combine_kernel)',
                      'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBPS, 'unit': 'GB/s',
                      'frac': round(achieved / HBM_PEAK_GBPS, 4),
                      'traffic': traffic.get('bytes_per_launch') if traffic else None,
