@@ -320,6 +320,15 @@ typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
 
 // acc + (the exact FP32 product of the BF16 halves of a and b_masked that
 // b_masked keeps; its other half is zero): v_dot2c_f32_bf16.
+// The same with a zero accumulator, as the VOP3P v_dot2_f32_bf16 with the
+// inline constant 0: the builtin with acc = 0 is selected as v_dot2c_f32_bf16,
+// whose accumulator is its destination, and costs a v_mov of zero first.
+__device__ __forceinline__ float dot_half(uint32_t a, uint32_t b_masked) {
+    float r;
+    asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b_masked));
+    return r;
+}
+
 __device__ __forceinline__ float dot_half_acc(float acc, uint32_t a, uint32_t b_masked) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v_t, a), __builtin_bit_cast(bf16x2v_t, b_masked),
                                            acc, false);
@@ -349,15 +358,15 @@ struct GatedValues<bf16_t, CPL> {
     // lo[i] = (bf(w[2i] pw), 0), hi[i] = (0, bf(w[2i+1] pw))
     uint32_t lo[CPL / 2], hi[CPL / 2];
     uint32_t v[CPL / 2];
-    // pw is a BF16 value (the route weight): w * pw is an exact FP32 product,
-    // formed by v_dot2c_f32_bf16 from the packed w pair and (pw, 0) or (0, pw)
+    // pw is a BF16 value (the route weight) widened to FP32, so its low 16
+    // bits are zero: w * pw is an exact FP32 product, formed by
+    // v_dot2_f32_bf16 from the packed w pair and (pw, 0) or (0, pw)
     __device__ __forceinline__ void make(const RawCols<bf16_t, CPL> &w, const RawCols<bf16_t, CPL> &vv, float pw) {
-        const uint32_t pb = __float_as_uint(pw) >> 16;
-        const uint32_t p_lo = pb, p_hi = pb << 16;
+        const uint32_t p_hi = __float_as_uint(pw), p_lo = p_hi >> 16;
 #pragma unroll
         for (int i = 0; i < CPL / 2; ++i) {
-            const float e0 = dot_half_acc(0.f, w.u[i], p_lo);
-            const float e1 = dot_half_acc(0.f, w.u[i], p_hi);
+            const float e0 = dot_half(w.u[i], p_lo);
+            const float e1 = dot_half(w.u[i], p_hi);
             lo[i] = pack_bf16x2(e0, 0.f);
             hi[i] = pack_bf16x2(0.f, e1);
             v[i] = vv.u[i];
@@ -465,6 +474,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     __shared__ int s_tok[3][NE];
     __shared__ int s_route[3][NE];
     __shared__ int s_wpos[3][NE + 1];  // stage positions of the writes, then n
+    __shared__ int s_wtok[3][NE];      // tokens of the writes, in write order
     __shared__ int s_nw[3];
     __shared__ int s_n[3];
     __shared__ unsigned s_rmask[3];    // bit e: event e of the stage is a read
@@ -589,7 +599,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
             s_tok[slot][tid] = p.k_shift >= 0 ? int(uint32_t(route) >> p.k_shift)
                                               : int(uint32_t(route) / uint32_t(rd ? p.kr : p.kw));
             s_route[slot][tid] = route;
-            if (live && !rd) s_wpos[slot][__popcll(write_mask & ((uint64_t(1) << tid) - 1))] = tid;
+            if (live && !rd) {
+                const int wk = __popcll(write_mask & ((uint64_t(1) << tid) - 1));
+                s_wpos[slot][wk] = tid;
+                s_wtok[slot][wk] = s_tok[slot][tid];
+            }
         }
         if (tid == 0) {
             const int n = __popcll(live_mask), nw = __popcll(write_mask);
@@ -728,8 +742,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     // into the set write k-1 does not use, so no registers are copied.  At a
     // stage start the stage's first write is in set A.
     RawCols<T, CPL> va, wa, vb, wb;
-    auto fetch = [&](int slot, int e, RawCols<T, CPL> &vv, RawCols<T, CPL> &ww) {
-        const int64_t row = int64_t(__builtin_amdgcn_readfirstlane(s_tok[slot][e])) * hw;
+    // v, w rows of write wk of a stage (its token from s_wtok: one LDS read)
+    auto fetch = [&](int slot, int wk, RawCols<T, CPL> &vv, RawCols<T, CPL> &ww) {
+        const int64_t row = int64_t(__builtin_amdgcn_readfirstlane(s_wtok[slot][wk])) * hw;
         vv.load(reinterpret_cast<const T *>(reinterpret_cast<const char *>(p.v + row) + lane_bytes));
         ww.load(reinterpret_cast<const T *>(reinterpret_cast<const char *>(p.w + row) + lane_bytes));
     };
@@ -842,7 +857,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         {
             if (nw > 0) {
                 if (!prefetched) {
-                    fetch(slot, __builtin_amdgcn_readfirstlane(s_wpos[slot][0]), va, wa);
+                    fetch(slot, 0, va, wa);
                 } else if (in_b) {
                     va = vb;
                     wa = wb;
@@ -863,7 +878,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
                     fe = 0;
                     prefetched = true;
                 }
-                fetch(fs, __builtin_amdgcn_readfirstlane(s_wpos[fs][fe]), vv, ww);
+                fetch(fs, fe, vv, ww);
             };
             int i = 0;
 #pragma unroll 1
