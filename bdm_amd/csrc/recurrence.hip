@@ -481,7 +481,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     // Row operands of the current stage (written by the prep of a stage after
     // every wave has left the previous stage's value loop): lazy [0] = -alpha,
     // [1] = beta; eager [0] = -a, [1] = k, [2] = d; a read [0] = gamma.
-    __shared__ float s_rows[NE][HB][3][S];
+    __shared__ __align__(16) float s_rows[NE][HB][3][S];
     __shared__ float s_fold[HB][S];  // s at the end of the stage (1 for eager)
     __shared__ float s_pw[NE];               // route weight of each event of the stage
     __shared__ int s_eager;
@@ -647,19 +647,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         const bool live = prep_head && pe < n && stage < nstages;
         const bool rd = live && ((s_rmask[slot] >> pe) & 1u);
         const float pw = live ? pl.weight_f() : 0.f;
+        // Branch-free over the stage's mix of reads and writes (both kinds
+        // share a wave): each case performs the same operations as its own
+        // formula, the others are computed and discarded.
+        //   write: d = exp(g p) (or exp(g)), k, a = bf(b p) k
+        //   read:  d = 1, gamma = scale bf(q p) (the key slot holds q)
+        const bool wr = live && !rd;
         float d[4], kk[4], a[4], sc[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            if (live && !rd) {
-                const float g = (&pl.gate.x)[r];
-                d[r] = __expf(p.routed_decay ? g * pw : g);
-                kk[r] = pl.key_at(r);
-                a[r] = round_to<T>(pl.erase_at(r) * pw) * kk[r];
-            } else {
-                d[r] = 1.f;
-                kk[r] = live ? p.scale * round_to<T>(pl.key_at(r) * pw) : 0.f;  // gamma for a read
-                a[r] = 0.f;
-            }
+            const float key = pl.key_at(r);
+            const float g = (&pl.gate.x)[r];
+            const float e = __expf(p.routed_decay ? g * pw : g);
+            const float xr = round_to<T>((rd ? key : pl.erase_at(r)) * pw);
+            const float prod = xr * (rd ? p.scale : key);  // gamma = bf(q p) scale; a = bf(b p) k
+            d[r] = wr ? e : 1.f;
+            kk[r] = wr ? key : (live ? prod : 0.f);
+            a[r] = wr ? prod : 0.f;
             sc[r] = row_prefix_product(d[r]);
         }
         bool low = false;
@@ -669,21 +673,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         __syncthreads();  // also: every wave has left the previous value loop
         const bool eager = s_flag[stage & 1] != 0;
         if (live) {
-            float(*row)[S] = s_rows[pe][ph];
+            // read: [0] = gamma (lazy: gamma s); lazy write: [0] = -(a s'),
+            // [1] = k / s' (v_rcp_f32); eager write: [0] = -a, [1] = k, [2] = d.
+            // All three rows are stored for every event (a read uses [0] only;
+            // [2] is read in eager stages only).
+            float4 *row = reinterpret_cast<float4 *>(&s_rows[pe][ph][0][4 * half]);
+            float r0[4], r1[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int rr = 4 * half + r;
-                if (rd) {
-                    row[0][rr] = eager ? kk[r] : kk[r] * sc[r];
-                } else if (!eager) {
-                    row[0][rr] = -(a[r] * sc[r]);
-                    row[1][rr] = kk[r] * __builtin_amdgcn_rcpf(sc[r]);  // k / s' (v_rcp_f32)
-                } else {
-                    row[0][rr] = -a[r];
-                    row[1][rr] = kk[r];
-                    row[2][rr] = d[r];
-                }
+                const float t = eager ? (rd ? kk[r] : a[r]) : (rd ? kk[r] : a[r]) * sc[r];
+                r0[r] = rd ? t : -t;
+                r1[r] = eager ? kk[r] : kk[r] * __builtin_amdgcn_rcpf(sc[r]);
             }
+            row[0] = make_float4(r0[0], r0[1], r0[2], r0[3]);
+            row[S / 4] = make_float4(r1[0], r1[1], r1[2], r1[3]);
+            row[2 * S / 4] = make_float4(d[0], d[1], d[2], d[3]);
             if (tid < NE) s_pw[pe] = pw;
             if (pe == n - 1) {
 #pragma unroll
@@ -761,10 +765,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         // stage) is a rounding/snapshot point when the offset is > 0.
         if (st > 0) {
             if (rounding) {
+                // two values per v_cvt_pk_bf16_f32
 #pragma unroll
                 for (int r = 0; r < S; ++r)
 #pragma unroll
-                    for (int c = 0; c < CPL; ++c) h[r][c] = round_bf16(h[r][c]);
+                    for (int c = 0; c < CPL; c += 2) round_pair<bf16_t>(h[r][c], h[r][c + 1]);
             }
             // snapshot of the state before event `base` (see routed_forward_kernel)
             if (void *snap = lds_ptr(P_SNAP)) {
