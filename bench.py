@@ -570,6 +570,42 @@ def c2_forward_only(layer, device, batch, time_, launches):
             'recurrence': os.environ.get('BDM_FORWARD_KERNEL', 'vector'), 'copy_probe_bytes': 2 * src.numel() * 2}
 
 
+def graph_step(step, final, steps, tokens):
+    """The same hot-path step captured in one HIP graph (torch.cuda.graph) and
+    replayed: the kernels' launch gaps without the host.  Replays, with eager
+    steps between them, must equal the eager step's y and final state."""
+    import torch
+    with torch.no_grad():
+        y_eager = step().clone()
+        torch.cuda.synchronize()
+        f_eager = final.clone()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                step()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            y_graph = step()
+        equal = True
+        for _ in range(3):
+            final.zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            equal = equal and torch.equal(y_graph, y_eager) and torch.equal(final, f_eager)
+            step()
+            torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            graph.replay()
+        torch.cuda.synchronize()
+        sec = (time.perf_counter() - t0) / steps
+    return {'ms_per_step': round(sec * 1e3, 4), 'tokens_per_s': round(tokens / sec, 1),
+            'replays_equal_eager': bool(equal)}
+
+
 def c1_config():
     """BASELINE configs[0] (the reference's CPU-runnable case): d_model 512, H4 of
     v = 64, J256 = 16x16, S8, K8, FP32 weights, FP32 training state."""
@@ -690,24 +726,28 @@ def main():
                         device=device, dtype=torch.bfloat16)
     j, kk, scale = cfg.bank_count, cfg.selected_banks, cfg.bank_size ** -0.5
     stream = torch.cuda.current_stream(device)
-    ev_start = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    ev_stop = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    # Timing events are recorded in a profiling pass after the timed steps: a
+    # timestamp event drains the stream before the next kernel starts, and five
+    # of them per step cost ~20 us of overlap between kernels.
+    prof_steps = min(args.steps, 10)
+    ev_front = [torch.cuda.Event(enable_timing=True) for _ in range(prof_steps)]
+    ev_start = [torch.cuda.Event(enable_timing=True) for _ in range(prof_steps)]
+    ev_stop = [torch.cuda.Event(enable_timing=True) for _ in range(prof_steps)]
     # recorded by bdm_forward itself: before the recurrence, before the combine, after it
-    ev_phase = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
-    record = {'on': False, 'i': 0}
+    ev_phase = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(prof_steps)]
 
-    def step():
+    def step(rec=None):
+        if rec is not None:
+            ev_front[rec].record(stream)
         (ww, wi), (rw, ri) = ops.router_select_pair(write_scores, read_scores, bank_count=j, selected_banks=kk)
         meta = ops.dispatch_build(wi, ri, j)
-        if record['on']:
-            ev_start[record['i']].record(stream)
-        phases = ev_phase[record['i']] if record['on'] else None
+        if rec is not None:
+            ev_start[rec].record(stream)
         y = ops.routed_forward(q, k, v, g, b, w, wi, ww, ri, rw, initial, meta, bank_count=j, scale=scale,
                                routed_decay=True, round_interval=ROUND_INTERVAL, final_state=final,
-                               phase_events=phases)
-        if record['on']:
-            ev_stop[record['i']].record(stream)
-            record['i'] += 1
+                               phase_events=ev_phase[rec] if rec is not None else None)
+        if rec is not None:
+            ev_stop[rec].record(stream)
         return y
 
     progress('hot path', batch, time_)
@@ -715,16 +755,19 @@ def main():
         for _ in range(args.warmup):
             step()
         torch.cuda.synchronize()
-        record['on'] = True
         t0 = time.perf_counter()
         for _ in range(args.steps):
             step()
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t0
-        record['on'] = False
+        progress('hot path profiling pass', prof_steps)
+        for i in range(prof_steps):
+            step(i)
+        torch.cuda.synchronize()
     sec = elapsed / args.steps
     tokens = batch * time_
     fwd_ms = statistics.mean(a.elapsed_time(bb) for a, bb in zip(ev_start, ev_stop))
+    front_ms = statistics.mean(a.elapsed_time(bb) for a, bb in zip(ev_front, ev_start))
     rec_ms = statistics.mean(e[0].elapsed_time(e[1]) for e in ev_phase)
     comb_ms = statistics.mean(e[1].elapsed_time(e[2]) for e in ev_phase)
     fwd_bytes = forward_algorithmic_bytes(cfg, batch, time_, initial.numel() * initial.element_size())
@@ -754,8 +797,12 @@ def main():
         'hot_path_roofline_frac': round(hot_bytes / sec / 1e9 / HBM_PEAK_GBPS, 4),
         'recurrence': recurrence_roofline(cfg, batch, time_, rec_ms),
         'combine': combine_roofline(cfg, batch, time_, comb_ms),
-        'front_end_ms': round(sec * 1e3 - fwd_ms, 4),
+        'front_end_ms': round(front_ms, 4),
+        'timing': ('ms_per_step: wall clock over the timed steps, no events inside; launch_ms, recurrence, '
+                   f'combine and front_end_ms: events of {prof_steps} further steps'),
     }
+    progress('hot path from one HIP graph')
+    result['hip_graph'] = graph_step(step, final, args.steps, tokens)
     if not args.no_extras:
         progress('full layer prefill')
         result['full_layer_prefill_tokens_per_s'] = full_layer_prefill(layer, device, batch, time_,
