@@ -487,26 +487,58 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     __shared__ int s_eager;
     __shared__ int s_flag[2];  // by stage parity: reset two barriers before its next use
 
-    int seg, piece = 0, pieces = 1, pslot = -1;
+    int seg = 0, piece = 0, pieces = 1, pslot = -1;
     int group = int(blockIdx.y);  // head group of the block
-    const int block = int(blockIdx.x);
-    if (MODE == 0 && p.seg_order) {
-        // Workgroups reach the XCDs round-robin in dispatch order (x
-        // fastest), so the k-th block of XCD x takes item k of that XCD's
-        // range (order_item): rounds of head groups, segments longest first.
-        const int64_t linear = int64_t(blockIdx.y) * gridDim.x + blockIdx.x;
+    int block = int(blockIdx.x);  // MODE 1, 2: the piece item
+    bool is_piece = MODE == 2;
+    // Blocks reach the XCDs round-robin in dispatch order (x fastest).  With
+    // p.seg_order the k-th segment block of XCD x takes item k of that XCD's
+    // range: rounds of head groups (order_item), segments longest first.
+    auto ordered_segment = [&](int64_t k, int gpr) {
         const int range = p.nseg / 8;
         int rank;
-        order_item(linear / 8, range, int(gridDim.y), p.order_gpr, rank, group);
-        seg = p.seg_order[int(linear % 8) * range + rank];
-    } else if (MODE == 0 || (MODE == 1 && block >= p.piece_blocks)) {
-        // (piece_blocks is a multiple of 8, so a segment keeps its XCD)
-        const int sb = MODE == 1 ? block - p.piece_blocks : block;
-        seg = p.xcd_remap ? int((sb % 8) * (p.nseg / 8) + sb / 8) : sb;
-        // a cut segment runs as its pieces (the whole workgroup leaves together)
-        if (MODE == 1 && p.cu[seg + 1] - p.cu[seg] > kPieceEvents) return;
-    } else {
-        // pieces take the first blocks; the grid is an upper bound on them
+        order_item(k / 8, range, int(gridDim.y), gpr, rank, group);
+        return p.seg_order[int(k % 8) * range + rank];
+    };
+    if constexpr (MODE == 0) {
+        if (p.seg_order) {
+            seg = ordered_segment(int64_t(blockIdx.y) * gridDim.x + blockIdx.x, p.order_gpr);
+        } else {
+            seg = p.xcd_remap ? int((block % 8) * (p.nseg / 8) + block / 8) : block;
+        }
+    } else if constexpr (MODE == 1) {
+        // Every head group's pieces first, then the segments: dispatched row
+        // by row, the later groups' pieces would wait behind the first
+        // group's thousands of short segments; the segments longest first
+        // (the cut ones, which leave at once, then the longest uncut), so no
+        // long segment starts last.  piece_blocks is a multiple of 8, so the
+        // segment part starts on XCD 0.
+        const int groups = int(gridDim.y);
+        const int64_t linear = int64_t(blockIdx.y) * gridDim.x + blockIdx.x;
+        const int64_t piece_part = int64_t(p.piece_blocks) * groups;
+        if (linear < piece_part) {
+            block = int(linear / groups);
+            group = int(linear % groups);
+            is_piece = true;
+        } else {
+            const int64_t k = linear - piece_part;
+            if (p.seg_order) {
+                seg = ordered_segment(k, groups);
+            } else if (p.xcd_remap) {
+                const int64_t k8 = k / 8;
+                group = int(k8 % groups);
+                const int sb = int((k8 / groups) * 8 + k % 8);
+                seg = (sb % 8) * (p.nseg / 8) + sb / 8;
+            } else {
+                group = int(k % groups);
+                seg = int(k / groups);
+            }
+            // a cut segment runs as its pieces (the whole workgroup leaves together)
+            if (p.cu[seg + 1] - p.cu[seg] > kPieceEvents) return;
+        }
+    }
+    if (is_piece) {
+        // the grid is an upper bound on the pieces
         if (block >= p.n_items[0]) return;
         const int4 it = p.items[block];
         seg = it.x;
@@ -1267,6 +1299,11 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, const PieceBuffers &pb, h
             p.ptrans = pb.ptrans;
             piece_table_kernel<<<1, 1024, 0, stream>>>(a.cu_seqlens, int(nseg), pb.items, pb.count);
             if (int rc = check_launch("piece_table_kernel")) return rc;
+            if (pb.seg_order) {
+                launch_segment_order(a.cu_seqlens, nseg, pb.seg_order, stream);
+                if (int rc = check_launch("segment_order_kernel")) return rc;
+                p.seg_order = pb.seg_order;
+            }
             // MODE 1: the pieces (in the first blocks, so the long ones start
             // first), then the uncut segments in the slots they leave free
             p.piece_blocks = int((pb.max_pieces + 7) / 8 * 8);
@@ -1330,12 +1367,10 @@ int64_t max_pieces(const bdm_forward_args &a) {
     return 2 * (events / kPieceEvents) + 1;
 }
 
-// Whether the lazy kernel's MODE 0 takes each XCD range's segments longest
-// first (segment_order_kernel): whole segments (no pieces), ranges that the
-// XCD remap forms, at most kOrderMaxRange segments each.
-bool order_path(const bdm_forward_args &a) {
-    return lazy_path(a) && max_pieces(a) == 0 && order_geometry(a.batch * a.bank_count);
-}
+// Whether the lazy kernel takes each XCD range's segments longest first
+// (segment_order_kernel; MODE 0, and MODE 1's segment blocks): ranges that
+// the XCD remap forms, at most kOrderMaxRange segments each.
+bool order_path(const bdm_forward_args &a) { return lazy_path(a) && order_geometry(a.batch * a.bank_count); }
 
 // BDM_FORWARD_KERNEL=mfma selects the matrix-core recurrence where it
 // applies; the vector-ALU kernel is the default (both are complete
