@@ -527,6 +527,43 @@ def test_segment_order_bit_identical(device, monkeypatch):
     assert torch.equal(y_lpt, y_ref)
     assert torch.equal(f_lpt, f_ref)
 
+def test_cut_segment_order_bit_identical(device, monkeypatch):
+    """Prefill policy with skewed routes (long segments cut into pieces, many
+    short uncut ones): MODE 1 runs every head group's pieces first and the
+    segments longest first.  y and the final state must equal those of the
+    bank-order launch (BDM_SEGMENT_ORDER=0) bit for bit."""
+    from bdm_amd import ops
+    gen = torch.Generator().manual_seed(92)
+    batch, time, heads, s, v, j, kk = 2, 2048, 4, 8, 128, 64, 8
+    _, ww, wi = routes(batch, time, j, kk, gen)
+    _, rw, ri = routes(batch, time, j, kk, gen)
+    for t in (wi, ri):  # half the tokens route slot 0 to one of banks 0..3 (banks stay distinct per token)
+        hot = torch.rand(batch, time, generator=gen) < 0.5
+        bank = torch.randint(0, 4, (batch, time), generator=gen)
+        present = (t == bank[..., None]).any(-1)
+        t[..., 0] = torch.where(hot & ~present, bank, t[..., 0])
+    q, k, v_, g, b, w = controllers(batch, time, heads, s, v, gen)
+    state = initial_state(j, heads, s, v, gen, scale=0.05)
+    dev = [x.to(device) for x in (q, k, v_, g, b, w, wi, ww, ri, rw, state)]
+    meta = ops.dispatch_build(dev[6], dev[8], j)
+    lengths = (meta.cu_seqlens[1:] - meta.cu_seqlens[:-1]).cpu()
+    assert int((lengths > 512).sum()) >= 8 and int((lengths <= 512).sum()) >= 64
+
+    def run():
+        final = torch.empty(batch, j, heads, s, v, device=device, dtype=torch.float32)
+        y = ops.routed_forward(*dev[:10], dev[10], meta, bank_count=j, scale=s ** -0.5, routed_decay=True,
+                               round_interval=0, final_state=final)
+        torch.cuda.synchronize()
+        return y, final
+
+    announce('cut-segment order')
+    y_o, f_o = run()
+    monkeypatch.setenv('BDM_SEGMENT_ORDER', '0')
+    y_b, f_b = run()
+    assert torch.equal(y_o, y_b)
+    assert torch.equal(f_o, f_b)
+
+
 @pytest.mark.parametrize('policy', ['module', 'prefill'])
 def test_full_size_prefill_c2(device, policy):
     """C2 geometry (B8 T4096 H8 S8 v128 J256 K8): dispatch bit-exact against the
