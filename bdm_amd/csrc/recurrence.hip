@@ -978,6 +978,8 @@ __global__ __launch_bounds__(1024) void piece_table_kernel(const int64_t *__rest
     const int per = (nseg + 1023) / 1024;
     const int s0 = min(nseg, t * per), s1 = min(nseg, s0 + per);
     int cut = 0;
+    // (unrolled: the loads of a thread's segments are independent and go out together)
+#pragma unroll 8
     for (int sg = s0; sg < s1; ++sg) {
         const int64_t len = cu[sg + 1] - cu[sg];
         if (len > kPieceEvents) cut += int((len + kPieceEvents - 1) / kPieceEvents);
@@ -992,6 +994,7 @@ __global__ __launch_bounds__(1024) void piece_table_kernel(const int64_t *__rest
         __syncthreads();
     }
     int pos = s_cut[t] - cut;
+#pragma unroll 8
     for (int sg = s0; sg < s1; ++sg) {
         const int64_t len = cu[sg + 1] - cu[sg];
         if (len > kPieceEvents) {

@@ -19,12 +19,14 @@ constexpr int kOrderMaxRange = 1024;
 // order[x * range + rank] = the segment of rank `rank` in XCD range x (the
 // `range` consecutive segments from x * range), by decreasing length, ties by
 // index: a segment's rank counts the longer segments and the equal ones
-// before it.  Grid (8, ceil(range / 64)) of 256 threads: a workgroup ranks 64
-// segments of its range, each wave against a quarter of the range, the four
-// counts summed in LDS.
-constexpr int kOrderRows = 64;
+// before it.  Grid (8, ceil(range / 16)) of 256 threads: a workgroup ranks 16
+// segments of its range, each against 16 slices of the range (one thread per
+// segment and slice), the 16 counts summed in LDS.
+constexpr int kOrderRows = 16;
+constexpr int kOrderParts = 256 / kOrderRows;
 __global__ __launch_bounds__(256) void segment_order_kernel(const int64_t *__restrict__ cu, int range,
                                                             int *__restrict__ order) {
+    // (launched with 256 threads per workgroup)
     // lengths padded to a multiple of 16 with -1 (never longer than or equal
     // to a real length), read four at a time
     __shared__ __align__(16) int s_len[kOrderMaxRange];
@@ -32,18 +34,27 @@ __global__ __launch_bounds__(256) void segment_order_kernel(const int64_t *__res
     const int base = int(blockIdx.x) * range;
     const int padded = (range + 15) & ~15;
     const int t = int(threadIdx.x);
-    for (int i = t; i < padded; i += blockDim.x) s_len[i] = i < range ? int(cu[base + i + 1] - cu[base + i]) : -1;
+    // (all of a thread's loads in flight together: at most kOrderMaxRange / 256 per thread)
+#pragma unroll
+    for (int n = 0; n < kOrderMaxRange / 256; ++n) {
+        const int i = t + n * 256;
+        if (i < padded) s_len[i] = i < range ? int(cu[base + i + 1] - cu[base + i]) : -1;
+    }
     if (t < kOrderRows) s_rank[t] = 0;
     __syncthreads();
     const int i = int(blockIdx.y) * kOrderRows + (t % kOrderRows);
-    const int quarter = t / kOrderRows;
+    const int part = t / kOrderRows;
     if (i < range) {
         const int li = s_len[i];
-        const int j0 = quarter * (padded / 4);
+        // slice `part`: groups [part * per, (part + 1) * per) of four
+        // lengths, the last slices short or empty
+        const int per = (padded / 4 + kOrderParts - 1) / kOrderParts;
+        const int g0 = part * per, g1 = min(padded / 4, g0 + per);
+        const int j0 = 4 * g0;
         const int4 *lens = reinterpret_cast<const int4 *>(s_len + j0);
         int rank = 0;
 #pragma unroll 4
-        for (int m = 0; m < padded / 16; ++m) {
+        for (int m = 0; m < g1 - g0; ++m) {
             const int4 l = lens[m];
             const int j = j0 + 4 * m;
             rank += (l.x > li || (l.x == li && j < i)) ? 1 : 0;
@@ -54,7 +65,7 @@ __global__ __launch_bounds__(256) void segment_order_kernel(const int64_t *__res
         atomicAdd(&s_rank[t % kOrderRows], rank);
     }
     __syncthreads();
-    if (quarter == 0 && i < range) order[base + s_rank[t]] = base + i;
+    if (part == 0 && i < range) order[base + s_rank[t]] = base + i;
 }
 
 // Launch of segment_order_kernel over `nseg` segments (8 ranges).
