@@ -643,7 +643,7 @@ def cpu_threads():
 
 
 def cpu_baseline():
-    """BASELINE.md's CPU plan: the reference backend='reference' forward at C1
+    """The reference's CPU path timed at C1: the backend='reference' forward
     (oracle/bdm_oracle.py OracleBankedDeltaMemory.forward, the per-event loop
     of reference_packed_gdn2 and index_add_), under no_grad, 1 warmup and 5
     timed runs, the median; tokens/s = 512 / median."""
