@@ -984,16 +984,30 @@ __global__ __launch_bounds__(1024) void piece_table_kernel(const int64_t *__rest
         const int64_t len = cu[sg + 1] - cu[sg];
         if (len > kPieceEvents) cut += int((len + kPieceEvents - 1) / kPieceEvents);
     }
-    s_cut[t] = cut;
-    __syncthreads();
-    // inclusive scan (Hillis-Steele over 1024 entries)
-    for (int off = 1; off < 1024; off <<= 1) {
-        const int a = t >= off ? s_cut[t - off] : 0;
-        __syncthreads();
-        s_cut[t] += a;
-        __syncthreads();
+    // inclusive scan: within each wave by shuffles, then over the 16 wave
+    // totals by the first wave
+    const int lane = t % kWave, wave = t / kWave;
+    int incl = cut;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const int up = __shfl_up(incl, off, kWave);
+        if (lane >= off) incl += up;
     }
-    int pos = s_cut[t] - cut;
+    if (lane == kWave - 1) s_cut[wave] = incl;
+    __syncthreads();
+    if (wave == 0) {
+        const int total = lane < 1024 / kWave ? s_cut[lane] : 0;
+        int w = total;
+#pragma unroll
+        for (int off = 1; off < 1024 / kWave; off <<= 1) {
+            const int up = __shfl_up(w, off, kWave);
+            if (lane >= off) w += up;
+        }
+        if (lane < 1024 / kWave) s_cut[64 + lane] = w - total;  // exclusive prefix of the waves
+        if (lane == 1024 / kWave - 1) s_cut[128] = w;           // all pieces
+    }
+    __syncthreads();
+    int pos = s_cut[64 + wave] + incl - cut;
 #pragma unroll 8
     for (int sg = s0; sg < s1; ++sg) {
         const int64_t len = cu[sg + 1] - cu[sg];
@@ -1002,7 +1016,7 @@ __global__ __launch_bounds__(1024) void piece_table_kernel(const int64_t *__rest
             for (int q = 0; q < np; ++q, ++pos) items[pos] = make_int4(sg, q, np, pos);
         }
     }
-    if (t == 0) n_items[0] = s_cut[1023];
+    if (t == 0) n_items[0] = s_cut[128];
 }
 
 // For each cut segment (its first piece's item) and head: M_0 = the
