@@ -7,6 +7,7 @@
 #pragma once
 
 #include <cstdlib>
+#include <mutex>
 
 #include "bdm_common.h"
 
@@ -89,15 +90,38 @@ __device__ __forceinline__ void order_item(int64_t k, int range, int groups, int
     group = round * gpr + w % in_round;
 }
 
-// Head groups per round: slots of one XCD (its CUs times the kernel's
-// resident blocks per CU) over the range's segments, in [1, groups].
-inline int order_groups_per_round(const void *kernel, int block_threads, int64_t nseg, int groups) {
-    int dev = 0, cus = 0, per_cu = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+// Blocks of `kernel` (block_threads each) that one XCD holds at once: its
+// CUs times the resident blocks per CU.  The occupancy query costs ~10 us of
+// host time, on the path between two launches, so each (kernel, threads,
+// device) is asked once; 0 if the runtime cannot tell.
+inline int64_t xcd_slots(const void *kernel, int block_threads) {
+    struct Entry {
+        const void *kernel;
+        int threads, dev, slots;
+    };
+    static std::mutex mu;
+    static Entry cache[64];
+    static int used = 0;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    std::lock_guard<std::mutex> lock(mu);
+    for (int i = 0; i < used; ++i)
+        if (cache[i].kernel == kernel && cache[i].threads == block_threads && cache[i].dev == dev)
+            return cache[i].slots;
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block_threads, 0) != hipSuccess)
-        return 1;
-    const int64_t slots = int64_t(cus / 8) * per_cu;
+        return 0;
+    const int slots = (cus / 8) * per_cu;
+    if (used < 64) cache[used++] = Entry{kernel, block_threads, dev, slots};
+    return slots;
+}
+
+// Head groups per round: slots of one XCD over the range's segments, in
+// [1, groups].
+inline int order_groups_per_round(const void *kernel, int block_threads, int64_t nseg, int groups) {
+    const int64_t slots = xcd_slots(kernel, block_threads);
+    if (slots <= 0) return 1;
     const int64_t gpr = slots / (nseg / 8);
     return int(gpr < 1 ? 1 : (gpr > groups ? groups : gpr));
 }
