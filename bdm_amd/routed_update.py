@@ -11,6 +11,8 @@ layout (q [B,T,H,S], state [J,H,S,v]) that runs every head on one dispatch.
 
 from __future__ import annotations
 
+import dataclasses
+
 import torch
 
 from . import ops
@@ -62,7 +64,14 @@ class RoutedUpdate(torch.autograd.Function):
                                  scale=scale, routed_decay=routed_decay, round_interval=interval,
                                  snapshots=snapshots, snapshot_interval=snap_interval, prepared=x)
         if wants_grad:
-            ctx.save_for_backward(q, k, v, g, b, w, wi, ww, ri, rw, state, meta.order, meta.cu_seqlens, snapshots)
+            # the validated operands themselves, so the backward needs no second
+            # pass of checks and copies; the callers' shapes and dtypes for the
+            # gradients
+            ctx.save_for_backward(x.q, x.k, x.g, x.b, x.v, x.w, x.ww, x.rw, x.ri, x.initial, meta.order,
+                                  meta.cu_seqlens, snapshots)
+            ctx.geometry = {f.name: getattr(x, f.name) for f in dataclasses.fields(x)
+                            if not isinstance(getattr(x, f.name), torch.Tensor)}
+            ctx.likes = [(t.shape, t.dtype) for t in (q, k, v, g, b, w, ww, rw, state)]
             ctx.options = (bank_count, scale, routed_decay, interval, snap_interval)
         if q.ndim == 3:
             raw = raw.view(q.shape[0], q.shape[1], v.shape[-1])
@@ -70,23 +79,26 @@ class RoutedUpdate(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_output):
-        q, k, v, g, b, w, wi, ww, ri, rw, state, order, cu, snapshots = ctx.saved_tensors
+        xq, xk, xg, xb, xv, xw, xww, xrw, xri, xinit, order, cu, snapshots = ctx.saved_tensors
         bank_count, scale, routed_decay, interval, snap_interval = ctx.options
         meta = ops.Dispatch(order, None, None, cu, None)
-        x = ops.prepare_routed(q, k, v, g, b, w, wi, ww, ri, rw, state, bank_count=bank_count)
+        x = ops.RoutedInputs(q=xq, k=xk, g=xg, b=xb, v=xv, w=xw, ww=xww, rw=xrw, ri=xri, initial=xinit,
+                             **ctx.geometry)
         grads = ops.routed_backward(x, meta, grad_output.contiguous(), snapshots, bank_count=bank_count,
                                     scale=scale, routed_decay=routed_decay, round_interval=interval,
                                     snapshot_interval=snap_interval)
-        shape = lambda t, like: t.reshape(like.shape).to(like.dtype)  # noqa: E731
-        dq, dk, dv, dg, db, dw = (shape(t, like) for t, like in ((grads.q, q), (grads.k, k), (grads.v, v),
-                                                                  (grads.g, g), (grads.b, b), (grads.w, w)))
+        (q_like, k_like, v_like, g_like, b_like, w_like, ww_like, rw_like, state_like) = ctx.likes
+        shape = lambda t, like: t.reshape(like[0]).to(like[1])  # noqa: E731
+        dq, dk, dv, dg, db, dw = (shape(t, like) for t, like in ((grads.q, q_like), (grads.k, k_like),
+                                                                  (grads.v, v_like), (grads.g, g_like),
+                                                                  (grads.b, b_like), (grads.w, w_like)))
         # role_bank_kernel.py:256 / routed_update.py:48: round to the state dtype,
         # then sum the per-sequence adjoints over the batch
-        ds = grads.initial.to(state.dtype)
+        ds = grads.initial.to(state_like[1])
         if x.initial_stride == 0:
             ds = ds.sum(0)
-        ds = ds.reshape(state.shape)
-        return (dq, dk, dv, dg, db, dw, None, grads.ww.to(ww.dtype), None, grads.rw.to(rw.dtype), ds,
+        ds = ds.reshape(state_like[0])
+        return (dq, dk, dv, dg, db, dw, None, grads.ww.to(ww_like[1]), None, grads.rw.to(rw_like[1]), ds,
                 None, None, None, None, None)
 
 

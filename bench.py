@@ -477,7 +477,7 @@ def whole_model_training(device, context, timed_steps=3, warmup=2):
     return out
 
 
-def c4_forward(device, steps=3):
+def c4_forward(device, steps=10):
     """C4: batch 4, T8192, J2048 (32x64), Zipf s=1.1 bias on the factor scores,
     hot-path prefill forward (router x2, dispatch, recurrence + combine, final
     state).  Reports tokens/s and the segment-length skew."""
@@ -514,7 +514,7 @@ def c4_forward(device, steps=3):
             'max_segment_events': int(lengths.max()), 'mean_segment_events': round(float(lengths.mean()), 1)}
 
 
-def c5_training(device, steps=3):
+def c5_training(device, steps=10):
     """C5: batch 4, T2048, H8, BF16 training state: routed operator forward +
     backward (bank_training with all controller, route and state gradients)."""
     import torch
