@@ -49,26 +49,33 @@ class BDMConfig:
     training_state_dtype: str = 'bfloat16'
 
     def __post_init__(self):
-        for name in ('dim', 'bank_count', 'bank_size', 'selected_banks', 'value_width', 'num_heads'):
-            value = getattr(self, name)
-            if type(value) is not int or value <= 0:
-                raise ValueError(f'{name} must be a positive integer')
-        if self.bank_size > 256:
-            raise ValueError('bank_size must be at most 256')
-        if self.value_width % self.num_heads:
-            raise ValueError('value_width must be divisible by num_heads')
-        if type(self.routed_decay) is not bool or type(self.output_bias) is not bool:
-            raise ValueError('routed_decay and output_bias must be boolean')
-        if self.qk_normalization not in ('original', 'nvidia'):
-            raise ValueError('unknown Q/K normalization')
-        if self.output_normalization not in ('rms', 'layer'):
-            raise ValueError('unknown output normalization')
-        if self.training_state_dtype not in ('float32', 'bfloat16'):
-            raise ValueError('training_state_dtype must be float32 or bfloat16')
-        if self.selected_banks > min(near_square_factors(self.bank_count)):
-            raise ValueError('current product selector requires selected_banks <= both factor widths')
-        if not math.isfinite(self.norm_eps) or self.norm_eps <= 0:
-            raise ValueError('norm_eps must be finite and positive')
+        # The same conditions as the reference config (config.py:31-51), so a
+        # geometry accepted there is accepted here and vice versa.
+        sizes = ('dim', 'bank_count', 'bank_size', 'selected_banks', 'value_width', 'num_heads')
+        bad = [name for name in sizes if type(getattr(self, name)) is not int or getattr(self, name) < 1]
+        if bad:
+            raise ValueError(f'BDM config: {", ".join(bad)} needs a positive int')
+        checks = (
+            (self.bank_size <= 256, f'BDM config: bank_size {self.bank_size} exceeds the 256-row limit'),
+            (self.value_width % self.num_heads == 0,
+             f'BDM config: {self.num_heads} heads do not split value_width {self.value_width} evenly'),
+            (type(self.routed_decay) is bool and type(self.output_bias) is bool,
+             'BDM config: routed_decay and output_bias take True or False'),
+            (self.qk_normalization in ('original', 'nvidia'),
+             f'BDM config: qk_normalization {self.qk_normalization!r} is neither original nor nvidia'),
+            (self.output_normalization in ('rms', 'layer'),
+             f'BDM config: output_normalization {self.output_normalization!r} is neither rms nor layer'),
+            (self.training_state_dtype in ('float32', 'bfloat16'),
+             f'BDM config: training_state_dtype {self.training_state_dtype!r} is neither float32 nor bfloat16'),
+            (self.selected_banks <= min(near_square_factors(self.bank_count)),
+             f'BDM config: the product-key router picks {self.selected_banks} banks, more than the smaller '
+             f'factor of {self.bank_count} holds'),
+            (math.isfinite(self.norm_eps) and self.norm_eps > 0,
+             f'BDM config: norm_eps {self.norm_eps} is not a finite positive number'),
+        )
+        for ok, message in checks:
+            if not ok:
+                raise ValueError(message)
 
     @property
     def logical_rows(self) -> int:
@@ -101,14 +108,15 @@ class BDMConfig:
 
     @classmethod
     def from_record(cls, record: dict) -> 'BDMConfig':
-        resolved = dict(record)
-        resolved.setdefault('num_heads', 1)
-        resolved.setdefault('training_state_dtype', 'float32')
-        for name in ('routed_decay', 'qk_normalization', 'output_normalization', 'output_bias'):
-            resolved.setdefault(name, cls.__dataclass_fields__[name].default)
-        config = cls(**{name: resolved[name] for name in cls.__dataclass_fields__})
-        if resolved != config.record():
-            raise ValueError('resolved geometry/access disagrees with the BDM configuration')
+        # Records older than a field leave it out; they load as one head, an
+        # FP32 training state and the class defaults for the other options.
+        optional = ('routed_decay', 'qk_normalization', 'output_normalization', 'output_bias')
+        filled = {'num_heads': 1, 'training_state_dtype': 'float32',
+                  **{name: cls.__dataclass_fields__[name].default for name in optional}, **record}
+        config = cls(**{name: filled[name] for name in cls.__dataclass_fields__})
+        if filled != config.record():
+            raise ValueError('BDM record: its derived fields (rows, reads, writes, router, rule) do not match '
+                             'the configuration they were stored with')
         return config
 
 

@@ -102,19 +102,44 @@ class RoutedUpdate(torch.autograd.Function):
                 None, None, None, None, None)
 
 
-def bank_training(q, k, v, g, b, w, wi, ww, ri, rw, state, bank_count, scale, *, compact_replay=None,
-                  state_dtype=torch.float32):
-    """Routed-decay bank operator (routed_update.py:52-53)."""
+def _options(compact_slot, dtype_slot, compact_replay, state_dtype):
+    """Resolve the two optional positions after ``scale``.
+
+    The reference's autograd functions take ``(..., bank_count, scale,
+    compact_replay, state_dtype)`` (routed_update.py:18, role_bank_kernel.py:233),
+    and the injection point ``heads.forward_heads`` calls its
+    ``training_function`` with ``None, None`` in those two positions and
+    ``compact_replay=`` as a keyword (heads.py:38-39).  A ``None`` slot defers to
+    the keyword; a slot and a keyword that both say something must agree."""
+    if compact_slot is not None:
+        if compact_replay is not None and compact_replay is not compact_slot:
+            raise ValueError(f'compact_replay given twice: {compact_slot!r} by position, {compact_replay!r} by name')
+        compact_replay = compact_slot
     if compact_replay is not None and type(compact_replay) is not bool:
         raise ValueError(f'compact_replay takes None or a bool, not {compact_replay!r}')
+    if dtype_slot is not None:
+        state_dtype = dtype_slot
+    if state_dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f'state_dtype must be torch.float32 or torch.bfloat16, not {state_dtype!r}')
+    return compact_replay, state_dtype
+
+
+def bank_training(q, k, v, g, b, w, wi, ww, ri, rw, state, bank_count, scale, compact_slot=None, dtype_slot=None,
+                  *, compact_replay=None, state_dtype=torch.float32):
+    """Routed-decay bank operator (routed_update.py:52-53).
+
+    Also the ``training_function`` of ``heads.forward_heads`` (heads.py:37-39):
+    the two positions after ``scale`` take ``None`` (or the compact-replay flag
+    and state dtype, as the reference's autograd function orders them)."""
+    compact_replay, state_dtype = _options(compact_slot, dtype_slot, compact_replay, state_dtype)
     return RoutedUpdate.apply(q, k, v, g, b, w, wi, ww, ri, rw, state, bank_count, scale, compact_replay,
                               state_dtype, True)
 
 
-def role_bank_training(q, k, v, g, b, w, wi, ww, ri, rw, state, bank_count, scale, *, compact_replay=None,
-                       state_dtype=torch.float32):
-    """Bank operator without routed decay (role_bank_kernel.py:258-259)."""
-    if compact_replay is not None and type(compact_replay) is not bool:
-        raise ValueError(f'compact_replay takes None or a bool, not {compact_replay!r}')
+def role_bank_training(q, k, v, g, b, w, wi, ww, ri, rw, state, bank_count, scale, compact_slot=None,
+                       dtype_slot=None, *, compact_replay=None, state_dtype=torch.float32):
+    """Bank operator without routed decay (role_bank_kernel.py:258-259); the
+    same argument positions as ``bank_training``."""
+    compact_replay, state_dtype = _options(compact_slot, dtype_slot, compact_replay, state_dtype)
     return RoutedUpdate.apply(q, k, v, g, b, w, wi, ww, ri, rw, state, bank_count, scale, compact_replay,
                               state_dtype, False)
