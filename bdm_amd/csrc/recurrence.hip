@@ -25,6 +25,7 @@
 // in increasing bank id, rounding after every add (the production readout
 // order), ordering the token's KR bank ids itself.
 #include <cstdlib>
+#include <mutex>
 #include <cstring>
 #include <type_traits>
 
@@ -77,6 +78,9 @@ struct ForwardParams {
     // keeps the range in bank order
     const int *seg_order;
     int order_gpr;
+    // MODE 0: the launch runs head groups group_base .. group_base + gridDim.y
+    // - 1 (one round of a launch split into rounds; 0 for a whole launch)
+    int group_base;
 };
 
 // Events per piece when long segments are cut (a multiple of the stage size).
@@ -506,6 +510,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         } else {
             seg = p.xcd_remap ? int((block % 8) * (p.nseg / 8) + block / 8) : block;
         }
+        group += p.group_base;
     } else if constexpr (MODE == 1) {
         // Every head group's pieces first, then the segments: dispatched row
         // by row, the later groups' pieces would wait behind the first
@@ -1094,12 +1099,14 @@ template <typename T, int CPL, int KFIX, bool EACH>
 __global__ __launch_bounds__(256) void ordered_combine_kernel(const T *__restrict__ zbuf,
                                                               const int64_t *__restrict__ read_indices,
                                                               T *__restrict__ y, int64_t nt, int kr, int row_width,
-                                                              int banks) {
-    const int chunks = row_width / CPL;
+                                                              int banks, int col_begin, int col_count) {
+    // columns col_begin .. col_begin + col_count - 1 of every token (all of
+    // them, or one round's heads when the combine runs beside the recurrence)
+    const int chunks = col_count / CPL;
     const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
     const int64_t token = idx / chunks;
     if (token >= nt) return;
-    const int col0 = int(idx - token * chunks) * CPL;
+    const int col0 = col_begin + int(idx - token * chunks) * CPL;
     const T *z = zbuf + token * kr * row_width + col0;
     const int64_t *ri = read_indices + token * kr;
     auto bank_of = [&](int j) -> uint32_t {
@@ -1208,34 +1215,41 @@ int record_phase(const bdm_forward_args &a, int which, hipStream_t stream) {
 // The read combine of bdm_forward: y from the read buffer (or zeros when the
 // routes have no reads).
 template <typename T>
-int launch_combine_kernels(const bdm_forward_args &a, const T *zbuf, hipStream_t stream) {
+int launch_combine_kernels(const bdm_forward_args &a, const T *zbuf, hipStream_t stream, int col_begin = 0,
+                           int col_count = -1) {
     const int row_width = a.heads * a.head_width;
+    if (col_count < 0) col_count = row_width;
     const int64_t nt = a.batch * a.time;
     if (a.read_banks > 0) {
         // 16-byte rows where the layout allows (8 BF16 or 4 FP32 columns)
         constexpr int CC = sizeof(T) == 2 ? 8 : 4;
+        const bool wide = row_width % CC == 0 && col_begin % CC == 0 && col_count % CC == 0;
+        const int cc = wide ? CC : 1;
+        const unsigned blocks = unsigned((nt * (col_count / cc) + 255) / 256);
+        T *y = static_cast<T *>(a.output);
+        const int kr = a.read_banks, banks = a.bank_count;
         if (a.head_width <= 32) {
             // narrow heads: FP32 sum, one rounding (index_add_)
-            const int cc = row_width % CC == 0 ? CC : 1;
-            const int64_t threads = nt * (row_width / cc);
-            if (cc == CC)
-                ordered_combine_kernel<T, CC, 0, false><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
-                    zbuf, a.read_indices, static_cast<T *>(a.output), nt, a.read_banks, row_width, a.bank_count);
+            if (wide)
+                ordered_combine_kernel<T, CC, 0, false><<<blocks, 256, 0, stream>>>(zbuf, a.read_indices, y, nt, kr,
+                                                                                    row_width, banks, col_begin,
+                                                                                    col_count);
             else
-                ordered_combine_kernel<T, 1, 0, false><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
-                    zbuf, a.read_indices, static_cast<T *>(a.output), nt, a.read_banks, row_width, a.bank_count);
-        } else if (row_width % CC == 0) {
-            const int64_t threads = nt * (row_width / CC);
+                ordered_combine_kernel<T, 1, 0, false><<<blocks, 256, 0, stream>>>(zbuf, a.read_indices, y, nt, kr,
+                                                                                   row_width, banks, col_begin,
+                                                                                   col_count);
+        } else if (wide) {
             if (a.read_banks == 8 && a.bank_count < (1 << 29))
-                ordered_combine_kernel<T, CC, 8, true><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
-                    zbuf, a.read_indices, static_cast<T *>(a.output), nt, a.read_banks, row_width, a.bank_count);
+                ordered_combine_kernel<T, CC, 8, true><<<blocks, 256, 0, stream>>>(zbuf, a.read_indices, y, nt, kr,
+                                                                                   row_width, banks, col_begin,
+                                                                                   col_count);
             else
-                ordered_combine_kernel<T, CC, 0, true><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
-                    zbuf, a.read_indices, static_cast<T *>(a.output), nt, a.read_banks, row_width, a.bank_count);
+                ordered_combine_kernel<T, CC, 0, true><<<blocks, 256, 0, stream>>>(zbuf, a.read_indices, y, nt, kr,
+                                                                                   row_width, banks, col_begin,
+                                                                                   col_count);
         } else {
-            const int64_t threads = nt * row_width;
-            ordered_combine_kernel<T, 1, 0, true><<<unsigned((threads + 255) / 256), 256, 0, stream>>>(
-                zbuf, a.read_indices, static_cast<T *>(a.output), nt, a.read_banks, row_width, a.bank_count);
+            ordered_combine_kernel<T, 1, 0, true><<<blocks, 256, 0, stream>>>(zbuf, a.read_indices, y, nt, kr,
+                                                                              row_width, banks, col_begin, col_count);
         }
     } else {
         const int64_t count = nt * row_width;
@@ -1248,6 +1262,126 @@ template <typename T>
 int launch_combine(const bdm_forward_args &a, const T *zbuf, hipStream_t stream) {
     if (int rc = record_phase(a, 1, stream)) return rc;
     if (int rc = launch_combine_kernels(a, zbuf, stream)) return rc;
+    return record_phase(a, 2, stream);
+}
+
+// ---- The read combine beside the recurrence.
+//
+// The combine of a token's columns can start once every segment of those
+// columns' heads has run.  Where the longest-first order runs the head
+// groups in rounds (each round fills every slot of the GPU), the rounds are
+// launched separately, alternating between the caller's stream and an
+// auxiliary one, and each round's combine over its own heads' columns
+// follows it on the same stream.  The combine of round r then runs beside
+// round r + 1: the recurrence holds 4 waves of <= 112 VGPRs per SIMD, which
+// leaves the 64 that a combine wave needs (ordered_combine_kernel takes 46),
+// and the combine is HBM-bound where the recurrence is VALU-bound.  Only the
+// last round's combine is left after the recurrence.  The columns a combine
+// reads are written by its own round only, and y's column ranges are
+// disjoint, so results are those of the serial order bit for bit.
+//
+// The auxiliary stream joins the caller's through events (a fork after the
+// segment order, a join after the last combine), so the sequence may be
+// captured in a graph.  A one-lane kernel ahead of the second round on the
+// auxiliary stream lets the first round's blocks reach every slot before the
+// second round's are dispatched (the two would otherwise share the slots
+// from the start, and the first round would end no earlier than the second).
+// Per device: one stream (default priority) and two events, created on the
+// first call that is not under capture; BDM_COMBINE_OVERLAP=0 keeps the
+// serial order.
+constexpr int kOverlapAux = 3;  // auxiliary streams: at most 4 parts
+
+struct OverlapAux {
+    hipStream_t stream[kOverlapAux] = {};
+    hipEvent_t fork = nullptr, join[kOverlapAux] = {};
+};
+
+bool overlap_enabled() {
+    const char *e = getenv("BDM_COMBINE_OVERLAP");
+    return !(e && e[0] == '0' && e[1] == 0);
+}
+
+// Launches the head groups are split into (2..4; default: one per round).
+int overlap_parts(int rounds, int groups) {
+    const char *e = getenv("BDM_COMBINE_PARTS");
+    int n = e ? atoi(e) : rounds;
+    n = n < 2 ? 2 : (n > kOverlapAux + 1 ? kOverlapAux + 1 : n);
+    return n > groups ? groups : n;
+}
+
+__global__ void overlap_gate_kernel() {}
+
+std::mutex &overlap_launch_mutex() {
+    static std::mutex mu;
+    return mu;
+}
+
+// The device's auxiliary streams and events, or null (then the serial order
+// runs): creation failed, or the caller's stream is being captured and they
+// do not exist yet (resources are not created under capture).
+const OverlapAux *overlap_aux(hipStream_t caller) {
+    constexpr int kMaxDev = 64;
+    static std::mutex mu;
+    static OverlapAux aux[kMaxDev];
+    static bool failed[kMaxDev] = {};
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return nullptr;
+    std::lock_guard<std::mutex> lock(mu);
+    if (aux[dev].fork) return &aux[dev];
+    if (failed[dev]) return nullptr;
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(caller, &status) != hipSuccess || status != hipStreamCaptureStatusNone) return nullptr;
+    OverlapAux made;
+    bool ok = hipEventCreateWithFlags(&made.fork, hipEventDisableTiming) == hipSuccess;
+    for (int i = 0; ok && i < kOverlapAux; ++i)
+        ok = hipStreamCreateWithFlags(&made.stream[i], hipStreamNonBlocking) == hipSuccess &&
+             hipEventCreateWithFlags(&made.join[i], hipEventDisableTiming) == hipSuccess;
+    if (!ok) {
+        (void)hipGetLastError();
+        failed[dev] = true;
+        return nullptr;
+    }
+    aux[dev] = made;
+    return &aux[dev];
+}
+
+// MODE 0 of the lazy kernel as `parts` launches over consecutive head
+// groups (each with its own longest-first rounds), part i on stream i (the
+// caller's, then the auxiliary ones) behind i one-lane gate kernels, each
+// part's combine over its heads' columns after it on the same stream.
+// Phase events: 0 before the first part, 1 after the last part's
+// recurrence, 2 after the join.
+template <typename T, int CPL, int HB>
+int launch_overlapped(const bdm_forward_args &a, ForwardParams<T> p, unsigned nseg, int groups, int threads,
+                      const T *zbuf, const OverlapAux &ax, hipStream_t stream) {
+    const int gpr = p.order_gpr;
+    const int parts = overlap_parts((groups + gpr - 1) / gpr, groups);
+    if (hipEventRecord(ax.fork, stream) != hipSuccess)
+        return fail(BDM_ERR_LAUNCH, "forward: forking the combine streams");
+    for (int i = 1; i < parts; ++i) {
+        if (hipStreamWaitEvent(ax.stream[i - 1], ax.fork, 0) != hipSuccess)
+            return fail(BDM_ERR_LAUNCH, "forward: forking the combine streams");
+        for (int gate = 0; gate < i; ++gate) overlap_gate_kernel<<<1, 1, 0, ax.stream[i - 1]>>>();
+        if (int rc = check_launch("overlap_gate_kernel")) return rc;
+    }
+    for (int i = 0; i < parts; ++i) {
+        hipStream_t st = i ? ax.stream[i - 1] : stream;
+        const int g0 = int(int64_t(groups) * i / parts), g1 = int(int64_t(groups) * (i + 1) / parts);
+        ForwardParams<T> pr = p;
+        pr.group_base = g0;
+        pr.order_gpr = min(gpr, g1 - g0);
+        lazy_forward_kernel<T, CPL, HB, 0><<<dim3(nseg, unsigned(g1 - g0)), threads, 0, st>>>(pr);
+        if (int rc = check_launch("lazy_forward_kernel")) return rc;
+        if (i == parts - 1)
+            if (int rc = record_phase(a, 1, st)) return rc;
+        const int h0 = g0 * p.heads_per_block;
+        const int h1 = min(g1 * p.heads_per_block, p.heads);
+        if (int rc = launch_combine_kernels<T>(a, zbuf, st, h0 * p.width, (h1 - h0) * p.width)) return rc;
+    }
+    for (int i = 1; i < parts; ++i)
+        if (hipEventRecord(ax.join[i - 1], ax.stream[i - 1]) != hipSuccess ||
+            hipStreamWaitEvent(stream, ax.join[i - 1], 0) != hipSuccess)
+            return fail(BDM_ERR_LAUNCH, "forward: joining the combine streams");
     return record_phase(a, 2, stream);
 }
 
@@ -1347,6 +1481,18 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, const PieceBuffers &pb, h
                 const void *kernel = lazy_hb == 2 ? reinterpret_cast<const void *>(&lazy_forward_kernel<T, CPL, 2, 0>)
                                                   : reinterpret_cast<const void *>(&lazy_forward_kernel<T, CPL, 8, 0>);
                 p.order_gpr = order_groups_per_round(kernel, lthreads, nseg, int(grid.y));
+                // rounds whose heads' columns split y in whole 16-byte groups
+                const bool aligned_rounds = (int64_t(p.heads_per_block) * p.width * sizeof(T)) % 16 == 0 &&
+                                            (int64_t(a.heads) * a.head_width * sizeof(T)) % 16 == 0;
+                if (a.read_banks > 0 && int(grid.y) > p.order_gpr && aligned_rounds && overlap_enabled()) {
+                    if (const OverlapAux *ax = overlap_aux(stream)) {
+                        // the shared events are recorded and waited for by one call at a time
+                        std::lock_guard<std::mutex> lock(overlap_launch_mutex());
+                        if (lazy_hb == 2)
+                            return launch_overlapped<T, CPL, 2>(a, p, grid.x, int(grid.y), lthreads, zbuf, *ax, stream);
+                        return launch_overlapped<T, CPL, 8>(a, p, grid.x, int(grid.y), lthreads, zbuf, *ax, stream);
+                    }
+                }
             }
             if (lazy_hb == 2)
                 lazy_forward_kernel<T, CPL, 2, 0><<<grid, lthreads, 0, stream>>>(p);
@@ -1395,6 +1541,8 @@ bool order_path(const bdm_forward_args &a) { return lazy_path(a) && order_geomet
 // On MI355X at the C2 geometry the matrix-core form is the slower one: its
 // coefficient scan and exact gated-value split cost more vector instructions
 // than the state update they move to the matrix cores.
+constexpr int64_t kChunkMaxReadEvents = 1024;
+
 bool chunk_enabled() {
     const char *e = getenv("BDM_FORWARD_KERNEL");
     return e && strcmp(e, "mfma") == 0;
@@ -1448,7 +1596,23 @@ int dispatch_forward(const bdm_forward_args &a, T *zbuf, const PieceBuffers &pb,
     // batch stride that keeps them aligned.
     const bool vec = a.initial_batch_stride % 8 == 0;
     if constexpr (std::is_same<T, bf16_t>::value) {
-        if (chunk_path(a) && chunk_enabled()) return launch_chunked(a, zbuf, stream);
+        if (chunk_path(a) && chunk_enabled()) {
+            // The matrix-core form drops the products of two BF16 low parts
+            // (relative 2^-16), so its FP32 sums before a BF16 rounding (the
+            // state every 16 events, the read fold after every add) differ
+            // from the sequential ones in the last bits and flip a rounding
+            // now and then.  The worst token's error grows with the token
+            // count: under 1e-2 on every tested shape (up to 800 read
+            // events), 1.08 % at C2's 262,144.  Launches beyond the tested
+            // range are refused rather than run outside the tolerance.
+            const int64_t reads = a.batch * a.time * int64_t(a.read_banks);
+            if (reads > kChunkMaxReadEvents)
+                return fail(BDM_ERR_UNSUPPORTED,
+                            "forward: BDM_FORWARD_KERNEL=mfma is limited to %lld read events (%lld asked): its "
+                            "worst-token error exceeds 1e-2 at larger sizes; unset it for the vector kernel",
+                            (long long)kChunkMaxReadEvents, (long long)reads);
+            return launch_chunked(a, zbuf, stream);
+        }
     }
     if (a.bank_size <= 8) {
         if (lazy_path(a)) return launch_forward<T, 8, 4, true>(a, zbuf, pb, stream);

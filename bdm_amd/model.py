@@ -33,7 +33,10 @@ class BankedDeltaMemory(nn.Module):
 
     # Inference steps run the controller epilogue, both routes and the decode
     # kernel as one launch (``ops.decode_fused``) where the geometry allows;
-    # False keeps the three separate kernels (same results).
+    # False keeps the three separate kernels.  The fused launch also forms
+    # f_proj's second factor, in another FP32 summation order than the GEMM,
+    # so f may differ by one BF16 rounding and y and the cache match the
+    # separate kernels within tolerance rather than bit for bit.
     fused_decode = True
 
     def __init__(self, config: BDMConfig, *, layer_id=0, seed=0, backend='hip', compact_replay=None):
@@ -458,7 +461,9 @@ class BankedDeltaMemory(nn.Module):
         block's residual add and RMSNorm formed inside the projection GEMV and
         the output interface inside the o_proj GEMV (``bdm_gemv_ex``):
         h = hidden + delta (delta None: h = hidden), out = step(RMSNorm(h)).
-        Returns (out, h); results equal the unfused kernels bit for bit."""
+        Returns (out, h).  It matches the unfused kernels within tolerance:
+        the decode launch forms f itself in another summation order, and the
+        layer-norm prologue may differ from the standalone kernel by an ulp."""
         weight, bias, _ = self._fused_weights()
         rows = hidden.shape[0]
         flat = hidden.reshape(rows, self.hidden_size)

@@ -132,9 +132,10 @@ class MasterAdamW:
 
     def state_dict(self) -> dict:
         """The FP32 masters and both moments per parameter (CPU copies), the
-        step count and the hyperparameters: what resuming needs, as the
-        reference wrapper saves its masters and optimizer state
-        (reproduction/experiments/optim.py:52-54)."""
+        step count and the hyperparameters: what resuming needs.  The content
+        is what the reference wrapper saves (reproduction/experiments/
+        optim.py:52-54), but not its layout ({'optimizer': torch AdamW state,
+        'masters': [...]}): the two checkpoint formats do not interchange."""
         count = len(self.params)
         return {'masters': [self.master_of(i).detach().cpu().clone() for i in range(count)],
                 'exp_avg': [self.moments_of(i)[0].detach().cpu().clone() for i in range(count)],
@@ -145,10 +146,14 @@ class MasterAdamW:
     @torch.no_grad()
     def load_state_dict(self, state: dict) -> None:
         """Restore masters, moments and the step count, with the reference's
-        checks (optim.py:57-71): FP32 tensors of the parameters' shapes.  The
+        checks (optim.py:57-71): FP32 tensors of the parameters' shapes, and
+        the same per-parameter weight decay as this optimizer's.  The
         BF16 weights are left as they are; call ``reload_masters`` first if the
         weights, not the saved masters, should win."""
         count = len(self.params)
+        if 'weight_decay' in state and [float(d) for d in state['weight_decay']] != [float(d) for d in self.decay]:
+            raise ValueError('Invalid optimizer checkpoint: per-parameter weight decay differs from this '
+                             "optimizer's (it is fixed at construction)")
         for key in ('masters', 'exp_avg', 'exp_avg_sq'):
             saved = state[key]
             if len(saved) != count:

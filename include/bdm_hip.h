@@ -263,8 +263,10 @@ int bdm_decode(const bdm_decode_args *args, void *stream);
  * The decode step of the inference path from the projection outputs, in one
  * launch: the controller epilogue (bdm_controller_epilogue, heads.py:11-22),
  * both routers (bdm_router_select_pair, gdn2_banks.py:74-114) and bdm_decode
- * (inference.py:161-194).  Replaces the three calls of a step; every input the
- * decode sees equals, bit for bit, what those kernels would have stored.
+ * (inference.py:161-194).  Replaces the three calls of a step.  Given f (the
+ * f pointer), every input the decode sees equals, bit for bit, what those
+ * kernels would have stored; with f_weight (below) f is formed in another
+ * summation order, and results match the separate kernels within tolerance.
  * proj is [batch, proj_stride] ctrl_dtype with the q, k, v, b, w slices and
  * the read and write route scores (J1 + J2 each) at the given column offsets;
  * f is the f_proj output [batch, f_stride]; a_log [H] and dt_bias [H*S] in

@@ -120,3 +120,18 @@ def test_chunk_forward_decay_extremes(device, decay):
     assert torch.isfinite(y).all() and torch.isfinite(final).all()
     err_y, err_f = rel_err(y, ref), rel_err(final, ref_final)
     assert err_y < TOL and err_f < TOL, (err_y, err_f)
+
+
+def test_chunk_forward_refuses_untested_sizes(device):
+    """Above 1,024 read events the matrix-core form is refused (its worst
+    token measured 1.08 % off the oracle at the full C2 size), before any
+    launch, instead of running outside the tolerance."""
+    batch, time, heads, s, v, j, kk = 1, 160, 1, 8, 128, 16, 8
+    gen = torch.Generator().manual_seed(7100)
+    _, ww, wi = routes(batch, time, j, kk, gen)
+    _, rw, ri = routes(batch, time, j, kk, gen)
+    q, k, v_, g, b, w = controllers(batch, time, heads, s, v, gen)
+    state = initial_state(j, heads, s, v, gen)
+    announce('chunk forward refusal', batch * time * kk)
+    with pytest.raises(NotImplementedError, match='limited to 1024 read events'):
+        run_forward(device, (q, k, v_, g, b, w, wi, ww, ri, rw, state), j, s, kernel='mfma')

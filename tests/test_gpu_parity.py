@@ -527,6 +527,66 @@ def test_segment_order_bit_identical(device, monkeypatch):
     assert torch.equal(y_lpt, y_ref)
     assert torch.equal(f_lpt, f_ref)
 
+@pytest.mark.gpu
+@pytest.mark.parametrize('snapshots', [False, True], ids=['prefill', 'training'])
+def test_combine_overlap_bit_identical(device, monkeypatch, snapshots):
+    """At C2 size the head-group rounds run as separate launches on two
+    streams with each round's combine beside the next round; y, the final
+    state and the snapshots must equal those of the serial order
+    (BDM_COMBINE_OVERLAP=0) bit for bit, from sentinel-filled outputs; and the
+    overlapped sequence captured in a HIP graph must replay to the same
+    results, with eager launches between the replays."""
+    from bdm_amd import ops
+    gen = torch.Generator().manual_seed(78)
+    batch, time, heads, s, v, j, kk = 8, 4096, 8, 8, 128, 256, 8
+    _, ww, wi = routes(batch, time, j, kk, gen)
+    _, rw, ri = routes(batch, time, j, kk, gen)
+    q, k, v_, g, b, w = controllers(batch, time, heads, s, v, gen)
+    state = initial_state(j, heads, s, v, gen, scale=0.05)
+    dev = [t.to(device) for t in (q, k, v_, g, b, w, wi, ww, ri, rw, state)]
+    meta = ops.dispatch_build(dev[6], dev[8], j)
+    x = ops.prepare_routed(*dev[:10], dev[10], bank_count=j)
+    final = torch.empty(batch, j, heads, s, v, device=device, dtype=torch.bfloat16)
+    snap = ops.snapshot_buffer(x, 16, torch.bfloat16) if snapshots else None
+
+    def run():
+        final.fill_(float('nan'))
+        if snap is not None:
+            snap.fill_(-3.0)  # a finite sentinel: slots past a segment's last boundary stay unwritten
+        return ops.routed_forward(*dev[:10], dev[10], meta, bank_count=j, scale=s ** -0.5, routed_decay=True,
+                                  round_interval=16, final_state=final, snapshots=snap,
+                                  snapshot_interval=16 if snapshots else 0, prepared=x)
+
+    def outputs(y):
+        torch.cuda.synchronize()
+        return [y.clone(), final.clone()] + ([snap.clone()] if snap is not None else [])
+
+    announce('combine overlap at C2 size', snapshots)
+    got = outputs(run())
+    monkeypatch.setenv('BDM_COMBINE_OVERLAP', '0')
+    want = outputs(run())
+    for a, c in zip(got, want):
+        assert torch.equal(a, c)
+    monkeypatch.delenv('BDM_COMBINE_OVERLAP')
+    announce('combine overlap under graph capture', snapshots)
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        run()
+    torch.cuda.current_stream(device).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y_graph = run()
+    for _ in range(3):
+        graph.replay()
+        replayed = outputs(y_graph)
+        for a, c in zip(replayed, want):
+            assert torch.equal(a, c)
+        outputs(run())  # eager work between the replays
+    del graph
+
+
 def test_cut_segment_order_bit_identical(device, monkeypatch):
     """Prefill policy with skewed routes (long segments cut into pieces, many
     short uncut ones): MODE 1 runs every head group's pieces first and the

@@ -76,6 +76,39 @@ def _case(batch, time, bank_count, kk, seed, device, bad=False):
     return wi.to(device), ri.to(device)
 
 
+def test_static_dispatch_under_graph_capture(device):
+    """Captured in a HIP graph (the callers it is for), and first called
+    there when this file runs alone: each replay, after new routes are copied
+    into the captured inputs and with eager work in between, equals the
+    workspace dispatch of those routes bit for bit."""
+    from bdm_amd import _lib
+    lib = _lib.library()
+    batch, time, bank_count, kk = 8, 4096, 256, 8
+    wi, ri = _case(batch, time, bank_count, kk, 11, device)
+    out = _outputs(batch, time, kk, kk, bank_count, device)
+    torch.cuda.synchronize()
+    announce('static dispatch under graph capture')
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = lib.bdm_dispatch_build_static(_ptr(wi), _ptr(ri), batch, time, kk, kk, bank_count, _ptr(out['order']),
+                                           _ptr(out['inverse']), _ptr(out['tokens']), _ptr(out['cu']),
+                                           _ptr(out['status']), _stream(device))
+    assert rc == 0, lib.bdm_last_error_string()
+    for replay, seed in enumerate((12, 13, 14)):
+        new_wi, new_ri = _case(batch, time, bank_count, kk, seed, device)
+        wi.copy_(new_wi)
+        ri.copy_(new_ri)
+        for t in out.values():
+            t.fill_(-7)
+        graph.replay()
+        torch.cuda.synchronize()
+        want = dispatch_with_workspace(new_wi, new_ri, bank_count)
+        torch.cuda.synchronize()
+        for key in ('order', 'inverse', 'tokens', 'cu', 'status'):
+            assert torch.equal(out[key], want[key]), (replay, key)
+    del graph
+
+
 def test_static_dispatch_matches_the_workspace_dispatch(device):
     # the C2 geometry, then a smaller one on the same (reused) static scratch,
     # then malformed routes, then the C2 geometry again
