@@ -22,40 +22,36 @@
 // and gates only, not on the value columns.  They are computed by running the
 // recurrence itself on a 24-column basis (the 8 rows of M0 and the W <= 16
 // write values; 4 rows per lane, the erase sum over rows completed across the
-// half-waves).  The value columns then cost four v_mfma_f32_32x32x16_bf16
-// per 32 columns:
-//     MFMA 1:  K 0..7 = Phi_hi . M0       K 8..15 = Psi_hi . xh (even writes)
-//     MFMA 2:  K 0..7 = Psi_hi . xh (odd) K 8..15 = Phi_lo . M0
-//     MFMA 3:  K 0..7 = Psi_lo . xh (odd) K 8..15 = Psi_lo . xh (even)
-//     MFMA 4:  K 0..7 = Psi_hi . xl (odd) K 8..15 = Psi_hi . xl (even)
-// Phi and Psi are split into their BF16 rounding and the BF16 rounding of the
-// remainder (~16 bits: a transition near 1 is not rounded to 1); M0 is exact
-// in BF16; x = bf(w p) v is a product of two BF16 values, 16 significant bits,
-// so its two BF16 parts xh + xl are exact.  Only products of two low parts
-// (relative 2^-16) are dropped.  The FP32 state before each BF16 rounding is
-// then close enough to the sequential one that roundings rarely differ; with
-// single BF16 terms (2^-9) they would differ often and the differences carry.
-// Accumulation is FP32.
+// half-waves).  The value columns then cost 4 + ceil(W / 2)
+// v_mfma_f32_32x32x2_f32 per 32 columns, K = 8 + W in steps of 2:
+//     steps 0..3:   Phi . M0          (basis rows 0..7)
+//     steps 4..11:  Psi . [x_1; ..]   (basis row 8 + j: write j)
+// all in FP32: Phi and Psi are the FP32 coefficients themselves, M0 is exact
+// in BF16, and x = bf(w p) v, a product of two BF16 values, is exact in FP32,
+// so every product is formed and accumulated at FP32 precision, as the
+// sequential form's FMAs are (only the order of the sums differs).  A form
+// on BF16 matrix cores with two-part (high/low BF16) coefficients was
+// measured first: their relative error of ~2^-16 flipped the BF16 roundings
+// of the state and of the read fold often enough to leave tokens 1.08 % off
+// the oracle at the full C2 size.
 //
 // Accumulator layout of a 32 x 32 tile (lane l, value i): row 8(i/4) +
 // 4(l/32) + i%4, column l%32.  Rows are assigned so that every lane's values
 // 0..7 are the 8 state rows of its column (tile rows 0-3, 8-11 are state rows
 // 0-7 and rows 4-7, 12-15 repeat them for the upper half-wave) and values
-// 8..15 are reads (0-7 in the lower half-wave, 8-15 in the upper).  The next
-// chunk's B operand (K 0..7 of a column in one lane) is then the lane's own
-// values 0..7 rounded to BF16: no data crosses lanes between chunks.  Column
-// n of tile t is value column TILES*n + t, so a lane owns TILES adjacent
-// columns and moves them with one vector access.
+// 8..15 are reads (0-7 in the lower half-wave, 8-15 in the upper).  A step's
+// operands: lane l gives A[row l%32][k = 2 step + l/32] and B[k][column
+// l%32], so the next chunk's state rows come from the lane's own values 0..7
+// (rounded to BF16): no data crosses lanes between chunks.  Column n of tile
+// t is value column TILES*n + t, so a lane owns TILES adjacent columns and
+// moves them with one vector access.
 
 #include "chunk_forward.h"
 
 namespace bdm {
 namespace {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
 
 constexpr int kChunk = 16;    // events per chunk: the rounding interval
 constexpr int kBasis = 24;    // coefficient columns: M0 rows 0-7, even writes, odd writes
@@ -210,14 +206,14 @@ __global__ __launch_bounds__(64) void chunk_forward_kernel(ChunkForwardParams p)
         }
         __syncthreads();
 
-        // ---- the gated values of this lane's writes: odd writes in the lower
-        //      half-wave, even writes in the upper; slot s holds write 2s + (1 - half)
+        // ---- this lane's writes: slot s holds write 2s + half, the B operand
+        //      of step 4 + s in this half-wave
         ColWords<TILES> vraw[8], wraw[8];
         float wp[8];
         const int nslots = (nw + 1) >> 1;
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
-            const int j = 2 * s + (half ^ 1);
+            const int j = 2 * s + half;
             wp[s] = 0.f;
             if (s < nslots && j < nw) {
                 const int base = s_wrow[j] + int(vcol);
@@ -259,7 +255,7 @@ __global__ __launch_bounds__(64) void chunk_forward_kernel(ChunkForwardParams p)
                     part = fmaf(a4.z, hd2, part);
                     part = fmaf(a4.w, hd3, part);
                     const float tot = half_wave_sum(part);
-                    const int col = 8 + ((wj & 1) << 3) + (wj >> 1);
+                    const int col = 8 + wj;
                     const float u = (c32 == col ? 1.f : 0.f) - tot;
                     nrow[0] = fmaf(k4.x, u, hd0);
                     nrow[1] = fmaf(k4.y, u, hd1);
@@ -275,56 +271,15 @@ __global__ __launch_bounds__(64) void chunk_forward_kernel(ChunkForwardParams p)
         }
         __syncthreads();
 
-        // ---- gated values in BF16 high and low parts (x = bf(w p) v has 16
-        //      significant bits, so xh + xl is exact), for the live slot pairs
-        u32x4_t xh[TILES], xl[TILES];
-#pragma unroll
-        for (int t = 0; t < TILES; ++t) xh[t] = xl[t] = u32x4_t{0u, 0u, 0u, 0u};
-        const int npairs = (nslots + 1) >> 1;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            if (i < npairs) {
-#pragma unroll
-                for (int t = 0; t < TILES; ++t) {
-                    const float x0 = round_bf16(wraw[2 * i].at(t) * wp[2 * i]) * vraw[2 * i].at(t);
-                    const float x1 = round_bf16(wraw[2 * i + 1].at(t) * wp[2 * i + 1]) * vraw[2 * i + 1].at(t);
-                    const uint32_t hi = pack_bf16x2(x0, x1);
-                    xh[t][i] = hi;
-                    xl[t][i] = pack_bf16x2(x0 - bf16_lo(hi), x1 - bf16_hi(hi));
-                }
-            }
-        }
-
-        // ---- A operands: lane (tile row m = c32, K block half); the write
-        //      coefficients of the lane's own parity (odd in the lower
-        //      half-wave, even in the upper), all split into high and low parts
-        u32x4_t a1, a2, a3, a4;
+        // ---- A operands: lane (tile row m = c32, K half): coefficient row
+        //      coefficient_row(m), basis column 2 step + half, for the four
+        //      state steps and the live write steps (0 in rows past the reads)
+        float a_op[12];
         {
             const int gr = coefficient_row(c32);
             const bool row_live = c32 < 16 || gr - 8 < nr;
-            const float4 *grow = reinterpret_cast<const float4 *>(s_g[gr]);
-            const float4 f0 = grow[0], f1 = grow[1];
-            const float4 s0 = grow[half ? 2 : 4], s1 = grow[half ? 3 : 5];
-            float phi[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
-            float psi[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-            u32x4_t ph, pl, sh, sl;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float x0 = row_live ? phi[2 * i] : 0.f, x1 = row_live ? phi[2 * i + 1] : 0.f;
-                const float y0 = row_live ? psi[2 * i] : 0.f, y1 = row_live ? psi[2 * i + 1] : 0.f;
-                ph[i] = pack_bf16x2(x0, x1);
-                pl[i] = pack_bf16x2(x0 - bf16_lo(ph[i]), x1 - bf16_hi(ph[i]));
-                sh[i] = pack_bf16x2(y0, y1);
-                sl[i] = pack_bf16x2(y0 - bf16_lo(sh[i]), y1 - bf16_hi(sh[i]));
-            }
-            // MFMA 1: [Phi_hi | Psi_hi even] x [M0; xh even]
-            // MFMA 2: [Psi_hi odd | Phi_lo]  x [xh odd; M0]
-            // MFMA 3: [Psi_lo odd | Psi_lo even] x [xh odd; xh even]
-            // MFMA 4: [Psi_hi odd | Psi_hi even] x [xl odd; xl even]
-            a1 = half ? sh : ph;
-            a2 = half ? pl : sh;
-            a3 = sl;
-            a4 = sh;
+            for (int st = 0; st < 12; ++st) a_op[st] = row_live ? s_g[gr][2 * st + half] : 0.f;
         }
 
         // ---- B operands and the products, one 32-column tile at a time
@@ -332,32 +287,38 @@ __global__ __launch_bounds__(64) void chunk_forward_kernel(ChunkForwardParams p)
         const int64_t snap_offset = (start / kChunk + ch - 1) * p.s_heads * 8 * p.row_stride + head_cols;
 #pragma unroll
         for (int t = 0; t < TILES; ++t) {
-            u32x4_t m0;
+            // the chunk's start state, rounded to BF16 (a rounding point)
+            float m0[8];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) m0[i] = pack_bf16x2(acc[t][2 * i], acc[t][2 * i + 1]);
-            const u32x4_t b1 = half ? xh[t] : m0;
-            const u32x4_t b2 = half ? m0 : xh[t];
+            for (int r = 0; r < 8; ++r) m0[r] = round_bf16(acc[t][r]);
             if (snap) {
                 // the state at this chunk's start, as rounded (a replay boundary)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int rr = 4 * half + r;
-                    const uint32_t w = m0[rr >> 1];
                     reinterpret_cast<uint16_t *>(p.snap)[snap_offset + int64_t(rr) * p.row_stride + t] =
-                        uint16_t((rr & 1) ? (w >> 16) : (w & 0xffffu));
+                        uint16_t(__float_as_uint(m0[rr]) >> 16);
                 }
             }
-            f32x16_t zero;
+            f32x16_t d;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) zero[i] = 0.f;
-            f32x16_t d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a3),
-                                                                __builtin_bit_cast(bf16x8_t, xh[t]), zero, 0, 0, 0);
-            d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a4),
-                                                       __builtin_bit_cast(bf16x8_t, xl[t]), d, 0, 0, 0);
-            d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a2),
-                                                       __builtin_bit_cast(bf16x8_t, b2), d, 0, 0, 0);
-            acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a1),
-                                                            __builtin_bit_cast(bf16x8_t, b1), d, 0, 0, 0);
+            for (int i = 0; i < 16; ++i) d[i] = 0.f;
+            // state row 2 st + half: a bit-mask select (a plain select of two
+            // array slots becomes a per-lane index into a scratch copy)
+            const uint32_t upper = half ? ~0u : 0u;
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const uint32_t b = (__float_as_uint(m0[2 * st + 1]) & upper) | (__float_as_uint(m0[2 * st]) & ~upper);
+                d = __builtin_amdgcn_mfma_f32_32x32x2f32(a_op[st], __uint_as_float(b), d, 0, 0, 0);
+            }
+#pragma unroll
+            for (int s = 0; s < 8; ++s) {
+                if (s < nslots) {  // wave-uniform
+                    const float x = round_bf16(wraw[s].at(t) * wp[s]) * vraw[s].at(t);
+                    d = __builtin_amdgcn_mfma_f32_32x32x2f32(a_op[4 + s], x, d, 0, 0, 0);
+                }
+            }
+            acc[t] = d;
         }
 
         // ---- the chunk's reads: values 8..15, read s + 8 half

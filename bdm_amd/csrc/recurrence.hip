@@ -1541,8 +1541,6 @@ bool order_path(const bdm_forward_args &a) { return lazy_path(a) && order_geomet
 // On MI355X at the C2 geometry the matrix-core form is the slower one: its
 // coefficient scan and exact gated-value split cost more vector instructions
 // than the state update they move to the matrix cores.
-constexpr int64_t kChunkMaxReadEvents = 1024;
-
 bool chunk_enabled() {
     const char *e = getenv("BDM_FORWARD_KERNEL");
     return e && strcmp(e, "mfma") == 0;
@@ -1596,23 +1594,7 @@ int dispatch_forward(const bdm_forward_args &a, T *zbuf, const PieceBuffers &pb,
     // batch stride that keeps them aligned.
     const bool vec = a.initial_batch_stride % 8 == 0;
     if constexpr (std::is_same<T, bf16_t>::value) {
-        if (chunk_path(a) && chunk_enabled()) {
-            // The matrix-core form drops the products of two BF16 low parts
-            // (relative 2^-16), so its FP32 sums before a BF16 rounding (the
-            // state every 16 events, the read fold after every add) differ
-            // from the sequential ones in the last bits and flip a rounding
-            // now and then.  The worst token's error grows with the token
-            // count: under 1e-2 on every tested shape (up to 800 read
-            // events), 1.08 % at C2's 262,144.  Launches beyond the tested
-            // range are refused rather than run outside the tolerance.
-            const int64_t reads = a.batch * a.time * int64_t(a.read_banks);
-            if (reads > kChunkMaxReadEvents)
-                return fail(BDM_ERR_UNSUPPORTED,
-                            "forward: BDM_FORWARD_KERNEL=mfma is limited to %lld read events (%lld asked): its "
-                            "worst-token error exceeds 1e-2 at larger sizes; unset it for the vector kernel",
-                            (long long)kChunkMaxReadEvents, (long long)reads);
-            return launch_chunked(a, zbuf, stream);
-        }
+        if (chunk_path(a) && chunk_enabled()) return launch_chunked(a, zbuf, stream);
     }
     if (a.bank_size <= 8) {
         if (lazy_path(a)) return launch_forward<T, 8, 4, true>(a, zbuf, pb, stream);

@@ -69,10 +69,13 @@ def parse_args():
     ap.add_argument('--no-cpu-baseline', dest='cpu_baseline', action='store_false',
                     help='skip the CPU baseline (the reference CPU path at C1, ~10 s)')
     ap.add_argument('--no-extras', action='store_true', help='skip the full-layer and decode measurements')
-    ap.add_argument('--only', choices=('c2-forward', 'c3', 'c4', 'c5', 'prefill', 'lm', 'lm-prefill', 'lm-train'),
+    ap.add_argument('--only', choices=('c2-forward', 'c3', 'c3-kernel', 'c4', 'c4-module', 'c5', 'prefill', 'lm',
+                                       'lm-prefill', 'lm-train'),
                     help='run one named workload alone (C3 decode, C4 skewed forward, C5 training, C2 full-layer '
                          'prefill, whole-model prefill and decode) and print its figures as one JSON line; used to '
                          'profile a workload on its own')
+    ap.add_argument('--c3-routes', choices=('init', 'independent'), default='independent',
+                    help='--only c3-kernel: the route case of the kernel-only decode leg (for profilers)')
     ap.add_argument('--lm-context', type=int, default=8192,
                     help='prompt length T (= memory rows N) of the whole-model L16/D2048 measurement')
     ap.add_argument('--lm-gemm-tuning', choices=('on', 'off'), default='on',
@@ -143,8 +146,48 @@ def recurrence_roofline(cfg, batch, time_, ms):
             'valu_fp32_peak_tflops': VALU_FP32_TFLOPS, 'frac_valu_fp32': round(tflops / VALU_FP32_TFLOPS, 4),
             'mfma_fp32_peak_tflops': MFMA_FP32_TFLOPS, 'frac_mfma_fp32': round(tflops / MFMA_FP32_TFLOPS, 4),
             'mfma_utilisation': None if kernel == 'mfma' else 0.0,
+            'fma_floor': fma_floor(cfg, batch, time_, ms),
             'note': 'FLOPs of the sequential form (5Sv per write, 2Sv per read, per head); the vector kernel '
                     'issues 2 FMAs per state element per write, 1 per read (lazy decay)'}
+
+
+# MI355X: 256 CUs, 64 non-packed FP32 FMA lanes per CU per clock; 2.4 GHz is
+# the clock of the 78.6 TFLOP/s figure, and PROFILED_CLOCK_GHZ the shader
+# clock the C2 recurrence ran at under rocprofv3 (GRBM_GUI_ACTIVE cycles over
+# the kernel's duration, profiles/bdm_forward_c2.md)
+CU_COUNT, FMA_PER_CU_CLOCK, RATED_CLOCK_GHZ, PROFILED_CLOCK_GHZ = 256, 64, 2.4, 2.0
+
+
+def fma_floor(cfg, batch, time_, ms):
+    """The lazy recurrence's state-update FMAs alone (2*S*v per write and head,
+    S*v per read and head), issued at the full non-packed FP32 rate: the time
+    no vector-ALU form of this recurrence can beat, at the rated and at the
+    profiled clock, and the kernel's fraction of it."""
+    s, v, h, k = cfg.bank_size, cfg.head_value_width, cfg.num_heads, cfg.selected_banks
+    fmas = batch * time_ * h * k * (2 * s * v + s * v)
+    floor = {}
+    for name, ghz in (('rated', RATED_CLOCK_GHZ), ('profiled', PROFILED_CLOCK_GHZ)):
+        us = fmas / (CU_COUNT * FMA_PER_CU_CLOCK * ghz * 1e9) * 1e6
+        floor[f'{name}_clock_ghz'] = ghz
+        floor[f'{name}_floor_us'] = round(us, 1)
+        floor[f'frac_of_{name}_floor'] = round(us / (ms * 1e3), 4)
+    floor['state_update_fmas'] = fmas
+    return floor
+
+
+def combine_exposed(cfg, batch, time_, ms):
+    """The read combine's time after the recurrence (bdm_forward's phase
+    events 1 -> 2).  With the combine beside the recurrence (the default) that
+    is the last head-group round's combine and the join; with
+    BDM_COMBINE_OVERLAP=0 the whole combine."""
+    overlapped = (os.environ.get('BDM_COMBINE_OVERLAP', '1') != '0'
+                  and os.environ.get('BDM_FORWARD_KERNEL', 'vector') != 'mfma')
+    if not overlapped:
+        return dict(combine_roofline(cfg, batch, time_, ms), exposed_ms=round(ms, 4), overlapped=False)
+    return {'kernel': 'ordered_combine_kernel', 'exposed_ms': round(ms, 4), 'overlapped': overlapped,
+            'note': ("the last round's combine (its heads' columns); the earlier rounds' combines run beside the "
+                     'recurrence and are inside the recurrence phase' if overlapped else
+                     'the whole combine after the recurrence')}
 
 
 def combine_roofline(cfg, batch, time_, ms):
@@ -183,42 +226,70 @@ def copy_probe(device):
     return 2 * n * 2 / sec / 1e9
 
 
-def decode_bench(layer, device, steps, seed=1):
-    """C3: batch 64, one token per sequence, resident BF16 state ~ N(0, 0.02)."""
+def decode_routes(layer, xs, routes, seed):
+    """Per-step inputs of the kernel-only decode legs: the layer's controllers
+    of each step's token and its routes.  routes='init': the layer's own
+    routers, which at random init give every token the same read and write
+    banks (the router residuals are zero, routing.py:37-68), so every read is
+    served from a bank the same token just wrote; 'independent': write and
+    read banks from independent N(0, 1) factor scores per step, so a token
+    touches up to 24 banks (BASELINE's byte count assumes 24)."""
     import torch
     from bdm_amd import ops
     cfg = layer.config
-    batch = 64
     gen = torch.Generator().manual_seed(seed)
-    state = (torch.randn(batch, cfg.bank_count, cfg.num_heads, cfg.bank_size, cfg.head_value_width,
-                         generator=gen) * 0.02).to(torch.bfloat16).to(device)
-    xs = torch.randn(steps, batch, 1, cfg.dim, generator=gen).to(torch.bfloat16).to(device)
-    # kernel-only: controllers and routes of every step precomputed
+    j1, j2 = cfg.route_factors
     pre = []
     with torch.no_grad():
-        for i in range(steps):
+        for i in range(xs.shape[0]):
             q, k, v, g, b, w = layer._controllers(xs[i])
-            rr, wr = layer._route_projections(xs[i])
-            ww, wi = layer._route(wr, cfg.selected_banks)
-            rw, ri = layer._route(rr, cfg.selected_banks)
+            if routes == 'init':
+                rr, wr = layer._route_projections(xs[i])
+                ww, wi = layer._route(wr, cfg.selected_banks)
+                rw, ri = layer._route(rr, cfg.selected_banks)
+            else:
+                scores = torch.randn(2, xs.shape[1], 1, j1 + j2, generator=gen).to(xs.dtype).to(xs.device)
+                ww, wi = ops.router_select(scores[0], bank_count=cfg.bank_count, selected_banks=cfg.selected_banks)
+                rw, ri = ops.router_select(scores[1], bank_count=cfg.bank_count, selected_banks=cfg.selected_banks)
             pre.append(tuple(t[:, 0].contiguous() for t in (q, k, v, g, b, w, wi, ww, ri, rw)))
-    torch.cuda.synchronize()
+    return pre
+
+
+def decode_moved_bytes(cfg, pre):
+    """Bank-state bytes one decode step must move, averaged over the steps:
+    each write bank read and written, each read bank that the same token does
+    not also write read once (a read of a written bank takes the written
+    value, which the kernel keeps on chip)."""
+    bank_bytes = cfg.num_heads * cfg.bank_size * cfg.head_value_width * 2
+    total = 0
+    for step in pre:
+        wi, ri = step[6].cpu(), step[8].cpu()
+        extra = sum(len(set(ri[b].tolist()) - set(wi[b].tolist())) for b in range(wi.shape[0]))
+        total += (2 * wi.numel() + extra) * bank_bytes
+    return total / len(pre)
+
+
+def decode_kernel_leg(layer, state, pre):
+    """All steps' bdm_decode launches captured in one HIP graph and replayed:
+    the kernel's time per step without host launch overhead."""
+    import torch
+    from bdm_amd import ops
+    cfg = layer.config
+    device = state.device
     scale = cfg.bank_size ** -0.5
     launch = lambda i: ops.decode_step(*pre[i], state, bank_count=cfg.bank_count, scale=scale,  # noqa: E731
                                        routed_decay=True)
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.no_grad():
-        for i in range(min(8, steps)):  # warmup
+        for i in range(min(8, len(pre))):  # warmup
             launch(i)
         torch.cuda.synchronize()
-        # kernel-only: the decode launches of every step captured in one HIP
-        # graph and replayed, so host launch overhead is not in the figure
         side = torch.cuda.Stream(device)
         side.wait_stream(torch.cuda.current_stream(device))
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.stream(side):
             with torch.cuda.graph(graph, stream=side):
-                for i in range(steps):
+                for i in range(len(pre)):
                     launch(i)
         torch.cuda.current_stream(device).wait_stream(side)
         graph.replay()
@@ -228,32 +299,49 @@ def decode_bench(layer, device, steps, seed=1):
         graph.replay()
         stop.record(stream)
         torch.cuda.synchronize()
-        kernel_us = start.elapsed_time(stop) * 1e3 / steps
-        # eager launches of the decode entry point (host overhead included)
-        eager_sec, _ = timed(lambda: [launch(i) for i in range(steps)], 1, 0)
-        # full step: controllers, routes, decode kernel and output interface
-        sec, _ = timed(lambda: [layer.step(xs[i], state) for i in range(steps)], 1, 1)
-        full_graph_us, graph_check = full_step_graph(layer, xs, state, steps)
+        eager_sec, _ = timed(lambda: [launch(i) for i in range(len(pre))], 1, 0)
+    del graph
+    return start.elapsed_time(stop) * 1e3 / len(pre), eager_sec * 1e6 / len(pre)
+
+
+def decode_bench(layer, device, steps, seed=1, legs=('init', 'independent'), full_step=True):
+    """C3: batch 64, one token per sequence, resident BF16 state ~ N(0, 0.02).
+    Kernel-only legs for both route cases (decode_routes), each reported on
+    the bytes it moves (decode_moved_bytes); the full layer step (controllers,
+    routes, decode, output interface) eagerly and from one HIP graph."""
+    import torch
+    cfg = layer.config
+    batch = 64
+    gen = torch.Generator().manual_seed(seed)
+    state = (torch.randn(batch, cfg.bank_count, cfg.num_heads, cfg.bank_size, cfg.head_value_width,
+                         generator=gen) * 0.02).to(torch.bfloat16).to(device)
+    xs = torch.randn(steps, batch, 1, cfg.dim, generator=gen).to(torch.bfloat16).to(device)
     bank_bytes = cfg.num_heads * cfg.bank_size * cfg.head_value_width * 2
-    # BASELINE's figure: every step reads and writes KW banks and reads KR banks
-    state_bytes = batch * (2 * cfg.selected_banks + cfg.selected_banks) * bank_bytes
-    # what the kernel must move: reads of banks written by the same token come
-    # from the written values (at random init the read and write routes of a
-    # token coincide, the router residuals being zero)
-    touched = 0
-    for i in range(steps):
-        wi, ri = pre[i][6].cpu(), pre[i][8].cpu()
-        extra = sum(len(set(ri[b].tolist()) - set(wi[b].tolist())) for b in range(batch))
-        touched += (2 * wi.numel() + extra) * bank_bytes
-    touched /= steps
-    return {'batch': batch, 'steps': steps, 'kernel_us_per_step': round(kernel_us, 3),
-            'touched_state_bytes_per_step': round(touched),
-            'touched_state_GBps': round(touched / (kernel_us * 1e-6) / 1e9, 1),
-            'eager_launch_us_per_step': round(eager_sec * 1e6 / steps, 2),
-            'full_step_us_eager': round(sec * 1e6 / steps, 2), 'full_step_us_graph': full_graph_us,
-            'full_step_graph_check': graph_check, 'state_bytes_per_step': state_bytes,
-            'state_GBps': round(state_bytes / (kernel_us * 1e-6) / 1e9, 1),
-            'state_frac_of_hbm_peak': round(state_bytes / (kernel_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
+    # BASELINE's count: every step reads and writes KW banks and reads KR banks
+    baseline_bytes = batch * (2 * cfg.selected_banks + cfg.selected_banks) * bank_bytes
+    out = {'batch': batch, 'steps': steps, 'baseline_state_bytes_per_step': baseline_bytes}
+    for routes in legs:
+        pre = decode_routes(layer, xs, routes, seed + 17)
+        kernel_us, eager_us = decode_kernel_leg(layer, state, pre)
+        moved = decode_moved_bytes(cfg, pre)
+        gbps = moved / (kernel_us * 1e-6) / 1e9
+        out[f'{routes}_routes'] = {
+            'kernel_us_per_step': round(kernel_us, 3), 'eager_launch_us_per_step': round(eager_us, 2),
+            'moved_state_bytes_per_step': round(moved), 'moved_state_GBps': round(gbps, 1),
+            'moved_state_frac_of_hbm_peak': round(gbps / HBM_PEAK_GBPS, 4)}
+        del pre
+    if full_step:
+        with torch.no_grad():
+            sec, _ = timed(lambda: [layer.step(xs[i], state) for i in range(steps)], 1, 1)
+            full_graph_us, graph_check = full_step_graph(layer, xs, state, steps)
+        out.update({'full_step_us_eager': round(sec * 1e6 / steps, 2), 'full_step_us_graph': full_graph_us,
+                    'full_step_graph_check': graph_check,
+                    'full_step_routes': 'the layer\'s own routers at random init (read banks = write banks)'})
+    # the kernel leg whose bytes match BASELINE's 24-bank count most closely
+    lead = out.get('independent_routes') or out.get('init_routes')
+    out['kernel_us_per_step'] = lead['kernel_us_per_step']
+    out['state_frac_of_hbm_peak'] = lead['moved_state_frac_of_hbm_peak']
+    return out
 
 
 def full_layer_prefill(layer, device, batch, time_, steps):
@@ -477,10 +565,17 @@ def whole_model_training(device, context, timed_steps=3, warmup=2):
     return out
 
 
-def c4_forward(device, steps=10):
+def c4_forward(device, steps=10, policy='prefill'):
     """C4: batch 4, T8192, J2048 (32x64), Zipf s=1.1 bias on the factor scores,
     hot-path prefill forward (router x2, dispatch, recurrence + combine, final
-    state).  Reports tokens/s and the segment-length skew."""
+    state).  policy 'prefill': FP32 state, never rounded inside the
+    recurrence (the reference's H = 1 prefill policy, inference.py:114-130),
+    which lets long segments run as pieces composed by a scan; 'module': the
+    module forward's BF16 training-state policy at H = 8 (heads.py:40-46,
+    state rounded every 16 events, role_bank_kernel.py:153-165), under which a
+    segment is not an affine map of its start state and runs as one serial
+    chain, so the step is bound by the longest segment.  Reports tokens/s and
+    the segment-length skew."""
     import torch
     from bdm_amd import BSDMConfig, BankedDeltaMemory, ops
     from bdm_amd.config import near_square_factors
@@ -495,20 +590,24 @@ def c4_forward(device, steps=10):
     wr = (wr.float() + bias).to(wr.dtype)
     final = torch.empty(4, cfg.bank_count, cfg.num_heads, cfg.bank_size, cfg.head_value_width, device=device,
                         dtype=torch.bfloat16)
+    interval = ROUND_INTERVAL if policy == 'module' else 0
 
     def step():
         (ww, wi), (rw, ri) = ops.router_select_pair(wr, rr, bank_count=cfg.bank_count, selected_banks=8)
         meta = ops.dispatch_build(wi, ri, cfg.bank_count)
         ops.routed_forward(q, k, v, g, b, w, wi, ww, ri, rw, initial, meta, bank_count=cfg.bank_count,
-                           scale=cfg.bank_size ** -0.5, routed_decay=True, round_interval=0, final_state=final)
+                           scale=cfg.bank_size ** -0.5, routed_decay=True, round_interval=interval,
+                           final_state=final)
         return meta
 
     with torch.no_grad():
         sec, meta = timed(step, steps, 1)
     lengths = (meta.cu_seqlens[1:] - meta.cu_seqlens[:-1]).float()
     hot_bytes = hot_path_algorithmic_bytes(cfg, 4, 8192)
-    return {'tokens_per_s': round(4 * 8192 / sec, 1), 'ms_per_step': round(sec * 1e3, 3),
-            'policy': 'FP32 state (prefill), long segments cut into pieces',
+    described = {'prefill': 'FP32 state (prefill), long segments cut into pieces',
+                 'module': 'BF16 state rounded every 16 events (module forward at H = 8), each segment serial'}
+    return {'tokens_per_s': round(4 * 8192 / sec, 1), 'ms_per_step': round(sec * 1e3, 3), 'steps': steps,
+            'policy': described[policy],
             'hot_path_bytes_per_token': hot_bytes // (4 * 8192),
             'hot_path_roofline_frac': round(hot_bytes / sec / 1e9 / HBM_PEAK_GBPS, 4),
             'max_segment_events': int(lengths.max()), 'mean_segment_events': round(float(lengths.mean()), 1)}
@@ -537,7 +636,36 @@ def c5_training(device, steps=10):
         y.backward(dy)
 
     sec, _ = timed(step, steps, 1)
-    return {'tokens_per_s': round(4 * 2048 / sec, 1), 'ms_per_step': round(sec * 1e3, 3)}
+    tokens = 4 * 2048
+    hbm = training_algorithmic_bytes(cfg, 4, 2048)
+    flop = training_flop(cfg, 4, 2048)
+    return {'tokens_per_s': round(tokens / sec, 1), 'ms_per_step': round(sec * 1e3, 3), 'steps': steps,
+            'hot_path_bytes_per_token': hbm // tokens,
+            'hot_path_roofline_frac': round(hbm / sec / 1e9 / HBM_PEAK_GBPS, 4),
+            'flop_per_token': flop // tokens, 'achieved_tflops': round(flop / sec / 1e12, 2),
+            'frac_valu_fp32': round(flop / sec / 1e12 / VALU_FP32_TFLOPS, 4),
+            'roofline_note': ('bytes: the forward hot path without the final state, the BF16 snapshot at every '
+                              '16th event written and read back, the controllers read again, dy read and every '
+                              'controller and route gradient written; FLOPs: the sequential forward (5Sv per '
+                              'write, 2Sv per read) plus the replay (5Sv per write) and the adjoint (11Sv per '
+                              'write, 4Sv per read), per head')}
+
+
+def training_algorithmic_bytes(cfg, batch, time_):
+    """C5 forward + backward bytes (the roofline_note of c5_training)."""
+    h, s, v_total, kk = cfg.num_heads, cfg.bank_size, cfg.value_width, cfg.selected_banks
+    controllers = 3 * h * s * 2 + h * s * 4 + 2 * v_total * 2
+    forward = hot_path_algorithmic_bytes(cfg, batch, time_) - batch * cfg.bank_count * h * s * (v_total // h) * 2
+    tokens = batch * time_
+    # one snapshot of S x v BF16 per head every 16 events; 2K events per token and head
+    snapshots = tokens * h * (2 * kk) // 16 * s * (v_total // h) * 2
+    backward = tokens * (controllers + v_total * 2 + controllers + 2 * kk * 2)
+    return forward + 2 * snapshots + backward
+
+
+def training_flop(cfg, batch, time_):
+    s, v, h, k = cfg.bank_size, cfg.head_value_width, cfg.num_heads, cfg.selected_banks
+    return batch * time_ * h * k * ((5 + 5 + 11) * s * v + (2 + 4) * s * v)
 
 
 def c2_forward_only(layer, device, batch, time_, launches):
@@ -628,7 +756,12 @@ def c1_gpu(device, steps=20):
     x = c1_input().to(device)
     with torch.no_grad():
         sec, _ = timed(lambda: layer(x), steps, 3)
+    # FP32 controllers and state: the hot-path bytes of hot_path_algorithmic_bytes at 4 bytes per element
+    cfg = c1_config()
+    hot = 2 * hot_path_algorithmic_bytes(cfg, 1, 512)
     return {'tokens_per_s': round(512 / sec, 1), 'ms_per_forward': round(sec * 1e3, 4),
+            'hot_path_roofline_frac': round(hot / sec / 1e9 / HBM_PEAK_GBPS, 6),
+            'roofline_note': 'host-bound: ~15 launches of microseconds for 512 tokens',
             'config': 'C1: batch 1, T 512, d_model 512, H4, v64, J256 (16x16), S8, K8, FP32, FP32 state'}
 
 
@@ -711,7 +844,10 @@ def main():
     layer = BankedDeltaMemory(cfg, layer_id=0, seed=0).to(device=device, dtype=torch.bfloat16)
     if args.only:
         run = {'c2-forward': lambda: c2_forward_only(layer, device, batch, time_, args.steps),
-               'c3': lambda: decode_bench(layer, device, args.decode_steps), 'c4': lambda: c4_forward(device),
+               'c3': lambda: decode_bench(layer, device, args.decode_steps),
+               'c3-kernel': lambda: decode_bench(layer, device, args.decode_steps, legs=(args.c3_routes,),
+                                                 full_step=False),
+               'c4': lambda: c4_forward(device), 'c4-module': lambda: c4_forward(device, steps=3, policy='module'),
                'c5': lambda: c5_training(device),
                'prefill': lambda: full_layer_prefill(layer, device, batch, time_, max(3, args.steps // 4)),
                'lm': lambda: whole_model(device, args.lm_context, tune=args.lm_gemm_tuning == 'on'),
@@ -786,7 +922,8 @@ def main():
                                '+ final BF16 state', 'state_rounding_interval': ROUND_INTERVAL, 'batch': batch, 'seq_len': time_, 'd_model': cfg.dim,
                    'heads': cfg.num_heads, 'bank_count': j, 'bank_size': cfg.bank_size,
                    'selected_banks': kk, 'head_value_width': cfg.head_value_width},
-        'roofline': {'bound': 'hbm', 'kernel': 'bdm_forward (segment_order_kernel + lazy_forward_kernel + ordered_combine_kernel)',
+        'roofline': {'bound': 'hbm', 'kernel': ('bdm_forward (segment_order_kernel, lazy_forward_kernel in head-group '
+                                                'rounds, ordered_combine_kernel per round beside the next)'),
                      'achieved': round(achieved, 1), 'peak': HBM_PEAK_GBPS, 'unit': 'GB/s',
                      'frac': round(achieved / HBM_PEAK_GBPS, 4),
                      'traffic': traffic.get('bytes_per_launch') if traffic else None,
@@ -796,7 +933,7 @@ def main():
                      'launch_ms': round(fwd_ms, 4), 'algorithmic_bytes': fwd_bytes},
         'hot_path_roofline_frac': round(hot_bytes / sec / 1e9 / HBM_PEAK_GBPS, 4),
         'recurrence': recurrence_roofline(cfg, batch, time_, rec_ms),
-        'combine': combine_roofline(cfg, batch, time_, comb_ms),
+        'combine': combine_exposed(cfg, batch, time_, comb_ms),
         'front_end_ms': round(front_ms, 4),
         'timing': ('ms_per_step: wall clock over the timed steps, no events inside; launch_ms, recurrence, '
                    f'combine and front_end_ms: events of {prof_steps} further steps'),
@@ -811,6 +948,8 @@ def main():
         result['decode_c3'] = decode_bench(layer, device, args.decode_steps)
         progress('skewed forward C4')
         result['forward_c4'] = c4_forward(device)
+        progress('skewed forward C4, module policy')
+        result['forward_c4_module_policy'] = c4_forward(device, steps=3, policy='module')
         progress('training C5')
         result['training_c5'] = c5_training(device)
         progress('whole model L16/D2048', args.lm_context)

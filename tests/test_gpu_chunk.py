@@ -1,5 +1,5 @@
-"""The matrix-core recurrence (chunk_forward.hip) against the oracle and the
-vector-ALU recurrence on the same inputs.
+"""The matrix-core recurrence (chunk_forward.hip, FP32 MFMA) against the
+oracle and the vector-ALU recurrence on the same inputs.
 
 The matrix-core path runs S = 8 with BF16 controllers and the state rounded
 to BF16 every 16 events (the reference module forward's policy at H > 1,
@@ -122,16 +122,25 @@ def test_chunk_forward_decay_extremes(device, decay):
     assert err_y < TOL and err_f < TOL, (err_y, err_f)
 
 
-def test_chunk_forward_refuses_untested_sizes(device):
-    """Above 1,024 read events the matrix-core form is refused (its worst
-    token measured 1.08 % off the oracle at the full C2 size), before any
-    launch, instead of running outside the tolerance."""
-    batch, time, heads, s, v, j, kk = 1, 160, 1, 8, 128, 16, 8
-    gen = torch.Generator().manual_seed(7100)
+
+def test_chunk_forward_full_size_c2(device):
+    """The C2 geometry (B8 T4096 H8 S8 v128 J256 K8) on the matrix cores:
+    reads and final states of the first and the last sequence against the
+    oracle recurrence, per token, to the forward tolerance."""
+    batch, time, heads, s, v, j, kk = 8, 4096, 8, 8, 128, 256, 8
+    gen = torch.Generator().manual_seed(2027)
     _, ww, wi = routes(batch, time, j, kk, gen)
     _, rw, ri = routes(batch, time, j, kk, gen)
     q, k, v_, g, b, w = controllers(batch, time, heads, s, v, gen)
-    state = initial_state(j, heads, s, v, gen)
-    announce('chunk forward refusal', batch * time * kk)
-    with pytest.raises(NotImplementedError, match='limited to 1024 read events'):
-        run_forward(device, (q, k, v_, g, b, w, wi, ww, ri, rw, state), j, s, kernel='mfma')
+    state = initial_state(j, heads, s, v, gen, scale=0.05)
+    tensors = (q, k, v_, g, b, w, wi, ww, ri, rw, state)
+    announce('chunk forward full size C2')
+    y, final, _ = run_forward(device, tensors, j, s, kernel='mfma')
+    for seq in (0, batch - 1):
+        one = lambda t: t[seq:seq + 1]  # noqa: E731
+        ref_y, ref_final = oracle_reads(*(one(t) for t in (q, k, v_, g, b, w, wi, ww, ri, rw)), state, j,
+                                        routed_decay=True, state_dtype=torch.bfloat16, interval=16,
+                                        return_final=True)
+        err_y, err_f = rel_err(one(y), ref_y), rel_err(one(final), ref_final)
+        print(f'chunk forward C2 sequence {seq}: read err {err_y:.4f}, state err {err_f:.4f}', flush=True)
+        assert err_y < TOL and err_f < TOL, (seq, err_y, err_f)
