@@ -333,6 +333,14 @@ __device__ __forceinline__ float dot_half(uint32_t a, uint32_t b_masked) {
     return r;
 }
 
+// The same with b_masked a wave-uniform value in a scalar register (one
+// scalar operand per VALU instruction).
+__device__ __forceinline__ float dot_half_s(uint32_t a, uint32_t b_masked) {
+    float r;
+    asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "s"(b_masked));
+    return r;
+}
+
 __device__ __forceinline__ float dot_half_acc(float acc, uint32_t a, uint32_t b_masked) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v_t, a), __builtin_bit_cast(bf16x2v_t, b_masked),
                                            acc, false);
@@ -365,6 +373,19 @@ struct GatedValues<bf16_t, CPL> {
     // pw is a BF16 value (the route weight) widened to FP32, so its low 16
     // bits are zero: w * pw is an exact FP32 product, formed by
     // v_dot2_f32_bf16 from the packed w pair and (pw, 0) or (0, pw)
+    // pw_bits: the route weight's FP32 bits, wave-uniform (a scalar register)
+    __device__ __forceinline__ void make_uniform(const RawCols<bf16_t, CPL> &w, const RawCols<bf16_t, CPL> &vv,
+                                                 uint32_t pw_bits) {
+        const uint32_t p_hi = pw_bits, p_lo = pw_bits >> 16;
+#pragma unroll
+        for (int i = 0; i < CPL / 2; ++i) {
+            const float e0 = dot_half_s(w.u[i], p_lo);
+            const float e1 = dot_half_s(w.u[i], p_hi);
+            lo[i] = pack_bf16x2(e0, 0.f);
+            hi[i] = pack_bf16x2(0.f, e1);
+            v[i] = vv.u[i];
+        }
+    }
     __device__ __forceinline__ void make(const RawCols<bf16_t, CPL> &w, const RawCols<bf16_t, CPL> &vv, float pw) {
         const uint32_t p_hi = __float_as_uint(pw), p_lo = p_hi >> 16;
 #pragma unroll
@@ -388,6 +409,10 @@ struct GatedValues<float, CPL> {
     __device__ __forceinline__ void make(const RawCols<float, CPL> &w, const RawCols<float, CPL> &vv, float pw) {
 #pragma unroll
         for (int c = 0; c < CPL; ++c) x[c] = (w.f[c] * pw) * vv.f[c];
+    }
+    __device__ __forceinline__ void make_uniform(const RawCols<float, CPL> &w, const RawCols<float, CPL> &vv,
+                                                 uint32_t pw_bits) {
+        make(w, vv, __uint_as_float(pw_bits));
     }
     __device__ __forceinline__ float add_to(float acc, int c) const { return acc + x[c]; }
 };
@@ -783,11 +808,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     // into the set write k-1 does not use, so no registers are copied.  At a
     // stage start the stage's first write is in set A.
     RawCols<T, CPL> va, wa, vb, wb;
-    // v, w rows of write wk of a stage (its token from s_wtok: one LDS read)
-    auto fetch = [&](int slot, int wk, RawCols<T, CPL> &vv, RawCols<T, CPL> &ww) {
-        const int64_t row = int64_t(__builtin_amdgcn_readfirstlane(s_wtok[slot][wk])) * hw;
+    // v, w rows of a write by its (wave-uniform) token
+    auto fetch_token = [&](int token, RawCols<T, CPL> &vv, RawCols<T, CPL> &ww) {
+        const int64_t row = int64_t(token) * hw;
         vv.load(reinterpret_cast<const T *>(reinterpret_cast<const char *>(p.v + row) + lane_bytes));
         ww.load(reinterpret_cast<const T *>(reinterpret_cast<const char *>(p.w + row) + lane_bytes));
+    };
+    // v, w rows of write wk of a stage (its token from s_wtok: one LDS read)
+    auto fetch = [&](int slot, int wk, RawCols<T, CPL> &vv, RawCols<T, CPL> &ww) {
+        fetch_token(__builtin_amdgcn_readfirstlane(s_wtok[slot][wk]), vv, ww);
     };
     bool prefetched = false;  // the current stage's first write was fetched by the previous stage
     bool in_b = false;        // ... into set B (an odd number of writes ran since)
@@ -819,13 +848,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 
         const int n = __builtin_amdgcn_readfirstlane(s_n[slot]);
         const int nw = __builtin_amdgcn_readfirstlane(s_nw[slot]);
-        const bool eager = __builtin_amdgcn_readfirstlane(s_eager) != 0;
+        const int eager = __builtin_amdgcn_readfirstlane(s_eager);
         const int next_slot = (st + 1) % 3;
         const bool next_has_write = st + 1 < nstages && s_nw[next_slot] > 0;
+        // The stage's event metadata in registers, lane e holding event e's
+        // (write position, write token, route, route weight), each taken to a
+        // scalar register by one v_readlane where an event uses it.
+        const int el = tid & (NE - 1);
+        const int m_wpos = s_wpos[slot][el];
+        const int m_wtok = s_wtok[slot][el];
+        const int m_route = s_route[slot][el];
+        const int m_pw = __float_as_int(s_pw[el]);
 
         auto read_event = [&](int i) {
             if (MODE == 1 && !reads_on) return;  // a read does not change the state (wave-uniform)
-            const int zrow = __builtin_amdgcn_readfirstlane(s_route[slot][i]);
+            const int zrow = __builtin_amdgcn_readlane(m_route, i);
             const float *row = &s_rows[i][lh][0][0];
             float gamma[S];
 #pragma unroll
@@ -847,8 +884,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         // write `wi_` of the stage with its v, w rows in (vc, wc)
         auto write_event = [&](int wi_, const RawCols<T, CPL> &vc, const RawCols<T, CPL> &wc) {
             const float *row = &s_rows[wi_][lh][0][0];
-            const float pw = s_pw[wi_];
-            if (eager) {
+            const uint32_t pw_bits = uint32_t(__builtin_amdgcn_readlane(m_pw, wi_));
+            if (eager != 0) {
                 // hd = diag(d) M first; the update below then uses a and k
                 // (a wave-uniform branch: the stage's form is uniform)
 #pragma unroll
@@ -876,7 +913,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
                 for (int r = 1; r < S; ++r) u[c] = fmaf(nalpha[r], h[r][c], u[c]);
             }
             GatedValues<T, CPL> x;
-            x.make(wc, vc, pw);
+            x.make_uniform(wc, vc, pw_bits);
 #pragma unroll
             for (int c = 0; c < CPL; ++c) {
                 u[c] = x.add_to(u[c], c);
@@ -899,7 +936,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         {
             if (nw > 0) {
                 if (!prefetched) {
-                    fetch(slot, 0, va, wa);
+                    fetch_token(__builtin_amdgcn_readlane(m_wtok, 0), va, wa);
                 } else if (in_b) {
                     va = vb;
                     wa = wb;
@@ -912,20 +949,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
             // the previous set with vmcnt(2) instead of draining these; with
             // no next write, write wk's rows are loaded again (harmless).
             auto fetch_next = [&](int wk, RawCols<T, CPL> &vv, RawCols<T, CPL> &ww) {
-                int fs = slot, fe = wk;
+                int token;
                 if (wk + 1 < nw) {
-                    fe = wk + 1;
+                    token = __builtin_amdgcn_readlane(m_wtok, wk + 1);
                 } else if (next_has_write) {
-                    fs = next_slot;
-                    fe = 0;
+                    token = __builtin_amdgcn_readfirstlane(s_wtok[next_slot][0]);
                     prefetched = true;
+                } else {
+                    token = __builtin_amdgcn_readlane(m_wtok, wk);
                 }
-                fetch(fs, fe, vv, ww);
+                fetch_token(token, vv, ww);
             };
             int i = 0;
 #pragma unroll 1
             for (int wk = 0; wk < nw; wk += 2) {
-                int wi_ = __builtin_amdgcn_readfirstlane(s_wpos[slot][wk]);
+                int wi_ = __builtin_amdgcn_readlane(m_wpos, wk);
                 fetch_next(wk, vb, wb);
 #pragma unroll 1
                 for (; i < wi_; ++i) read_event(i);
@@ -935,7 +973,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
                     in_b = prefetched;
                     break;
                 }
-                wi_ = __builtin_amdgcn_readfirstlane(s_wpos[slot][wk + 1]);
+                wi_ = __builtin_amdgcn_readlane(m_wpos, wk + 1);
                 fetch_next(wk + 1, va, wa);
 #pragma unroll 1
                 for (; i < wi_; ++i) read_event(i);
