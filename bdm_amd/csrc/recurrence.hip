@@ -34,6 +34,15 @@
 #include "chunk_forward.h"
 #include "segment_order.h"
 
+// The raw buffer load and store intrinsics (MUBUF) of the AMDGPU backend, by
+// their intrinsic names (declared at file scope: external linkage).
+typedef int32_t i32x2_t __attribute__((ext_vector_type(2)));
+typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
+__device__ i32x2_t raw_buffer_load_x2(i32x4_t rsrc, int32_t voffset, int32_t soffset,
+                                      int32_t aux) __asm("llvm.amdgcn.raw.buffer.load.v2i32");
+__device__ void raw_buffer_store_x2(i32x2_t data, i32x4_t rsrc, int32_t voffset, int32_t soffset,
+                                    int32_t aux) __asm("llvm.amdgcn.raw.buffer.store.v2i32");
+
 namespace bdm {
 namespace {
 
@@ -295,6 +304,23 @@ __global__ __launch_bounds__(256) void routed_forward_kernel(ForwardParams<T> p)
 // half multiplies a finite neighbour column).  w*p itself is formed the same
 // way, against (p, 0) or (0, p).
 
+// Raw buffer access (MUBUF): a wave-uniform 128-bit resource (base address,
+// no stride, no range limit), a per-lane byte offset in a vector register and
+// a wave-uniform byte offset in a scalar register, so a row address costs no
+// vector instruction.  Offsets are 32-bit: the launcher takes this form only
+// for tensors below 4 GiB.
+constexpr int32_t kBufferNontemporal = 2;  // cache policy bit: nt
+
+__device__ __forceinline__ i32x4_t buffer_resource(const void *base) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    i32x4_t r;
+    r[0] = __builtin_amdgcn_readfirstlane(int32_t(uint32_t(a)));
+    r[1] = __builtin_amdgcn_readfirstlane(int32_t(uint32_t(a >> 32) & 0xffffu));  // stride 0
+    r[2] = -1;                                                                     // records: no limit
+    r[3] = 0x00020000;                                                             // 32-bit data format
+    return r;
+}
+
 // CPL consecutive columns of T kept as raw 32-bit words (BF16 pairs unpacked
 // on use), so a prefetched row costs CPL/2 (BF16) or CPL (FP32) registers.
 template <typename T, int CPL>
@@ -304,6 +330,8 @@ template <int CPL>
 struct RawCols<bf16_t, CPL> {
     static_assert(CPL % 4 == 0, "BF16 column groups of 4");
     uint32_t u[CPL / 2];
+    // through a buffer resource: row at byte soffset, this lane's columns at voffset
+    __device__ __forceinline__ void load_buffer(i32x4_t rsrc, uint32_t voffset, uint32_t soffset);
     __device__ __forceinline__ void load(const bf16_t *p) {
 #pragma unroll
         for (int i = 0; i < CPL / 4; ++i) {
@@ -313,6 +341,16 @@ struct RawCols<bf16_t, CPL> {
         }
     }
 };
+
+template <int CPL>
+__device__ __forceinline__ void RawCols<bf16_t, CPL>::load_buffer(i32x4_t rsrc, uint32_t voffset, uint32_t soffset) {
+#pragma unroll
+    for (int i = 0; i < CPL / 4; ++i) {
+        const i32x2_t q = raw_buffer_load_x2(rsrc, int32_t(voffset + 8 * i), int32_t(soffset), 0);
+        u[2 * i] = uint32_t(q[0]);
+        u[2 * i + 1] = uint32_t(q[1]);
+    }
+}
 
 template <int CPL>
 struct RawCols<float, CPL> {
@@ -494,9 +532,14 @@ __device__ __forceinline__ void load_vec4(const float *p, float4 &out) { out = *
 //          initial state;
 //   MODE 2 runs pieces 1.. of each cut segment from their start states M_q,
 //          with reads; the last piece stores the final state.
-template <typename T, int CPL, int HB, int MODE>
+//
+// BUF: v, w rows are read and read rows written through buffer resources
+// with 32-bit offsets (BF16 controllers; v, w and the read buffer below
+// 4 GiB), which spares the vector address arithmetic of every event.
+template <typename T, int CPL, int HB, int MODE, bool BUF = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void lazy_forward_kernel(
     ForwardParams<T> p) {
+    static_assert(!BUF || (std::is_same<T, bf16_t>::value && CPL == 4), "buffer form: BF16, 4 columns per lane");
     constexpr int S = 8;
     constexpr int NE = kLazyStage;
     // event metadata ring: stage s lives in slot s % 3
@@ -809,15 +852,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     // stage start the stage's first write is in set A.
     RawCols<T, CPL> va, wa, vb, wb;
     // v, w rows of a write by its (wave-uniform) token
+    i32x4_t rsrc_v{}, rsrc_w{}, rsrc_z{};
+    if constexpr (BUF) {
+        rsrc_v = buffer_resource(p.v);
+        rsrc_w = buffer_resource(p.w);
+        rsrc_z = buffer_resource(p.zbuf);
+    }
+    const uint32_t row_bytes = uint32_t(hw) * uint32_t(sizeof(T));  // one token row of v, w or z (BUF)
     auto fetch_token = [&](int token, RawCols<T, CPL> &vv, RawCols<T, CPL> &ww) {
-        const int64_t row = int64_t(token) * hw;
-        vv.load(reinterpret_cast<const T *>(reinterpret_cast<const char *>(p.v + row) + lane_bytes));
-        ww.load(reinterpret_cast<const T *>(reinterpret_cast<const char *>(p.w + row) + lane_bytes));
+        if constexpr (BUF) {
+            const uint32_t off = uint32_t(token) * row_bytes;
+            vv.load_buffer(rsrc_v, lane_bytes, off);
+            ww.load_buffer(rsrc_w, lane_bytes, off);
+        } else {
+            const int64_t row = int64_t(token) * hw;
+            vv.load(reinterpret_cast<const T *>(reinterpret_cast<const char *>(p.v + row) + lane_bytes));
+            ww.load(reinterpret_cast<const T *>(reinterpret_cast<const char *>(p.w + row) + lane_bytes));
+        }
     };
-    // v, w rows of write wk of a stage (its token from s_wtok: one LDS read)
-    auto fetch = [&](int slot, int wk, RawCols<T, CPL> &vv, RawCols<T, CPL> &ww) {
-        fetch_token(__builtin_amdgcn_readfirstlane(s_wtok[slot][wk]), vv, ww);
-    };
+
     bool prefetched = false;  // the current stage's first write was fetched by the previous stage
     bool in_b = false;        // ... into set B (an odd number of writes ran since)
 
@@ -878,14 +931,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
             // nontemporal: the rows are read once, by the combine after the
             // recurrence, and should not displace the v, w rows that the
             // token's other write banks are about to read from L2
-            store_row_nt<CPL>(reinterpret_cast<T *>(reinterpret_cast<char *>(p.zbuf + int64_t(zrow) * hw) + lane_bytes),
-                              z);
+            if constexpr (BUF) {
+                const i32x2_t packed{int32_t(pack_bf16x2(z[0], z[1])), int32_t(pack_bf16x2(z[2], z[3]))};
+                raw_buffer_store_x2(packed, rsrc_z, int32_t(lane_bytes), int32_t(uint32_t(zrow) * row_bytes),
+                                    kBufferNontemporal);
+            } else {
+                store_row_nt<CPL>(
+                    reinterpret_cast<T *>(reinterpret_cast<char *>(p.zbuf + int64_t(zrow) * hw) + lane_bytes), z);
+            }
         };
         // write `wi_` of the stage with its v, w rows in (vc, wc)
         auto write_event = [&](int wi_, const RawCols<T, CPL> &vc, const RawCols<T, CPL> &wc) {
             const float *row = &s_rows[wi_][lh][0][0];
             const uint32_t pw_bits = uint32_t(__builtin_amdgcn_readlane(m_pw, wi_));
-            if (eager != 0) {
+            if (__builtin_amdgcn_readfirstlane(eager) != 0) {
                 // hd = diag(d) M first; the update below then uses a and k
                 // (a wave-uniform branch: the stage's form is uniform)
 #pragma unroll
@@ -993,7 +1052,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
             if constexpr (MODE == 1) pc[r] *= f;
         }
         // metadata of stage st+2 and operands of stage st+1
-        if (tid < 64) decode_order(st + 2, o2);
+        // (wave 0; with one wave per workgroup, unconditionally, so the order
+        // load is consumed on every path and the next stage's load into the
+        // same register does not wait for every outstanding memory access)
+        if (HB == 2 || tid < 64) decode_order(st + 2, o2);
         if (st + 1 < nstages) finish_prep(st + 1);
     }
     if (MODE == 1 && pslot >= 0) {
@@ -1383,15 +1445,47 @@ const OverlapAux *overlap_aux(hipStream_t caller) {
     return &aux[dev];
 }
 
+// The lazy kernel's MODE 0 instance: HB heads per workgroup, buffer form
+// where it applies.
+template <typename T, int CPL>
+const void *mode0_kernel(int hb, bool buf) {
+    if constexpr (std::is_same<T, bf16_t>::value && CPL == 4) {
+        if (buf)
+            return hb == 2 ? reinterpret_cast<const void *>(&lazy_forward_kernel<T, CPL, 2, 0, true>)
+                           : reinterpret_cast<const void *>(&lazy_forward_kernel<T, CPL, 8, 0, true>);
+    }
+    return hb == 2 ? reinterpret_cast<const void *>(&lazy_forward_kernel<T, CPL, 2, 0>)
+                   : reinterpret_cast<const void *>(&lazy_forward_kernel<T, CPL, 8, 0>);
+}
+
+// Whether the v, w rows and the read buffer fit the buffer form's 32-bit
+// byte offsets (BF16 controllers, 4 columns per lane).
+template <typename T, int CPL>
+bool buffer_form(const bdm_forward_args &a) {
+    if (!(std::is_same<T, bf16_t>::value && CPL == 4)) return false;
+    const uint64_t row = uint64_t(a.heads) * uint64_t(a.head_width) * sizeof(T);
+    const uint64_t nt = uint64_t(a.batch) * uint64_t(a.time);
+    const uint64_t reads = nt * uint64_t(a.read_banks > 0 ? a.read_banks : 1);
+    return nt * row < (uint64_t(1) << 32) && reads * row < (uint64_t(1) << 32);
+}
+
+template <typename T>
+int launch_mode0(const void *kernel, dim3 grid, int threads, ForwardParams<T> p, hipStream_t stream) {
+    void *args[] = {&p};
+    const hipError_t err = hipLaunchKernel(kernel, grid, dim3(unsigned(threads)), args, 0, stream);
+    if (err != hipSuccess) return fail(BDM_ERR_LAUNCH, "lazy_forward_kernel: %s", hipGetErrorString(err));
+    return check_launch("lazy_forward_kernel");
+}
+
 // MODE 0 of the lazy kernel as `parts` launches over consecutive head
 // groups (each with its own longest-first rounds), part i on stream i (the
 // caller's, then the auxiliary ones) behind i one-lane gate kernels, each
 // part's combine over its heads' columns after it on the same stream.
 // Phase events: 0 before the first part, 1 after the last part's
 // recurrence, 2 after the join.
-template <typename T, int CPL, int HB>
-int launch_overlapped(const bdm_forward_args &a, ForwardParams<T> p, unsigned nseg, int groups, int threads,
-                      const T *zbuf, const OverlapAux &ax, hipStream_t stream) {
+template <typename T, int CPL>
+int launch_overlapped(const bdm_forward_args &a, ForwardParams<T> p, const void *kernel, unsigned nseg, int groups,
+                      int threads, const T *zbuf, const OverlapAux &ax, hipStream_t stream) {
     const int gpr = p.order_gpr;
     const int parts = overlap_parts((groups + gpr - 1) / gpr, groups);
     if (hipEventRecord(ax.fork, stream) != hipSuccess)
@@ -1408,8 +1502,7 @@ int launch_overlapped(const bdm_forward_args &a, ForwardParams<T> p, unsigned ns
         ForwardParams<T> pr = p;
         pr.group_base = g0;
         pr.order_gpr = min(gpr, g1 - g0);
-        lazy_forward_kernel<T, CPL, HB, 0><<<dim3(nseg, unsigned(g1 - g0)), threads, 0, st>>>(pr);
-        if (int rc = check_launch("lazy_forward_kernel")) return rc;
+        if (int rc = launch_mode0<T>(kernel, dim3(nseg, unsigned(g1 - g0)), threads, pr, st)) return rc;
         if (i == parts - 1)
             if (int rc = record_phase(a, 1, st)) return rc;
         const int h0 = g0 * p.heads_per_block;
@@ -1512,12 +1605,11 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, const PieceBuffers &pb, h
             else
                 lazy_forward_kernel<T, CPL, 8, 2><<<g2, lthreads, 0, stream>>>(p);
         } else {
+            const void *kernel = mode0_kernel<T, CPL>(lazy_hb, buffer_form<T, CPL>(a));
             if (pb.seg_order) {
                 launch_segment_order(a.cu_seqlens, nseg, pb.seg_order, stream);
                 if (int rc = check_launch("segment_order_kernel")) return rc;
                 p.seg_order = pb.seg_order;
-                const void *kernel = lazy_hb == 2 ? reinterpret_cast<const void *>(&lazy_forward_kernel<T, CPL, 2, 0>)
-                                                  : reinterpret_cast<const void *>(&lazy_forward_kernel<T, CPL, 8, 0>);
                 p.order_gpr = order_groups_per_round(kernel, lthreads, nseg, int(grid.y));
                 // rounds whose heads' columns split y in whole 16-byte groups
                 const bool aligned_rounds = (int64_t(p.heads_per_block) * p.width * sizeof(T)) % 16 == 0 &&
@@ -1526,16 +1618,12 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, const PieceBuffers &pb, h
                     if (const OverlapAux *ax = overlap_aux(stream)) {
                         // the shared events are recorded and waited for by one call at a time
                         std::lock_guard<std::mutex> lock(overlap_launch_mutex());
-                        if (lazy_hb == 2)
-                            return launch_overlapped<T, CPL, 2>(a, p, grid.x, int(grid.y), lthreads, zbuf, *ax, stream);
-                        return launch_overlapped<T, CPL, 8>(a, p, grid.x, int(grid.y), lthreads, zbuf, *ax, stream);
+                        return launch_overlapped<T, CPL>(a, p, kernel, grid.x, int(grid.y), lthreads, zbuf, *ax,
+                                                         stream);
                     }
                 }
             }
-            if (lazy_hb == 2)
-                lazy_forward_kernel<T, CPL, 2, 0><<<grid, lthreads, 0, stream>>>(p);
-            else
-                lazy_forward_kernel<T, CPL, 8, 0><<<grid, lthreads, 0, stream>>>(p);
+            if (int rc = launch_mode0<T>(kernel, grid, lthreads, p, stream)) return rc;
         }
         if (int rc = check_launch("lazy_forward_kernel")) return rc;
     } else {
