@@ -295,7 +295,7 @@ __global__ __launch_bounds__(256) void routed_forward_kernel(ForwardParams<T> p)
 // The prep of stage s+1 overlaps the value loop of stage s: its row loads are
 // issued before the value loop and consumed after it, and the packed order of
 // stage s+2 is loaded one stage earlier still (event metadata ring of 3).
-// v and w of the next write are prefetched one write ahead, across stages.
+// v and w of the next write are prefetched one write ahead within a stage.
 //
 // x = bf(w*p) * v: w*p is an exact FP32 product of two BF16 values, rounded
 // to nearest even by v_cvt_pk_bf16_f32; the product bf(w*p) * v is added to
@@ -871,9 +871,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         }
     };
 
-    bool prefetched = false;  // the current stage's first write was fetched by the previous stage
-    bool in_b = false;        // ... into set B (an odd number of writes ran since)
-
     for (int st = 0; st < nstages; ++st) {
         const int slot = st % 3;
         // next stages' loads, in flight during this stage's value loop
@@ -902,8 +899,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         const int n = __builtin_amdgcn_readfirstlane(s_n[slot]);
         const int nw = __builtin_amdgcn_readfirstlane(s_nw[slot]);
         const int eager = __builtin_amdgcn_readfirstlane(s_eager);
-        const int next_slot = (st + 1) % 3;
-        const bool next_has_write = st + 1 < nstages && s_nw[next_slot] > 0;
         // The stage's event metadata in registers, lane e holding event e's
         // (write position, write token, route, route weight), each taken to a
         // scalar register by one v_readlane where an event uses it.
@@ -991,33 +986,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         // Events in packed order, as runs: the reads before each write, then
         // the write, so the state is updated exactly once per iteration and
         // never merged from branches.  Writes alternate between the register
-        // sets A and B (two writes per loop iteration).
+        // sets A and B (two writes per loop iteration).  The stage's first
+        // write is fetched here, into A, not prefetched by the previous stage:
+        // a stage that found it in B would have to copy the set, and the copy
+        // waits for every memory access issued before it.
         {
-            if (nw > 0) {
-                if (!prefetched) {
-                    fetch_token(__builtin_amdgcn_readlane(m_wtok, 0), va, wa);
-                } else if (in_b) {
-                    va = vb;
-                    wa = wb;
-                }
-            }
-            prefetched = false;
-            in_b = false;
-            // the rows of write wk + 1 (of this stage, or the next stage's
-            // first).  Always two loads, so that the compiler can wait for
-            // the previous set with vmcnt(2) instead of draining these; with
-            // no next write, write wk's rows are loaded again (harmless).
+            if (nw > 0) fetch_token(__builtin_amdgcn_readlane(m_wtok, 0), va, wa);
+            // the rows of write wk + 1.  Always two loads, so that the compiler
+            // can wait for the previous set with vmcnt(2) instead of draining
+            // these; with no next write, write wk's rows are loaded again
+            // (harmless).
             auto fetch_next = [&](int wk, RawCols<T, CPL> &vv, RawCols<T, CPL> &ww) {
-                int token;
-                if (wk + 1 < nw) {
-                    token = __builtin_amdgcn_readlane(m_wtok, wk + 1);
-                } else if (next_has_write) {
-                    token = __builtin_amdgcn_readfirstlane(s_wtok[next_slot][0]);
-                    prefetched = true;
-                } else {
-                    token = __builtin_amdgcn_readlane(m_wtok, wk);
-                }
-                fetch_token(token, vv, ww);
+                fetch_token(__builtin_amdgcn_readlane(m_wtok, wk + 1 < nw ? wk + 1 : wk), vv, ww);
             };
             int i = 0;
 #pragma unroll 1
@@ -1028,10 +1008,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
                 for (; i < wi_; ++i) read_event(i);
                 i = wi_ + 1;
                 write_event(wi_, va, wa);
-                if (wk + 1 >= nw) {
-                    in_b = prefetched;
-                    break;
-                }
+                if (wk + 1 >= nw) break;
                 wi_ = __builtin_amdgcn_readlane(m_wpos, wk + 1);
                 fetch_next(wk + 1, va, wa);
 #pragma unroll 1
