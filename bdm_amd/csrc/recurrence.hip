@@ -293,8 +293,9 @@ __global__ __launch_bounds__(256) void routed_forward_kernel(ForwardParams<T> p)
 //    registers and runs the stage's events in order, reading the row
 //    operands from LDS by broadcast.
 // The prep of stage s+1 overlaps the value loop of stage s: its row loads are
-// issued before the value loop and consumed after it, and the packed order of
-// stage s+2 is loaded one stage earlier still (event metadata ring of 3).
+// issued before the value loop and consumed after it; the packed order is
+// loaded and decoded four stages at a time, two such groups ahead of its use
+// (an event metadata ring of 8 stages).
 // v and w of the next write are prefetched one write ahead within a stage.
 //
 // x = bf(w*p) * v: w*p is an exact FP32 product of two BF16 values, rounded
@@ -542,14 +543,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     static_assert(!BUF || (std::is_same<T, bf16_t>::value && CPL == 4), "buffer form: BF16, 4 columns per lane");
     constexpr int S = 8;
     constexpr int NE = kLazyStage;
-    // event metadata ring: stage s lives in slot s % 3
-    __shared__ int s_tok[3][NE];
-    __shared__ int s_route[3][NE];
-    __shared__ int s_wpos[3][NE + 1];  // stage positions of the writes, then n
-    __shared__ int s_wtok[3][NE];      // tokens of the writes, in write order
-    __shared__ int s_nw[3];
-    __shared__ int s_n[3];
-    __shared__ unsigned s_rmask[3];    // bit e: event e of the stage is a read
+    // Event metadata ring: stage s lives in slot s % kRing.  The packed order
+    // is loaded and decoded kGroup stages at a time (64 events, one per lane
+    // of wave 0), two groups ahead of their use.
+    constexpr int kGroup = 4, kRing = 2 * kGroup;
+    __shared__ int s_tok[kRing][NE];
+    __shared__ int s_route[kRing][NE];
+    __shared__ int s_wpos[kRing][NE + 1];  // stage positions of the writes, then n
+    __shared__ int s_wtok[kRing][NE];      // tokens of the writes, in write order
+    __shared__ int s_nw[kRing];
+    __shared__ int s_n[kRing];
+    __shared__ unsigned s_rmask[kRing];    // bit e: event e of the stage is a read
     // Row operands of the current stage (written by the prep of a stage after
     // every wave has left the previous stage's value loop): lazy [0] = -alpha,
     // [1] = beta; eager [0] = -a, [1] = k, [2] = d; a read [0] = gamma.
@@ -683,46 +687,47 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         return (void *)(__attribute__((address_space(1))) char *)(s_ptr[which]);
     };
 
-    // ---- metadata of a stage from its packed order entries (lanes 0..15)
-    auto load_order = [&](int stage) -> int {
-        const int64_t pos = start + int64_t(stage) * NE + tid;
-        if (tid < NE && stage < nstages && pos < end) return int(static_cast<const int64_t *>(lds_ptr(P_ORDER))[pos]);
+    // ---- metadata of a group of kGroup stages from its packed order entries
+    //      (lane e of wave 0: event e % 16 of the group's stage e / 16)
+    auto load_group = [&](int group) -> int {
+        const int64_t pos = start + int64_t(group) * (kGroup * NE) + tid;
+        if (tid < kGroup * NE && pos < end) return int(static_cast<const int64_t *>(lds_ptr(P_ORDER))[pos]);
         return -1;
     };
-    auto decode_order = [&](int stage, int o) {
-        // lanes 0..15 of wave 0; the other lanes of the wave take part in the ballot
-        const int slot = stage % 3;
+    auto decode_group = [&](int group, int o) {
+        const int sub = (tid >> 4) & (kGroup - 1), e = tid & (NE - 1);
+        const int slot = (group * kGroup + sub) % kRing;
         const bool live = o >= 0;
         o = o < 0 ? 0 : (o >= events ? events - 1 : o);
         const bool rd = o >= write_events;
         const int route = rd ? o - write_events : o;
-        const uint64_t live_mask = __ballot(live && tid < NE);
-        const uint64_t read_mask = __ballot(live && rd && tid < NE);
+        const uint64_t live_mask = __ballot(live);
+        const uint64_t read_mask = __ballot(live && rd);
         const uint64_t write_mask = live_mask & ~read_mask;
-        if (tid < NE) {
-            // (a wave-uniform choice: the shift when KW = KR = 2^k, else a division)
-            s_tok[slot][tid] = p.k_shift >= 0 ? int(uint32_t(route) >> p.k_shift)
-                                              : int(uint32_t(route) / uint32_t(rd ? p.kr : p.kw));
-            s_route[slot][tid] = route;
-            if (live && !rd) {
-                const int wk = __popcll(write_mask & ((uint64_t(1) << tid) - 1));
-                s_wpos[slot][wk] = tid;
-                s_wtok[slot][wk] = s_tok[slot][tid];
-            }
+        const uint64_t stage_bits = uint64_t(0xffff) << (NE * sub);
+        // (a wave-uniform choice: the shift when KW = KR = 2^k, else a division)
+        const int tok = p.k_shift >= 0 ? int(uint32_t(route) >> p.k_shift)
+                                       : int(uint32_t(route) / uint32_t(rd ? p.kr : p.kw));
+        s_tok[slot][e] = tok;
+        s_route[slot][e] = route;
+        if (live && !rd) {
+            const int wk = __popcll(write_mask & stage_bits & ((uint64_t(1) << (tid & 63)) - 1));
+            s_wpos[slot][wk] = e;
+            s_wtok[slot][wk] = tok;
         }
-        if (tid == 0) {
-            const int n = __popcll(live_mask), nw = __popcll(write_mask);
+        if (e == 0) {
+            const int n = __popcll(live_mask & stage_bits), nw = __popcll(write_mask & stage_bits);
             s_n[slot] = n;
             s_nw[slot] = nw;
             s_wpos[slot][nw] = n;
-            s_rmask[slot] = unsigned(read_mask);
+            s_rmask[slot] = unsigned((read_mask >> (NE * sub)) & 0xffffu);
         }
     };
 
     // ---- prep loads of a stage (issued before, consumed after a value loop)
     PrepLoads<T> pl{};
     auto issue_prep = [&](int stage) {
-        const int slot = stage % 3;
+        const int slot = stage % kRing;
         if (stage >= nstages || !prep_head || pe >= s_n[slot]) return;
         const bool rd = (s_rmask[slot] >> pe) & 1u;
         const int64_t row = (int64_t(s_tok[slot][pe]) * p.s_heads + (head0 + ph) / p.split) * S + 4 * half;
@@ -747,7 +752,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     };
     // compute the row operands of `stage` into buffer stage & 1 (two barriers)
     auto finish_prep = [&](int stage) {
-        const int slot = stage % 3;
+        const int slot = stage % kRing;
         const int n = s_n[slot];
         const bool live = prep_head && pe < n && stage < nstages;
         const bool rd = live && ((s_rmask[slot] >> pe) & 1u);
@@ -836,10 +841,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     }
     if (tid < 2) s_flag[tid] = 0;
     {
-        const int o0 = load_order(0), o1 = load_order(1);
-        if (tid < 64) {
-            decode_order(0, o0);
-            decode_order(1, o1);
+        const int o0 = load_group(0), o1 = load_group(1);
+        if (HB == 2 || tid < 64) {
+            decode_group(0, o0);
+            decode_group(1, o1);
         }
     }
     __syncthreads();
@@ -871,10 +876,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         }
     };
 
-    for (int st = 0; st < nstages; ++st) {
-        const int slot = st % 3;
-        // next stages' loads, in flight during this stage's value loop
-        const int o2 = load_order(st + 2);
+    // Groups of kGroup stages: the packed order of the group after next is
+    // loaded at a group's start and decoded after its last stage, so the load
+    // is consumed on every path through the loop.
+#pragma unroll 1
+    for (int st0 = 0; st0 < nstages; st0 += kGroup) {
+    const int o_group = load_group(st0 / kGroup + 2);
+    const int st1 = min(nstages, st0 + kGroup);
+#pragma unroll 1
+    for (int st = st0; st < st1; ++st) {
+        const int slot = st % kRing;
+        // next stage's prep loads, in flight during this stage's value loop
         issue_prep(st + 1);
 
         // The state at the stage start (folded at the end of the previous
@@ -1028,12 +1040,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
             for (int c = 0; c < CPL; ++c) h[r][c] *= f;
             if constexpr (MODE == 1) pc[r] *= f;
         }
-        // metadata of stage st+2 and operands of stage st+1
-        // (wave 0; with one wave per workgroup, unconditionally, so the order
-        // load is consumed on every path and the next stage's load into the
-        // same register does not wait for every outstanding memory access)
-        if (HB == 2 || tid < 64) decode_order(st + 2, o2);
+        // operands of stage st+1
         if (st + 1 < nstages) finish_prep(st + 1);
+    }
+    // the metadata of the group after next, into this group's slots (wave 0;
+    // the barriers of the stages in between publish it)
+    if (HB == 2 || tid < 64) decode_group(st0 / kGroup + 2, o_group);
     }
     if (MODE == 1 && pslot >= 0) {
         // R_q and P_q of this piece (a first piece: its end state and P = 0,
