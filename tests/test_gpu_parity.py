@@ -528,6 +528,38 @@ def test_segment_order_bit_identical(device, monkeypatch):
     assert torch.equal(f_lpt, f_ref)
 
 @pytest.mark.gpu
+@pytest.mark.parametrize('size', ['small', 'c2'])
+def test_combine_fold_bit_exact(device, size):
+    """The ordered read combine against a CPU fold of the same read rows: each
+    token's KR rows (from the forward's workspace) added in increasing bank id
+    (route slot for equal banks), each sum formed in FP32 and rounded to BF16,
+    as torch adds BF16 tensors (role_bank_dispatch.py:209-215).  Bit for bit,
+    for every token and column."""
+    from bdm_amd import ops
+    gen = torch.Generator().manual_seed(79)
+    batch, time, heads, s, v, j, kk = (2, 300, 2, 8, 128, 16, 8) if size == 'small' else (8, 4096, 8, 8, 128, 256, 8)
+    _, ww, wi = routes(batch, time, j, kk, gen)
+    _, rw, ri = routes(batch, time, j, kk, gen)
+    q, k, v_, g, b, w = controllers(batch, time, heads, s, v, gen)
+    state = initial_state(j, heads, s, v, gen, scale=0.05)
+    dev = [t.to(device) for t in (q, k, v_, g, b, w, wi, ww, ri, rw, state)]
+    meta = ops.dispatch_build(dev[6], dev[8], j)
+    nt, hv = batch * time, heads * v
+    ws = torch.zeros(nt * kk * hv * 2 + (1 << 20) + batch * j * 4, device=device, dtype=torch.uint8)
+    announce('combine fold bit-exact', size)
+    y = ops.routed_forward(*dev[:10], dev[10], meta, bank_count=j, scale=s ** -0.5, routed_decay=True,
+                           round_interval=16, workspace=ws)
+    torch.cuda.synchronize()
+    rows = ws[:nt * kk * hv * 2].view(torch.bfloat16).view(nt, kk, hv).cpu()
+    banks = ri.reshape(nt, kk)
+    order = torch.sort(banks * kk + torch.arange(kk), dim=-1).indices  # bank, then slot
+    total = torch.zeros(nt, hv, dtype=torch.bfloat16)
+    for step in range(kk):
+        total = total + rows[torch.arange(nt), order[:, step]]  # BF16 + BF16: FP32 sum, rounded
+    assert torch.equal(y.reshape(nt, hv).cpu().view(torch.int16), total.view(torch.int16))
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize('snapshots', [False, True], ids=['prefill', 'training'])
 def test_combine_overlap_bit_identical(device, monkeypatch, snapshots):
     """At C2 size the head-group rounds run as separate launches on two
