@@ -36,6 +36,8 @@ EXPORTED_SYMBOLS = (
     'bdm_dispatch_workspace_size_ex',
     'bdm_dispatch_build_static',
     'bdm_router_select_pair',
+    'bdm_route_dispatch_workspace_size',
+    'bdm_route_dispatch',
 )
 
 _i32, _i64, _f32, _vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_void_p
@@ -55,6 +57,19 @@ class ForwardArgs(ctypes.Structure):
         ('routed_decay', _i32), ('round_interval', _i32), ('scale', _f32),
         ('snapshots', _vp), ('snapshot_interval', _i32), ('snapshot_dtype', _i32),
         ('phase_events', _vp * 3),
+        ('segment_order', _vp),
+    ]
+
+
+class RouteDispatchArgs(ctypes.Structure):
+    """Mirror of ``bdm_route_dispatch_args``."""
+    _fields_ = [
+        ('write_scores', _vp), ('write_stride', _i64), ('read_scores', _vp), ('read_stride', _i64),
+        ('score_dtype', _i32), ('batch', _i64), ('time', _i64),
+        ('factor_first', _i32), ('factor_second', _i32), ('selected', _i32),
+        ('write_weights', _vp), ('write_indices', _vp), ('read_weights', _vp), ('read_indices', _vp),
+        ('order', _vp), ('inverse', _vp), ('tokens', _vp), ('cu_seqlens', _vp), ('status', _vp),
+        ('segment_order', _vp),
     ]
 
 
@@ -219,6 +234,10 @@ def library() -> ctypes.CDLL:
     lib.bdm_swiglu_backward.restype = _i32
     lib.bdm_dispatch_workspace_size_ex.argtypes = [_i64, _i64, _i32, _i32, _i32]
     lib.bdm_dispatch_workspace_size_ex.restype = _size_t
+    lib.bdm_route_dispatch_workspace_size.argtypes = [ctypes.POINTER(RouteDispatchArgs)]
+    lib.bdm_route_dispatch_workspace_size.restype = _size_t
+    lib.bdm_route_dispatch.argtypes = [ctypes.POINTER(RouteDispatchArgs), _vp, _size_t, _vp]
+    lib.bdm_route_dispatch.restype = _i32
     return lib
 
 

@@ -30,6 +30,8 @@
 #include <mutex>
 
 #include "bdm_common.h"
+#include "route_dispatch.h"
+#include "segment_order.h"
 
 namespace bdm {
 namespace {
@@ -141,6 +143,8 @@ __global__ __launch_bounds__(kScanWaves * kWave) void dispatch_tile_scan(Dispatc
 // the tile's events goes to start + its tile's offset in the segment + its
 // rank in the tile's mask.  Batch b's segments start at b*T*(KW+KR): every
 // token adds exactly KW+KR events to its own batch.
+//
+// inverse and tokens may be null (not stored).
 __global__ __launch_bounds__(512) void dispatch_scatter(const int64_t *__restrict__ wi,
                                                         const int64_t *__restrict__ ri, DispatchGeometry g,
                                                         const int32_t *__restrict__ tile_base,
@@ -195,8 +199,8 @@ __global__ __launch_bounds__(512) void dispatch_scatter(const int64_t *__restric
         pos = pos < 0 ? 0 : (pos >= events ? events - 1 : pos);
         const int64_t original = j < g.kw ? token * g.kw + j : g.nt * g.kw + token * g.kr + (j - g.kw);
         order[pos] = original;
-        inverse[original] = pos;
-        tokens[pos] = token;
+        if (inverse) inverse[original] = pos;
+        if (tokens) tokens[pos] = token;
     }
 }
 
@@ -266,12 +270,14 @@ __global__ void dispatch_clear_status(int32_t *status) {
 // element written before it is read.
 int launch_mask_dispatch(const int64_t *wi, const int64_t *ri, const DispatchGeometry &g, int64_t *order,
                          int64_t *inverse, int64_t *tokens, int64_t *cu_seqlens, int32_t *status, void *scratch,
-                         hipStream_t s) {
+                         hipStream_t s, bool counted = false) {
     auto *tile_counts = static_cast<int32_t *>(scratch);
     const size_t mask_bytes = size_t(g.banks) * sizeof(unsigned long long);
     const dim3 tiles(unsigned(g.tiles), unsigned(g.batch));
-    dispatch_tile_count<<<tiles, 512, mask_bytes, s>>>(wi, ri, g, tile_counts, status);
-    if (int rc = check_launch("dispatch_tile_count")) return rc;
+    if (!counted) {  // (the fused routing pass already stored the per-tile counts)
+        dispatch_tile_count<<<tiles, 512, mask_bytes, s>>>(wi, ri, g, tile_counts, status);
+        if (int rc = check_launch("dispatch_tile_count")) return rc;
+    }
     int32_t *totals = tile_counts + int64_t(g.batch) * g.tiles * g.banks;
     dispatch_tile_scan<<<dim3(unsigned(g.batch), unsigned((g.banks + kWave - 1) / kWave)), kScanWaves * kWave, 0,
                          s>>>(g, tile_counts, totals, status);
@@ -447,4 +453,74 @@ extern "C" int bdm_dispatch_build_static(const int64_t *write_indices, const int
     const DispatchGeometry g{batch, time, nt, write_banks, read_banks, bank_count, int(tiles_per_batch(time))};
     return launch_mask_dispatch(write_indices, read_indices, g, order, inverse, tokens, cu_seqlens, status, ptr,
                                 as_stream(stream));
+}
+
+// ---- routing and dispatch in one call
+
+extern "C" size_t bdm_route_dispatch_workspace_size(const bdm_route_dispatch_args *a) {
+    if (!a) return 0;
+    return bdm_dispatch_workspace_size_ex(a->batch, a->time, a->factor_first * a->factor_second, a->selected,
+                                          a->selected);
+}
+
+extern "C" int bdm_route_dispatch(const bdm_route_dispatch_args *a, void *workspace, size_t workspace_bytes,
+                                  void *stream) {
+    using namespace bdm;
+    if (!a) return fail(BDM_ERR_INVALID, "route_dispatch: null args");
+    if (a->batch <= 0 || a->time <= 0 || a->factor_first <= 0 || a->factor_second <= 0 || a->selected <= 0)
+        return fail(BDM_ERR_INVALID, "route_dispatch: bad geometry batch=%lld time=%lld factors %d x %d, %d banks",
+                    (long long)a->batch, (long long)a->time, a->factor_first, a->factor_second, a->selected);
+    if (!a->write_scores || !a->read_scores || !a->write_weights || !a->read_weights || !a->write_indices ||
+        !a->read_indices || !a->order || !a->cu_seqlens || !a->status)
+        return fail(BDM_ERR_INVALID, "route_dispatch: null pointer");
+    const int64_t banks64 = int64_t(a->factor_first) * a->factor_second;
+    if (banks64 > INT32_MAX) return fail(BDM_ERR_UNSUPPORTED, "route_dispatch: too many banks");
+    const int32_t banks = int32_t(banks64);
+    const int64_t nt = a->batch * a->time;
+    const int k = a->selected;
+    const size_t need = bdm_route_dispatch_workspace_size(a);
+    if (!workspace || workspace_bytes < need)
+        return fail(BDM_ERR_WORKSPACE, "route_dispatch: workspace %zu < %zu bytes", workspace_bytes, need);
+    hipStream_t s = as_stream(stream);
+    const void *scores[2] = {a->write_scores, a->read_scores};
+    const int64_t strides[2] = {a->write_stride, a->read_stride};
+    void *weights[2] = {a->write_weights, a->read_weights};
+    int64_t *indices[2] = {a->write_indices, a->read_indices};
+    const bool fused = banks <= kMaxBanks && nt * 2 * k < (int64_t(1) << 31) && a->batch <= 65535 &&
+                       route_tile_count_supported(scores, strides, weights, indices, a->score_dtype,
+                                                  a->factor_first, a->factor_second, k);
+    if (!fused) {
+        // the router and the dispatch as separate launches
+        if (int rc = bdm_router_select_pair(a->write_scores, a->write_stride, a->read_scores, a->read_stride,
+                                            a->score_dtype, nt, a->factor_first, a->factor_second, k,
+                                            a->write_weights, a->write_indices, a->read_weights, a->read_indices,
+                                            stream))
+            return rc;
+        if (a->inverse && a->tokens) {
+            if (int rc = bdm_dispatch_build(a->write_indices, a->read_indices, a->batch, a->time, k, k, banks,
+                                            a->order, a->inverse, a->tokens, a->cu_seqlens, a->status, workspace,
+                                            workspace_bytes, stream))
+                return rc;
+        } else {
+            if (banks > kMaxBanks)
+                return fail(BDM_ERR_UNSUPPORTED, "route_dispatch: %d banks need the inverse and token maps", banks);
+            const DispatchGeometry g{a->batch, a->time, nt, k, k, banks, int(tiles_per_batch(a->time))};
+            if (int rc = launch_mask_dispatch(a->write_indices, a->read_indices, g, a->order, a->inverse, a->tokens,
+                                              a->cu_seqlens, a->status, workspace, s))
+                return rc;
+        }
+    } else {
+        const DispatchGeometry g{a->batch, a->time, nt, k, k, banks, int(tiles_per_batch(a->time))};
+        if (int rc = launch_route_tile_count(scores, strides, weights, indices, a->batch, a->time, a->factor_first,
+                                             a->factor_second, static_cast<int32_t *>(workspace), a->status, s))
+            return rc;
+        if (int rc = launch_mask_dispatch(a->write_indices, a->read_indices, g, a->order, a->inverse, a->tokens,
+                                          a->cu_seqlens, a->status, workspace, s, true))
+            return rc;
+    }
+    if (a->segment_order && order_geometry(a->batch * int64_t(banks))) {
+        launch_segment_order(a->cu_seqlens, a->batch * int64_t(banks), a->segment_order, s);
+        return check_launch("segment_order_kernel");
+    }
+    return BDM_OK;
 }

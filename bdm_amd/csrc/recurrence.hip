@@ -1290,6 +1290,7 @@ struct PieceBuffers {
     float *pstate = nullptr, *ptrans = nullptr;
     int64_t max_pieces = 0;  // 0: the path is off
     int *seg_order = nullptr;  // null: segments in bank order
+    bool order_given = false;  // seg_order holds the caller's order (bdm_route_dispatch): no ranking launch
 };
 
 // Profiling events of bdm_forward (phase_events): 0 before the recurrence,
@@ -1571,8 +1572,10 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, const PieceBuffers &pb, h
             piece_table_kernel<<<1, 1024, 0, stream>>>(a.cu_seqlens, int(nseg), pb.items, pb.count);
             if (int rc = check_launch("piece_table_kernel")) return rc;
             if (pb.seg_order) {
-                launch_segment_order(a.cu_seqlens, nseg, pb.seg_order, stream);
-                if (int rc = check_launch("segment_order_kernel")) return rc;
+                if (!pb.order_given) {
+                    launch_segment_order(a.cu_seqlens, nseg, pb.seg_order, stream);
+                    if (int rc = check_launch("segment_order_kernel")) return rc;
+                }
                 p.seg_order = pb.seg_order;
             }
             // MODE 1: the pieces (in the first blocks, so the long ones start
@@ -1596,8 +1599,10 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, const PieceBuffers &pb, h
         } else {
             const void *kernel = mode0_kernel<T, CPL>(lazy_hb, buffer_form<T, CPL>(a));
             if (pb.seg_order) {
-                launch_segment_order(a.cu_seqlens, nseg, pb.seg_order, stream);
-                if (int rc = check_launch("segment_order_kernel")) return rc;
+                if (!pb.order_given) {
+                    launch_segment_order(a.cu_seqlens, nseg, pb.seg_order, stream);
+                    if (int rc = check_launch("segment_order_kernel")) return rc;
+                }
                 p.seg_order = pb.seg_order;
                 p.order_gpr = order_groups_per_round(kernel, lthreads, nseg, int(grid.y));
                 // rounds whose heads' columns split y in whole 16-byte groups
@@ -1812,8 +1817,11 @@ extern "C" int bdm_forward(const bdm_forward_args *a, void *workspace, size_t wo
         at += round256(n * a->heads * 8 * size_t(a->head_width) * 4);
         pb.ptrans = reinterpret_cast<float *>(at);
     }
-    if (order_path(*a) && order_enabled())
+    if (order_path(*a) && order_enabled()) {
         pb.seg_order = reinterpret_cast<int *>(ws + forward_zbuf_bytes(a) + forward_piece_bytes(a));
+        pb.order_given = a->segment_order != nullptr;
+        if (pb.order_given) pb.seg_order = const_cast<int *>(a->segment_order);
+    }
     if (a->ctrl_dtype == BDM_BF16)
         return dispatch_forward<bf16_t>(*a, static_cast<bf16_t *>(workspace), pb, s);
     return dispatch_forward<float>(*a, static_cast<float *>(workspace), pb, s);

@@ -19,6 +19,7 @@
 
 #include "bdm_common.h"
 #include "router_ops.h"
+#include "route_dispatch.h"
 
 namespace bdm {
 namespace {
@@ -412,15 +413,15 @@ __global__ __launch_bounds__(256) void router_quad_kernel(RouterRoles<bf16_t> ro
 // candidate pairs of flattened index 0..9 and lane 1 the other 10, each
 // sorts its 10 into a top 8, and one swap and merge leaves the selection in
 // both lanes; lane h keeps slots 4h..4h+3.
+// One row's routes, with two lanes (h = 0, 1: adjacent lanes of a quad) per
+// row: lane h returns selection slots 4h .. 4h + 3 (bank ids and BF16 weight
+// bits).  ids: this lane's 16 bytes of LDS (the row's factor ids, read back
+// by both lanes of the pair).
 template <int NB>
-__global__ __launch_bounds__(256) void router_pair_kernel(RouterRoles<bf16_t> roles, int64_t rows, int j1, int j2) {
-    const int role = int(blockIdx.y);
-    const int h = int(threadIdx.x) & 1;
-    const int64_t row_raw = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) >> 1;
-    const bool live = row_raw < rows;  // uniform over a pair
-    const int64_t row = live ? row_raw : rows - 1;
+__device__ __forceinline__ void route_pair_row(const bf16_t *zrow, int j1, int j2, int h, uint32_t *ids_lds,
+                                               int64_t (&bank)[4], uint32_t (&wbits)[4]) {
     const int jf = h ? j2 : j1;
-    const bf16_t *zf = roles.scores[role] + row * roles.stride[role] + (h ? j1 : 0);
+    const bf16_t *zf = zrow + (h ? j1 : 0);
 
     // (1) top 8 of factor h
     uint4 raw[NB];
@@ -452,7 +453,6 @@ __global__ __launch_bounds__(256) void router_pair_kernel(RouterRoles<bf16_t> ro
         f0[p] = h ? other : top[p];
         f1[p] = h ? top[p] : other;
     }
-    __shared__ uint32_t s_ids[256][4];
     uint32_t packed[4];
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
@@ -461,7 +461,7 @@ __global__ __launch_bounds__(256) void router_pair_kernel(RouterRoles<bf16_t> ro
         packed[w] = uint32_t(entry_id(f[p0])) | uint32_t(entry_id(f[p0 + 1])) << 8 |
                     uint32_t(entry_id(f[p0 + 2])) << 16 | uint32_t(entry_id(f[p0 + 3])) << 24;
     }
-    *reinterpret_cast<uint4 *>(s_ids[threadIdx.x]) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    *reinterpret_cast<uint4 *>(ids_lds) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
 
     // (2) candidates: lane 0 (0,0..7), (1,0), (1,1); lane 1 (1,2), (1,3),
     // (2,0), (2,1), (3,0), (3,1), (4..7,0); ids i*8 + l, sums in BF16
@@ -511,15 +511,26 @@ __global__ __launch_bounds__(256) void router_pair_kernel(RouterRoles<bf16_t> ro
     float total = 0.f;
 #pragma unroll
     for (int p = 0; p < 8; ++p) total += ex[p];
-    const uint8_t *ids = reinterpret_cast<const uint8_t *>(s_ids[threadIdx.x]);
-    int64_t bank[4];
-    uint32_t wbits[4];
+    const uint8_t *ids = reinterpret_cast<const uint8_t *>(ids_lds);
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const int cid = entry_id(e[k]) & 63;
         bank[k] = int64_t(ids[cid >> 3]) * j2 + int64_t(ids[8 + (cid & 7)]);
         wbits[k] = __float_as_uint(round_to<bf16_t>(xs[k] / total)) >> 16;
     }
+}
+
+template <int NB>
+__global__ __launch_bounds__(256) void router_pair_kernel(RouterRoles<bf16_t> roles, int64_t rows, int j1, int j2) {
+    const int role = int(blockIdx.y);
+    const int h = int(threadIdx.x) & 1;
+    const int64_t row_raw = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) >> 1;
+    const bool live = row_raw < rows;  // uniform over a pair
+    const int64_t row = live ? row_raw : rows - 1;
+    __shared__ uint32_t s_ids[256][4];
+    int64_t bank[4];
+    uint32_t wbits[4];
+    route_pair_row<NB>(roles.scores[role] + row * roles.stride[role], j1, j2, h, s_ids[threadIdx.x], bank, wbits);
     if (live) {
         *reinterpret_cast<uint2 *>(roles.weights[role] + row * 8 + 4 * h) =
             make_uint2(wbits[0] | wbits[1] << 16, wbits[2] | wbits[3] << 16);
@@ -660,7 +671,87 @@ int route(const void *const *scores, const int64_t *strides, void *const *weight
     }
 }
 
+// Routing fused with the dispatch's tile count (bdm_route_dispatch): one
+// workgroup per tile of 32 tokens of one sequence routes the tile's rows for
+// both roles (two lanes per row, route_pair_row), stores the routes, and sets
+// bit 2 t + role of the LDS mask of every selected bank (t the token in the
+// tile, role 1 for a read), as dispatch_tile_count does from stored routes;
+// the popcount of a bank's mask is the tile's count of events in it.
+template <int NB>
+__global__ __launch_bounds__(128) void route_tile_count_kernel(RouterRoles<bf16_t> roles, int64_t time, int tiles,
+                                                               int j1, int j2, int32_t *__restrict__ tile_counts,
+                                                               int32_t *__restrict__ status) {
+    extern __shared__ unsigned long long masks[];  // one per bank
+    __shared__ uint32_t s_ids[128][4];
+    const int banks = j1 * j2;
+    const int tile = int(blockIdx.x), b = int(blockIdx.y);
+    const int t = int(threadIdx.x), role = t >> 6, tl = (t & 63) >> 1, h = t & 1;
+    for (int x = t; x < banks; x += 128) masks[x] = 0ull;
+    const int64_t tt = int64_t(tile) * 32 + tl;
+    const bool live = tt < time;  // uniform over a pair
+    const int64_t row = int64_t(b) * time + (live ? tt : time - 1);
+    int64_t bank[4];
+    uint32_t wbits[4];
+    route_pair_row<NB>(roles.scores[role] + row * roles.stride[role], j1, j2, h, s_ids[t], bank, wbits);
+    if (live) {
+        *reinterpret_cast<uint2 *>(roles.weights[role] + row * 8 + 4 * h) =
+            make_uint2(wbits[0] | wbits[1] << 16, wbits[2] | wbits[3] << 16);
+        longlong2 *iout = reinterpret_cast<longlong2 *>(roles.indices[role] + row * 8 + 4 * h);
+        iout[0] = make_longlong2(bank[0], bank[1]);
+        iout[1] = make_longlong2(bank[2], bank[3]);
+    }
+    __syncthreads();  // the masks are clear
+    if (live) {
+        const unsigned long long bit = 1ull << (2 * tl + role);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const unsigned long long old = atomicOr(&masks[bank[k]], bit);
+            if (old & bit) atomicOr(status, int(BDM_ROUTE_DUPLICATE));
+        }
+    }
+    __syncthreads();
+    int32_t *out = tile_counts + (int64_t(b) * tiles + tile) * banks;
+    for (int x = t; x < banks; x += 128) out[x] = __popcll(masks[x]);
+}
+
 }  // namespace
+
+// Whether route_tile_count_kernel takes this routing: BF16 scores, 8 banks per
+// role from factors of 8..32 (multiples of 8), 16-byte aligned score rows,
+// 8-byte aligned weights and 16-byte aligned indices.
+bool route_tile_count_supported(const void *const *scores, const int64_t *strides, void *const *weights,
+                                int64_t *const *indices, int32_t score_dtype, int32_t j1, int32_t j2,
+                                int32_t selected) {
+    bool ok = score_dtype == BDM_BF16 && selected == 8 && j1 >= 8 && j2 >= 8 && j1 <= 32 && j2 <= 32 &&
+              j1 % 8 == 0 && j2 % 8 == 0;
+    for (int r = 0; r < 2; ++r)
+        ok = ok && aligned(scores[r], 16) && strides[r] % 8 == 0 && strides[r] >= j1 + j2 && aligned(weights[r], 8) &&
+             aligned(indices[r], 16);
+    return ok;
+}
+
+int launch_route_tile_count(const void *const *scores, const int64_t *strides, void *const *weights,
+                            int64_t *const *indices, int64_t batch, int64_t time, int32_t j1, int32_t j2,
+                            int32_t *tile_counts, int32_t *status, hipStream_t stream) {
+    RouterRoles<bf16_t> roles{};
+    for (int r = 0; r < 2; ++r) {
+        roles.scores[r] = static_cast<const bf16_t *>(scores[r]);
+        roles.stride[r] = strides[r];
+        roles.weights[r] = static_cast<bf16_t *>(weights[r]);
+        roles.indices[r] = indices[r];
+    }
+    const int tiles = int((time + 31) / 32);
+    const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(batch));
+    const size_t lds = size_t(j1) * size_t(j2) * sizeof(unsigned long long);
+    switch ((max(j1, j2) + 7) / 8) {
+        case 1: route_tile_count_kernel<1><<<grid, 128, lds, stream>>>(roles, time, tiles, j1, j2, tile_counts, status); break;
+        case 2: route_tile_count_kernel<2><<<grid, 128, lds, stream>>>(roles, time, tiles, j1, j2, tile_counts, status); break;
+        case 3: route_tile_count_kernel<3><<<grid, 128, lds, stream>>>(roles, time, tiles, j1, j2, tile_counts, status); break;
+        default: route_tile_count_kernel<4><<<grid, 128, lds, stream>>>(roles, time, tiles, j1, j2, tile_counts, status); break;
+    }
+    return check_launch("route_tile_count_kernel");
+}
+
 }  // namespace bdm
 
 extern "C" int bdm_router_select(const void *scores, int32_t score_dtype, int64_t rows, int64_t row_stride,

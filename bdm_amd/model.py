@@ -22,7 +22,7 @@ from torch import nn
 
 from . import ops
 from .config import BDMConfig, near_square_factors
-from .routed_update import bank_training, role_bank_training
+from .routed_update import _round_interval, bank_training, role_bank_training
 from .routing import SharedResidualRouter, product_key_route
 
 Tensor = torch.Tensor
@@ -184,6 +184,18 @@ class BankedDeltaMemory(nn.Module):
                                           selected_banks=self.num_writes)
         return self._route(write_routes, self.num_writes), self._route(read_routes, self.num_reads)
 
+    def _route_and_dispatch(self, write_routes: Tensor, read_routes: Tensor):
+        """Both roles' routes and the dispatch over them: one library call
+        (ops.route_dispatch) when no gradient flows to the scores and the
+        roles select equally many banks, else the two steps."""
+        needs_grad = torch.is_grad_enabled() and (write_routes.requires_grad or read_routes.requires_grad)
+        if (not needs_grad and self.num_writes == self.num_reads and write_routes.ndim == 3
+                and write_routes.shape == read_routes.shape and write_routes.dtype == read_routes.dtype):
+            return ops.route_dispatch(write_routes, read_routes, bank_count=self.bank_count,
+                                      selected_banks=self.num_writes)
+        (ww, wi), (rw, ri) = self._route_both(write_routes, read_routes)
+        return (ww, wi), (rw, ri), ops.dispatch_build(wi, ri, self.bank_count)
+
     def _normalize_qk(self, value: Tensor) -> Tensor:
         """'nvidia': x * rsqrt(sum x^2 + 1e-6) in FP32 (the in-file formula of
         _parameters.py:219; the reference calls FLA's l2norm on GPU, which is not
@@ -326,12 +338,16 @@ class BankedDeltaMemory(nn.Module):
         snapshots) and the output interface in one epilogue before o_proj --
         about a third of the launches of the autograd path."""
         controllers, (read_routes, write_routes), gate = self._fused_controllers(hidden)
-        (ww, wi), (rw, ri) = self._route_both(write_routes, read_routes)
+        (ww, wi), (rw, ri), meta = self._route_and_dispatch(write_routes, read_routes)
         q, k, v, g, b, w = controllers
         state = self._state_heads(self.materialize_initial_state())
-        operator = bank_training if self.config.routed_decay else role_bank_training
-        raw = operator(q, k, v, g, b, w, wi, ww, ri, rw, state, self.bank_count, self.bank_size ** -0.5,
-                       compact_replay=self.compact_replay, state_dtype=getattr(torch, self.config.training_state_dtype))
+        # the routed operator's forward (bank_training, routed_update.py:16-53)
+        # on this dispatch: its state policy, no snapshots under no_grad
+        interval = _round_interval(self.bank_size, getattr(torch, self.config.training_state_dtype),
+                                   self.compact_replay, q.dtype)
+        raw = ops.routed_forward(q, k, v, g, b, w, wi, ww, ri, rw, state, meta, bank_count=self.bank_count,
+                                 scale=self.bank_size ** -0.5, routed_decay=self.config.routed_decay,
+                                 round_interval=interval)
         return self._fused_output(gate, raw)
 
     # -- stateful inference (inference.py:88-194) -----------------------------------
@@ -381,8 +397,7 @@ class BankedDeltaMemory(nn.Module):
         elif state_dtype is not None and state_dtype != state.dtype:
             raise ValueError('state_dtype must match the supplied cache')
         (q, k, v, g, b, w), (read_routes, write_routes), gate = self._inference_inputs(hidden)
-        (ww, wi), (rw, ri) = self._route_both(write_routes, read_routes)
-        meta = ops.dispatch_build(wi, ri, self.bank_count)
+        (ww, wi), (rw, ri), meta = self._route_and_dispatch(write_routes, read_routes)
         heads_view = state.view(hidden.shape[0], self.bank_count, self.num_heads, self.bank_size,
                                 self.head_value_width)
         raw = ops.routed_forward(q, k, v, g, b, w, wi, ww, ri, rw, heads_view, meta,

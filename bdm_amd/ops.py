@@ -168,12 +168,15 @@ def route_validation() -> bool:
 
 @dataclass
 class Dispatch:
-    """Packed-event metadata (role_bank_dispatch.py:135-140)."""
+    """Packed-event metadata (role_bank_dispatch.py:135-140).  inverse and
+    tokens are None where they were not asked for (route_dispatch); the
+    recurrence and its backward read order and cu_seqlens only."""
     order: Tensor
-    inverse: Tensor
-    tokens: Tensor
+    inverse: Tensor | None
+    tokens: Tensor | None
     cu_seqlens: Tensor
     status: Tensor  # int32 on device: bdm_route_flags raised while building
+    segment_order: Tensor | None = None  # the forward's longest-first order, when the dispatch ranked it
 
     def check_routes(self) -> None:
         """Synchronise and raise ValueError if the routes were malformed."""
@@ -210,6 +213,63 @@ def dispatch_build(write_indices: Tensor, read_indices: Tensor, bank_count: int)
     if _validate_routes:
         meta.check_routes()
     return meta
+
+
+def route_dispatch(write_scores: Tensor, read_scores: Tensor, *, bank_count: int, selected_banks: int,
+                   maps: bool = False) -> tuple[tuple[Tensor, Tensor], tuple[Tensor, Tensor], Dispatch]:
+    """Both routers and the dispatch of one step in one call
+    (bdm_route_dispatch): ``router_select_pair`` of the [batch, time, J1 + J2]
+    write and read scores, then ``dispatch_build`` on those routes, with the
+    tile counting done by the routing launch and the forward's longest-first
+    segment order ranked in the same call.  ``maps``: also build inverse and
+    tokens.  Returns
+    ``((ww, wi), (rw, ri), dispatch)``."""
+    if write_scores.ndim != 3 or write_scores.shape != read_scores.shape or write_scores.dtype != read_scores.dtype:
+        raise ValueError('route scores must be two [batch, time, J1 + J2] tensors of one shape and dtype')
+    j1, j2 = near_square_factors(bank_count)
+    if write_scores.shape[-1] != j1 + j2:
+        raise ValueError('projected route width does not match the bank table')
+    s = min(selected_banks, j1, j2)
+    if not 1 <= selected_banks <= s * s:
+        raise ValueError('selected bank count is outside what the product key can select')
+    device = _require_gpu(write_scores, read_scores)
+    views = []
+    for t in (write_scores, read_scores):
+        stride = _row_stride(t)
+        scores = t if stride else _aligned(t)
+        views.append((scores, stride or scores.shape[-1]))
+    batch, time = write_scores.shape[:2]
+    k = selected_banks
+    events = batch * time * 2 * k
+    ww, rw = (torch.empty(batch, time, k, device=device, dtype=write_scores.dtype) for _ in range(2))
+    wi, ri = (torch.empty(batch, time, k, device=device, dtype=torch.int64) for _ in range(2))
+    order = torch.empty(events, device=device, dtype=torch.int64)
+    inverse = torch.empty(events, device=device, dtype=torch.int64) if maps else None
+    tokens = torch.empty(events, device=device, dtype=torch.int64) if maps else None
+    cu = torch.empty(batch * bank_count + 1, device=device, dtype=torch.int64)
+    status = torch.empty(1, device=device, dtype=torch.int32)
+    seg_order = torch.empty(batch * bank_count, device=device, dtype=torch.int32)
+    args = _lib.RouteDispatchArgs()
+    args.write_scores, args.write_stride = _ptr(views[0][0]), views[0][1]
+    args.read_scores, args.read_stride = _ptr(views[1][0]), views[1][1]
+    args.score_dtype = _dtype_code(write_scores.dtype)
+    args.batch, args.time = batch, time
+    args.factor_first, args.factor_second, args.selected = j1, j2, k
+    args.write_weights, args.write_indices = _ptr(ww), _ptr(wi)
+    args.read_weights, args.read_indices = _ptr(rw), _ptr(ri)
+    args.order, args.cu_seqlens, args.status = _ptr(order), _ptr(cu), _ptr(status)
+    args.inverse = _ptr(inverse) if maps else None
+    args.tokens = _ptr(tokens) if maps else None
+    args.segment_order = _ptr(seg_order)
+    lib = _lib.library()
+    ws_bytes = lib.bdm_route_dispatch_workspace_size(ctypes.byref(args))
+    workspace = torch.empty(max(int(ws_bytes), 1), device=device, dtype=torch.uint8)
+    _lib.check(lib.bdm_route_dispatch(ctypes.byref(args), _ptr(workspace), ws_bytes, _stream(device)),
+               'bdm_route_dispatch')
+    meta = Dispatch(order, inverse, tokens, cu, status, seg_order)
+    if _validate_routes:
+        meta.check_routes()
+    return (ww, wi), (rw, ri), meta
 
 
 # ---------------------------------------------------------------------------
@@ -347,6 +407,10 @@ def routed_forward(q, k, v, g, b, w, wi, ww, ri, rw, initial: Tensor, meta: Disp
         args.snapshots = snapshots.data_ptr()
         args.snapshot_interval = int(snapshot_interval)
         args.snapshot_dtype = _dtype_code(snapshots.dtype)
+    if meta.segment_order is not None:
+        if meta.segment_order.numel() != x.batch * bank_count:
+            raise ValueError('the dispatch was built for another geometry')
+        args.segment_order = meta.segment_order.data_ptr()
     if phase_events is not None:
         for i, ev in enumerate(phase_events):
             if ev.cuda_event == 0:  # torch creates the HIP event on first use

@@ -9,7 +9,7 @@ seeded random init of ``BankedDeltaMemory``, x ~ N(0,1) (synthetic data).
 Controllers and router scores are computed once before the timed region; a
 timed step is one prefill pass of the hot path over the batch:
 
-    router (write and read roles) -> dispatch -> recurrence + ordered read
+    router (write and read roles) and dispatch in one call -> recurrence + ordered read
     combine, final bank state written (BF16 cache), FP32 recurrence math on a
     state rounded to BF16 every 16 packed events (the reference module
     forward's policy at this geometry)
@@ -593,8 +593,7 @@ def c4_forward(device, steps=10, policy='prefill'):
     interval = ROUND_INTERVAL if policy == 'module' else 0
 
     def step():
-        (ww, wi), (rw, ri) = ops.router_select_pair(wr, rr, bank_count=cfg.bank_count, selected_banks=8)
-        meta = ops.dispatch_build(wi, ri, cfg.bank_count)
+        (ww, wi), (rw, ri), meta = ops.route_dispatch(wr, rr, bank_count=cfg.bank_count, selected_banks=8)
         ops.routed_forward(q, k, v, g, b, w, wi, ww, ri, rw, initial, meta, bank_count=cfg.bank_count,
                            scale=cfg.bank_size ** -0.5, routed_decay=True, round_interval=interval,
                            final_state=final)
@@ -678,9 +677,8 @@ def c2_forward_only(layer, device, batch, time_, launches):
     final = torch.empty(batch, cfg.bank_count, cfg.num_heads, cfg.bank_size, cfg.head_value_width,
                         device=device, dtype=torch.bfloat16)
     with torch.no_grad():
-        ww, wi = ops.router_select(write_scores, bank_count=cfg.bank_count, selected_banks=cfg.selected_banks)
-        rw, ri = ops.router_select(read_scores, bank_count=cfg.bank_count, selected_banks=cfg.selected_banks)
-        meta = ops.dispatch_build(wi, ri, cfg.bank_count)
+        (ww, wi), (rw, ri), meta = ops.route_dispatch(write_scores, read_scores, bank_count=cfg.bank_count,
+                                                       selected_banks=cfg.selected_banks)
         t0 = time.perf_counter()
         for _ in range(launches):
             ops.routed_forward(q, k, v, g, b, w, wi, ww, ri, rw, initial, meta, bank_count=cfg.bank_count,
@@ -875,8 +873,7 @@ def main():
     def step(rec=None):
         if rec is not None:
             ev_front[rec].record(stream)
-        (ww, wi), (rw, ri) = ops.router_select_pair(write_scores, read_scores, bank_count=j, selected_banks=kk)
-        meta = ops.dispatch_build(wi, ri, j)
+        (ww, wi), (rw, ri), meta = ops.route_dispatch(write_scores, read_scores, bank_count=j, selected_banks=kk)
         if rec is not None:
             ev_start[rec].record(stream)
         y = ops.routed_forward(q, k, v, g, b, w, wi, ww, ri, rw, initial, meta, bank_count=j, scale=scale,

@@ -101,6 +101,39 @@ int bdm_dispatch_build(const int64_t *write_indices, const int64_t *read_indices
                        int32_t *status, void *workspace, size_t workspace_bytes, void *stream);
 
 /*
+ * Both routers and the dispatch of one layer step in one call: the results of
+ * bdm_router_select_pair (write role to write_*, read role to read_*, the
+ * selected count per role) followed by bdm_dispatch_build on those routes
+ * (model.py:96-97 routing, then role_bank_dispatch.py:143-153).  Where the
+ * geometry allows (BF16 scores, 8 banks per role from factors of 8..32, the
+ * alignment of bdm_router_select_pair's two-lanes-per-row kernel) the routing
+ * launch also counts the dispatch tiles.  inverse and tokens may be NULL (not
+ * stored; bdm_forward and bdm_backward do not read them).
+ * segment_order: NULL, or [batch*bank_count] int32 receiving the longest-first
+ * order bdm_forward would compute itself (pass it in bdm_forward_args); it is
+ * written where that order applies (batch*bank_count a multiple of 8, ranges
+ * of at most 1024 segments).
+ */
+typedef struct bdm_route_dispatch_args {
+    const void *write_scores;  /* [rows, write_stride] score_dtype, rows = batch*time */
+    int64_t write_stride;
+    const void *read_scores;   /* [rows, read_stride] */
+    int64_t read_stride;
+    int32_t score_dtype;
+    int64_t batch, time;
+    int32_t factor_first, factor_second, selected;
+    void *write_weights;       /* [rows, selected] score_dtype */
+    int64_t *write_indices;    /* [rows, selected] */
+    void *read_weights;
+    int64_t *read_indices;
+    int64_t *order, *inverse, *tokens, *cu_seqlens;
+    int32_t *status;
+    int32_t *segment_order;
+} bdm_route_dispatch_args;
+size_t bdm_route_dispatch_workspace_size(const bdm_route_dispatch_args *args);
+int bdm_route_dispatch(const bdm_route_dispatch_args *args, void *workspace, size_t workspace_bytes, void *stream);
+
+/*
  * bdm_dispatch_build without a workspace, for callers that cannot allocate
  * (code under HIP graph capture, serving loops, harnesses that forbid
  * hipMalloc).  It has no counterpart in the reference.  Same arguments,
@@ -170,10 +203,15 @@ typedef struct bdm_forward_args {
     void *snapshots;           /* NULL or [rows, H, S, v] of snapshot_dtype (see above) */
     int32_t snapshot_interval;
     int32_t snapshot_dtype;    /* BDM_BF16 only with round_interval == snapshot_interval */
-    /* Profiling: NULL, or three hipEvent_t the call records on its stream
-     * before the recurrence kernels, between them and the read combine, and
-     * after the combine, so a caller can time the two phases apart. */
+    /* Profiling: NULL, or three hipEvent_t the call records: before the
+     * recurrence kernels, after the last recurrence launch (the last head-group
+     * round, whose read combine follows it; the earlier rounds' combines run
+     * beside the later rounds on an auxiliary stream) and after the combine,
+     * so a caller can time the recurrence and the combine left after it. */
     void *phase_events[3];
+    /* NULL, or the longest-first segment order bdm_route_dispatch wrote for
+     * this dispatch ([batch*J] int32); the call computes it itself otherwise. */
+    const int32_t *segment_order;
 } bdm_forward_args;
 
 /* Rows of the snapshot buffer for E packed events: E / interval. */

@@ -77,6 +77,12 @@ def test_invalid_arguments_are_rejected_without_a_launch(lib):
     assert lib.bdm_forward(ctypes.byref(args), None, 0, None) == -2
     dargs = _lib.DecodeArgs()
     assert lib.bdm_decode(ctypes.byref(dargs), None) == -1
+    rargs = _lib.RouteDispatchArgs()
+    assert lib.bdm_route_dispatch(None, None, 0, None) == -1
+    assert lib.bdm_route_dispatch(ctypes.byref(rargs), None, 0, None) == -1
+    rargs.batch, rargs.time, rargs.factor_first, rargs.factor_second, rargs.selected = 2, 64, 16, 16, 8
+    rc = lib.bdm_route_dispatch(ctypes.byref(rargs), None, 0, None)
+    assert rc == -1 and b'null pointer' in lib.bdm_last_error_string()
 
 
 def test_python_errors_mirror_the_reference():
@@ -135,7 +141,8 @@ def test_struct_layouts_match_the_header(tmp_path):
                'bdm_decode_args': _lib.DecodeArgs, 'bdm_decode_fused_args': _lib.DecodeFusedArgs,
                'bdm_controller_args': _lib.ControllerArgs,
                'bdm_output_args': _lib.OutputArgs, 'bdm_gemv_args': _lib.GemvArgs,
-               'bdm_adamw_tensor': _lib.AdamwTensor, 'bdm_adamw_args': _lib.AdamwArgs}
+               'bdm_adamw_tensor': _lib.AdamwTensor, 'bdm_adamw_args': _lib.AdamwArgs,
+               'bdm_route_dispatch_args': _lib.RouteDispatchArgs}
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', 'int main(void) {']
     for struct, mirror in mirrors.items():
         lines.append(f'printf("{struct} size %zu\\n", sizeof({struct}));')
