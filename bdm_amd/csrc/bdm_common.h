@@ -31,23 +31,28 @@ template <> __device__ __forceinline__ bf16_t from_f32<bf16_t>(float x) {
     return bf16_t{__builtin_bit_cast(uint16_t, b)};
 }
 
-// Round an FP32 value to the storage type T and widen it back.
-template <typename T> __device__ __forceinline__ float round_to(float x) { return to_f32(from_f32<T>(x)); }
-
-__device__ __forceinline__ float round_bf16(float x) { return float((__bf16)x); }
-
-// Round two values to T with one conversion instruction (v_cvt_pk_bf16_f32
-// rounds both halves to nearest even) and widen them back.
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// x rounded to BF16 (nearest even) and widened back to FP32 by one
+// v_cvt_pk_bf16_f32 with a zero low operand: the high half of its result is
+// bf16(x) and the low half bf16(0) = 0, so the 32 bits are the widened value.
+__device__ __forceinline__ float round_bf16(float x) {
+    const f32x2_t f = {0.f, x};
+    return __builtin_bit_cast(float, __builtin_convertvector(f, bf16x2_t));
+}
+
+// Round an FP32 value to the storage type T and widen it back.
+template <typename T> __device__ __forceinline__ float round_to(float x) { return to_f32(from_f32<T>(x)); }
+template <> __device__ __forceinline__ float round_to<bf16_t>(float x) { return round_bf16(x); }
+
+// Round two values to T and widen them back (one conversion each: cheaper
+// than one packed conversion and two instructions to unpack it).
 template <typename T> __device__ __forceinline__ void round_pair(float &a, float &b);
 template <> __device__ __forceinline__ void round_pair<float>(float &, float &) {}
 template <> __device__ __forceinline__ void round_pair<bf16_t>(float &a, float &b) {
-    const f32x2_t f = {a, b};
-    const bf16x2_t h = __builtin_convertvector(f, bf16x2_t);
-    const uint32_t bits = __builtin_bit_cast(uint32_t, h);
-    a = __uint_as_float(bits << 16);
-    b = __uint_as_float(bits & 0xffff0000u);
+    a = round_bf16(a);
+    b = round_bf16(b);
 }
 
 // Load `N` consecutive elements of T starting at p (16-byte aligned when the

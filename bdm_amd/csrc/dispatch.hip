@@ -12,9 +12,13 @@
 //      for every event of the tile (64-bit LDS atomic OR; order-independent,
 //      so deterministic).  popcount(mask[bank]) is the tile's bucket count.
 //   2. scan: an exclusive scan over tiles for every (batch, bank) — a tile's
-//      base inside its segment — in parallel over banks and tile ranges, then
-//      per batch an exclusive scan over banks (segment starts).  Batch b's segments start at b*T*(KW+KR): every token adds
-//      exactly KW+KR events to its own batch.
+//      base inside its segment — in parallel over banks and tile ranges, and
+//      per batch an exclusive scan over banks (segment starts): one
+//      workgroup per batch for up to 1024 banks, a multiple of 4
+//      (dispatch_batch_scan, which adds the starts to the tile bases and can
+//      rank the segments for the recurrence's longest-first order), else per
+//      (batch, 64 banks) with the starts left to the scatter.  Batch b's segments start at
+//      b*T*(KW+KR): every token adds exactly KW+KR events to its own batch.
 //   3. scatter: rebuild the masks; an event's rank inside its tile-bucket is
 //      popcount(mask[bank] & below(bit)), i.e. the number of earlier
 //      (t, phase) slots of the tile that hit the same bank.  That is the
@@ -137,14 +141,177 @@ __global__ __launch_bounds__(kScanWaves * kWave) void dispatch_tile_scan(Dispatc
     if (live && wave == kScanWaves - 1) totals[int64_t(b) * g.banks + bank] = running;
 }
 
-// One workgroup per (tile, batch): the batch's segment starts (an exclusive
-// scan of the segment lengths over banks, in LDS; every tile of the batch
-// computes the same scan, and tile 0 stores it as cu_seqlens), then each of
-// the tile's events goes to start + its tile's offset in the segment + its
-// rank in the tile's mask.  Batch b's segments start at b*T*(KW+KR): every
-// token adds exactly KW+KR events to its own batch.
+// Per batch, for up to kBatchScanBanks banks (a multiple of 4): one
+// workgroup of 16 waves does the tile scan, the segment starts and, when
+// asked, the longest-first segment ranking, so that the scatter after it
+// reads each event's position base with one load.  A lane owns 4 consecutive
+// banks (16-byte loads and stores: a workgroup moves a batch's counts
+// through one CU, whose vector memory unit takes a wave's addresses at a
+// fixed rate per lane), the banks split into chunks of 256 (a wave's lanes)
+// and the batch's tiles into 16 / chunks ranges, a wave per (chunk, range):
+//   1. each wave sums its banks' counts over its tile range;
+//   2. a bank's segment length is the sum of its ranges' sums; the exclusive
+//      scan of the lengths over banks gives the segment starts, stored as
+//      cu_seqlens (batch b's events start at b*T*(KW+KR));
+//   3. each wave rewrites its counts as start + the counts of the earlier
+//      tiles: the number of the segment's events before the tile, counted
+//      from the batch's first event;
+//   4. with seg_order, each XCD range inside the batch (the `range`
+//      consecutive segments from x * range, the caller's check that the
+//      batch holds whole ranges) is ranked by decreasing length, ties by
+//      index, as segment_order_kernel ranks it.
+// It also clears the route flags, as dispatch_tile_scan does.
+constexpr int kBatchScanBanks = 16 * kWave;
+constexpr int kBatchScanHold = 8;  // tiles whose counts a lane keeps between passes 1 and 3
+
+__global__ __launch_bounds__(kBatchScanBanks) void dispatch_batch_scan(DispatchGeometry g,
+                                                                       int32_t *__restrict__ tile_counts,
+                                                                       int64_t *__restrict__ cu_seqlens,
+                                                                       int32_t *status, int *__restrict__ seg_order,
+                                                                       int range) {
+    __shared__ int4 part[16][kWave];
+    __shared__ int32_t s_len[kBatchScanBanks];
+    __shared__ int32_t s_start[kBatchScanBanks];
+    __shared__ int32_t wave_sums[16];
+    const int b = int(blockIdx.x), t = int(threadIdx.x);
+    if (b == 0 && t == 0) *status = 0;
+    // (wave-uniform values in scalar registers, so that a row's address is
+    // scalar arithmetic plus the lane's fixed offset)
+    const int wave = __builtin_amdgcn_readfirstlane(t / kWave), lane = t % kWave;
+    const int chunks = (g.banks + 4 * kWave - 1) / (4 * kWave), slices = 16 / chunks;
+    const int chunk = wave % chunks, slice = wave / chunks;
+    const int bank4 = 4 * (chunk * kWave + lane);  // the lane's first bank
+    const bool active = slice < slices, live = active && bank4 < g.banks;
+    const int per = (g.tiles + slices - 1) / slices;
+    const int t0 = min(g.tiles, slice * per), t1 = min(g.tiles, t0 + per);
+    // a batch's counts take under 4 GiB; lanes past the last bank read banks
+    // 0..3 and keep nothing
+    char *base = reinterpret_cast<char *>(tile_counts + int64_t(b) * g.tiles * g.banks);
+    const uint32_t row_bytes = uint32_t(g.banks) * 4u, lane_off = uint32_t(live ? bank4 : 0) * 4u;
+    auto cell = [&](int tt) -> int4 & {
+        return *reinterpret_cast<int4 *>(base + size_t(uint32_t(tt) * row_bytes) + lane_off);
+    };
+    // counts of tiles tt .. tt + kBatchScanHold - 1 of the wave's range (0 past it)
+    auto load_cells = [&](int tt, int4 (&c)[kBatchScanHold]) {
+        if (tt + kBatchScanHold <= t1) {
+#pragma unroll
+            for (int k = 0; k < kBatchScanHold; ++k) c[k] = cell(tt + k);
+        } else {
+#pragma unroll
+            for (int k = 0; k < kBatchScanHold; ++k) c[k] = tt + k < t1 ? cell(tt + k) : make_int4(0, 0, 0, 0);
+        }
+    };
+    // 1. range sums
+    int4 c[kBatchScanHold];
+    int4 sum = make_int4(0, 0, 0, 0);
+    if (active) {
+        for (int tt = t0; tt < t1; tt += kBatchScanHold) {
+            load_cells(tt, c);
+#pragma unroll
+            for (int k = 0; k < kBatchScanHold; ++k) {
+                sum.x += c[k].x;
+                sum.y += c[k].y;
+                sum.z += c[k].z;
+                sum.w += c[k].w;
+            }
+        }
+        part[wave][lane] = sum;
+    }
+    __syncthreads();
+    // 2. lengths and starts (thread t takes bank t)
+    int32_t len = 0;
+    if (t < g.banks) {
+        const int c4 = t / (4 * kWave), l4 = (t / 4) % kWave, e = t % 4;
+        for (int s = 0; s < slices; ++s) len += reinterpret_cast<const int32_t *>(&part[s * chunks + c4][l4])[e];
+        s_len[t] = len;
+    }
+    int32_t incl = len;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const int32_t up = __shfl_up(incl, d, kWave);
+        if (lane >= d) incl += up;
+    }
+    if (lane == kWave - 1) wave_sums[wave] = incl;
+    __syncthreads();
+    int32_t start = incl - len;
+    for (int w = 0; w < wave; ++w) start += wave_sums[w];
+    const int64_t batch_base = int64_t(b) * g.time * (g.kw + g.kr);
+    if (t < g.banks) {
+        s_start[t] = start;
+        cu_seqlens[int64_t(b) * g.banks + t] = batch_base + start;
+    }
+    if (b == g.batch - 1 && t == 0) cu_seqlens[g.batch * g.banks] = g.nt * (g.kw + g.kr);
+    __syncthreads();
+    // 3. tile bases
+    if (active) {
+        int4 running = make_int4(s_start[lane_off / 4u], s_start[lane_off / 4u + 1], s_start[lane_off / 4u + 2],
+                                 s_start[lane_off / 4u + 3]);
+        for (int s = 0; s < slice; ++s) {
+            const int4 q = part[s * chunks + chunk][lane];
+            running.x += q.x;
+            running.y += q.y;
+            running.z += q.z;
+            running.w += q.w;
+        }
+        const bool held = t1 - t0 <= kBatchScanHold;  // c still holds the wave's whole range
+        for (int tt = t0; tt < t1; tt += kBatchScanHold) {
+            if (!held) load_cells(tt, c);
+#pragma unroll
+            for (int k = 0; k < kBatchScanHold; ++k) {
+                if (tt + k < t1 && live) cell(tt + k) = running;
+                running.x += c[k].x;
+                running.y += c[k].y;
+                running.z += c[k].z;
+                running.w += c[k].w;
+            }
+        }
+    }
+    // 4. ranking: kBatchScanBanks / banks threads per segment, each counting
+    //    the longer (or equal and earlier) segments in a slice of its range
+    if (seg_order) {
+        __shared__ int32_t s_rank[kBatchScanBanks];
+        if (t < g.banks) s_rank[t] = 0;
+        __syncthreads();
+        const int parts = kBatchScanBanks / g.banks;
+        const int i = t / parts, q = t - i * parts;
+        if (i < g.banks) {
+            const int li = s_len[i];
+            const int r0 = i / range * range, per = (range + parts - 1) / parts;
+            const int j0 = r0 + min(range, q * per), j1 = r0 + min(range, (q + 1) * per);
+            // before i: the longer or equal ones; from i on: the longer ones
+            const int jm = max(j0, min(j1, i));
+            int rank = 0;
+#pragma unroll 8
+            for (int j = j0; j < jm; ++j) rank += s_len[j] >= li ? 1 : 0;
+#pragma unroll 8
+            for (int j = jm; j < j1; ++j) rank += s_len[j] > li ? 1 : 0;
+            atomicAdd(&s_rank[i], rank);
+        }
+        __syncthreads();
+        if (t < g.banks) {
+            const int seg = b * g.banks + t;
+            seg_order[seg / range * range + s_rank[t]] = seg;
+        }
+    }
+}
+
+// One workgroup per (tile, batch).  With STARTS, the batch's segment starts
+// first (an exclusive scan of the segment lengths over banks, in LDS; every
+// tile of the batch computes the same scan, and tile 0 stores it as
+// cu_seqlens), and each of the tile's events goes to start + its tile's
+// offset in the segment + its rank in the tile's mask.  Without, tile_base
+// already holds start + offset (dispatch_batch_scan).  Batch b's segments
+// start at b*T*(KW+KR): every token adds exactly KW+KR events to its own
+// batch.
+//
+// The grid is one-dimensional.  When its size is a multiple of 8, XCD x (the
+// blocks x, x + 8, ... in dispatch order) takes the x-th eighth of the
+// (batch, tile) items in batch-major order, so one batch's segments are
+// written through one XCD's L2 and their cache lines fill there before they
+// go to HBM; otherwise block i takes item i.
 //
 // inverse and tokens may be null (not stored).
+template <bool STARTS>
 __global__ __launch_bounds__(512) void dispatch_scatter(const int64_t *__restrict__ wi,
                                                         const int64_t *__restrict__ ri, DispatchGeometry g,
                                                         const int32_t *__restrict__ tile_base,
@@ -155,8 +322,10 @@ __global__ __launch_bounds__(512) void dispatch_scatter(const int64_t *__restric
     extern __shared__ unsigned long long masks[];
     int32_t *starts = reinterpret_cast<int32_t *>(masks + g.banks);
     __shared__ int32_t wave_sums[512 / kWave];
-    const int tile = blockIdx.x, b = blockIdx.y;
-    {
+    const int64_t items = int64_t(g.tiles) * g.batch, lin = blockIdx.x;
+    const int64_t item = items % 8 == 0 ? (lin % 8) * (items / 8) + lin / 8 : lin;
+    const int b = int(item / g.tiles), tile = int(item % g.tiles);
+    if (STARTS) {
         const int32_t *tot = totals + int64_t(b) * g.banks;
         const int per = (g.banks + int(blockDim.x) - 1) / int(blockDim.x);
         const int lo = min(g.banks, int(threadIdx.x) * per), hi = min(g.banks, lo + per);
@@ -195,7 +364,7 @@ __global__ __launch_bounds__(512) void dispatch_scatter(const int64_t *__restric
         const int bank = raw < 0 ? 0 : (raw >= g.banks ? g.banks - 1 : int(raw));
         const int bit = 2 * tl + (j >= g.kw);
         const int rank = __popcll(masks[bank] & ((1ull << bit) - 1ull));
-        int64_t pos = batch_base + starts[bank] + tb[bank] + rank;
+        int64_t pos = batch_base + (STARTS ? starts[bank] : 0) + tb[bank] + rank;
         pos = pos < 0 ? 0 : (pos >= events ? events - 1 : pos);
         const int64_t original = j < g.kw ? token * g.kw + j : g.nt * g.kw + token * g.kr + (j - g.kw);
         order[pos] = original;
@@ -264,31 +433,51 @@ __global__ void dispatch_clear_status(int32_t *status) {
     if (threadIdx.x == 0) *status = 0;
 }
 
-// The LDS-mask path (bank_count <= kMaxBanks): per-tile counts, per-bank tile
-// offsets and segment lengths (clearing the route flags), then the scatter
-// with the segment starts.  Scratch: batch * (tiles + 1) * banks int32, every
-// element written before it is read.
+// The LDS-mask path (bank_count <= kMaxBanks): per-tile counts, then, for up
+// to kBatchScanBanks banks (a multiple of 4) and a batch's counts under 4 GiB,
+// dispatch_batch_scan (tile bases with the segment starts, cu_seqlens, the
+// ranking when seg_order is given) and the scatter; otherwise
+// dispatch_tile_scan (per-bank tile offsets and segment lengths) and the
+// scatter with the segment starts.  Both scans clear the route flags.
+// Scratch: batch * (tiles + 1) * banks int32, every element written before
+// it is read.  *ranked tells whether seg_order was written (the batch scan
+// ranks when every batch holds whole ranges of the order's 8).
 int launch_mask_dispatch(const int64_t *wi, const int64_t *ri, const DispatchGeometry &g, int64_t *order,
                          int64_t *inverse, int64_t *tokens, int64_t *cu_seqlens, int32_t *status, void *scratch,
-                         hipStream_t s, bool counted = false) {
+                         hipStream_t s, bool counted = false, int *seg_order = nullptr, bool *ranked = nullptr) {
     auto *tile_counts = static_cast<int32_t *>(scratch);
     const size_t mask_bytes = size_t(g.banks) * sizeof(unsigned long long);
-    const dim3 tiles(unsigned(g.tiles), unsigned(g.batch));
+    if (ranked) *ranked = false;
     if (!counted) {  // (the fused routing pass already stored the per-tile counts)
-        dispatch_tile_count<<<tiles, 512, mask_bytes, s>>>(wi, ri, g, tile_counts, status);
+        dispatch_tile_count<<<dim3(unsigned(g.tiles), unsigned(g.batch)), 512, mask_bytes, s>>>(wi, ri, g,
+                                                                                              tile_counts, status);
         if (int rc = check_launch("dispatch_tile_count")) return rc;
     }
+    const unsigned items = unsigned(int64_t(g.tiles) * g.batch);
     int32_t *totals = tile_counts + int64_t(g.batch) * g.tiles * g.banks;
+    if (g.banks <= kBatchScanBanks && g.banks % 4 == 0 && int64_t(g.tiles) * g.banks * 4 < (int64_t(1) << 32) &&
+        aligned(scratch, 16)) {
+        const int64_t nseg = g.batch * int64_t(g.banks);
+        const bool rank = seg_order && order_geometry(nseg) && 8 % g.batch == 0;
+        dispatch_batch_scan<<<unsigned(g.batch), kBatchScanBanks, 0, s>>>(g, tile_counts, cu_seqlens, status,
+                                                                         rank ? seg_order : nullptr,
+                                                                         int(nseg / 8));
+        if (int rc = check_launch("dispatch_batch_scan")) return rc;
+        if (ranked) *ranked = rank;
+        dispatch_scatter<false><<<items, 512, mask_bytes, s>>>(wi, ri, g, tile_counts, nullptr, cu_seqlens, order,
+                                                               inverse, tokens, status);
+        return check_launch("dispatch_scatter");
+    }
     dispatch_tile_scan<<<dim3(unsigned(g.batch), unsigned((g.banks + kWave - 1) / kWave)), kScanWaves * kWave, 0,
                          s>>>(g, tile_counts, totals, status);
     if (int rc = check_launch("dispatch_tile_scan")) return rc;
     const size_t scatter_lds = mask_bytes + size_t(g.banks) * sizeof(int32_t);
     if (scatter_lds > 64 * 1024 &&
-        hipFuncSetAttribute(reinterpret_cast<const void *>(dispatch_scatter),
+        hipFuncSetAttribute(reinterpret_cast<const void *>(dispatch_scatter<true>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, int(scatter_lds)) != hipSuccess)
         return fail(BDM_ERR_LAUNCH, "dispatch: %zu bytes of LDS for %d banks", scatter_lds, g.banks);
-    dispatch_scatter<<<tiles, 512, scatter_lds, s>>>(wi, ri, g, tile_counts, totals, cu_seqlens, order, inverse,
-                                                    tokens, status);
+    dispatch_scatter<true><<<items, 512, scatter_lds, s>>>(wi, ri, g, tile_counts, totals, cu_seqlens, order,
+                                                           inverse, tokens, status);
     return check_launch("dispatch_scatter");
 }
 
@@ -489,6 +678,7 @@ extern "C" int bdm_route_dispatch(const bdm_route_dispatch_args *a, void *worksp
     const bool fused = banks <= kMaxBanks && nt * 2 * k < (int64_t(1) << 31) && a->batch <= 65535 &&
                        route_tile_count_supported(scores, strides, weights, indices, a->score_dtype,
                                                   a->factor_first, a->factor_second, k);
+    bool ranked = false;  // the dispatch's scan ranked the segments
     if (!fused) {
         // the router and the dispatch as separate launches
         if (int rc = bdm_router_select_pair(a->write_scores, a->write_stride, a->read_scores, a->read_stride,
@@ -506,7 +696,8 @@ extern "C" int bdm_route_dispatch(const bdm_route_dispatch_args *a, void *worksp
                 return fail(BDM_ERR_UNSUPPORTED, "route_dispatch: %d banks need the inverse and token maps", banks);
             const DispatchGeometry g{a->batch, a->time, nt, k, k, banks, int(tiles_per_batch(a->time))};
             if (int rc = launch_mask_dispatch(a->write_indices, a->read_indices, g, a->order, a->inverse, a->tokens,
-                                              a->cu_seqlens, a->status, workspace, s))
+                                              a->cu_seqlens, a->status, workspace, s, false, a->segment_order,
+                                              &ranked))
                 return rc;
         }
     } else {
@@ -515,10 +706,10 @@ extern "C" int bdm_route_dispatch(const bdm_route_dispatch_args *a, void *worksp
                                              a->factor_second, static_cast<int32_t *>(workspace), a->status, s))
             return rc;
         if (int rc = launch_mask_dispatch(a->write_indices, a->read_indices, g, a->order, a->inverse, a->tokens,
-                                          a->cu_seqlens, a->status, workspace, s, true))
+                                          a->cu_seqlens, a->status, workspace, s, true, a->segment_order, &ranked))
             return rc;
     }
-    if (a->segment_order && order_geometry(a->batch * int64_t(banks))) {
+    if (a->segment_order && !ranked && order_geometry(a->batch * int64_t(banks))) {
         launch_segment_order(a->cu_seqlens, a->batch * int64_t(banks), a->segment_order, s);
         return check_launch("segment_order_kernel");
     }

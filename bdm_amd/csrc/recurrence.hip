@@ -733,7 +733,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         const int64_t row = (int64_t(s_tok[slot][pe]) * p.s_heads + (head0 + ph) / p.split) * S + 4 * half;
         const int route = s_route[slot][pe];
         if (rd) {
-            load_vec4(static_cast<const T *>(lds_ptr(P_Q)) + row, pl.key);
+            // q in the erase slot: the prep rounds (erase slot) * p for both kinds
+            load_vec4(static_cast<const T *>(lds_ptr(P_Q)) + row, pl.erase);
             const T *rw = static_cast<const T *>(lds_ptr(P_RW));
             if constexpr (std::is_same<T, bf16_t>::value)
                 pl.weight = rw[route].bits;
@@ -758,22 +759,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         const bool rd = live && ((s_rmask[slot] >> pe) & 1u);
         const float pw = live ? pl.weight_f() : 0.f;
         // Branch-free over the stage's mix of reads and writes (both kinds
-        // share a wave): each case performs the same operations as its own
-        // formula, the others are computed and discarded.
-        //   write: d = exp(g p) (or exp(g)), k, a = bf(b p) k
-        //   read:  d = 1, gamma = scale bf(q p) (the key slot holds q)
+        // share a wave):
+        //   write: d = exp(g p) (or exp(g)), prod = -(bf(b p) k) = -a
+        //   read:  d = 1, prod = bf(q p) scale = gamma (q sits in the erase slot)
+        // Lanes past the stage's events keep d = 1 (the prefix products) and
+        // store nothing.
         const bool wr = live && !rd;
-        float d[4], kk[4], a[4], sc[4];
+        const float gscale = p.routed_decay ? pw : 1.f;  // g * 1 is g exactly
+        float d[4], prod[4], sc[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const float key = pl.key_at(r);
-            const float g = (&pl.gate.x)[r];
-            const float e = __expf(p.routed_decay ? g * pw : g);
-            const float xr = round_to<T>((rd ? key : pl.erase_at(r)) * pw);
-            const float prod = xr * (rd ? p.scale : key);  // gamma = bf(q p) scale; a = bf(b p) k
+            const float e = __expf((&pl.gate.x)[r] * gscale);
+            prod[r] = round_to<T>(pl.erase_at(r) * pw) * (rd ? p.scale : -pl.key_at(r));
             d[r] = wr ? e : 1.f;
-            kk[r] = wr ? key : (live ? prod : 0.f);
-            a[r] = wr ? prod : 0.f;
             sc[r] = row_prefix_product(d[r]);
         }
         bool low = false;
@@ -781,19 +779,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         for (int r = 0; r < 4; ++r) low |= !(sc[r] >= kScaleFloor);  // NaN also takes the eager form
         if (__ballot(low) != 0 && (tid & 63) == 0) atomicOr(&s_flag[stage & 1], 1);
         __syncthreads();  // also: every wave has left the previous value loop
-        const bool eager = s_flag[stage & 1] != 0;
+        const bool eager = __builtin_amdgcn_readfirstlane(s_flag[stage & 1]) != 0;
         if (live) {
-            // read: [0] = gamma (lazy: gamma s); lazy write: [0] = -(a s'),
-            // [1] = k / s' (v_rcp_f32); eager write: [0] = -a, [1] = k, [2] = d.
+            // lazy: [0] = prod s' (a read: gamma s; a write: -(a s')),
+            // [1] = k / s' (v_rcp_f32); eager: [0] = prod, [1] = k, [2] = d.
             // All three rows are stored for every event (a read uses [0] only;
             // [2] is read in eager stages only).
             float4 *row = reinterpret_cast<float4 *>(&s_rows[pe][ph][0][4 * half]);
             float r0[4], r1[4];
+            if (eager) {  // (wave-uniform)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float t = eager ? (rd ? kk[r] : a[r]) : (rd ? kk[r] : a[r]) * sc[r];
-                r0[r] = rd ? t : -t;
-                r1[r] = eager ? kk[r] : kk[r] * __builtin_amdgcn_rcpf(sc[r]);
+                for (int r = 0; r < 4; ++r) {
+                    r0[r] = prod[r];
+                    r1[r] = pl.key_at(r);
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    r0[r] = prod[r] * sc[r];
+                    r1[r] = pl.key_at(r) * __builtin_amdgcn_rcpf(sc[r]);
+                }
             }
             row[0] = make_float4(r0[0], r0[1], r0[2], r0[3]);
             row[S / 4] = make_float4(r1[0], r1[1], r1[2], r1[3]);
