@@ -1493,7 +1493,10 @@ int launch_overlapped(const bdm_forward_args &a, ForwardParams<T> p, const void 
     }
     for (int i = 0; i < parts; ++i) {
         hipStream_t st = i ? ax.stream[i - 1] : stream;
-        const int g0 = int(int64_t(groups) * i / parts), g1 = int(int64_t(groups) * (i + 1) / parts);
+        // the larger parts first: the last part's combine is the one left
+        // exposed after the recurrence
+        const int g0 = groups - int(int64_t(groups) * (parts - i) / parts);
+        const int g1 = groups - int(int64_t(groups) * (parts - i - 1) / parts);
         ForwardParams<T> pr = p;
         pr.group_base = g0;
         pr.order_gpr = min(gpr, g1 - g0);
