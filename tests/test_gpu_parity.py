@@ -374,8 +374,9 @@ def test_module_forward_matches_oracle(device):
         ref = oracle_reads(*(t.cpu() for t in (q, k, v, g, b, w)), wi, ww, ri, rw, state, cfg.bank_count,
                            routed_decay=True, state_dtype=torch.bfloat16)
         assert rel_err(raw, ref) < TOL
+        # the output interface on the same reads: 0.0000 measured (rms and layer norm)
         ref_out = oracle.project_output(x, raw.cpu())
-        assert rel_err(out, ref_out) < 2e-2
+        assert rel_err(out, ref_out) < TOL
 
 
 def test_prefill_and_step_match_oracle(device):
@@ -438,7 +439,7 @@ def test_prefill_and_step_match_oracle(device):
             raw1 = torch.cat(heads, -1)
             assert rel_err(state, oracle_state) < TOL
             ref_out1 = oracle.project_output(nxt, raw1.to(torch.bfloat16).unsqueeze(1))
-            assert rel_err(out1, ref_out1) < 2e-2
+            assert rel_err(out1, ref_out1) < TOL
 
 
 @pytest.mark.parametrize('heads,v', [(3, 128), (2, 384), (1, 2048)], ids=['h3v128', 'h2v384', 'h1v2048'])
