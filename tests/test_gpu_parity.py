@@ -98,6 +98,9 @@ def test_router_module_autograd(device):
 
 @pytest.mark.parametrize('batch,time,bank_count,kw,kr', [
     (2, 100, 16, 4, 4), (3, 64, 256, 8, 8), (1, 7, 12, 3, 5), (4, 33, 2048, 8, 8), (2, 40, 16, 0, 4),
+    # the per-batch scan: a wave's tile range reloaded (256 tiles over 16 ranges), 2 and 4 chunks of 256 banks,
+    # a partial last chunk with a range of 17 tiles (two full loads and a tail); 15 banks take the per-chunk scan
+    (1, 8192, 256, 8, 8), (2, 200, 512, 4, 4), (2, 300, 1024, 8, 8), (1, 2100, 1000, 8, 8), (2, 90, 15, 3, 3),
     # the largest bank count of the LDS-mask path (masks and segment starts: 96 KiB of LDS)
     (2, 70, 8192, 8, 8), (1, 5, 4096, 2, 3),
     # above 8192 banks: the radix-sort path
