@@ -856,11 +856,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     issue_prep(0);
     finish_prep(0);
 
-    // v, w of the writes in stream order (across stages), in two register
-    // sets used alternately: write k's rows are loaded while write k-1 runs,
-    // into the set write k-1 does not use, so no registers are copied.  At a
-    // stage start the stage's first write is in set A.
-    RawCols<T, CPL> va, wa, vb, wb;
+    // v, w of the writes in stream order, in register sets used in turn
+    // (three in MODE 0, two otherwise): write k's rows are loaded into the
+    // set that the write before write k's predecessors used, so no registers
+    // are copied.
+    RawCols<T, CPL> va, wa, vb, wb, vc, wc;
     // v, w rows of a write by its (wave-uniform) token
     i32x4_t rsrc_v{}, rsrc_w{}, rsrc_z{};
     if constexpr (BUF) {
@@ -1002,36 +1002,68 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         };
         // Events in packed order, as runs: the reads before each write, then
         // the write, so the state is updated exactly once per iteration and
-        // never merged from branches.  Writes alternate between the register
-        // sets A and B (two writes per loop iteration).  The stage's first
-        // write is fetched here, into A, not prefetched by the previous stage:
-        // a stage that found it in B would have to copy the set, and the copy
-        // waits for every memory access issued before it.
+        // never merged from branches.  MODE 0: writes rotate over the register
+        // sets A, B and C (three writes per loop iteration), each write's rows
+        // loaded two writes ahead; MODE 1 and 2 alternate A and B, one write
+        // ahead (a third set would spill there).  A stage's first writes are
+        // fetched here, not prefetched by the previous stage: a stage that
+        // found them in other sets would have to copy them, and a copy waits
+        // for every memory access issued before it.
         {
-            if (nw > 0) fetch_token(__builtin_amdgcn_readlane(m_wtok, 0), va, wa);
-            // the rows of write wk + 1.  Always two loads, so that the compiler
-            // can wait for the previous set with vmcnt(2) instead of draining
-            // these; with no next write, write wk's rows are loaded again
-            // (harmless).
-            auto fetch_next = [&](int wk, RawCols<T, CPL> &vv, RawCols<T, CPL> &ww) {
-                fetch_token(__builtin_amdgcn_readlane(m_wtok, wk + 1 < nw ? wk + 1 : wk), vv, ww);
+            // the rows of write k (past the last write, the last write's rows
+            // again: harmless).  Always two loads, so that the compiler can
+            // wait for a set with a count instead of draining the loads issued
+            // after it.
+            auto fetch_write = [&](int k, RawCols<T, CPL> &vv, RawCols<T, CPL> &ww) {
+                fetch_token(__builtin_amdgcn_readlane(m_wtok, k < nw ? k : nw - 1), vv, ww);
             };
             int i = 0;
+            if constexpr (MODE == 0) {
+                if (nw > 0) {
+                    fetch_write(0, va, wa);
+                    fetch_write(1, vb, wb);
+                }
 #pragma unroll 1
-            for (int wk = 0; wk < nw; wk += 2) {
-                int wi_ = __builtin_amdgcn_readlane(m_wpos, wk);
-                fetch_next(wk, vb, wb);
+                for (int wk = 0; wk < nw; wk += 3) {
+                    int wi_ = __builtin_amdgcn_readlane(m_wpos, wk);
+                    fetch_write(wk + 2, vc, wc);
 #pragma unroll 1
-                for (; i < wi_; ++i) read_event(i);
-                i = wi_ + 1;
-                write_event(wi_, va, wa);
-                if (wk + 1 >= nw) break;
-                wi_ = __builtin_amdgcn_readlane(m_wpos, wk + 1);
-                fetch_next(wk + 1, va, wa);
+                    for (; i < wi_; ++i) read_event(i);
+                    i = wi_ + 1;
+                    write_event(wi_, va, wa);
+                    if (wk + 1 >= nw) break;
+                    wi_ = __builtin_amdgcn_readlane(m_wpos, wk + 1);
+                    fetch_write(wk + 3, va, wa);
 #pragma unroll 1
-                for (; i < wi_; ++i) read_event(i);
-                i = wi_ + 1;
-                write_event(wi_, vb, wb);
+                    for (; i < wi_; ++i) read_event(i);
+                    i = wi_ + 1;
+                    write_event(wi_, vb, wb);
+                    if (wk + 2 >= nw) break;
+                    wi_ = __builtin_amdgcn_readlane(m_wpos, wk + 2);
+                    fetch_write(wk + 4, vb, wb);
+#pragma unroll 1
+                    for (; i < wi_; ++i) read_event(i);
+                    i = wi_ + 1;
+                    write_event(wi_, vc, wc);
+                }
+            } else {
+                if (nw > 0) fetch_write(0, va, wa);
+#pragma unroll 1
+                for (int wk = 0; wk < nw; wk += 2) {
+                    int wi_ = __builtin_amdgcn_readlane(m_wpos, wk);
+                    fetch_write(wk + 1, vb, wb);
+#pragma unroll 1
+                    for (; i < wi_; ++i) read_event(i);
+                    i = wi_ + 1;
+                    write_event(wi_, va, wa);
+                    if (wk + 1 >= nw) break;
+                    wi_ = __builtin_amdgcn_readlane(m_wpos, wk + 1);
+                    fetch_write(wk + 2, va, wa);
+#pragma unroll 1
+                    for (; i < wi_; ++i) read_event(i);
+                    i = wi_ + 1;
+                    write_event(wi_, vb, wb);
+                }
             }
 #pragma unroll 1
             for (; i < n; ++i) read_event(i);
