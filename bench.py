@@ -153,9 +153,9 @@ def recurrence_roofline(cfg, batch, time_, ms):
 
 # MI355X: 256 CUs, 64 non-packed FP32 FMA lanes per CU per clock; 2.4 GHz is
 # the clock of the 78.6 TFLOP/s figure, and PROFILED_CLOCK_GHZ the shader
-# clock the C2 recurrence ran at under rocprofv3 (GRBM_GUI_ACTIVE cycles over
-# the kernel's duration, profiles/bdm_forward_c2.md)
-CU_COUNT, FMA_PER_CU_CLOCK, RATED_CLOCK_GHZ, PROFILED_CLOCK_GHZ = 256, 64, 2.4, 2.0
+# clock the C2 recurrence ran at under rocprofv3 (GRBM_GUI_ACTIVE cycles of
+# one XCD over the kernel's duration: 403 K in 182 us, profiles/bdm_forward_c2.md)
+CU_COUNT, FMA_PER_CU_CLOCK, RATED_CLOCK_GHZ, PROFILED_CLOCK_GHZ = 256, 64, 2.4, 2.2
 
 
 def fma_floor(cfg, batch, time_, ms):
