@@ -162,6 +162,39 @@ __global__ __launch_bounds__(kScanWaves * kWave) void dispatch_tile_scan(Dispatc
 //      index, as segment_order_kernel ranks it.
 // It also clears the route flags, as dispatch_tile_scan does.
 constexpr int kBatchScanBanks = 16 * kWave;
+
+// Ascending bitonic sort of 256 keys held by one wave, 4 per lane (item
+// 4 * lane + r in k[r]): compare-exchanges of partners 1 and 2 apart inside a
+// lane, of partners 4..128 apart across lanes (__shfl_xor).
+constexpr int kWaveSortItems = 4 * kWave;
+__device__ __forceinline__ void wave_bitonic_sort(uint32_t (&k)[4], int lane) {
+#pragma unroll
+    for (int size = 2; size <= kWaveSortItems; size <<= 1) {
+#pragma unroll
+        for (int j = size >> 1; j > 0; j >>= 1) {
+            if (j >= 4) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int e = 4 * lane + r;
+                    const uint32_t other = __shfl_xor(k[r], j >> 2, kWave);
+                    // the lower index of a pair keeps the smaller key in an
+                    // ascending block, the larger in a descending one
+                    const bool keep_min = ((e & j) == 0) == ((e & size) == 0);
+                    k[r] = keep_min ? min(k[r], other) : max(k[r], other);
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    if (r & j) continue;
+                    const bool up = ((4 * lane + r) & size) == 0;
+                    const uint32_t lo = min(k[r], k[r | j]), hi = max(k[r], k[r | j]);
+                    k[r] = up ? lo : hi;
+                    k[r | j] = up ? hi : lo;
+                }
+            }
+        }
+    }
+}
 constexpr int kBatchScanHold = 8;  // tiles whose counts a lane keeps between passes 1 and 3
 
 __global__ __launch_bounds__(kBatchScanBanks) void dispatch_batch_scan(DispatchGeometry g,
@@ -266,9 +299,32 @@ __global__ __launch_bounds__(kBatchScanBanks) void dispatch_batch_scan(DispatchG
             }
         }
     }
-    // 4. ranking: kBatchScanBanks / banks threads per segment, each counting
-    //    the longer (or equal and earlier) segments in a slice of its range
-    if (seg_order) {
+    // 4. ranking (a range divides the batch's banks).  Ranges of up to 256
+    //    segments whose lengths fit in 24 bits (segments hold at most
+    //    time * (kw + kr) events): wave w sorts range w of the batch by keys
+    //    that order longest first, then lowest index — the complemented
+    //    length above the 8-bit index — with padding keys last.
+    constexpr uint32_t kSortLenMax = (1u << 24) - 1;
+    if (seg_order && range <= kWaveSortItems && g.time * (g.kw + g.kr) <= int64_t(kSortLenMax)) {
+        if (wave < g.banks / range) {
+            uint32_t k[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int i = 4 * lane + r;
+                k[r] = i < range ? ((kSortLenMax - uint32_t(s_len[wave * range + i])) << 8) | uint32_t(i)
+                                 : 0xffffffffu;
+            }
+            wave_bitonic_sort(k, lane);
+            const int seg0 = b * g.banks + wave * range;  // the range's first segment
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int pos = 4 * lane + r;
+                if (pos < range) seg_order[seg0 + pos] = seg0 + int(k[r] & 255u);
+            }
+        }
+    } else if (seg_order) {
+        // kBatchScanBanks / banks threads per segment, each counting the
+        // longer (or equal and earlier) segments in a slice of its range
         __shared__ int32_t s_rank[kBatchScanBanks];
         if (t < g.banks) s_rank[t] = 0;
         __syncthreads();

@@ -29,6 +29,11 @@ CASES = [
     (4, 512, 2048, 8),
     # 4 banks per role (not the fused geometry)
     (2, 90, 16, 4),
+    # ranges of 128 segments, 4 and 8 of them per sequence, each sorted by one wave
+    (2, 200, 512, 8),
+    (1, 300, 1024, 8),
+    # ranges of 512 segments: ranked pairwise
+    (8, 64, 512, 8),
 ]
 
 
