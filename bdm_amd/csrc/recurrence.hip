@@ -361,25 +361,28 @@ struct RawCols<float, CPL> {
 
 typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
 
+// The exact FP32 products of the BF16 halves of a0 and a1 with p (whose
+// other half is zero in p_lo = (p, 0) and p_hi = (0, p)): e = {lo(a0) p,
+// hi(a0) p, lo(a1) p, hi(a1) p}, as the VOP3P v_dot2_f32_bf16 with the
+// inline constant 0 (the builtin with a zero accumulator is selected as
+// v_dot2c_f32_bf16, whose accumulator is its destination, and costs a v_mov
+// of zero first).  A VALU read of a DOT instruction's result needs 3 wait
+// states after it; the compiler inserts them for the DOT instructions it
+// generates but cannot see the ones in inline assembly, so the block ends
+// with them (s_nop 2), whatever the compiler schedules next.
+__device__ __forceinline__ void dot_products4(uint32_t a0, uint32_t a1, uint32_t p_lo, uint32_t p_hi,
+                                              float (&e)[4]) {
+    asm("v_dot2_f32_bf16 %0, %4, %6, 0\n\t"
+        "v_dot2_f32_bf16 %1, %4, %7, 0\n\t"
+        "v_dot2_f32_bf16 %2, %5, %6, 0\n\t"
+        "v_dot2_f32_bf16 %3, %5, %7, 0\n\t"
+        "s_nop 2"
+        : "=&v"(e[0]), "=&v"(e[1]), "=&v"(e[2]), "=&v"(e[3])
+        : "v"(a0), "v"(a1), "v"(p_lo), "v"(p_hi));
+}
+
 // acc + (the exact FP32 product of the BF16 halves of a and b_masked that
 // b_masked keeps; its other half is zero): v_dot2c_f32_bf16.
-// The same with a zero accumulator, as the VOP3P v_dot2_f32_bf16 with the
-// inline constant 0: the builtin with acc = 0 is selected as v_dot2c_f32_bf16,
-// whose accumulator is its destination, and costs a v_mov of zero first.
-__device__ __forceinline__ float dot_half(uint32_t a, uint32_t b_masked) {
-    float r;
-    asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b_masked));
-    return r;
-}
-
-// The same with b_masked a wave-uniform value in a scalar register (one
-// scalar operand per VALU instruction).
-__device__ __forceinline__ float dot_half_s(uint32_t a, uint32_t b_masked) {
-    float r;
-    asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "s"(b_masked));
-    return r;
-}
-
 __device__ __forceinline__ float dot_half_acc(float acc, uint32_t a, uint32_t b_masked) {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v_t, a), __builtin_bit_cast(bf16x2v_t, b_masked),
                                            acc, false);
@@ -412,29 +415,24 @@ struct GatedValues<bf16_t, CPL> {
     // pw is a BF16 value (the route weight) widened to FP32, so its low 16
     // bits are zero: w * pw is an exact FP32 product, formed by
     // v_dot2_f32_bf16 from the packed w pair and (pw, 0) or (0, pw)
-    // pw_bits: the route weight's FP32 bits, wave-uniform (a scalar register)
-    __device__ __forceinline__ void make_uniform(const RawCols<bf16_t, CPL> &w, const RawCols<bf16_t, CPL> &vv,
-                                                 uint32_t pw_bits) {
-        const uint32_t p_hi = pw_bits, p_lo = pw_bits >> 16;
+    // (CPL a multiple of 4).
+    // p_hi: the weight's FP32 bits, p_lo: the same >> 16 (vector registers:
+    // a scalar operand of the inline instruction is outside the compiler's
+    // hazard checks, and a scalar write right after it can change the value
+    // the instruction reads)
+    __device__ __forceinline__ void make_pair(const RawCols<bf16_t, CPL> &w, const RawCols<bf16_t, CPL> &vv,
+                                              uint32_t p_hi, uint32_t p_lo) {
 #pragma unroll
-        for (int i = 0; i < CPL / 2; ++i) {
-            const float e0 = dot_half_s(w.u[i], p_lo);
-            const float e1 = dot_half_s(w.u[i], p_hi);
-            lo[i] = pack_bf16x2(e0, 0.f);
-            hi[i] = pack_bf16x2(0.f, e1);
-            v[i] = vv.u[i];
+        for (int i = 0; i < CPL / 2; i += 2) {
+            float e[4];
+            dot_products4(w.u[i], w.u[i + 1], p_lo, p_hi, e);
+            lo[i] = pack_bf16x2(e[0], 0.f);
+            hi[i] = pack_bf16x2(0.f, e[1]);
+            lo[i + 1] = pack_bf16x2(e[2], 0.f);
+            hi[i + 1] = pack_bf16x2(0.f, e[3]);
         }
-    }
-    __device__ __forceinline__ void make(const RawCols<bf16_t, CPL> &w, const RawCols<bf16_t, CPL> &vv, float pw) {
-        const uint32_t p_hi = __float_as_uint(pw), p_lo = p_hi >> 16;
 #pragma unroll
-        for (int i = 0; i < CPL / 2; ++i) {
-            const float e0 = dot_half(w.u[i], p_lo);
-            const float e1 = dot_half(w.u[i], p_hi);
-            lo[i] = pack_bf16x2(e0, 0.f);
-            hi[i] = pack_bf16x2(0.f, e1);
-            v[i] = vv.u[i];
-        }
+        for (int i = 0; i < CPL / 2; ++i) v[i] = vv.u[i];
     }
     // acc + x[c]
     __device__ __forceinline__ float add_to(float acc, int c) const {
@@ -449,9 +447,9 @@ struct GatedValues<float, CPL> {
 #pragma unroll
         for (int c = 0; c < CPL; ++c) x[c] = (w.f[c] * pw) * vv.f[c];
     }
-    __device__ __forceinline__ void make_uniform(const RawCols<float, CPL> &w, const RawCols<float, CPL> &vv,
-                                                 uint32_t pw_bits) {
-        make(w, vv, __uint_as_float(pw_bits));
+    __device__ __forceinline__ void make_pair(const RawCols<float, CPL> &w, const RawCols<float, CPL> &vv,
+                                              uint32_t p_hi, uint32_t) {
+        make(w, vv, __uint_as_float(p_hi));
     }
     __device__ __forceinline__ float add_to(float acc, int c) const { return acc + x[c]; }
 };
@@ -556,10 +554,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     __shared__ unsigned s_rmask[kRing];    // bit e: event e of the stage is a read
     // Row operands of the current stage (written by the prep of a stage after
     // every wave has left the previous stage's value loop): lazy [0] = -alpha,
-    // [1] = beta; eager [0] = -a, [1] = k, [2] = d; a read [0] = gamma.
-    __shared__ __align__(16) float s_rows[NE][HB][3][S];
+    // [1] = beta; eager [0] = -a, [1] = k, [2] = d; a read [0] = gamma; and
+    // [3][0..1] the event's route weight bits and bits >> 16 (read with the
+    // row's address, into vector registers).
+    __shared__ __align__(16) float s_rows[NE][HB][4][S];
     __shared__ float s_fold[HB][S];  // s at the end of the stage (1 for eager)
-    __shared__ float s_pw[NE];               // route weight of each event of the stage
     __shared__ int s_eager;
     __shared__ int s_flag[2];  // by stage parity: reset two barriers before its next use
 
@@ -803,7 +802,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
             row[0] = make_float4(r0[0], r0[1], r0[2], r0[3]);
             row[S / 4] = make_float4(r1[0], r1[1], r1[2], r1[3]);
             row[2 * S / 4] = make_float4(d[0], d[1], d[2], d[3]);
-            if (tid < NE) s_pw[pe] = pw;
+            if (half == 0) {
+                const uint32_t bits = __float_as_uint(pw);
+                *reinterpret_cast<uint2 *>(&s_rows[pe][ph][3][0]) = make_uint2(bits, bits >> 16);
+            }
             if (pe == n - 1) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) s_fold[ph][4 * half + r] = eager ? 1.f : sc[r];
@@ -923,7 +925,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         const int m_wpos = s_wpos[slot][el];
         const int m_wtok = s_wtok[slot][el];
         const int m_route = s_route[slot][el];
-        const int m_pw = __float_as_int(s_pw[el]);
 
         auto read_event = [&](int i) {
             if (MODE == 1 && !reads_on) return;  // a read does not change the state (wave-uniform)
@@ -955,7 +956,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         // write `wi_` of the stage with its v, w rows in (vc, wc)
         auto write_event = [&](int wi_, const RawCols<T, CPL> &vc, const RawCols<T, CPL> &wc) {
             const float *row = &s_rows[wi_][lh][0][0];
-            const uint32_t pw_bits = uint32_t(__builtin_amdgcn_readlane(m_pw, wi_));
             if (__builtin_amdgcn_readfirstlane(eager) != 0) {
                 // hd = diag(d) M first; the update below then uses a and k
                 // (a wave-uniform branch: the stage's form is uniform)
@@ -984,7 +984,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
                 for (int r = 1; r < S; ++r) u[c] = fmaf(nalpha[r], h[r][c], u[c]);
             }
             GatedValues<T, CPL> x;
-            x.make_uniform(wc, vc, pw_bits);
+            const uint2 pw2 = *reinterpret_cast<const uint2 *>(row + 3 * S);
+            x.make_pair(wc, vc, pw2.x, pw2.y);
 #pragma unroll
             for (int c = 0; c < CPL; ++c) {
                 u[c] = x.add_to(u[c], c);
