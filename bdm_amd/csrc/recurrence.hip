@@ -24,6 +24,7 @@
 // combine kernel then streams each token's KR consecutive rows and adds them
 // in increasing bank id, rounding after every add (the production readout
 // order), ordering the token's KR bank ids itself.
+#include <algorithm>
 #include <cstdlib>
 #include <mutex>
 #include <cstring>
@@ -90,6 +91,16 @@ struct ForwardParams {
     // MODE 0: the launch runs head groups group_base .. group_base + gridDim.y
     // - 1 (one round of a launch split into rounds; 0 for a whole launch)
     int group_base;
+    // Stage path of the rounding policy (MODE 3 and stage_scan_kernel):
+    // MODE 0 leaves segments longer than kPieceEvents to it (skip_long), and
+    // MODE 3 stores, per stage slot, R and P in pstate / ptrans and, per read
+    // route slot, the zero-start read row (z0buf, [NT*KR, H*v] FP32) and its
+    // coefficients on the stage's start state (cbuf, [NT*KR, H, S] FP32),
+    // and per stage slot the read route slot of each of its 16 events, -1
+    // for a write or past the segment (tgt, [slots, 16] int32).
+    int skip_long;
+    float *z0buf, *cbuf;
+    int *tgt;
 };
 
 // Events per piece when long segments are cut (a multiple of the stage size).
@@ -531,12 +542,24 @@ __device__ __forceinline__ void load_vec4(const float *p, float4 &out) { out = *
 //          initial state;
 //   MODE 2 runs pieces 1.. of each cut segment from their start states M_q,
 //          with reads; the last piece stores the final state.
+// Under the rounding policy the state is rounded at every stage start, so a
+// segment is affine per stage only.  Segments longer than kPieceEvents then
+// take the stage path (MODE 0 skips them):
+//   MODE 3 runs every piece of those segments with each 16-event stage
+//          started from zero: at the stage end it stores the stage's R and P
+//          (P carried by lanes 0..7 as in MODE 1) in the stage's slot, and
+//          for each read the zero-start row z0 = gamma^T R_t and the
+//          coefficients c = gamma^T P_t on the stage's start state;
+//   stage_scan_kernel runs M_(k+1) = round(P_k M_k + R_k) along each segment
+//          from its rounded initial state and forms each read of stage k as
+//          c^T M_k + z0.
+// The sums differ from the sequential form's only in FP32 association.
 //
 // BUF: v, w rows are read and read rows written through buffer resources
 // with 32-bit offsets (BF16 controllers; v, w and the read buffer below
 // 4 GiB), which spares the vector address arithmetic of every event.
 template <typename T, int CPL, int HB, int MODE, bool BUF = false>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void lazy_forward_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == 3 ? 3 : 4, 8))) void lazy_forward_kernel(
     ForwardParams<T> p) {
     static_assert(!BUF || (std::is_same<T, bf16_t>::value && CPL == 4), "buffer form: BF16, 4 columns per lane");
     constexpr int S = 8;
@@ -582,6 +605,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
             seg = p.xcd_remap ? int((block % 8) * (p.nseg / 8) + block / 8) : block;
         }
         group += p.group_base;
+        // the stage path runs the long segments (the whole workgroup leaves together)
+        if (p.skip_long && p.cu[seg + 1] - p.cu[seg] > kPieceEvents) return;
+    } else if constexpr (MODE == 3) {
+        is_piece = true;  // every piece of every long segment, one per block
     } else if constexpr (MODE == 1) {
         // Every head group's pieces first, then the segments: dispatched row
         // by row, the later groups' pieces would wait behind the first
@@ -626,8 +653,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     }
     // MODE 1 roles: a middle piece runs from zero with its transition and no
     // reads; a first piece from the segment's initial state with its reads,
-    // storing its end state as R and a zero P; an uncut segment whole
-    const bool from_zero = MODE == 1 && pslot >= 0 && piece > 0;
+    // storing its end state as R and a zero P; an uncut segment whole.
+    // MODE 3: every stage from zero with its transition, reads kept apart.
+    constexpr bool kTrans = MODE == 1 || MODE == 3;  // lanes 0..7 may carry P
+    const bool from_zero = (MODE == 1 && pslot >= 0 && piece > 0) || MODE == 3;
     const bool reads_on = MODE != 1 || !from_zero;
     const int bank = seg % p.banks;
     const int64_t bidx = seg / p.banks;
@@ -650,6 +679,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     const bool prep_head = ph < nheads;
 
     int64_t start = p.cu[seg], end = p.cu[seg + 1];
+    // MODE 3: the slot of the piece's first stage (stage k of segment s has
+    // slot cu[s] / 16 + s + k, distinct over all segments' stages)
+    const int64_t stage_slot0 = start / NE + seg + int64_t(piece) * (kPieceEvents / NE);
     if constexpr (MODE != 0) {
         if (pieces > 1) {
             start += int64_t(piece) * kPieceEvents;
@@ -941,6 +973,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
                 for (int r = 0; r < S; ++r) acc = fmaf(gamma[r], h[r][c], acc);
                 z[c] = acc;
             }
+            if constexpr (MODE == 3) {
+                // the zero-start row in FP32, and in lanes 0..7 of the head
+                // the coefficient c_j = gamma^T P e_j of the read on the
+                // stage's start state
+                float zc = 0.f;
+#pragma unroll
+                for (int r = 0; r < S; ++r) zc = fmaf(gamma[r], pc[r], zc);
+                float *zr = p.z0buf + int64_t(zrow) * hw + (head * p.width + col0);
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) __builtin_nontemporal_store(z[c], zr + c);
+                if (pcol < S && tid < nheads * p.lanes_per_head)
+                    p.cbuf[(int64_t(zrow) * p.heads + head) * S + pcol] = zc;
+                return;
+            }
             // nontemporal: the rows are read once, by the combine after the
             // recurrence, and should not displace the v, w rows that the
             // token's other write banks are about to read from L2
@@ -964,7 +1010,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
                     const float d = row[2 * S + r];
 #pragma unroll
                     for (int c = 0; c < CPL; ++c) h[r][c] *= d;
-                    if constexpr (MODE == 1) pc[r] *= d;
+                    if constexpr (kTrans) pc[r] *= d;
                 }
             }
             float nalpha[S], beta[S];
@@ -992,7 +1038,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 #pragma unroll
                 for (int r = 0; r < S; ++r) h[r][c] = fmaf(beta[r], u[c], h[r][c]);
             }
-            if (MODE == 1 && from_zero) {
+            if (kTrans && from_zero) {
                 // the transition column: the same update with x = 0
                 float uc = nalpha[0] * pc[0];
 #pragma unroll
@@ -1076,7 +1122,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
             const float f = s_fold[lh][r];
 #pragma unroll
             for (int c = 0; c < CPL; ++c) h[r][c] *= f;
-            if constexpr (MODE == 1) pc[r] *= f;
+            if constexpr (kTrans) pc[r] *= f;
+        }
+        if constexpr (MODE == 3) {
+            // the stage's R and P into its slot, then the next stage from zero
+            const int64_t sl = stage_slot0 + st;
+            if (group == 0 && tid < NE)
+                p.tgt[sl * NE + tid] = (tid < n && ((s_rmask[slot] >> tid) & 1u)) ? s_route[slot][tid] : -1;
+            store_state<S, CPL>(p.pstate, BDM_F32, ((sl * p.heads + head) * S) * p.width + col0, p.width, S, h);
+            if (pcol < S && tid < nheads * p.lanes_per_head) {
+                float *pt = p.ptrans + ((sl * p.heads + head) * S) * S;
+#pragma unroll
+                for (int r = 0; r < S; ++r) pt[r * S + pcol] = pc[r];
+            }
+#pragma unroll
+            for (int r = 0; r < S; ++r) {
+#pragma unroll
+                for (int c = 0; c < CPL; ++c) h[r][c] = 0.f;
+                pc[r] = r == pcol ? 1.f : 0.f;
+            }
         }
         // operands of stage st+1
         if (st + 1 < nstages) finish_prep(st + 1);
@@ -1094,61 +1158,81 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 #pragma unroll
             for (int r = 0; r < S; ++r) pt[r * S + pcol] = from_zero ? pc[r] : 0.f;
         }
-    } else if (lds_ptr(P_FINAL) && piece == pieces - 1) {
+    } else if (MODE != 3 && lds_ptr(P_FINAL) && piece == pieces - 1) {
         const int64_t final_offset = bidx * (int64_t(p.banks) * p.s_heads * S * p.row_stride) + state_offset;
         store_state<S, CPL>(lds_ptr(P_FINAL), p.final_dtype, final_offset, p.row_stride, S, h);
     }
 }
 
-// The piece list: a segment longer than kPieceEvents becomes
-// ceil(len / kPieceEvents) pieces with consecutive piece-state slots.  One
-// workgroup of 1024 threads; thread t handles a contiguous run of segments.
-__global__ __launch_bounds__(1024) void piece_table_kernel(const int64_t *__restrict__ cu, int nseg,
-                                                           int4 *__restrict__ items, int *__restrict__ n_items) {
-    __shared__ int s_cut[1024];
-    const int t = threadIdx.x;
-    const int per = (nseg + 1023) / 1024;
-    const int s0 = min(nseg, t * per), s1 = min(nseg, s0 + per);
-    int cut = 0;
-    // (unrolled: the loads of a thread's segments are independent and go out together)
-#pragma unroll 8
-    for (int sg = s0; sg < s1; ++sg) {
-        const int64_t len = cu[sg + 1] - cu[sg];
-        if (len > kPieceEvents) cut += int((len + kPieceEvents - 1) / kPieceEvents);
-    }
-    // inclusive scan: within each wave by shuffles, then over the 16 wave
-    // totals by the first wave
-    const int lane = t % kWave, wave = t / kWave;
-    int incl = cut;
+// Exclusive prefix of x over the 1024 threads of the workgroup, and the
+// total in *total: within each wave by shuffles, then over the 16 wave totals
+// by the first wave.  lds: 1024 / kWave + 1 ints.
+__device__ int block_exclusive_scan(int x, int *lds, int *total) {
+    const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
+    constexpr int kWaves = 1024 / kWave;
+    int incl = x;
 #pragma unroll
     for (int off = 1; off < kWave; off <<= 1) {
         const int up = __shfl_up(incl, off, kWave);
         if (lane >= off) incl += up;
     }
-    if (lane == kWave - 1) s_cut[wave] = incl;
+    if (lane == kWave - 1) lds[wave] = incl;
     __syncthreads();
     if (wave == 0) {
-        const int total = lane < 1024 / kWave ? s_cut[lane] : 0;
-        int w = total;
+        // (lane l reads lds[l] before it rewrites it; one wave, in order)
+        const int wt = lane < kWaves ? lds[lane] : 0;
+        int w = wt;
 #pragma unroll
-        for (int off = 1; off < 1024 / kWave; off <<= 1) {
+        for (int off = 1; off < kWaves; off <<= 1) {
             const int up = __shfl_up(w, off, kWave);
             if (lane >= off) w += up;
         }
-        if (lane < 1024 / kWave) s_cut[64 + lane] = w - total;  // exclusive prefix of the waves
-        if (lane == 1024 / kWave - 1) s_cut[128] = w;           // all pieces
+        if (lane < kWaves) lds[lane] = w - wt;  // exclusive prefix of the waves
+        if (lane == kWaves - 1) lds[kWaves] = w;
     }
     __syncthreads();
-    int pos = s_cut[64 + wave] + incl - cut;
+    *total = lds[kWaves];
+    return lds[wave] + incl - x;
+}
+
+// The piece list: a segment longer than kPieceEvents becomes
+// ceil(len / kPieceEvents) pieces with consecutive piece-state slots.  One
+// workgroup of 1024 threads; thread t handles a contiguous run of segments.
+// With segs: also the item of each cut segment's first piece, in segment
+// order, and their count in n_segs.
+__global__ __launch_bounds__(1024) void piece_table_kernel(const int64_t *__restrict__ cu, int nseg,
+                                                           int4 *__restrict__ items, int *__restrict__ n_items,
+                                                           int *__restrict__ segs, int *__restrict__ n_segs) {
+    __shared__ int s_scan[2][1024 / kWave + 1];
+    const int t = threadIdx.x;
+    const int per = (nseg + 1023) / 1024;
+    const int s0 = min(nseg, t * per), s1 = min(nseg, s0 + per);
+    int cut = 0, cut_segs = 0;
+    // (unrolled: the loads of a thread's segments are independent and go out together)
+#pragma unroll 8
+    for (int sg = s0; sg < s1; ++sg) {
+        const int64_t len = cu[sg + 1] - cu[sg];
+        if (len > kPieceEvents) {
+            cut += int((len + kPieceEvents - 1) / kPieceEvents);
+            ++cut_segs;
+        }
+    }
+    int pieces_total = 0, segs_total = 0;
+    int pos = block_exclusive_scan(cut, s_scan[0], &pieces_total);
+    int spos = segs ? block_exclusive_scan(cut_segs, s_scan[1], &segs_total) : 0;
 #pragma unroll 8
     for (int sg = s0; sg < s1; ++sg) {
         const int64_t len = cu[sg + 1] - cu[sg];
         if (len > kPieceEvents) {
             const int np = int((len + kPieceEvents - 1) / kPieceEvents);
+            if (segs) segs[spos++] = pos;
             for (int q = 0; q < np; ++q, ++pos) items[pos] = make_int4(sg, q, np, pos);
         }
     }
-    if (t == 0) n_items[0] = s_cut[128];
+    if (t == 0) {
+        n_items[0] = pieces_total;
+        if (segs) n_segs[0] = segs_total;
+    }
 }
 
 // For each cut segment (its first piece's item) and head: M_0 = the
@@ -1194,6 +1278,175 @@ __global__ __launch_bounds__(256) void piece_scan_kernel(const int4 *__restrict_
                 pstate[base + int64_t(r) * width] = nm[r];
             }
         }
+    }
+}
+
+// The scan of the stage path (rounding policy, segments longer than
+// kPieceEvents).  One wave per (long segment, virtual head, 64 value
+// columns), a lane per column: M_0 = the segment's initial state rounded to
+// BF16; per stage k, each read of the stage gets z = c^T M_k + z0 (c and z0
+// from MODE 3), stored to the read buffer, then M_(k+1) = P_k M_k + R_k,
+// rounded to BF16 except after the last stage (the final state).
+//
+// The chain is one stage after another, so memory latency must stay off it:
+// the operands of stage k + 2 (R, P, the coefficients and zero-start rows of
+// its 16 events, and the read targets of stage k + 3) are loaded while stage
+// k is computed, into the third of three register sets.  Every load and
+// store is issued whatever the stage holds (events that are not reads load
+// row 0 and store to a scratch word), so the number of memory operations
+// between a load and its use is fixed and the compiler waits for that load
+// only.  P and the coefficients reach every lane through LDS.  Grid:
+// (blocks, heads, column tiles); block b takes long segments b,
+// b + gridDim.x, ...
+template <typename T>
+struct StageScanParams {
+    const int *segs, *n_segs;  // first-piece item of each long segment (piece_table_kernel)
+    const int4 *items;
+    const int64_t *cu;
+    const int *tgt;            // [slots, 16]: read route slot of each event, -1 otherwise
+    const void *initial;
+    void *final_state;
+    const float *pstate, *ptrans, *z0buf, *cbuf;
+    T *zbuf;
+    T *sink;                   // scratch for the stores of events that are not reads
+    int64_t init_bstride, row_stride;
+    int init_dtype, final_dtype;
+    int banks, heads, s_heads, split, width;
+};
+
+struct ScanStage {
+    float r[8];    // R_k rows of the lane's column
+    float pt;      // P_k element `lane` (row lane / 8, column lane % 8)
+    float2 c;      // coefficients 2 (lane % 4), +1 of event lane / 4
+    float z0[16];  // zero-start value of the lane's column for each event
+    int tgt;       // lane e < 16: read route slot of event e, or -1
+};
+
+template <typename T>
+__global__ __launch_bounds__(64) void stage_scan_kernel(StageScanParams<T> p) {
+    constexpr int S = 8, NE = 16;
+    __shared__ __align__(16) float s_p[S * S];
+    __shared__ __align__(16) float s_c[NE][S];
+    const int lane = threadIdx.x;
+    const int head = blockIdx.y;
+    const int col = int(blockIdx.z) * kWave + lane;
+    const bool live = col < p.width;
+    const int colc = live ? col : p.width - 1;  // loads stay in the row
+    const int64_t hw = int64_t(p.heads) * p.width;
+    const int64_t zcol = int64_t(head) * p.width + colc;
+    const int nsegs = p.n_segs[0];
+    for (int j = blockIdx.x; j < nsegs; j += gridDim.x) {
+        const int seg = p.items[p.segs[j]].x;
+        const int64_t start = p.cu[seg], end = p.cu[seg + 1];
+        const int nst = int((end - start + NE - 1) / NE);
+        const int64_t slot0 = start / NE + seg;
+        const int bank = seg % p.banks;
+        const int64_t bidx = seg / p.banks;
+        const int64_t state_offset = int64_t(bank) * p.s_heads * S * p.row_stride +
+                                     int64_t(head / p.split) * S * p.row_stride +
+                                     int64_t(head % p.split) * p.width + colc;
+        float m[S];
+        {
+            const int64_t off = bidx * p.init_bstride + state_offset;
+#pragma unroll
+            for (int r = 0; r < S; ++r)
+                m[r] = round_bf16(p.init_dtype == BDM_BF16
+                                      ? to_f32(static_cast<const bf16_t *>(p.initial)[off + r * p.row_stride])
+                                      : static_cast<const float *>(p.initial)[off + r * p.row_stride]);
+        }
+        // stage indices past the last are clamped to it (their loads are
+        // not used)
+        auto slot_of = [&](int k) { return slot0 + min(k, nst - 1); };
+        auto load_tgt = [&](int k) { return p.tgt[slot_of(k) * NE + (lane & (NE - 1))]; };
+        // loads of stage k into sg, whose tgt (lane e < 16) is already loaded
+        auto issue = [&](int k, ScanStage &sg) {
+            const int64_t sl = slot_of(k);
+            const float *rr = p.pstate + ((sl * p.heads + head) * S) * p.width + colc;
+#pragma unroll
+            for (int r = 0; r < S; ++r) sg.r[r] = rr[r * p.width];
+            sg.pt = p.ptrans[(sl * p.heads + head) * S * S + lane];
+            const int zr = max(__shfl(sg.tgt, lane >> 2, kWave), 0);
+            sg.c = *reinterpret_cast<const float2 *>(p.cbuf + (int64_t(zr) * p.heads + head) * S + 2 * (lane & 3));
+#pragma unroll
+            for (int e = 0; e < NE; ++e) {
+                const int row = max(__builtin_amdgcn_readlane(sg.tgt, e), 0);
+                sg.z0[e] = p.z0buf[int64_t(row) * hw + zcol];
+            }
+        };
+        auto compute = [&](int k, const ScanStage &sg) {
+            __syncthreads();  // the previous stage's LDS reads are done
+            s_p[lane] = sg.pt;
+            *reinterpret_cast<float2 *>(&s_c[lane >> 2][2 * (lane & 3)]) = sg.c;
+            __syncthreads();
+#pragma unroll
+            for (int e = 0; e < NE; ++e) {
+                const int row = __builtin_amdgcn_readlane(sg.tgt, e);
+                float z = 0.f;
+                if (row >= 0) {
+                    const float4 c0 = *reinterpret_cast<const float4 *>(&s_c[e][0]);
+                    const float4 c1 = *reinterpret_cast<const float4 *>(&s_c[e][4]);
+                    const float cv[S] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+                    z = sg.z0[e];
+#pragma unroll
+                    for (int r = 0; r < S; ++r) z = fmaf(cv[r], m[r], z);
+                }
+                T *dst = (row >= 0 && live) ? p.zbuf + int64_t(row) * hw + int64_t(head) * p.width + col
+                                            : p.sink + lane;
+                *dst = from_f32<T>(z);
+            }
+            float nm[S];
+#pragma unroll
+            for (int r = 0; r < S; ++r) {
+                const float4 p0 = *reinterpret_cast<const float4 *>(&s_p[r * S]);
+                const float4 p1 = *reinterpret_cast<const float4 *>(&s_p[r * S + 4]);
+                const float pv[S] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+                float acc = sg.r[r];
+#pragma unroll
+                for (int q = 0; q < S; ++q) acc = fmaf(pv[q], m[q], acc);
+                nm[r] = acc;
+            }
+            const bool last = k + 1 >= nst;
+#pragma unroll
+            for (int r = 0; r < S; ++r) m[r] = last ? nm[r] : round_bf16(nm[r]);
+        };
+        // three register sets in turn, each stage's operands loaded two
+        // stages ahead (a set is never copied: a copy would wait for the
+        // loads in flight into it); the read targets of the stage to issue
+        // next are loaded one stage before (tn)
+        ScanStage sa, sb, sc;
+        sa.tgt = load_tgt(0);
+        issue(0, sa);
+        sb.tgt = load_tgt(1);
+        issue(1, sb);
+        int tn = load_tgt(2);
+#pragma unroll 1
+        for (int k = 0; k < nst; k += 3) {
+            sc.tgt = tn;
+            tn = load_tgt(k + 3);
+            issue(k + 2, sc);
+            compute(k, sa);
+            if (k + 1 >= nst) break;
+            sa.tgt = tn;
+            tn = load_tgt(k + 4);
+            issue(k + 3, sa);
+            compute(k + 1, sb);
+            if (k + 2 >= nst) break;
+            sb.tgt = tn;
+            tn = load_tgt(k + 5);
+            issue(k + 4, sb);
+            compute(k + 2, sc);
+        }
+        if (p.final_state && live) {
+            const int64_t off = bidx * (int64_t(p.banks) * p.s_heads * S * p.row_stride) + state_offset;
+#pragma unroll
+            for (int r = 0; r < S; ++r) {
+                if (p.final_dtype == BDM_BF16)
+                    static_cast<bf16_t *>(p.final_state)[off + r * p.row_stride] = from_f32<bf16_t>(m[r]);
+                else
+                    static_cast<float *>(p.final_state)[off + r * p.row_stride] = m[r];
+            }
+        }
+        __syncthreads();  // LDS reused by the block's next segment
     }
 }
 
@@ -1329,6 +1582,16 @@ struct PieceBuffers {
     int64_t max_pieces = 0;  // 0: the path is off
     int *seg_order = nullptr;  // null: segments in bank order
     bool order_given = false;  // seg_order holds the caller's order (bdm_route_dispatch): no ranking launch
+    // The rounding policy's stage path (0 pieces: off): its piece list and
+    // counts ([0] pieces, [1] long segments), the long segments' first
+    // pieces, the stage slots' R and P, the reads' zero-start rows and
+    // coefficients.
+    int64_t stage_pieces = 0;
+    int4 *st_items = nullptr;
+    int *st_count = nullptr, *st_segs = nullptr;
+    float *st_r = nullptr, *st_p = nullptr, *st_z0 = nullptr, *st_c = nullptr;
+    int *st_tgt = nullptr;
+    void *st_sink = nullptr;
 };
 
 // Profiling events of bdm_forward (phase_events): 0 before the recurrence,
@@ -1422,6 +1685,9 @@ constexpr int kOverlapAux = 3;  // auxiliary streams: at most 4 parts
 struct OverlapAux {
     hipStream_t stream[kOverlapAux] = {};
     hipEvent_t fork = nullptr, join[kOverlapAux] = {};
+    // the stage path's stream and its completion (rounding policy, long segments)
+    hipStream_t stage = nullptr;
+    hipEvent_t stage_done = nullptr;
 };
 
 bool overlap_enabled() {
@@ -1464,6 +1730,8 @@ const OverlapAux *overlap_aux(hipStream_t caller) {
     for (int i = 0; ok && i < kOverlapAux; ++i)
         ok = hipStreamCreateWithFlags(&made.stream[i], hipStreamNonBlocking) == hipSuccess &&
              hipEventCreateWithFlags(&made.join[i], hipEventDisableTiming) == hipSuccess;
+    ok = ok && hipStreamCreateWithFlags(&made.stage, hipStreamNonBlocking) == hipSuccess &&
+         hipEventCreateWithFlags(&made.stage_done, hipEventDisableTiming) == hipSuccess;
     if (!ok) {
         (void)hipGetLastError();
         failed[dev] = true;
@@ -1511,13 +1779,74 @@ int launch_mode0(const void *kernel, dim3 grid, int threads, ForwardParams<T> p,
 // part's combine over its heads' columns after it on the same stream.
 // Phase events: 0 before the first part, 1 after the last part's
 // recurrence, 2 after the join.
+// The rounding policy's stage path on stream st (see lazy_forward_kernel):
+// the piece list of the segments longer than kPieceEvents, MODE 3 over their
+// pieces, the scan.  p0: the MODE 0 parameters; groups: all head groups.
+template <typename T, int CPL>
+int launch_stage_path(const ForwardParams<T> &p0, const PieceBuffers &pb, int threads, int groups, hipStream_t st) {
+    piece_table_kernel<<<1, 1024, 0, st>>>(p0.cu, p0.nseg, pb.st_items, pb.st_count, pb.st_segs, pb.st_count + 1);
+    if (int rc = check_launch("piece_table_kernel")) return rc;
+    ForwardParams<T> p = p0;
+    p.items = pb.st_items;
+    p.n_items = pb.st_count;
+    p.pstate = pb.st_r;
+    p.ptrans = pb.st_p;
+    p.z0buf = pb.st_z0;
+    p.cbuf = pb.st_c;
+    p.tgt = pb.st_tgt;
+    p.seg_order = nullptr;
+    p.skip_long = 0;
+    p.group_base = 0;
+    const dim3 grid(unsigned(pb.stage_pieces), unsigned(groups));
+    if (threads == 64)
+        lazy_forward_kernel<T, CPL, 2, 3><<<grid, 64, 0, st>>>(p);
+    else
+        lazy_forward_kernel<T, CPL, 8, 3><<<grid, 256, 0, st>>>(p);
+    if (int rc = check_launch("lazy_forward_kernel")) return rc;
+    StageScanParams<T> sp{};
+    sp.segs = pb.st_segs;
+    sp.n_segs = pb.st_count + 1;
+    sp.items = pb.st_items;
+    sp.cu = p.cu;
+    sp.tgt = pb.st_tgt;
+    sp.initial = p.initial;
+    sp.final_state = p.final_state;
+    sp.pstate = pb.st_r;
+    sp.ptrans = pb.st_p;
+    sp.z0buf = pb.st_z0;
+    sp.cbuf = pb.st_c;
+    sp.zbuf = p.zbuf;
+    sp.sink = static_cast<T *>(pb.st_sink);
+    sp.init_bstride = p.init_bstride;
+    sp.row_stride = p.row_stride;
+    sp.init_dtype = p.init_dtype;
+    sp.final_dtype = p.final_dtype;
+    sp.banks = p.banks;
+    sp.heads = p.heads;
+    sp.s_heads = p.s_heads;
+    sp.split = p.split;
+    sp.width = p.width;
+    // one block per long segment up to 256 of them (a segment's chain is
+    // the longest stage sequence; more segments than blocks take turns)
+    const int64_t long_max = std::min<int64_t>(p.nseg, p.nt * (p.kw + p.kr) / (kPieceEvents + 1));
+    const unsigned blocks = unsigned(std::max<int64_t>(1, std::min<int64_t>(long_max, 256)));
+    stage_scan_kernel<T><<<dim3(blocks, unsigned(p.heads), unsigned((p.width + kWave - 1) / kWave)), kWave, 0, st>>>(
+        sp);
+    return check_launch("stage_scan_kernel");
+}
+
 template <typename T, int CPL>
 int launch_overlapped(const bdm_forward_args &a, ForwardParams<T> p, const void *kernel, unsigned nseg, int groups,
-                      int threads, const T *zbuf, const OverlapAux &ax, hipStream_t stream) {
+                      int threads, const T *zbuf, const OverlapAux &ax, const PieceBuffers &pb, hipStream_t stream) {
     const int gpr = p.order_gpr;
     const int parts = overlap_parts((groups + gpr - 1) / gpr, groups);
     if (hipEventRecord(ax.fork, stream) != hipSuccess)
         return fail(BDM_ERR_LAUNCH, "forward: forking the combine streams");
+    // the stage path beside the MODE 0 parts (which leave it the long
+    // segments), enqueued after the first part so that part's blocks go out
+    // first; every combine waits for it
+    const bool stage = pb.stage_pieces > 0;
+    if (stage) p.skip_long = 1;
     for (int i = 1; i < parts; ++i) {
         if (hipStreamWaitEvent(ax.stream[i - 1], ax.fork, 0) != hipSuccess)
             return fail(BDM_ERR_LAUNCH, "forward: forking the combine streams");
@@ -1534,6 +1863,15 @@ int launch_overlapped(const bdm_forward_args &a, ForwardParams<T> p, const void 
         pr.group_base = g0;
         pr.order_gpr = min(gpr, g1 - g0);
         if (int rc = launch_mode0<T>(kernel, dim3(nseg, unsigned(g1 - g0)), threads, pr, st)) return rc;
+        if (stage && i == 0) {
+            if (hipStreamWaitEvent(ax.stage, ax.fork, 0) != hipSuccess)
+                return fail(BDM_ERR_LAUNCH, "forward: forking the stage path");
+            if (int rc = launch_stage_path<T, CPL>(p, pb, threads, groups, ax.stage)) return rc;
+            if (hipEventRecord(ax.stage_done, ax.stage) != hipSuccess)
+                return fail(BDM_ERR_LAUNCH, "forward: joining the stage path");
+        }
+        if (stage && hipStreamWaitEvent(st, ax.stage_done, 0) != hipSuccess)
+            return fail(BDM_ERR_LAUNCH, "forward: joining the stage path");
         if (i == parts - 1)
             if (int rc = record_phase(a, 1, st)) return rc;
         const int h0 = g0 * p.heads_per_block;
@@ -1610,7 +1948,8 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, const PieceBuffers &pb, h
             p.n_items = pb.count;
             p.pstate = pb.pstate;
             p.ptrans = pb.ptrans;
-            piece_table_kernel<<<1, 1024, 0, stream>>>(a.cu_seqlens, int(nseg), pb.items, pb.count);
+            piece_table_kernel<<<1, 1024, 0, stream>>>(a.cu_seqlens, int(nseg), pb.items, pb.count, nullptr,
+                                                       nullptr);
             if (int rc = check_launch("piece_table_kernel")) return rc;
             if (pb.seg_order) {
                 if (!pb.order_given) {
@@ -1653,10 +1992,18 @@ int launch_forward(const bdm_forward_args &a, T *zbuf, const PieceBuffers &pb, h
                     if (const OverlapAux *ax = overlap_aux(stream)) {
                         // the shared events are recorded and waited for by one call at a time
                         std::lock_guard<std::mutex> lock(overlap_launch_mutex());
-                        return launch_overlapped<T, CPL>(a, p, kernel, grid.x, int(grid.y), lthreads, zbuf, *ax,
+                        return launch_overlapped<T, CPL>(a, p, kernel, grid.x, int(grid.y), lthreads, zbuf, *ax, pb,
                                                          stream);
                     }
                 }
+            }
+            // the stage path after the sequential kernel, on the same stream
+            if (pb.stage_pieces > 0) {
+                ForwardParams<T> ps = p;
+                ps.skip_long = 1;
+                if (int rc = launch_mode0<T>(kernel, grid, lthreads, ps, stream)) return rc;
+                if (int rc = launch_stage_path<T, CPL>(p, pb, lthreads, int(grid.y), stream)) return rc;
+                return launch_combine<T>(a, zbuf, stream);
             }
             if (int rc = launch_mode0<T>(kernel, grid, lthreads, p, stream)) return rc;
         }
@@ -1689,6 +2036,32 @@ int64_t max_pieces(const bdm_forward_args &a) {
     if (!lazy_path(a) || a.round_interval > 0 || a.snapshots) return 0;
     const int64_t events = a.batch * a.time * (int64_t(a.write_banks) + a.read_banks);
     return 2 * (events / kPieceEvents) + 1;
+}
+
+// BDM_STAGE_PATH=1 runs segments longer than kPieceEvents under the
+// rounding policy on the stage path; otherwise they run whole (the default:
+// its launches cost a forward without long segments ~3 % at C2, and its
+// buffers ~2-3 GiB of workspace at the C2 and C4 sizes).
+bool stage_enabled() {
+    const char *e = getenv("BDM_STAGE_PATH");
+    return e && e[0] == '1' && e[1] == 0;
+}
+
+// Upper bound on the stage path's pieces (0: the path is off).  It runs
+// beside the longest-first MODE 0 launches (their order and auxiliary
+// streams), under the rounding policy without snapshots, where reads exist.
+int64_t stage_pieces(const bdm_forward_args &a) {
+    if (!lazy_path(a) || a.round_interval <= 0 || a.snapshots || a.read_banks <= 0 ||
+        !order_geometry(a.batch * a.bank_count) || !stage_enabled())
+        return 0;
+    const int64_t events = a.batch * a.time * (int64_t(a.write_banks) + a.read_banks);
+    return 2 * (events / kPieceEvents) + 1;
+}
+
+// Stage slots: stage k of segment s has slot cu[s] / 16 + s + k < E / 16 + segments.
+int64_t stage_slots(const bdm_forward_args &a) {
+    const int64_t events = a.batch * a.time * (int64_t(a.write_banks) + a.read_banks);
+    return events / kLazyStage + a.batch * a.bank_count + 1;
 }
 
 // Whether the lazy kernel takes each XCD range's segments longest first
@@ -1799,11 +2172,38 @@ static size_t forward_order_bytes(const bdm_forward_args *a) {
     return bdm::order_path(*a) ? round256(size_t(a->batch) * size_t(a->bank_count) * 4) : 0;
 }
 
+// The stage path's buffers, in this order (sizes in bytes).
+static void forward_stage_parts(const bdm_forward_args *a, size_t (&part)[9]) {
+    const size_t n = size_t(bdm::stage_pieces(*a));
+    for (size_t &x : part) x = 0;
+    if (!n) return;
+    const size_t slots = size_t(bdm::stage_slots(*a));
+    const size_t reads = size_t(a->batch) * size_t(a->time) * size_t(a->read_banks);
+    const size_t cols = size_t(a->heads) * size_t(a->head_width);
+    const size_t vheads = size_t(a->heads) * size_t(bdm::lazy_split(*a));
+    part[0] = round256(n * sizeof(int4));  // piece list
+    part[1] = 256;                          // counts
+    part[2] = round256(n * 4);              // first pieces of the long segments
+    part[3] = round256(slots * 8 * cols * 4);     // R per stage slot: [slots, heads, 8, width]
+    part[4] = round256(slots * vheads * 64 * 4);  // P per stage slot: [slots, heads, 8, 8]
+    part[5] = round256(reads * cols * 4);         // zero-start read rows: [NT*KR, H*v]
+    part[6] = round256(reads * vheads * 8 * 4);   // read coefficients: [NT*KR, heads, 8]
+    part[7] = round256(slots * 16 * 4);           // read targets per stage slot: [slots, 16]
+    part[8] = 256;                                // the scan's scratch word per lane
+}
+
+static size_t forward_stage_bytes(const bdm_forward_args *a) {
+    size_t part[9], total = 0;
+    forward_stage_parts(a, part);
+    for (size_t x : part) total += x;
+    return total;
+}
+
 extern "C" size_t bdm_forward_workspace_size(const bdm_forward_args *a) {
     if (!a || a->batch <= 0 || a->time <= 0 || a->heads <= 0 || a->head_width <= 0 || a->read_banks < 0 ||
         a->write_banks < 0 || a->bank_size <= 0)
         return 0;
-    return forward_zbuf_bytes(a) + forward_piece_bytes(a) + forward_order_bytes(a);
+    return forward_zbuf_bytes(a) + forward_piece_bytes(a) + forward_order_bytes(a) + forward_stage_bytes(a);
 }
 
 extern "C" int bdm_forward(const bdm_forward_args *a, void *workspace, size_t workspace_bytes, void *stream) {
@@ -1862,6 +2262,27 @@ extern "C" int bdm_forward(const bdm_forward_args *a, void *workspace, size_t wo
         pb.seg_order = reinterpret_cast<int *>(ws + forward_zbuf_bytes(a) + forward_piece_bytes(a));
         pb.order_given = a->segment_order != nullptr;
         if (pb.order_given) pb.seg_order = const_cast<int *>(a->segment_order);
+    }
+    pb.stage_pieces = stage_pieces(*a);
+    if (pb.stage_pieces > INT32_MAX / 2) return fail(BDM_ERR_UNSUPPORTED, "forward: too many pieces");
+    if (pb.stage_pieces) {
+        size_t part[9];
+        forward_stage_parts(a, part);
+        char *at = ws + forward_zbuf_bytes(a) + forward_piece_bytes(a) + forward_order_bytes(a);
+        char *ptr[9];
+        for (int i = 0; i < 9; ++i) {
+            ptr[i] = at;
+            at += part[i];
+        }
+        pb.st_items = reinterpret_cast<int4 *>(ptr[0]);
+        pb.st_count = reinterpret_cast<int *>(ptr[1]);
+        pb.st_segs = reinterpret_cast<int *>(ptr[2]);
+        pb.st_r = reinterpret_cast<float *>(ptr[3]);
+        pb.st_p = reinterpret_cast<float *>(ptr[4]);
+        pb.st_z0 = reinterpret_cast<float *>(ptr[5]);
+        pb.st_c = reinterpret_cast<float *>(ptr[6]);
+        pb.st_tgt = reinterpret_cast<int *>(ptr[7]);
+        pb.st_sink = ptr[8];
     }
     if (a->ctrl_dtype == BDM_BF16)
         return dispatch_forward<bf16_t>(*a, static_cast<bf16_t *>(workspace), pb, s);

@@ -575,7 +575,9 @@ def c4_forward(device, steps=10, policy='prefill'):
     state rounded every 16 events, role_bank_kernel.py:153-165), under which a
     segment is not an affine map of its start state and runs as one serial
     chain, so the step is bound by the longest segment.  Reports tokens/s and
-    the segment-length skew."""
+    the segment-length skew; under 'module' also the step with the opt-in
+    stage path (BDM_STAGE_PATH=1: segments longer than 512 events as
+    per-stage affine maps and a scan along the stages)."""
     import torch
     from bdm_amd import BSDMConfig, BankedDeltaMemory, ops
     from bdm_amd.config import near_square_factors
@@ -605,11 +607,26 @@ def c4_forward(device, steps=10, policy='prefill'):
     hot_bytes = hot_path_algorithmic_bytes(cfg, 4, 8192)
     described = {'prefill': 'FP32 state (prefill), long segments cut into pieces',
                  'module': 'BF16 state rounded every 16 events (module forward at H = 8), each segment serial'}
-    return {'tokens_per_s': round(4 * 8192 / sec, 1), 'ms_per_step': round(sec * 1e3, 3), 'steps': steps,
-            'policy': described[policy],
-            'hot_path_bytes_per_token': hot_bytes // (4 * 8192),
-            'hot_path_roofline_frac': round(hot_bytes / sec / 1e9 / HBM_PEAK_GBPS, 4),
-            'max_segment_events': int(lengths.max()), 'mean_segment_events': round(float(lengths.mean()), 1)}
+    result = {'tokens_per_s': round(4 * 8192 / sec, 1), 'ms_per_step': round(sec * 1e3, 3), 'steps': steps,
+              'policy': described[policy],
+              'hot_path_bytes_per_token': hot_bytes // (4 * 8192),
+              'hot_path_roofline_frac': round(hot_bytes / sec / 1e9 / HBM_PEAK_GBPS, 4),
+              'max_segment_events': int(lengths.max()), 'mean_segment_events': round(float(lengths.mean()), 1)}
+    if policy == 'module':
+        previous = os.environ.get('BDM_STAGE_PATH')
+        os.environ['BDM_STAGE_PATH'] = '1'
+        try:
+            with torch.no_grad():
+                sec_stage, _ = timed(step, steps, 1)
+        finally:
+            if previous is None:
+                del os.environ['BDM_STAGE_PATH']
+            else:
+                os.environ['BDM_STAGE_PATH'] = previous
+        result['stage_path'] = {'ms_per_step': round(sec_stage * 1e3, 3),
+                                'tokens_per_s': round(4 * 8192 / sec_stage, 1),
+                                'switch': 'BDM_STAGE_PATH=1'}
+    return result
 
 
 def c5_training(device, steps=10):
