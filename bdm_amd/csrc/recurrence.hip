@@ -380,16 +380,18 @@ typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
 // of zero first).  A VALU read of a DOT instruction's result needs 3 wait
 // states after it; the compiler inserts them for the DOT instructions it
 // generates but cannot see the ones in inline assembly, so the block ends
-// with them (s_nop 2), whatever the compiler schedules next.
+// with them (s_nop 2), whatever the compiler schedules next.  `after` is a
+// value the block is placed after (an unused operand: the block waits for
+// a0, a1 from memory, so it goes after work that does not).
 __device__ __forceinline__ void dot_products4(uint32_t a0, uint32_t a1, uint32_t p_lo, uint32_t p_hi,
-                                              float (&e)[4]) {
+                                              float (&e)[4], float after) {
     asm("v_dot2_f32_bf16 %0, %4, %6, 0\n\t"
         "v_dot2_f32_bf16 %1, %4, %7, 0\n\t"
         "v_dot2_f32_bf16 %2, %5, %6, 0\n\t"
         "v_dot2_f32_bf16 %3, %5, %7, 0\n\t"
         "s_nop 2"
         : "=&v"(e[0]), "=&v"(e[1]), "=&v"(e[2]), "=&v"(e[3])
-        : "v"(a0), "v"(a1), "v"(p_lo), "v"(p_hi));
+        : "v"(a0), "v"(a1), "v"(p_lo), "v"(p_hi), "v"(after));
 }
 
 // acc + (the exact FP32 product of the BF16 halves of a and b_masked that
@@ -432,11 +434,11 @@ struct GatedValues<bf16_t, CPL> {
     // hazard checks, and a scalar write right after it can change the value
     // the instruction reads)
     __device__ __forceinline__ void make_pair(const RawCols<bf16_t, CPL> &w, const RawCols<bf16_t, CPL> &vv,
-                                              uint32_t p_hi, uint32_t p_lo) {
+                                              uint32_t p_hi, uint32_t p_lo, float after) {
 #pragma unroll
         for (int i = 0; i < CPL / 2; i += 2) {
             float e[4];
-            dot_products4(w.u[i], w.u[i + 1], p_lo, p_hi, e);
+            dot_products4(w.u[i], w.u[i + 1], p_lo, p_hi, e, after);
             lo[i] = pack_bf16x2(e[0], 0.f);
             hi[i] = pack_bf16x2(0.f, e[1]);
             lo[i + 1] = pack_bf16x2(e[2], 0.f);
@@ -459,7 +461,7 @@ struct GatedValues<float, CPL> {
         for (int c = 0; c < CPL; ++c) x[c] = (w.f[c] * pw) * vv.f[c];
     }
     __device__ __forceinline__ void make_pair(const RawCols<float, CPL> &w, const RawCols<float, CPL> &vv,
-                                              uint32_t p_hi, uint32_t) {
+                                              uint32_t p_hi, uint32_t, float) {
         make(w, vv, __uint_as_float(p_hi));
     }
     __device__ __forceinline__ float add_to(float acc, int c) const { return acc + x[c]; }
@@ -1002,6 +1004,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == 3 ?
         // write `wi_` of the stage with its v, w rows in (vc, wc)
         auto write_event = [&](int wi_, const RawCols<T, CPL> &vc, const RawCols<T, CPL> &wc) {
             const float *row = &s_rows[wi_][lh][0][0];
+            // (first: the gated value's wait then covers this read only)
+            const uint2 pw2 = *reinterpret_cast<const uint2 *>(row + 3 * S);
             if (__builtin_amdgcn_readfirstlane(eager) != 0) {
                 // hd = diag(d) M first; the update below then uses a and k
                 // (a wave-uniform branch: the stage's form is uniform)
@@ -1030,8 +1034,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == 3 ?
                 for (int r = 1; r < S; ++r) u[c] = fmaf(nalpha[r], h[r][c], u[c]);
             }
             GatedValues<T, CPL> x;
-            const uint2 pw2 = *reinterpret_cast<const uint2 *>(row + 3 * S);
-            x.make_pair(wc, vc, pw2.x, pw2.y);
+            x.make_pair(wc, vc, pw2.x, pw2.y, u[CPL - 1]);
 #pragma unroll
             for (int c = 0; c < CPL; ++c) {
                 u[c] = x.add_to(u[c], c);
