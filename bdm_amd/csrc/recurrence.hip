@@ -1132,7 +1132,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == 3 ?
             const int64_t sl = stage_slot0 + st;
             if (group == 0 && tid < NE)
                 p.tgt[sl * NE + tid] = (tid < n && ((s_rmask[slot] >> tid) & 1u)) ? s_route[slot][tid] : -1;
-            store_state<S, CPL>(p.pstate, BDM_F32, ((sl * p.heads + head) * S) * p.width + col0, p.width, S, h);
+            // R by column: [slot, head, width, 8] (the scan loads a column's 8 rows at once)
+            float *rc = p.pstate + ((sl * p.heads + head) * p.width + col0) * S;
+#pragma unroll
+            for (int c = 0; c < CPL; ++c) {
+                reinterpret_cast<float4 *>(rc + c * S)[0] = make_float4(h[0][c], h[1][c], h[2][c], h[3][c]);
+                reinterpret_cast<float4 *>(rc + c * S)[1] = make_float4(h[4][c], h[5][c], h[6][c], h[7][c]);
+            }
             if (pcol < S && tid < nheads * p.lanes_per_head) {
                 float *pt = p.ptrans + ((sl * p.heads + head) * S) * S;
 #pragma unroll
@@ -1284,59 +1290,59 @@ __global__ __launch_bounds__(256) void piece_scan_kernel(const int4 *__restrict_
     }
 }
 
-// The scan of the stage path (rounding policy, segments longer than
-// kPieceEvents).  One wave per (long segment, virtual head, 64 value
-// columns), a lane per column: M_0 = the segment's initial state rounded to
-// BF16; per stage k, each read of the stage gets z = c^T M_k + z0 (c and z0
-// from MODE 3), stored to the read buffer, then M_(k+1) = P_k M_k + R_k,
-// rounded to BF16 except after the last stage (the final state).
+// The stage path after MODE 3 (rounding policy, segments longer than
+// kPieceEvents), in two kernels on one wave per (..., virtual head, 64 value
+// columns), a lane per column.
 //
-// The chain is one stage after another, so memory latency must stay off it:
-// the operands of stage k + 2 (R, P, the coefficients and zero-start rows of
-// its 16 events, and the read targets of stage k + 3) are loaded while stage
-// k is computed, into the third of three register sets.  Every load and
-// store is issued whatever the stage holds (events that are not reads load
-// row 0 and store to a scratch word), so the number of memory operations
-// between a load and its use is fixed and the compiler waits for that load
-// only.  P and the coefficients reach every lane through LDS.  Grid:
-// (blocks, heads, column tiles); block b takes long segments b,
+// stage_scan_kernel, per long segment: M_0 = the segment's initial state
+// rounded to BF16; M_(k+1) = round(P_k M_k + R_k) along the stages, the last
+// map unrounded (the final state); each stage start state M_k (BF16 values,
+// the rounding points) is stored over R_k, which it no longer needs.  This is
+// the serial chain, so it holds the state update only: a stage is 2 loads of
+// R (a column's 8 rows, [slot, head, width, 8]), 1 of P and 1 store of M_k,
+// and the loads of stage k + 7 are issued while stage k is computed (eight
+// register sets used in turn, every load and store unconditional, so the
+// compiler waits for counted loads and the wave's counter of outstanding
+// memory operations does not fill).  P
+// reaches every lane through LDS.  Block b takes long segments b,
 // b + gridDim.x, ...
+//
+// stage_reads_kernel, per piece (in parallel): each read of stage k gets
+// z = c^T M_k + z0 (c and z0 from MODE 3), stored to the read buffer.
 template <typename T>
-struct StageScanParams {
+struct StageParams {
     const int *segs, *n_segs;  // first-piece item of each long segment (piece_table_kernel)
     const int4 *items;
+    const int *n_items;
     const int64_t *cu;
     const int *tgt;            // [slots, 16]: read route slot of each event, -1 otherwise
     const void *initial;
     void *final_state;
-    const float *pstate, *ptrans, *z0buf, *cbuf;
+    float *pstate;             // R per stage slot ([slots, heads, width, 8]), then M_k (BF16) over it
+    const float *ptrans, *z0buf, *cbuf;
     T *zbuf;
-    T *sink;                   // scratch for the stores of events that are not reads
     int64_t init_bstride, row_stride;
     int init_dtype, final_dtype;
     int banks, heads, s_heads, split, width;
 };
 
-struct ScanStage {
-    float r[8];    // R_k rows of the lane's column
-    float pt;      // P_k element `lane` (row lane / 8, column lane % 8)
-    float2 c;      // coefficients 2 (lane % 4), +1 of event lane / 4
-    float z0[16];  // zero-start value of the lane's column for each event
-    int tgt;       // lane e < 16: read route slot of event e, or -1
+struct ScanOperands {
+    float r[8];  // R_k rows of the lane's column
+    float pt;    // P_k element `lane` (row lane / 8, column lane % 8)
 };
+constexpr int kScanDepth = 8;
 
 template <typename T>
-__global__ __launch_bounds__(64) void stage_scan_kernel(StageScanParams<T> p) {
+__global__ __launch_bounds__(64) void stage_scan_kernel(StageParams<T> p) {
     constexpr int S = 8, NE = 16;
     __shared__ __align__(16) float s_p[S * S];
-    __shared__ __align__(16) float s_c[NE][S];
     const int lane = threadIdx.x;
     const int head = blockIdx.y;
     const int col = int(blockIdx.z) * kWave + lane;
     const bool live = col < p.width;
-    const int colc = live ? col : p.width - 1;  // loads stay in the row
-    const int64_t hw = int64_t(p.heads) * p.width;
-    const int64_t zcol = int64_t(head) * p.width + colc;
+    // lanes past the width repeat the last column: same values to the same
+    // addresses, so their stores need no mask
+    const int colc = live ? col : p.width - 1;
     const int nsegs = p.n_segs[0];
     for (int j = blockIdx.x; j < nsegs; j += gridDim.x) {
         const int seg = p.items[p.segs[j]].x;
@@ -1357,87 +1363,56 @@ __global__ __launch_bounds__(64) void stage_scan_kernel(StageScanParams<T> p) {
                                       ? to_f32(static_cast<const bf16_t *>(p.initial)[off + r * p.row_stride])
                                       : static_cast<const float *>(p.initial)[off + r * p.row_stride]);
         }
-        // stage indices past the last are clamped to it (their loads are
-        // not used)
-        auto slot_of = [&](int k) { return slot0 + min(k, nst - 1); };
-        auto load_tgt = [&](int k) { return p.tgt[slot_of(k) * NE + (lane & (NE - 1))]; };
-        // loads of stage k into sg, whose tgt (lane e < 16) is already loaded
-        auto issue = [&](int k, ScanStage &sg) {
-            const int64_t sl = slot_of(k);
-            const float *rr = p.pstate + ((sl * p.heads + head) * S) * p.width + colc;
-#pragma unroll
-            for (int r = 0; r < S; ++r) sg.r[r] = rr[r * p.width];
-            sg.pt = p.ptrans[(sl * p.heads + head) * S * S + lane];
-            const int zr = max(__shfl(sg.tgt, lane >> 2, kWave), 0);
-            sg.c = *reinterpret_cast<const float2 *>(p.cbuf + (int64_t(zr) * p.heads + head) * S + 2 * (lane & 3));
-#pragma unroll
-            for (int e = 0; e < NE; ++e) {
-                const int row = max(__builtin_amdgcn_readlane(sg.tgt, e), 0);
-                sg.z0[e] = p.z0buf[int64_t(row) * hw + zcol];
-            }
+        auto rows_of = [&](int k) {  // stage k's R (then M_k) column; k past the last: the last
+            return p.pstate + (((slot0 + min(k, nst - 1)) * p.heads + head) * p.width + colc) * S;
         };
-        auto compute = [&](int k, const ScanStage &sg) {
+        auto issue = [&](int k, ScanOperands &o) {
+            const float4 *rr = reinterpret_cast<const float4 *>(rows_of(k));
+            const float4 a = rr[0], b = rr[1];
+            o.r[0] = a.x, o.r[1] = a.y, o.r[2] = a.z, o.r[3] = a.w;
+            o.r[4] = b.x, o.r[5] = b.y, o.r[6] = b.z, o.r[7] = b.w;
+            o.pt = p.ptrans[((slot0 + min(k, nst - 1)) * p.heads + head) * S * S + lane];
+        };
+        auto compute = [&](int k, const ScanOperands &o) {
             __syncthreads();  // the previous stage's LDS reads are done
-            s_p[lane] = sg.pt;
-            *reinterpret_cast<float2 *>(&s_c[lane >> 2][2 * (lane & 3)]) = sg.c;
+            s_p[lane] = o.pt;
             __syncthreads();
-#pragma unroll
-            for (int e = 0; e < NE; ++e) {
-                const int row = __builtin_amdgcn_readlane(sg.tgt, e);
-                float z = 0.f;
-                if (row >= 0) {
-                    const float4 c0 = *reinterpret_cast<const float4 *>(&s_c[e][0]);
-                    const float4 c1 = *reinterpret_cast<const float4 *>(&s_c[e][4]);
-                    const float cv[S] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-                    z = sg.z0[e];
-#pragma unroll
-                    for (int r = 0; r < S; ++r) z = fmaf(cv[r], m[r], z);
-                }
-                T *dst = (row >= 0 && live) ? p.zbuf + int64_t(row) * hw + int64_t(head) * p.width + col
-                                            : p.sink + lane;
-                *dst = from_f32<T>(z);
-            }
             float nm[S];
 #pragma unroll
             for (int r = 0; r < S; ++r) {
                 const float4 p0 = *reinterpret_cast<const float4 *>(&s_p[r * S]);
                 const float4 p1 = *reinterpret_cast<const float4 *>(&s_p[r * S + 4]);
                 const float pv[S] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
-                float acc = sg.r[r];
+                float acc = o.r[r];
 #pragma unroll
                 for (int q = 0; q < S; ++q) acc = fmaf(pv[q], m[q], acc);
                 nm[r] = acc;
             }
+            // M_k over R_k (read above into o.r, whose use in nm has waited
+            // for it), as 8 BF16 values (exact: the rounded start state)
+            *reinterpret_cast<uint4 *>(rows_of(k)) =
+                make_uint4(pack_bf16x2(m[0], m[1]), pack_bf16x2(m[2], m[3]), pack_bf16x2(m[4], m[5]),
+                           pack_bf16x2(m[6], m[7]));
             const bool last = k + 1 >= nst;
 #pragma unroll
             for (int r = 0; r < S; ++r) m[r] = last ? nm[r] : round_bf16(nm[r]);
         };
-        // three register sets in turn, each stage's operands loaded two
-        // stages ahead (a set is never copied: a copy would wait for the
-        // loads in flight into it); the read targets of the stage to issue
-        // next are loaded one stage before (tn)
-        ScanStage sa, sb, sc;
-        sa.tgt = load_tgt(0);
-        issue(0, sa);
-        sb.tgt = load_tgt(1);
-        issue(1, sb);
-        int tn = load_tgt(2);
+        // kScanDepth register sets in turn, each stage's operands loaded
+        // kScanDepth - 1 stages ahead (more than an HBM round trip of this
+        // loop's stages); the loop is unrolled so every set is a fixed
+        // register range, never copied (a copy would wait for the loads in
+        // flight into it)
+        ScanOperands o[kScanDepth];
+#pragma unroll
+        for (int i = 0; i + 1 < kScanDepth; ++i) issue(i, o[i]);
 #pragma unroll 1
-        for (int k = 0; k < nst; k += 3) {
-            sc.tgt = tn;
-            tn = load_tgt(k + 3);
-            issue(k + 2, sc);
-            compute(k, sa);
-            if (k + 1 >= nst) break;
-            sa.tgt = tn;
-            tn = load_tgt(k + 4);
-            issue(k + 3, sa);
-            compute(k + 1, sb);
-            if (k + 2 >= nst) break;
-            sb.tgt = tn;
-            tn = load_tgt(k + 5);
-            issue(k + 4, sb);
-            compute(k + 2, sc);
+        for (int k = 0; k < nst; k += kScanDepth) {
+#pragma unroll
+            for (int i = 0; i < kScanDepth; ++i) {
+                issue(k + i + kScanDepth - 1, o[(i + kScanDepth - 1) % kScanDepth]);
+                compute(k + i, o[i]);
+                if (k + i + 1 >= nst) break;
+            }
         }
         if (p.final_state && live) {
             const int64_t off = bidx * (int64_t(p.banks) * p.s_heads * S * p.row_stride) + state_offset;
@@ -1450,6 +1425,57 @@ __global__ __launch_bounds__(64) void stage_scan_kernel(StageScanParams<T> p) {
             }
         }
         __syncthreads();  // LDS reused by the block's next segment
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(64) void stage_reads_kernel(StageParams<T> p) {
+    constexpr int S = 8, NE = 16;
+    __shared__ __align__(16) float s_c[NE][S];
+    if (int(blockIdx.x) >= p.n_items[0]) return;
+    const int4 it = p.items[blockIdx.x];
+    const int seg = it.x, piece = it.y;
+    const int lane = threadIdx.x;
+    const int head = blockIdx.y;
+    const int col = int(blockIdx.z) * kWave + lane;
+    const bool live = col < p.width;
+    const int colc = live ? col : p.width - 1;
+    const int64_t hw = int64_t(p.heads) * p.width;
+    const int64_t zcol = int64_t(head) * p.width + colc;
+    const int64_t seg_start = p.cu[seg];
+    const int64_t start = seg_start + int64_t(piece) * kPieceEvents;
+    const int64_t end = min(p.cu[seg + 1], start + kPieceEvents);
+    const int nst = int((end - start + NE - 1) / NE);
+    const int64_t slot0 = seg_start / NE + seg + int64_t(piece) * (kPieceEvents / NE);
+#pragma unroll 1
+    for (int st = 0; st < nst; ++st) {
+        const int64_t sl = slot0 + st;
+        const uint4 mq = *reinterpret_cast<const uint4 *>(p.pstate + ((sl * p.heads + head) * p.width + colc) * S);
+        const uint32_t mw[4] = {mq.x, mq.y, mq.z, mq.w};
+        float m[S];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            m[2 * i] = __uint_as_float(mw[i] << 16);
+            m[2 * i + 1] = __uint_as_float(mw[i] & 0xffff0000u);
+        }
+        const int t = p.tgt[sl * NE + (lane & (NE - 1))];
+        const int zr = max(__shfl(t, lane >> 2, kWave), 0);
+        const float2 cc = *reinterpret_cast<const float2 *>(p.cbuf + (int64_t(zr) * p.heads + head) * S + 2 * (lane & 3));
+        __syncthreads();  // the previous stage's LDS reads are done
+        *reinterpret_cast<float2 *>(&s_c[lane >> 2][2 * (lane & 3)]) = cc;
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < NE; ++e) {
+            const int row = __builtin_amdgcn_readlane(t, e);
+            if (row < 0) continue;
+            const float4 c0 = *reinterpret_cast<const float4 *>(&s_c[e][0]);
+            const float4 c1 = *reinterpret_cast<const float4 *>(&s_c[e][4]);
+            const float cv[S] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+            float z = p.z0buf[int64_t(row) * hw + zcol];
+#pragma unroll
+            for (int r = 0; r < S; ++r) z = fmaf(cv[r], m[r], z);
+            if (live) p.zbuf[int64_t(row) * hw + int64_t(head) * p.width + col] = from_f32<T>(z);
+        }
     }
 }
 
@@ -1594,7 +1620,6 @@ struct PieceBuffers {
     int *st_count = nullptr, *st_segs = nullptr;
     float *st_r = nullptr, *st_p = nullptr, *st_z0 = nullptr, *st_c = nullptr;
     int *st_tgt = nullptr;
-    void *st_sink = nullptr;
 };
 
 // Profiling events of bdm_forward (phase_events): 0 before the recurrence,
@@ -1806,10 +1831,11 @@ int launch_stage_path(const ForwardParams<T> &p0, const PieceBuffers &pb, int th
     else
         lazy_forward_kernel<T, CPL, 8, 3><<<grid, 256, 0, st>>>(p);
     if (int rc = check_launch("lazy_forward_kernel")) return rc;
-    StageScanParams<T> sp{};
+    StageParams<T> sp{};
     sp.segs = pb.st_segs;
     sp.n_segs = pb.st_count + 1;
     sp.items = pb.st_items;
+    sp.n_items = pb.st_count;
     sp.cu = p.cu;
     sp.tgt = pb.st_tgt;
     sp.initial = p.initial;
@@ -1819,7 +1845,6 @@ int launch_stage_path(const ForwardParams<T> &p0, const PieceBuffers &pb, int th
     sp.z0buf = pb.st_z0;
     sp.cbuf = pb.st_c;
     sp.zbuf = p.zbuf;
-    sp.sink = static_cast<T *>(pb.st_sink);
     sp.init_bstride = p.init_bstride;
     sp.row_stride = p.row_stride;
     sp.init_dtype = p.init_dtype;
@@ -1829,13 +1854,15 @@ int launch_stage_path(const ForwardParams<T> &p0, const PieceBuffers &pb, int th
     sp.s_heads = p.s_heads;
     sp.split = p.split;
     sp.width = p.width;
+    const unsigned tiles = unsigned((p.width + kWave - 1) / kWave);
     // one block per long segment up to 256 of them (a segment's chain is
     // the longest stage sequence; more segments than blocks take turns)
     const int64_t long_max = std::min<int64_t>(p.nseg, p.nt * (p.kw + p.kr) / (kPieceEvents + 1));
     const unsigned blocks = unsigned(std::max<int64_t>(1, std::min<int64_t>(long_max, 256)));
-    stage_scan_kernel<T><<<dim3(blocks, unsigned(p.heads), unsigned((p.width + kWave - 1) / kWave)), kWave, 0, st>>>(
-        sp);
-    return check_launch("stage_scan_kernel");
+    stage_scan_kernel<T><<<dim3(blocks, unsigned(p.heads), tiles), kWave, 0, st>>>(sp);
+    if (int rc = check_launch("stage_scan_kernel")) return rc;
+    stage_reads_kernel<T><<<dim3(unsigned(pb.stage_pieces), unsigned(p.heads), tiles), kWave, 0, st>>>(sp);
+    return check_launch("stage_reads_kernel");
 }
 
 template <typename T, int CPL>
@@ -2176,7 +2203,7 @@ static size_t forward_order_bytes(const bdm_forward_args *a) {
 }
 
 // The stage path's buffers, in this order (sizes in bytes).
-static void forward_stage_parts(const bdm_forward_args *a, size_t (&part)[9]) {
+static void forward_stage_parts(const bdm_forward_args *a, size_t (&part)[8]) {
     const size_t n = size_t(bdm::stage_pieces(*a));
     for (size_t &x : part) x = 0;
     if (!n) return;
@@ -2192,11 +2219,10 @@ static void forward_stage_parts(const bdm_forward_args *a, size_t (&part)[9]) {
     part[5] = round256(reads * cols * 4);         // zero-start read rows: [NT*KR, H*v]
     part[6] = round256(reads * vheads * 8 * 4);   // read coefficients: [NT*KR, heads, 8]
     part[7] = round256(slots * 16 * 4);           // read targets per stage slot: [slots, 16]
-    part[8] = 256;                                // the scan's scratch word per lane
 }
 
 static size_t forward_stage_bytes(const bdm_forward_args *a) {
-    size_t part[9], total = 0;
+    size_t part[8], total = 0;
     forward_stage_parts(a, part);
     for (size_t x : part) total += x;
     return total;
@@ -2269,11 +2295,11 @@ extern "C" int bdm_forward(const bdm_forward_args *a, void *workspace, size_t wo
     pb.stage_pieces = stage_pieces(*a);
     if (pb.stage_pieces > INT32_MAX / 2) return fail(BDM_ERR_UNSUPPORTED, "forward: too many pieces");
     if (pb.stage_pieces) {
-        size_t part[9];
+        size_t part[8];
         forward_stage_parts(a, part);
         char *at = ws + forward_zbuf_bytes(a) + forward_piece_bytes(a) + forward_order_bytes(a);
-        char *ptr[9];
-        for (int i = 0; i < 9; ++i) {
+        char *ptr[8];
+        for (int i = 0; i < 8; ++i) {
             ptr[i] = at;
             at += part[i];
         }
@@ -2285,7 +2311,6 @@ extern "C" int bdm_forward(const bdm_forward_args *a, void *workspace, size_t wo
         pb.st_z0 = reinterpret_cast<float *>(ptr[5]);
         pb.st_c = reinterpret_cast<float *>(ptr[6]);
         pb.st_tgt = reinterpret_cast<int *>(ptr[7]);
-        pb.st_sink = ptr[8];
     }
     if (a->ctrl_dtype == BDM_BF16)
         return dispatch_forward<bf16_t>(*a, static_cast<bf16_t *>(workspace), pb, s);
