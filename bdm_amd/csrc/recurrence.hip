@@ -581,8 +581,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == 3 ?
     // every wave has left the previous stage's value loop): lazy [0] = -alpha,
     // [1] = beta; eager [0] = -a, [1] = k, [2] = d; a read [0] = gamma; and
     // [3][0..1] the event's route weight bits and bits >> 16 (read with the
-    // row's address, into vector registers).
-    __shared__ __align__(16) float s_rows[NE][HB][4][S];
+    // row's address, into vector registers).  An event's rows are padded by
+    // 16 bytes, so that the prep's 16-byte stores from the 16 event lanes of
+    // a row fall in distinct banks.
+    constexpr int kEventRow = HB * 4 * S + 4;
+    __shared__ __align__(16) float s_rows[NE][kEventRow];
     __shared__ float s_fold[HB][S];  // s at the end of the stage (1 for eager)
     __shared__ int s_eager;
     __shared__ int s_flag[2];  // by stage parity: reset two barriers before its next use
@@ -818,7 +821,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == 3 ?
             // [1] = k / s' (v_rcp_f32); eager: [0] = prod, [1] = k, [2] = d.
             // All three rows are stored for every event (a read uses [0] only;
             // [2] is read in eager stages only).
-            float4 *row = reinterpret_cast<float4 *>(&s_rows[pe][ph][0][4 * half]);
+            float4 *row = reinterpret_cast<float4 *>(&s_rows[pe][ph * 4 * S + 4 * half]);
             float r0[4], r1[4];
             if (eager) {  // (wave-uniform)
 #pragma unroll
@@ -838,7 +841,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == 3 ?
             row[2 * S / 4] = make_float4(d[0], d[1], d[2], d[3]);
             if (half == 0) {
                 const uint32_t bits = __float_as_uint(pw);
-                *reinterpret_cast<uint2 *>(&s_rows[pe][ph][3][0]) = make_uint2(bits, bits >> 16);
+                *reinterpret_cast<uint2 *>(&s_rows[pe][ph * 4 * S + 3 * S]) = make_uint2(bits, bits >> 16);
             }
             if (pe == n - 1) {
 #pragma unroll
@@ -963,7 +966,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == 3 ?
         auto read_event = [&](int i) {
             if (MODE == 1 && !reads_on) return;  // a read does not change the state (wave-uniform)
             const int zrow = __builtin_amdgcn_readlane(m_route, i);
-            const float *row = &s_rows[i][lh][0][0];
+            const float *row = &s_rows[i][lh * 4 * S];
             float gamma[S];
 #pragma unroll
             for (int r = 0; r < S; ++r) gamma[r] = row[r];
@@ -1003,7 +1006,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MODE == 3 ?
         };
         // write `wi_` of the stage with its v, w rows in (vc, wc)
         auto write_event = [&](int wi_, const RawCols<T, CPL> &vc, const RawCols<T, CPL> &wc) {
-            const float *row = &s_rows[wi_][lh][0][0];
+            const float *row = &s_rows[wi_][lh * 4 * S];
             // (first: the gated value's wait then covers this read only)
             const uint2 pw2 = *reinterpret_cast<const uint2 *>(row + 3 * S);
             if (__builtin_amdgcn_readfirstlane(eager) != 0) {
