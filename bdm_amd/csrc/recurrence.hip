@@ -1702,23 +1702,20 @@ int launch_combine(const bdm_forward_args &a, const T *zbuf, hipStream_t stream)
 // reads are written by its own round only, and y's column ranges are
 // disjoint, so results are those of the serial order bit for bit.
 //
-// The auxiliary stream joins the caller's through events (a fork after the
-// segment order, a join after the last combine), so the sequence may be
-// captured in a graph.  A one-lane kernel ahead of the second round on the
-// auxiliary stream lets the first round's blocks reach every slot before the
-// second round's are dispatched (the two would otherwise share the slots
-// from the start, and the first round would end no earlier than the second).
-// Per device: one stream (default priority) and two events, created on the
-// first call that is not under capture; BDM_COMBINE_OVERLAP=0 keeps the
-// serial order.
+// The auxiliary streams join the caller's through events (a fork after the
+// segment order, a join after each auxiliary stream's combine), so the
+// sequence may be captured in a graph.  One-lane kernels ahead of each later
+// round on its auxiliary stream (one per earlier round) let the earlier
+// rounds' blocks reach every slot before its own are dispatched (otherwise
+// the rounds would share the slots from the start, and the first would end
+// no earlier than the last).  Per device: three streams (default priority)
+// and their events, created on the first call that is not under capture;
+// BDM_COMBINE_OVERLAP=0 keeps the serial order.
 constexpr int kOverlapAux = 3;  // auxiliary streams: at most 4 parts
 
 struct OverlapAux {
     hipStream_t stream[kOverlapAux] = {};
     hipEvent_t fork = nullptr, join[kOverlapAux] = {};
-    // the stage path's stream and its completion (rounding policy, long segments)
-    hipStream_t stage = nullptr;
-    hipEvent_t stage_done = nullptr;
 };
 
 bool overlap_enabled() {
@@ -1761,8 +1758,6 @@ const OverlapAux *overlap_aux(hipStream_t caller) {
     for (int i = 0; ok && i < kOverlapAux; ++i)
         ok = hipStreamCreateWithFlags(&made.stream[i], hipStreamNonBlocking) == hipSuccess &&
              hipEventCreateWithFlags(&made.join[i], hipEventDisableTiming) == hipSuccess;
-    ok = ok && hipStreamCreateWithFlags(&made.stage, hipStreamNonBlocking) == hipSuccess &&
-         hipEventCreateWithFlags(&made.stage_done, hipEventDisableTiming) == hipSuccess;
     if (!ok) {
         (void)hipGetLastError();
         failed[dev] = true;
@@ -1814,7 +1809,8 @@ int launch_mode0(const void *kernel, dim3 grid, int threads, ForwardParams<T> p,
 // the piece list of the segments longer than kPieceEvents, MODE 3 over their
 // pieces, the scan.  p0: the MODE 0 parameters; groups: all head groups.
 template <typename T, int CPL>
-int launch_stage_path(const ForwardParams<T> &p0, const PieceBuffers &pb, int threads, int groups, hipStream_t st) {
+int launch_stage_path(const ForwardParams<T> &p0, const PieceBuffers &pb, int threads, int groups, hipStream_t st,
+                      hipEvent_t pieces_done = nullptr) {
     piece_table_kernel<<<1, 1024, 0, st>>>(p0.cu, p0.nseg, pb.st_items, pb.st_count, pb.st_segs, pb.st_count + 1);
     if (int rc = check_launch("piece_table_kernel")) return rc;
     ForwardParams<T> p = p0;
@@ -1834,6 +1830,8 @@ int launch_stage_path(const ForwardParams<T> &p0, const PieceBuffers &pb, int th
     else
         lazy_forward_kernel<T, CPL, 8, 3><<<grid, 256, 0, st>>>(p);
     if (int rc = check_launch("lazy_forward_kernel")) return rc;
+    if (pieces_done && hipEventRecord(pieces_done, st) != hipSuccess)
+        return fail(BDM_ERR_LAUNCH, "forward: recording the stage pieces' end");
     StageParams<T> sp{};
     sp.segs = pb.st_segs;
     sp.n_segs = pb.st_count + 1;
@@ -1868,18 +1866,38 @@ int launch_stage_path(const ForwardParams<T> &p0, const PieceBuffers &pb, int th
     return check_launch("stage_reads_kernel");
 }
 
+// With the stage path (long segments under the rounding policy) its chain of
+// kernels is the critical path, and all of it runs on the caller's stream:
+// the pieces (MODE 3) alone on the device, then the scan, which is bound by
+// its chain's latency, beside the sequential kernel over the other segments
+// (on an auxiliary stream, after the pieces), then the reads and the
+// combine over every column.
+template <typename T, int CPL>
+int launch_overlapped_stage(const bdm_forward_args &a, ForwardParams<T> p, const void *kernel, unsigned nseg,
+                            int groups, int threads, const T *zbuf, const OverlapAux &ax, const PieceBuffers &pb,
+                            hipStream_t stream) {
+    p.skip_long = 1;  // the sequential kernel leaves the long segments to the stage path
+    if (int rc = launch_stage_path<T, CPL>(p, pb, threads, groups, stream, ax.fork)) return rc;
+    hipStream_t side = ax.stream[0];
+    if (hipStreamWaitEvent(side, ax.fork, 0) != hipSuccess)
+        return fail(BDM_ERR_LAUNCH, "forward: forking the stage path");
+    if (int rc = launch_mode0<T>(kernel, dim3(nseg, unsigned(groups)), threads, p, side)) return rc;
+    if (hipEventRecord(ax.join[0], side) != hipSuccess || hipStreamWaitEvent(stream, ax.join[0], 0) != hipSuccess)
+        return fail(BDM_ERR_LAUNCH, "forward: joining the stage path");
+    if (int rc = record_phase(a, 1, stream)) return rc;
+    if (int rc = launch_combine_kernels<T>(a, zbuf, stream)) return rc;
+    return record_phase(a, 2, stream);
+}
+
 template <typename T, int CPL>
 int launch_overlapped(const bdm_forward_args &a, ForwardParams<T> p, const void *kernel, unsigned nseg, int groups,
                       int threads, const T *zbuf, const OverlapAux &ax, const PieceBuffers &pb, hipStream_t stream) {
+    if (pb.stage_pieces > 0)
+        return launch_overlapped_stage<T, CPL>(a, p, kernel, nseg, groups, threads, zbuf, ax, pb, stream);
     const int gpr = p.order_gpr;
     const int parts = overlap_parts((groups + gpr - 1) / gpr, groups);
     if (hipEventRecord(ax.fork, stream) != hipSuccess)
         return fail(BDM_ERR_LAUNCH, "forward: forking the combine streams");
-    // the stage path beside the MODE 0 parts (which leave it the long
-    // segments), enqueued after the first part so that part's blocks go out
-    // first; every combine waits for it
-    const bool stage = pb.stage_pieces > 0;
-    if (stage) p.skip_long = 1;
     for (int i = 1; i < parts; ++i) {
         if (hipStreamWaitEvent(ax.stream[i - 1], ax.fork, 0) != hipSuccess)
             return fail(BDM_ERR_LAUNCH, "forward: forking the combine streams");
@@ -1896,15 +1914,6 @@ int launch_overlapped(const bdm_forward_args &a, ForwardParams<T> p, const void 
         pr.group_base = g0;
         pr.order_gpr = min(gpr, g1 - g0);
         if (int rc = launch_mode0<T>(kernel, dim3(nseg, unsigned(g1 - g0)), threads, pr, st)) return rc;
-        if (stage && i == 0) {
-            if (hipStreamWaitEvent(ax.stage, ax.fork, 0) != hipSuccess)
-                return fail(BDM_ERR_LAUNCH, "forward: forking the stage path");
-            if (int rc = launch_stage_path<T, CPL>(p, pb, threads, groups, ax.stage)) return rc;
-            if (hipEventRecord(ax.stage_done, ax.stage) != hipSuccess)
-                return fail(BDM_ERR_LAUNCH, "forward: joining the stage path");
-        }
-        if (stage && hipStreamWaitEvent(st, ax.stage_done, 0) != hipSuccess)
-            return fail(BDM_ERR_LAUNCH, "forward: joining the stage path");
         if (i == parts - 1)
             if (int rc = record_phase(a, 1, st)) return rc;
         const int h0 = g0 * p.heads_per_block;
