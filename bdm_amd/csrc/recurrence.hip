@@ -1250,46 +1250,88 @@ __global__ __launch_bounds__(1024) void piece_table_kernel(const int64_t *__rest
 // For each cut segment (its first piece's item) and head: M_0 = the
 // segment's initial state, M_(q+1) = P_q M_q + R_q in FP32, stored over R_q
 // (the slot that piece q+1 reads its start state from).  One thread per value
-// column.
+// column.  R_q and P_q do not depend on the chain, so they are loaded
+// kPieceScanDepth steps ahead: a step's 8 R loads, 8 stores and one P load
+// (lane l of each wave loads entry l of P_q, taken to scalar registers by
+// v_readlane) keep 51 memory operations in flight, under the 63 the wave's
+// counter holds.
+constexpr int kPieceScanDepth = 3;
+
 __global__ __launch_bounds__(256) void piece_scan_kernel(const int4 *__restrict__ items,
                                                          const int *__restrict__ n_items, const void *initial,
                                                          int init_dtype, int64_t init_bstride, int banks, int heads,
                                                          int width, int split, int64_t row_stride,
                                                          float *__restrict__ pstate,
                                                          const float *__restrict__ ptrans) {
-    constexpr int S = 8;
+    constexpr int S = 8, D = kPieceScanDepth;
     if (int(blockIdx.x) >= n_items[0]) return;
     const int4 it = items[blockIdx.x];
     if (it.y != 0) return;  // not a first piece
     const int seg = it.x, pieces = it.z, slot0 = it.w, head = blockIdx.y;
     const int bank = seg % banks;
     const int64_t bidx = seg / banks;
-    for (int c = threadIdx.x; c < width; c += blockDim.x) {
+    const int steps = pieces - 1;  // a cut segment has at least two pieces
+    const int lane = int(threadIdx.x) % kWave;
+    for (int c0 = 0; c0 < width; c0 += int(blockDim.x)) {
+        // (every lane of a wave takes part in the P loads; lanes past the
+        // last column shadow it)
+        const int c = c0 + int(threadIdx.x);
+        const int cc = c < width ? c : width - 1;
         float m[S];
         // heads, width: virtual heads of the column split (split per real head)
         const int64_t off = bidx * init_bstride + ((int64_t(bank) * (heads / split) + head / split) * S) * row_stride +
-                            int64_t(head % split) * width + c;
+                            int64_t(head % split) * width + cc;
+        if (init_dtype == BDM_BF16) {
 #pragma unroll
-        for (int r = 0; r < S; ++r)
-            m[r] = init_dtype == BDM_BF16 ? to_f32(static_cast<const bf16_t *>(initial)[off + int64_t(r) * row_stride])
-                                          : static_cast<const float *>(initial)[off + int64_t(r) * row_stride];
-        for (int q = 0; q + 1 < pieces; ++q) {
-            const int64_t base = ((int64_t(slot0 + q) * heads + head) * S) * width + c;
-            const float *pt = ptrans + ((int64_t(slot0 + q) * heads + head) * S) * S;
+            for (int r = 0; r < S; ++r) m[r] = to_f32(static_cast<const bf16_t *>(initial)[off + int64_t(r) * row_stride]);
+        } else {
+#pragma unroll
+            for (int r = 0; r < S; ++r) m[r] = static_cast<const float *>(initial)[off + int64_t(r) * row_stride];
+        }
+        // step q's R column and this lane's entry of P (past the last step,
+        // the last step's again: loaded, never used)
+        auto load_step = [&](int q, float (&rq)[S], float &pq) {
+            const int qq = q < steps ? q : steps - 1;
+            const int64_t slot = int64_t(slot0 + qq) * heads + head;
+#pragma unroll
+            for (int r = 0; r < S; ++r) rq[r] = pstate[(slot * S + r) * width + cc];
+            pq = ptrans[slot * S * S + lane];
+        };
+        // step q from the registers of depth d, then the loads of step q + D
+        // into them (issued before the stores; lanes past the last column
+        // store the values of the column they shadow, which its own lane
+        // stores too)
+        float rq[D][S], pq[D];
+        auto step = [&](int q, int d) {
             float nm[S];
 #pragma unroll
             for (int r = 0; r < S; ++r) {
-                float acc = pstate[base + int64_t(r) * width];
+                float acc = rq[d][r];
 #pragma unroll
-                for (int j = 0; j < S; ++j) acc = fmaf(pt[r * S + j], m[j], acc);
+                for (int j = 0; j < S; ++j)
+                    acc = fmaf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(pq[d]), r * S + j)), m[j], acc);
                 nm[r] = acc;
             }
+            load_step(q + D, rq[d], pq[d]);
+            const int64_t slot = int64_t(slot0 + q) * heads + head;
 #pragma unroll
             for (int r = 0; r < S; ++r) {
                 m[r] = nm[r];
-                pstate[base + int64_t(r) * width] = nm[r];
+                pstate[(slot * S + r) * width + cc] = nm[r];
             }
+        };
+#pragma unroll
+        for (int d = 0; d < D; ++d) load_step(d, rq[d], pq[d]);
+        // whole groups of D steps: every step issues the same memory
+        // operations, so each waits with a count for the loads D steps back
+        int q0 = 0;
+        for (; q0 + D <= steps; q0 += D) {
+#pragma unroll
+            for (int d = 0; d < D; ++d) step(q0 + d, d);
         }
+#pragma unroll
+        for (int d = 0; d < D - 1; ++d)
+            if (q0 + d < steps) step(q0 + d, d);
     }
 }
 
