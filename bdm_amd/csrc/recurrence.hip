@@ -553,9 +553,12 @@ __device__ __forceinline__ void load_vec4(const float *p, float4 &out) { out = *
 //          for each read the zero-start row z0 = gamma^T R_t and the
 //          coefficients c = gamma^T P_t on the stage's start state;
 //   stage_scan_kernel runs M_(k+1) = round(P_k M_k + R_k) along each segment
-//          from its rounded initial state and forms each read of stage k as
-//          c^T M_k + z0.
-// The sums differ from the sequential form's only in FP32 association.
+//          from its rounded initial state, storing each M_k;
+//   stage_reads_kernel forms each read of stage k as c^T M_k + z0.
+// The sums differ from the sequential form's in FP32 association (and so in
+// the BF16 roundings that flips).  MODE 3 takes three waves per SIMD (148
+// VGPRs): held to four (128, a few per-lane addresses spilled and reloaded
+// once per stage) it ran no faster at C4.
 //
 // BUF: v, w rows are read and read rows written through buffer resources
 // with 32-bit offsets (BF16 controllers; v, w and the read buffer below
