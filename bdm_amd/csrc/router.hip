@@ -677,14 +677,22 @@ int route(const void *const *scores, const int64_t *strides, void *const *weight
 // bit 2 t + role of the LDS mask of every selected bank (t the token in the
 // tile, role 1 for a read), as dispatch_tile_count does from stored routes;
 // the popcount of a bank's mask is the tile's count of events in it.
+// The grid is one-dimensional over the (sequence, tile) items, mapped as the
+// scatter maps them: when their number is a multiple of 8, XCD x (blocks x,
+// x + 8, ... in dispatch order) takes the x-th eighth in sequence-major
+// order, so the routes and counts of a sequence stay in the L2 of the XCD
+// whose scatter (and, for 8 sequences, tile scan) reads them next.
 template <int NB>
 __global__ __launch_bounds__(128) void route_tile_count_kernel(RouterRoles<bf16_t> roles, int64_t time, int tiles,
-                                                               int j1, int j2, int32_t *__restrict__ tile_counts,
+                                                               int batch, int j1, int j2,
+                                                               int32_t *__restrict__ tile_counts,
                                                                int32_t *__restrict__ status) {
     extern __shared__ unsigned long long masks[];  // one per bank
     __shared__ uint32_t s_ids[128][4];
     const int banks = j1 * j2;
-    const int tile = int(blockIdx.x), b = int(blockIdx.y);
+    const int64_t items = int64_t(tiles) * batch, lin = blockIdx.x;
+    const int64_t item = items % 8 == 0 ? (lin % 8) * (items / 8) + lin / 8 : lin;
+    const int tile = int(item % tiles), b = int(item / tiles);
     const int t = int(threadIdx.x), role = t >> 6, tl = (t & 63) >> 1, h = t & 1;
     for (int x = t; x < banks; x += 128) masks[x] = 0ull;
     const int64_t tt = int64_t(tile) * 32 + tl;
@@ -741,13 +749,16 @@ int launch_route_tile_count(const void *const *scores, const int64_t *strides, v
         roles.indices[r] = indices[r];
     }
     const int tiles = int((time + 31) / 32);
-    const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(batch));
+    if (batch > INT32_MAX || int64_t(tiles) * batch > int64_t(UINT32_MAX))
+        return fail(BDM_ERR_UNSUPPORTED, "route_dispatch: too many tiles");
+    const unsigned grid = unsigned(int64_t(tiles) * batch);
+    const int nb = int(batch);
     const size_t lds = size_t(j1) * size_t(j2) * sizeof(unsigned long long);
     switch ((max(j1, j2) + 7) / 8) {
-        case 1: route_tile_count_kernel<1><<<grid, 128, lds, stream>>>(roles, time, tiles, j1, j2, tile_counts, status); break;
-        case 2: route_tile_count_kernel<2><<<grid, 128, lds, stream>>>(roles, time, tiles, j1, j2, tile_counts, status); break;
-        case 3: route_tile_count_kernel<3><<<grid, 128, lds, stream>>>(roles, time, tiles, j1, j2, tile_counts, status); break;
-        default: route_tile_count_kernel<4><<<grid, 128, lds, stream>>>(roles, time, tiles, j1, j2, tile_counts, status); break;
+        case 1: route_tile_count_kernel<1><<<grid, 128, lds, stream>>>(roles, time, tiles, nb, j1, j2, tile_counts, status); break;
+        case 2: route_tile_count_kernel<2><<<grid, 128, lds, stream>>>(roles, time, tiles, nb, j1, j2, tile_counts, status); break;
+        case 3: route_tile_count_kernel<3><<<grid, 128, lds, stream>>>(roles, time, tiles, nb, j1, j2, tile_counts, status); break;
+        default: route_tile_count_kernel<4><<<grid, 128, lds, stream>>>(roles, time, tiles, nb, j1, j2, tile_counts, status); break;
     }
     return check_launch("route_tile_count_kernel");
 }
