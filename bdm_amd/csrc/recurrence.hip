@@ -1356,7 +1356,10 @@ __global__ __launch_bounds__(256) void piece_scan_kernel(const int4 *__restrict_
 // b + gridDim.x, ...
 //
 // stage_reads_kernel, per piece (in parallel): each read of stage k gets
-// z = c^T M_k + z0 (c and z0 from MODE 3), stored to the read buffer.
+// z = c^T M_k + z0 (c and z0 from MODE 3), stored to the read buffer.  A
+// stage's M_k and targets are loaded one stage ahead; its c rows and the 16
+// events' z0 rows (a missing read loads row 0) go out together, before any of
+// its stores, so a stage waits for one round trip.
 template <typename T>
 struct StageParams {
     const int *segs, *n_segs;  // first-piece item of each long segment (piece_table_kernel)
@@ -1495,10 +1498,22 @@ __global__ __launch_bounds__(64) void stage_reads_kernel(StageParams<T> p) {
     const int64_t end = min(p.cu[seg + 1], start + kPieceEvents);
     const int nst = int((end - start + NE - 1) / NE);
     const int64_t slot0 = seg_start / NE + seg + int64_t(piece) * (kPieceEvents / NE);
+    // stage st's M_k column (8 BF16 values) and its events' targets (lane e
+    // % 16: event e's read route slot, -1 for a write); past the last stage,
+    // the last stage's again
+    auto load_stage = [&](int st, uint4 &mq, int &t) {
+        const int64_t sl = slot0 + min(st, nst - 1);
+        mq = *reinterpret_cast<const uint4 *>(p.pstate + ((sl * p.heads + head) * p.width + colc) * S);
+        t = p.tgt[sl * NE + (lane & (NE - 1))];
+    };
+    uint4 mq;
+    int t;
+    load_stage(0, mq, t);
 #pragma unroll 1
     for (int st = 0; st < nst; ++st) {
-        const int64_t sl = slot0 + st;
-        const uint4 mq = *reinterpret_cast<const uint4 *>(p.pstate + ((sl * p.heads + head) * p.width + colc) * S);
+        uint4 mq_next;
+        int t_next;
+        load_stage(st + 1, mq_next, t_next);
         const uint32_t mw[4] = {mq.x, mq.y, mq.z, mq.w};
         float m[S];
 #pragma unroll
@@ -1506,24 +1521,27 @@ __global__ __launch_bounds__(64) void stage_reads_kernel(StageParams<T> p) {
             m[2 * i] = __uint_as_float(mw[i] << 16);
             m[2 * i + 1] = __uint_as_float(mw[i] & 0xffff0000u);
         }
-        const int t = p.tgt[sl * NE + (lane & (NE - 1))];
         const int zr = max(__shfl(t, lane >> 2, kWave), 0);
         const float2 cc = *reinterpret_cast<const float2 *>(p.cbuf + (int64_t(zr) * p.heads + head) * S + 2 * (lane & 3));
+        float z[NE];
+#pragma unroll
+        for (int e = 0; e < NE; ++e) z[e] = p.z0buf[int64_t(max(__builtin_amdgcn_readlane(t, e), 0)) * hw + zcol];
         __syncthreads();  // the previous stage's LDS reads are done
         *reinterpret_cast<float2 *>(&s_c[lane >> 2][2 * (lane & 3)]) = cc;
         __syncthreads();
 #pragma unroll
         for (int e = 0; e < NE; ++e) {
             const int row = __builtin_amdgcn_readlane(t, e);
-            if (row < 0) continue;
             const float4 c0 = *reinterpret_cast<const float4 *>(&s_c[e][0]);
             const float4 c1 = *reinterpret_cast<const float4 *>(&s_c[e][4]);
             const float cv[S] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-            float z = p.z0buf[int64_t(row) * hw + zcol];
+            float ze = z[e];
 #pragma unroll
-            for (int r = 0; r < S; ++r) z = fmaf(cv[r], m[r], z);
-            if (live) p.zbuf[int64_t(row) * hw + int64_t(head) * p.width + col] = from_f32<T>(z);
+            for (int r = 0; r < S; ++r) ze = fmaf(cv[r], m[r], ze);
+            if (live && row >= 0) p.zbuf[int64_t(row) * hw + int64_t(head) * p.width + col] = from_f32<T>(ze);
         }
+        mq = mq_next;
+        t = t_next;
     }
 }
 
